@@ -1,0 +1,126 @@
+/*
+ * refcpu — CPU restatement of the reference ncnn-compile lowering for the
+ * Convolution / ConvolutionDepthWise / InnerProduct / int8 hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  Only tests/, __graft_entry__.smoke() and the
+ * cpu_baseline leg of bench.py may load this library, and only as the checker
+ * or the timed CPU baseline.  The product (libnhip) never calls it.
+ *
+ * Every function restates the arithmetic that
+ * /root/reference/lib/Conversion/NCNNToTosa/NCNNToTosa.cpp lowers each ncnn op
+ * to (TOSA -> Linalg -> LLVM loops), in the same operation order and with
+ * every fp32 operation separately rounded (built with -ffp-contract=off, as
+ * the reference's LLVM IR carries no contraction flags).
+ *
+ * Tensors are batches of independent ncnn blobs: [N][C][H][W] where each
+ * [C][H][W] slice is what one call of the reference's generated entry point
+ * sees (ncnn blobs have no batch axis).  `threads` = 0 uses every core
+ * (reference --threads=0, tools/ncnn-compile.cpp:109-114).
+ */
+#ifndef NCNN_AMD_REFCPU_H
+#define NCNN_AMD_REFCPU_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Convolution geometry, reference attribute names (NCNNOps.td:90-121). */
+typedef struct ref_conv_geom {
+  int32_t n, c, h, w;          /* input batch, channels, height, width */
+  int32_t k;                   /* num_output */
+  int32_t kernel_h, kernel_w;
+  int32_t stride_h, stride_w;
+  int32_t dilation_h, dilation_w;
+  int32_t pad_top, pad_bottom, pad_left, pad_right;
+} ref_conv_geom;
+
+int ref_conv_out_h(const ref_conv_geom* g);
+int ref_conv_out_w(const ref_conv_geom* g);
+
+/* a1: fp32 Convolution (bias-initialised accumulator, kh->kw->c reduction). */
+void ref_conv2d_f32(const ref_conv_geom* g, const float* input,
+                    const float* weight, const float* bias, float* output,
+                    int threads);
+
+/* a3: fp32 ConvolutionDepthWise (zero-initialised, then bias add). */
+void ref_dwconv2d_f32(const ref_conv_geom* g, const float* input,
+                      const float* weight, const float* bias, float* output,
+                      int threads);
+
+/* a4: fp32 InnerProduct, out[m][n] = (sum_k in[m][k] W[n][k]) + bias[n]. */
+void ref_innerproduct_f32(int32_t m, int32_t k, int32_t n, const float* input,
+                          const float* weight, const float* bias,
+                          float* output, int threads);
+
+/* a5: quantizeSignedI8 for one value. */
+int8_t ref_quantize_one(float x, float scale);
+
+/* a5: elementwise quantize; scale_count is 1 (scalar) or the channel count,
+ * channel_size = elements per channel (scale index = offset / channel_size). */
+void ref_quantize_f32_i8(int64_t count, const float* input, const float* scale,
+                         int32_t scale_count, int64_t channel_size,
+                         int8_t* output);
+
+/* a6: dequantizeAccumulator reciprocal table r[c] = ws[c]==0 ? 0 : 1/(ws[c]*is). */
+void ref_dequant_reciprocal(int32_t count, const float* weight_scale,
+                            float input_scale, float* reciprocal);
+
+/* a2: int8 Convolution.  input is fp32 (quantized by input_scale) when
+ * input_is_i8 == 0, else int8 (used as is).  weight is int8 [K][C][kh][kw]
+ * (already quantized).  bias may be NULL.  weight_scale has k entries or 1.
+ * scale_term > 100 writes int8 output (requantized by output_scale), else fp32.
+ * activation 1 applies the separate ncnn.relu op afterwards. */
+void ref_conv2d_int8(const ref_conv_geom* g, const void* input,
+                     int32_t input_is_i8, const int8_t* weight,
+                     const float* bias, const float* weight_scale,
+                     int32_t weight_scale_count, float input_scale,
+                     float output_scale, int32_t scale_term,
+                     int32_t activation, void* output, int threads);
+
+/* Integer-only accumulator of the int8 convolution (int64, for brute-force
+ * pinning: exact for any reduction order). */
+void ref_conv2d_i8_acc(const ref_conv_geom* g, const int8_t* input,
+                       const int8_t* weight, int64_t* acc, int threads);
+
+/* a7: ncnn Requantize: dequantizeNcnn(acc, in_scale, bias), optional ReLU,
+ * quantizeSignedI8(out_scale).  Scales/bias per channel (count c) or scalar. */
+void ref_requantize_i32_i8(int32_t c, int64_t channel_size, const int32_t* input,
+                           const float* in_scale, int32_t in_scale_count,
+                           const float* out_scale, int32_t out_scale_count,
+                           const float* bias, int32_t bias_count,
+                           int32_t activation, int8_t* output);
+
+/* ncnn Dequantize: (float)x * scale [+ bias], per channel or scalar. */
+void ref_dequantize_i32_f32(int32_t c, int64_t channel_size, const int32_t* input,
+                            const float* scale, int32_t scale_count,
+                            const float* bias, int32_t bias_count, float* output);
+
+/* a8: ncnn.relu (slope 0) as tosa.clamp; fp32 and int8 variants. */
+void ref_relu_f32(int64_t count, const float* input, float* output);
+void ref_relu_i8(int64_t count, const int8_t* input, int8_t* output);
+
+/* a9: BinaryOp add / Eltwise SUM of equal-shaped tensors. */
+void ref_add_f32(int64_t count, const float* a, const float* b, float* output);
+
+/* a10: Pooling global average: per channel sum over h then w, divided by h*w. */
+void ref_global_avgpool_f32(int32_t n, int32_t c, int32_t h, int32_t w,
+                            const float* input, float* output);
+
+/* a11: foldBatchNormIntoConvolution.  weight [k][per_out] scaled in place,
+ * bias (k entries, may be NULL -> treated as absent) written to bias_out. */
+int ref_bn_fold(int32_t k, int64_t per_out, float* weight, const float* bias,
+                const float* slope, const float* mean, const float* variance,
+                const float* bn_bias, float epsilon, float* bias_out);
+
+/* a12: computeSamePadding.  type -233 = SAME_UPPER, -234 = SAME_LOWER. */
+void ref_same_padding(int32_t input, int32_t kernel, int32_t stride,
+                      int32_t dilation, int32_t type, int32_t* before,
+                      int32_t* after);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif
