@@ -1,0 +1,378 @@
+// Bandwidth-bound kernels of the hot path:
+//   - fp32 ConvolutionDepthWise (NCNNToTosa.cpp:3376-3503): zero-init
+//     depthwise sum over (kh, kw), then the bias add, then the importer's
+//     separate relu (ImportOps.cpp:1004-1010);
+//   - relu, add, global average pooling, quantize / requantize / dequantize.
+//
+// This file is compiled with -ffp-contract=off: the quantize family must
+// round every fp32 step separately to match the reference bit for bit.
+#include <algorithm>
+
+#include "nhip_internal.h"
+
+namespace nhip {
+namespace {
+
+// ---------------------------------------------------------------------------
+// Depthwise.  A workgroup owns `ppb` planes (image x channel) and a band of
+// `ob` output rows of each.  The input rows the band needs are staged in LDS
+// once (coalesced along x, zero halo), every output then reads its
+// kh x kw window from LDS.  HBM traffic is one read of the input and one
+// write of the output.
+struct DwArgs {
+  const float* x;
+  float* y;
+  const float* w;     // [C][kh*kw]
+  const float* bias;  // [C] (zeros when absent)
+  int C, H, W, OH, OW;
+  int kh, kw, sh, sw, dh, dw, pt, pl;
+  int planes;         // n*C
+  int ppb, ob, bands; // planes per block, output rows per band, bands per plane
+  int ir, lw;         // LDS rows / row width per plane
+  int act;
+};
+
+__global__ __launch_bounds__(256) void dwconv_f32_kernel(DwArgs a) {
+  extern __shared__ float lds[];
+  const int band = blockIdx.x % a.bands;
+  const int pgrp = blockIdx.x / a.bands;
+  const int plane0 = pgrp * a.ppb;
+  const int oy0 = band * a.ob;
+  const int iy0 = oy0 * a.sh - a.pt;
+  const int ix0 = -a.pl;
+  const int per_plane = a.ir * a.lw;
+  const int total_in = a.ppb * per_plane;
+  for (int e = threadIdx.x; e < total_in; e += blockDim.x) {
+    const int pi = e / per_plane;
+    const int r = e - pi * per_plane;
+    const int ry = r / a.lw, rx = r - (r / a.lw) * a.lw;
+    const int plane = plane0 + pi;
+    const int y = iy0 + ry, x = ix0 + rx;
+    float v = 0.f;
+    if (plane < a.planes && (unsigned)y < (unsigned)a.H && (unsigned)x < (unsigned)a.W)
+      v = a.x[(int64_t)plane * a.H * a.W + (int64_t)y * a.W + x];
+    lds[e] = v;
+  }
+  __syncthreads();
+  const int rows = min(a.ob, a.OH - oy0);
+  const int per_out = rows * a.OW;
+  const int total_out = a.ppb * per_out;
+  for (int e = threadIdx.x; e < total_out; e += blockDim.x) {
+    const int pi = e / per_out;
+    const int r = e - pi * per_out;
+    const int oy = r / a.OW, ox = r - (r / a.OW) * a.OW;
+    const int plane = plane0 + pi;
+    if (plane >= a.planes) break;
+    const int c = plane % a.C;
+    const float* wc = a.w + (int64_t)c * a.kh * a.kw;
+    const float* src = lds + pi * per_plane + (oy * a.sh) * a.lw + ox * a.sw;
+    float acc = 0.f;
+    for (int i = 0; i < a.kh; ++i)
+      for (int j = 0; j < a.kw; ++j)
+        acc += src[i * a.dh * a.lw + j * a.dw] * wc[i * a.kw + j];
+    acc = acc + a.bias[c];
+    if (a.act == NHIP_ACT_RELU) acc = acc < 0.f ? 0.f : acc;
+    a.y[(int64_t)plane * a.OH * a.OW + (int64_t)(oy0 + oy) * a.OW + ox] = acc;
+  }
+}
+
+// Same 3x3 stride-1 case with the window unrolled and each thread producing
+// four consecutive outputs of a row (one 3x6 LDS window).
+__global__ __launch_bounds__(256) void dwconv3x3s1_f32_kernel(DwArgs a) {
+  extern __shared__ float lds[];
+  const int band = blockIdx.x % a.bands;
+  const int pgrp = blockIdx.x / a.bands;
+  const int plane0 = pgrp * a.ppb;
+  const int oy0 = band * a.ob;
+  const int iy0 = oy0 - a.pt;
+  const int ix0 = -a.pl;
+  const int per_plane = a.ir * a.lw;
+  const int total_in = a.ppb * per_plane;
+  for (int e = threadIdx.x; e < total_in; e += blockDim.x) {
+    const int pi = e / per_plane;
+    const int r = e - pi * per_plane;
+    const int ry = r / a.lw, rx = r - (r / a.lw) * a.lw;
+    const int plane = plane0 + pi;
+    const int y = iy0 + ry, x = ix0 + rx;
+    float v = 0.f;
+    if (plane < a.planes && (unsigned)y < (unsigned)a.H && (unsigned)x < (unsigned)a.W)
+      v = a.x[(int64_t)plane * a.H * a.W + (int64_t)y * a.W + x];
+    lds[e] = v;
+  }
+  __syncthreads();
+  const int rows = min(a.ob, a.OH - oy0);
+  const int quads = (a.OW + 3) / 4;
+  const int per_out = rows * quads;
+  const int total_out = a.ppb * per_out;
+  for (int e = threadIdx.x; e < total_out; e += blockDim.x) {
+    const int pi = e / per_out;
+    const int r = e - pi * per_out;
+    const int oy = r / quads, ox = (r - (r / quads) * quads) * 4;
+    const int plane = plane0 + pi;
+    if (plane >= a.planes) break;
+    const int c = plane % a.C;
+    const float* wc = a.w + (int64_t)c * 9;
+    float wr[9];
+#pragma unroll
+    for (int t = 0; t < 9; ++t) wr[t] = wc[t];
+    const float* src = lds + pi * per_plane + oy * a.lw + ox;
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+      float row[6];
+#pragma unroll
+      for (int t = 0; t < 6; ++t) row[t] = (ox + t < a.lw) ? src[i * a.lw + t] : 0.f;
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int j = 0; j < 3; ++j) acc[q] += row[q + j] * wr[i * 3 + j];
+    }
+    const float b = a.bias[c];
+    float* dst = a.y + (int64_t)plane * a.OH * a.OW + (int64_t)(oy0 + oy) * a.OW + ox;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      if (ox + q < a.OW) {
+        float v = acc[q] + b;
+        if (a.act == NHIP_ACT_RELU) v = v < 0.f ? 0.f : v;
+        dst[q] = v;
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ int8_t quantize_i8(float x, float scale) {
+#pragma clang fp contract(off)
+  const float s = x * scale;
+  if (s != s) return 0;
+  float r = (s >= 0.0f) ? floorf(s + 0.5f) : ceilf(s - 0.5f);
+  r = fminf(r, 127.0f);
+  r = fmaxf(r, -127.0f);
+  return (int8_t)(int)r;
+}
+
+__global__ void relu_f32_kernel(const float* x, float* y, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const float v = x[i];
+    y[i] = v < 0.f ? 0.f : v;
+  }
+}
+
+__global__ void relu_i8_kernel(const int8_t* x, int8_t* y, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int8_t v = x[i];
+    y[i] = v < 0 ? 0 : v;
+  }
+}
+
+__global__ void add_f32_kernel(const float* a, const float* b, float* y, int64_t n, int relu) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    float v = a[i] + b[i];
+    if (relu) v = v < 0.f ? 0.f : v;
+    y[i] = v;
+  }
+}
+
+// One wave per (image, channel) plane: sum, then divide by h*w.
+__global__ __launch_bounds__(256) void gap_f32_kernel(const float* x, float* y, int64_t planes, int hw) {
+  const int64_t plane = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (plane >= planes) return;
+  const float* p = x + plane * hw;
+  float s = 0.f;
+  for (int i = lane; i < hw; i += 64) s += p[i];
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
+  if (lane == 0) y[plane] = s / (float)hw;
+}
+
+__global__ void quantize_f32_i8_kernel(const float* x, int8_t* y, int64_t n, int c,
+                                       int64_t plane, const float* scale, int scale_count) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int ch = (int)((i / plane) % c);
+    y[i] = quantize_i8(x[i], scale[scale_count == 1 ? 0 : ch]);
+  }
+}
+
+__global__ void requantize_kernel(const int32_t* x, int8_t* y, int64_t n, int c, int64_t plane,
+                                  const float* isc, int isn, const float* osc, int osn,
+                                  const float* bias, int bn, int act) {
+#pragma clang fp contract(off)
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int ch = (int)((i / plane) % c);
+    float f = (float)x[i] * isc[isn == 1 ? 0 : ch];
+    if (bias) f = f + bias[bn == 1 ? 0 : ch];
+    if (act == NHIP_ACT_RELU) f = f < 0.f ? 0.f : f;
+    y[i] = quantize_i8(f, osc[osn == 1 ? 0 : ch]);
+  }
+}
+
+__global__ void dequantize_kernel(const int32_t* x, float* y, int64_t n, int c, int64_t plane,
+                                  const float* sc, int sn, const float* bias, int bn) {
+#pragma clang fp contract(off)
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int ch = (int)((i / plane) % c);
+    float f = (float)x[i] * sc[sn == 1 ? 0 : ch];
+    if (bias) f = f + bias[bn == 1 ? 0 : ch];
+    y[i] = f;
+  }
+}
+
+unsigned grid_for(int64_t n) {
+  const int64_t blocks = ceil_div(n, 256);
+  const int64_t cap = 64LL * cu_count();
+  return (unsigned)(blocks < cap ? (blocks > 0 ? blocks : 1) : cap);
+}
+
+}  // namespace
+
+int launch_dwconv_f32(const nhip_conv_plan* p, const float* in, float* out,
+                      int n, int h, int w, int oh, int ow, hipStream_t s) {
+  DwArgs a{};
+  a.x = in;
+  a.y = out;
+  a.w = p->weight;
+  a.bias = p->bias;
+  a.C = p->g.c;
+  a.H = h;
+  a.W = w;
+  a.OH = oh;
+  a.OW = ow;
+  a.kh = p->g.kh;
+  a.kw = p->g.kw;
+  a.sh = p->g.sh;
+  a.sw = p->g.sw;
+  a.dh = p->g.dh;
+  a.dw = p->g.dw;
+  a.pt = p->g.pt;
+  a.pl = p->g.pl;
+  a.planes = n * p->g.c;
+  a.act = p->g.act;
+  a.lw = (ow - 1) * a.sw + (a.kw - 1) * a.dw + 1;
+  // Band sizing: about 1024 outputs per workgroup.
+  const int plane_out = oh * ow;
+  if (plane_out >= 512) {
+    a.ppb = 1;
+    a.ob = std::max(1, std::min(oh, 1024 / ow));
+  } else {
+    a.ppb = std::max(1, 1024 / plane_out);
+    a.ob = oh;
+  }
+  a.ir = (a.ob - 1) * a.sh + (a.kh - 1) * a.dh + 1;
+  // Keep the LDS footprint within 32 KB per workgroup.
+  while (a.ppb > 1 && (int64_t)a.ppb * a.ir * a.lw * 4 > 32768) a.ppb /= 2;
+  while (a.ob > 1 && (int64_t)a.ppb * a.ir * a.lw * 4 > 32768) {
+    a.ob = (a.ob + 1) / 2;
+    a.ir = (a.ob - 1) * a.sh + (a.kh - 1) * a.dh + 1;
+  }
+  const int64_t lds = (int64_t)a.ppb * a.ir * a.lw * 4;
+  if (lds > 65536)
+    return fail(NHIP_STATUS_UNSUPPORTED, "depthwise: input rows too wide for LDS staging");
+  a.bands = (int)ceil_div(oh, a.ob);
+  const int64_t blocks = ceil_div(a.planes, a.ppb) * a.bands;
+  const bool fast = a.kh == 3 && a.kw == 3 && a.sh == 1 && a.sw == 1 && a.dh == 1 && a.dw == 1;
+  if (fast) {
+    NHIP_LAUNCH("dwconv3x3s1_f32", s, dwconv3x3s1_f32_kernel, dim3((unsigned)blocks), dim3(256), (size_t)lds, s, a);
+    return check_launch("dwconv3x3s1_f32");
+  }
+  NHIP_LAUNCH("dwconv_f32", s, dwconv_f32_kernel, dim3((unsigned)blocks), dim3(256), (size_t)lds, s, a);
+  return check_launch("dwconv_f32");
+}
+
+}  // namespace nhip
+
+using namespace nhip;
+
+extern "C" {
+
+int nhip_relu_f32(const float* input, float* output, int64_t count, void* stream) {
+  if (!input || !output) return fail(NHIP_STATUS_NULL_POINTER, "relu: null pointer");
+  if (count < 0) return fail(NHIP_STATUS_INVALID_SHAPE, "relu: negative count");
+  if (count == 0) return ok();
+  NHIP_LAUNCH("relu_f32", as_stream(stream), relu_f32_kernel, dim3(grid_for(count)), dim3(256), 0, as_stream(stream), input,
+                     output, count);
+  return check_launch("relu_f32");
+}
+
+int nhip_relu_i8(const int8_t* input, int8_t* output, int64_t count, void* stream) {
+  if (!input || !output) return fail(NHIP_STATUS_NULL_POINTER, "relu_i8: null pointer");
+  if (count < 0) return fail(NHIP_STATUS_INVALID_SHAPE, "relu_i8: negative count");
+  if (count == 0) return ok();
+  NHIP_LAUNCH("relu_i8", as_stream(stream), relu_i8_kernel, dim3(grid_for(count)), dim3(256), 0, as_stream(stream), input,
+                     output, count);
+  return check_launch("relu_i8");
+}
+
+int nhip_add_f32(const float* a, const float* b, float* output, int64_t count, int32_t relu,
+                 void* stream) {
+  if (!a || !b || !output) return fail(NHIP_STATUS_NULL_POINTER, "add: null pointer");
+  if (count < 0) return fail(NHIP_STATUS_INVALID_SHAPE, "add: negative count");
+  if (count == 0) return ok();
+  NHIP_LAUNCH("add_f32", as_stream(stream), add_f32_kernel, dim3(grid_for(count)), dim3(256), 0, as_stream(stream), a, b,
+                     output, count, relu ? 1 : 0);
+  return check_launch("add_f32");
+}
+
+int nhip_global_avgpool_f32(const float* input, float* output, int32_t n, int32_t c, int32_t h,
+                            int32_t w, void* stream) {
+  if (!input || !output) return fail(NHIP_STATUS_NULL_POINTER, "global_avgpool: null pointer");
+  if (n < 0 || c <= 0 || h <= 0 || w <= 0)
+    return fail(NHIP_STATUS_INVALID_SHAPE, "global_avgpool: invalid shape");
+  if (n == 0) return ok();
+  const int64_t planes = (int64_t)n * c;
+  NHIP_LAUNCH("global_avgpool_f32", as_stream(stream), gap_f32_kernel, dim3((unsigned)ceil_div(planes, 4)), dim3(256), 0,
+                     as_stream(stream), input, output, planes, h * w);
+  return check_launch("global_avgpool_f32");
+}
+
+int nhip_quantize_f32_i8(const float* input, int8_t* output, int32_t n, int32_t c, int64_t plane,
+                         const float* scale, int32_t scale_count, void* stream) {
+  if (!input || !output || !scale) return fail(NHIP_STATUS_NULL_POINTER, "quantize: null pointer");
+  if (n < 0 || c <= 0 || plane <= 0 || (scale_count != 1 && scale_count != c))
+    return fail(NHIP_STATUS_INVALID_SHAPE, "quantize: invalid shape or scale count");
+  const int64_t count = (int64_t)n * c * plane;
+  if (count == 0) return ok();
+  NHIP_LAUNCH("quantize_f32_i8", as_stream(stream), quantize_f32_i8_kernel, dim3(grid_for(count)), dim3(256), 0, as_stream(stream),
+                     input, output, count, c, plane, scale, scale_count);
+  return check_launch("quantize_f32_i8");
+}
+
+int nhip_requantize_i32_i8(const int32_t* input, int8_t* output, int32_t n, int32_t c,
+                           int64_t plane, const float* in_scale, int32_t in_scale_count,
+                           const float* out_scale, int32_t out_scale_count, const float* bias,
+                           int32_t bias_count, int32_t activation, void* stream) {
+  if (!input || !output || !in_scale || !out_scale)
+    return fail(NHIP_STATUS_NULL_POINTER, "requantize: null pointer");
+  if (n < 0 || c <= 0 || plane <= 0 || (in_scale_count != 1 && in_scale_count != c) ||
+      (out_scale_count != 1 && out_scale_count != c) ||
+      (bias && bias_count != 1 && bias_count != c))
+    return fail(NHIP_STATUS_INVALID_SHAPE, "requantize: invalid shape or scale count");
+  const int64_t count = (int64_t)n * c * plane;
+  if (count == 0) return ok();
+  NHIP_LAUNCH("requantize_i32_i8", as_stream(stream), requantize_kernel, dim3(grid_for(count)), dim3(256), 0, as_stream(stream),
+                     input, output, count, c, plane, in_scale, in_scale_count, out_scale,
+                     out_scale_count, bias, bias_count, activation);
+  return check_launch("requantize_i32_i8");
+}
+
+int nhip_dequantize_i32_f32(const int32_t* input, float* output, int32_t n, int32_t c,
+                            int64_t plane, const float* scale, int32_t scale_count,
+                            const float* bias, int32_t bias_count, void* stream) {
+  if (!input || !output || !scale) return fail(NHIP_STATUS_NULL_POINTER, "dequantize: null pointer");
+  if (n < 0 || c <= 0 || plane <= 0 || (scale_count != 1 && scale_count != c) ||
+      (bias && bias_count != 1 && bias_count != c))
+    return fail(NHIP_STATUS_INVALID_SHAPE, "dequantize: invalid shape or scale count");
+  const int64_t count = (int64_t)n * c * plane;
+  if (count == 0) return ok();
+  NHIP_LAUNCH("dequantize_i32_f32", as_stream(stream), dequantize_kernel, dim3(grid_for(count)), dim3(256), 0, as_stream(stream),
+                     input, output, count, c, plane, scale, scale_count, bias, bias_count);
+  return check_launch("dequantize_i32_f32");
+}
+
+}  // extern "C"

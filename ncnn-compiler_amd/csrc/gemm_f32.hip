@@ -1,0 +1,475 @@
+// fp32 MFMA GEMM core (v_mfma_f32_32x32x2_f32, wave64) and the three
+// contractions that use it:
+//   - implicit-GEMM Convolution over NCHW blobs (reference ConvertConvolution
+//     fp32 path, NCNNToTosa.cpp:1316-1529, lowered upstream to
+//     linalg.conv_2d_nhwc_hwcf: out = bias + sum_{kh,kw,c} x*w);
+//   - the 36 batched GEMMs of Winograd F(4,3) (M[xi] = U[xi] * V[xi]);
+//   - InnerProduct (NCNNToTosa.cpp:5254-5392: zero-init matmul, then bias).
+//
+// GEMM view: D[i][j] = sum_k A[i][k] * B[k][j].  A rows i are output channels
+// (conv, Winograd) or input rows m (InnerProduct); B columns j are output
+// pixels, Winograd tiles, or InnerProduct outputs.  One workgroup = 4 waves
+// (2x2) computes a BM x BN tile; each wave a (BM/2) x (BN/2) tile built from
+// 32x32 MFMA blocks.  K advances in chunks of 16 through double-buffered LDS.
+//
+// MFMA k mapping: in chunk-local step s (0..7) lane l supplies k = 8*(l/32)+s
+// for both operands, so each lane reads 8 consecutive k of its A row (two
+// ds_read_b128) instead of 16 scattered words.  Any permutation of k is valid
+// for a dot product as long as A and B use the same one.
+#include "nhip_internal.h"
+
+namespace nhip {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kBK = 16;
+constexpr int kRowPad = 4;  // LDS row padding (floats): conflict-free b128 reads
+
+enum class Mode { Conv, Wino, IP };
+
+struct GemmArgs {
+  // A operand
+  const float* a;        // conv/wino: weights [m_pad][lda]; IP: input [M][lda]
+  int64_t a_batch;       // elements between Winograd batches (xi)
+  int lda;
+  int m;                 // valid rows of the problem (out channels / IP rows)
+  // B operand
+  const float* b;        // conv: input NCHW; wino: V [36][c_pad][ldb]; IP: W [n_pad][ldb]
+  int64_t b_batch;
+  int ldb;
+  int n;                 // valid columns (pixels / tiles / IP outputs)
+  int kdim;              // reduction length (multiple of kBK after padding)
+  int k_valid;           // IP: valid input length (loads past it read 0)
+  // conv geometry
+  const int* ktab;
+  int C, H, W, OW, OHW, sh, sw, pt, pl;
+  // epilogue
+  float* d;              // conv: out NCHW; wino: M [36][m_pad][ldd]; IP: out [M][ldd]
+  int64_t d_batch;
+  int ldd;
+  const float* bias;
+  const float* residual;
+  int act;
+  int splits;            // split-K factor (IP): >1 writes raw partials to d
+  int a_vec4;            // IP: lda % 4 == 0 (float4 A loads allowed)
+};
+
+__device__ __forceinline__ float apply_act(float v, int act) {
+  if (act == NHIP_ACT_RELU) return v < 0.0f ? 0.0f : v;
+  if (act == NHIP_ACT_SIGMOID) return 1.0f / (1.0f + __expf(-v));
+  return v;
+}
+
+template <int BM, int BN, Mode MODE>
+__global__ __launch_bounds__(kThreads) void gemm_f32_kernel(GemmArgs g) {
+  constexpr int TM = BM / 64;  // 32x32 blocks per wave along i
+  constexpr int TN = BN / 64;  // along j
+  constexpr int AS = kBK + kRowPad;                 // As[BM][AS]
+  constexpr bool B_KJ = (MODE == Mode::Wino);       // Bs[kBK][BN+pad] else Bs[BN][AS]
+  constexpr int BS_ROW = B_KJ ? (BN + kRowPad) : AS;
+  constexpr int B_ELEMS = B_KJ ? kBK * BS_ROW : BN * AS;
+  __shared__ __attribute__((aligned(16))) float As[2][BM * AS];
+  __shared__ __attribute__((aligned(16))) float Bs[2][B_ELEMS];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int li = lane & 31, lh = lane >> 5;
+
+  const int j0 = blockIdx.x * BN;
+  const int i0 = blockIdx.y * BM;
+  int batch = 0, split = 0;
+  if constexpr (MODE == Mode::Wino) batch = blockIdx.z;
+  if constexpr (MODE == Mode::IP) split = blockIdx.z;
+
+  const float* A = g.a + (int64_t)batch * g.a_batch;
+  const float* B = g.b + (int64_t)batch * g.b_batch;
+
+  const int nk_total = g.kdim / kBK;
+  int kt_begin = 0, kt_end = nk_total;
+  if constexpr (MODE == Mode::IP) {
+    const int per = (nk_total + g.splits - 1) / g.splits;
+    kt_begin = split * per;
+    kt_end = min(nk_total, kt_begin + per);
+  }
+
+  // ---- A loader: BM x 16 floats = BM*4 float4, (BM*4)/256 per thread.
+  constexpr int A_LD = BM * 4 / kThreads;
+  float4 ra[A_LD];
+  auto load_a = [&](int kt) {
+#pragma unroll
+    for (int u = 0; u < A_LD; ++u) {
+      const int q = tid + u * kThreads;
+      const int row = q >> 2, kq = (q & 3) * 4;
+      const int k = kt * kBK + kq;
+      if constexpr (MODE == Mode::IP) {
+        const int r = i0 + row;
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (r < g.m) {
+          const float* src = A + (int64_t)r * g.lda;
+          if (g.a_vec4) {
+            if (k < g.k_valid) v = *reinterpret_cast<const float4*>(src + k);
+          } else {
+            v.x = (k + 0 < g.k_valid) ? src[k + 0] : 0.f;
+            v.y = (k + 1 < g.k_valid) ? src[k + 1] : 0.f;
+            v.z = (k + 2 < g.k_valid) ? src[k + 2] : 0.f;
+            v.w = (k + 3 < g.k_valid) ? src[k + 3] : 0.f;
+          }
+        }
+        ra[u] = v;
+      } else {
+        ra[u] = *reinterpret_cast<const float4*>(A + (int64_t)(i0 + row) * g.lda + k);
+      }
+    }
+  };
+  auto store_a = [&](int buf) {
+#pragma unroll
+    for (int u = 0; u < A_LD; ++u) {
+      const int q = tid + u * kThreads;
+      const int row = q >> 2, kq = (q & 3) * 4;
+      *reinterpret_cast<float4*>(&As[buf][row * AS + kq]) = ra[u];
+    }
+  };
+
+  // ---- B loader.
+  // Conv: im2col gather; thread owns pixel column jj = tid % BN and KPT
+  // consecutive k (KPT = 16*BN/256).  Wino: V rows [k][j] are contiguous in j
+  // -> float4 loads.  IP: W [j][k] rows, like A.
+  constexpr int KPT = kBK * BN / kThreads;
+  constexpr int B_LD4 = BN * 4 / kThreads;  // float4 per thread (Wino / IP)
+  float rb[(MODE == Mode::Conv) ? KPT : 1];
+  float4 rb4[(MODE == Mode::Conv) ? 1 : B_LD4];
+
+  // Conv per-thread pixel state (fixed for the whole block).
+  const int jj = tid % BN;
+  const int kg = __builtin_amdgcn_readfirstlane(tid / BN);
+  const float* img_base = nullptr;
+  int iy0 = 0, ix0 = 0;
+  bool pix_ok = false;
+  if constexpr (MODE == Mode::Conv) {
+    const int p = j0 + jj;
+    pix_ok = p < g.n;
+    const int pp = pix_ok ? p : 0;
+    const int img = pp / g.OHW;
+    const int rem = pp - img * g.OHW;
+    const int oh = rem / g.OW;
+    const int ow = rem - oh * g.OW;
+    iy0 = oh * g.sh - g.pt;
+    ix0 = ow * g.sw - g.pl;
+    img_base = B + (int64_t)img * g.C * g.H * g.W;
+  }
+
+  auto load_b = [&](int kt) {
+    if constexpr (MODE == Mode::Conv) {
+      const int kbase = kt * kBK + kg * KPT;
+#pragma unroll
+      for (int u = 0; u < KPT; ++u) {
+        const int t = g.ktab[kbase + u];  // wave-uniform
+        const int c = t >> 16, dy = (t >> 8) & 255, dx = t & 255;
+        const int y = iy0 + dy, x = ix0 + dx;
+        float v = 0.f;
+        if (pix_ok && c < g.C && (unsigned)y < (unsigned)g.H && (unsigned)x < (unsigned)g.W)
+          v = img_base[((int64_t)c * g.H + y) * g.W + x];
+        rb[u] = v;
+      }
+    } else if constexpr (MODE == Mode::Wino) {
+#pragma unroll
+      for (int u = 0; u < B_LD4; ++u) {
+        const int q = tid + u * kThreads;
+        const int row = q / (BN / 4), jq = (q % (BN / 4)) * 4;
+        rb4[u] = *reinterpret_cast<const float4*>(
+            B + (int64_t)(kt * kBK + row) * g.ldb + j0 + jq);
+      }
+    } else {
+#pragma unroll
+      for (int u = 0; u < B_LD4; ++u) {
+        const int q = tid + u * kThreads;
+        const int row = q >> 2, kq = (q & 3) * 4;
+        rb4[u] = *reinterpret_cast<const float4*>(
+            B + (int64_t)(j0 + row) * g.ldb + kt * kBK + kq);
+      }
+    }
+  };
+  auto store_b = [&](int buf) {
+    if constexpr (MODE == Mode::Conv) {
+#pragma unroll
+      for (int u = 0; u < KPT; u += 4)
+        *reinterpret_cast<float4*>(&Bs[buf][jj * AS + kg * KPT + u]) =
+            make_float4(rb[u], rb[u + 1], rb[u + 2], rb[u + 3]);
+    } else if constexpr (MODE == Mode::Wino) {
+#pragma unroll
+      for (int u = 0; u < B_LD4; ++u) {
+        const int q = tid + u * kThreads;
+        const int row = q / (BN / 4), jq = (q % (BN / 4)) * 4;
+        *reinterpret_cast<float4*>(&Bs[buf][row * BS_ROW + jq]) = rb4[u];
+      }
+    } else {
+#pragma unroll
+      for (int u = 0; u < B_LD4; ++u) {
+        const int q = tid + u * kThreads;
+        const int row = q >> 2, kq = (q & 3) * 4;
+        *reinterpret_cast<float4*>(&Bs[buf][row * AS + kq]) = rb4[u];
+      }
+    }
+  };
+
+  v16f acc[TM][TN];
+#pragma unroll
+  for (int a = 0; a < TM; ++a)
+#pragma unroll
+    for (int b = 0; b < TN; ++b)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.f;
+
+  auto compute = [&](int buf) {
+    float af[TM][8], bf[TN][8];
+#pragma unroll
+    for (int a = 0; a < TM; ++a) {
+      const float* pa = &As[buf][(wm * (BM / 2) + a * 32 + li) * AS + lh * 8];
+      const float4 x0 = *reinterpret_cast<const float4*>(pa);
+      const float4 x1 = *reinterpret_cast<const float4*>(pa + 4);
+      af[a][0] = x0.x; af[a][1] = x0.y; af[a][2] = x0.z; af[a][3] = x0.w;
+      af[a][4] = x1.x; af[a][5] = x1.y; af[a][6] = x1.z; af[a][7] = x1.w;
+    }
+#pragma unroll
+    for (int b = 0; b < TN; ++b) {
+      const int col = wn * (BN / 2) + b * 32 + li;
+      if constexpr (B_KJ) {
+#pragma unroll
+        for (int s = 0; s < 8; ++s) bf[b][s] = Bs[buf][(lh * 8 + s) * BS_ROW + col];
+      } else {
+        const float* pb = &Bs[buf][col * AS + lh * 8];
+        const float4 y0 = *reinterpret_cast<const float4*>(pb);
+        const float4 y1 = *reinterpret_cast<const float4*>(pb + 4);
+        bf[b][0] = y0.x; bf[b][1] = y0.y; bf[b][2] = y0.z; bf[b][3] = y0.w;
+        bf[b][4] = y1.x; bf[b][5] = y1.y; bf[b][6] = y1.z; bf[b][7] = y1.w;
+      }
+    }
+#pragma unroll
+    for (int s = 0; s < 8; ++s)
+#pragma unroll
+      for (int a = 0; a < TM; ++a)
+#pragma unroll
+        for (int b = 0; b < TN; ++b)
+          acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[a][s], bf[b][s], acc[a][b], 0, 0, 0);
+  };
+
+  if (kt_begin < kt_end) {
+    load_a(kt_begin);
+    load_b(kt_begin);
+    store_a(0);
+    store_b(0);
+    __syncthreads();
+    for (int kt = kt_begin; kt < kt_end; ++kt) {
+      const int buf = (kt - kt_begin) & 1;
+      const bool more = kt + 1 < kt_end;
+      if (more) {
+        load_a(kt + 1);
+        load_b(kt + 1);
+      }
+      compute(buf);
+      if (more) {
+        store_a(buf ^ 1);
+        store_b(buf ^ 1);
+      }
+      __syncthreads();
+    }
+  }
+
+  // ---- epilogue.  32x32 accumulator layout: register r of lane l holds
+  // row (r%4) + 8*(r/4) + 4*(l/32), column l%32.
+#pragma unroll
+  for (int b = 0; b < TN; ++b) {
+    const int j = j0 + wn * (BN / 2) + b * 32 + li;
+    if constexpr (MODE == Mode::Conv) {
+      if (j >= g.n) continue;
+      const int img = j / g.OHW;
+      const int rem = j - img * g.OHW;
+      const int64_t obase = (int64_t)img * g.m * g.OHW + rem;
+#pragma unroll
+      for (int a = 0; a < TM; ++a)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int i = i0 + wm * (BM / 2) + a * 32 + (r & 3) + 8 * (r >> 2) + 4 * lh;
+          if (i < g.m) {
+            const int64_t o = obase + (int64_t)i * g.OHW;
+            float v = acc[a][b][r] + g.bias[i];
+            if (g.residual) v += g.residual[o];
+            g.d[o] = apply_act(v, g.act);
+          }
+        }
+    } else if constexpr (MODE == Mode::Wino) {
+      float* D = g.d + (int64_t)batch * g.d_batch;
+#pragma unroll
+      for (int a = 0; a < TM; ++a)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int i = i0 + wm * (BM / 2) + a * 32 + (r & 3) + 8 * (r >> 2) + 4 * lh;
+          D[(int64_t)i * g.ldd + j] = acc[a][b][r];
+        }
+    } else {
+      if (j >= g.n) continue;
+#pragma unroll
+      for (int a = 0; a < TM; ++a)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int i = i0 + wm * (BM / 2) + a * 32 + (r & 3) + 8 * (r >> 2) + 4 * lh;
+          if (i < g.m) {
+            if (g.splits > 1) {
+              g.d[((int64_t)split * g.m + i) * g.ldd + j] = acc[a][b][r];
+            } else {
+              g.d[(int64_t)i * g.ldd + j] = apply_act(acc[a][b][r] + g.bias[j], g.act);
+            }
+          }
+        }
+    }
+  }
+}
+
+// Split-K reduction for InnerProduct: out = act((sum_s part[s]) + bias).
+__global__ void ip_splitk_reduce(const float* part, const float* bias,
+                                 float* out, int m, int n, int ldp,
+                                 int splits, int act) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (int64_t)m * n) return;
+  const int i = (int)(idx / n), j = (int)(idx - (int64_t)i * n);
+  float s = 0.f;
+  for (int z = 0; z < splits; ++z) s += part[((int64_t)z * m + i) * ldp + j];
+  out[idx] = apply_act(s + bias[j], act);
+}
+
+template <int BM, int BN, Mode MODE>
+int launch(const GemmArgs& g, dim3 grid, hipStream_t s, const char* name) {
+  NHIP_LAUNCH(name, s, (gemm_f32_kernel<BM, BN, MODE>), grid, dim3(kThreads), 0, s, g);
+  return check_launch(name);
+}
+
+}  // namespace
+
+// ------------------------------- Convolution ------------------------------
+uint64_t conv_igemm_f32_workspace(const nhip_conv_plan*, int, int, int) { return 0; }
+
+int launch_conv_igemm_f32(const nhip_conv_plan* p, const float* in,
+                          const float* residual, float* out, int n, int h,
+                          int w, int oh, int ow, void*, uint64_t,
+                          hipStream_t s) {
+  GemmArgs g{};
+  g.a = p->weight;
+  g.lda = p->kred_pad;
+  g.m = p->g.k;
+  g.b = in;
+  g.n = n * oh * ow;
+  g.kdim = p->kred_pad;
+  g.ktab = p->ktab;
+  g.C = p->g.c;
+  g.H = h;
+  g.W = w;
+  g.OW = ow;
+  g.OHW = oh * ow;
+  g.sh = p->g.sh;
+  g.sw = p->g.sw;
+  g.pt = p->g.pt;
+  g.pl = p->g.pl;
+  g.d = out;
+  g.bias = p->bias;
+  g.residual = residual;
+  g.act = p->g.act;
+  g.splits = 1;
+  // Tile choice: the largest tile that still gives about two workgroups per
+  // CU; 64x64 otherwise.
+  const int64_t target = 2LL * cu_count();
+  const int mt128 = (int)ceil_div(p->g.k, 128), mt64 = (int)ceil_div(p->g.k, 64);
+  const int nt128 = (int)ceil_div(g.n, 128), nt64 = (int)ceil_div(g.n, 64);
+  const bool m_is_128 = p->m_pad % 128 == 0;
+  if (m_is_128 && (int64_t)mt128 * nt128 >= target)
+    return launch<128, 128, Mode::Conv>(g, dim3(nt128, mt128), s, "conv_igemm_f32<128,128>");
+  if ((int64_t)mt64 * nt128 >= target)
+    return launch<64, 128, Mode::Conv>(g, dim3(nt128, mt64), s, "conv_igemm_f32<64,128>");
+  return launch<64, 64, Mode::Conv>(g, dim3(nt64, mt64), s, "conv_igemm_f32<64,64>");
+}
+
+// Winograd batched GEMM: M[xi][m_pad][t_pad] = U[xi][m_pad][c_pad] * V[xi][c_pad][t_pad].
+int launch_wino_gemm(const float* U, const float* V, float* M, int m_pad,
+                     int c_pad, int t_pad, hipStream_t s) {
+  GemmArgs g{};
+  g.a = U;
+  g.a_batch = (int64_t)m_pad * c_pad;
+  g.lda = c_pad;
+  g.m = m_pad;
+  g.b = V;
+  g.b_batch = (int64_t)c_pad * t_pad;
+  g.ldb = t_pad;
+  g.n = t_pad;
+  g.kdim = c_pad;
+  g.d = M;
+  g.d_batch = (int64_t)m_pad * t_pad;
+  g.ldd = t_pad;
+  g.splits = 1;
+  const int64_t target = 2LL * cu_count();
+  if (m_pad % 128 == 0 && 36LL * (m_pad / 128) * (t_pad / 128) >= target)
+    return launch<128, 128, Mode::Wino>(g, dim3(t_pad / 128, m_pad / 128, 36), s, "wino_gemm<128,128>");
+  if (36LL * (m_pad / 64) * (t_pad / 128) >= target)
+    return launch<64, 128, Mode::Wino>(g, dim3(t_pad / 128, m_pad / 64, 36), s, "wino_gemm<64,128>");
+  return launch<64, 64, Mode::Wino>(g, dim3(t_pad / 64, m_pad / 64, 36), s, "wino_gemm<64,64>");
+}
+
+// ------------------------------- InnerProduct -----------------------------
+static int ip_splits(const nhip_ip_plan* p, int m) {
+  const int64_t tiles = ceil_div(m, 64) * ceil_div(p->n_out, 64);
+  const int nk = p->k_pad / kBK;
+  int splits = 1;
+  while (tiles * splits < 2LL * cu_count() && nk / (splits * 2) >= 8) splits *= 2;
+  return splits;
+}
+
+uint64_t innerproduct_workspace(const nhip_ip_plan* p, int m) {
+  const int splits = ip_splits(p, m);
+  if (splits == 1) return 0;
+  return (uint64_t)splits * m * p->n_pad * sizeof(float);
+}
+
+int launch_innerproduct_f32(const nhip_ip_plan* p, const float* in,
+                            float* out, int m, void* ws, uint64_t ws_bytes,
+                            hipStream_t s) {
+  GemmArgs g{};
+  g.a = in;
+  g.lda = p->k_in;
+  g.m = m;
+  g.k_valid = p->k_in;
+  g.a_vec4 = (p->k_in % 4 == 0 && (reinterpret_cast<uintptr_t>(in) & 15) == 0) ? 1 : 0;
+  g.b = p->weight;
+  g.ldb = p->k_pad;
+  g.n = p->n_out;
+  g.kdim = p->k_pad;
+  g.bias = p->bias;
+  g.act = p->act;
+  const int splits = ip_splits(p, m);
+  g.splits = splits;
+  if (splits > 1) {
+    const uint64_t need = innerproduct_workspace(p, m);
+    if (ws == nullptr || ws_bytes < need)
+      return fail(NHIP_STATUS_OUTPUT_CAPACITY_INSUFFICIENT,
+                  "innerproduct: workspace of " + std::to_string(need) +
+                      " bytes required");
+    g.d = static_cast<float*>(ws);
+    g.ldd = p->n_pad;
+  } else {
+    g.d = out;
+    g.ldd = p->n_out;
+  }
+  // B rows (weights) are padded to n_pad (multiple of 64); j bounds are
+  // checked in the epilogue only.
+  NHIP_TRY((launch<64, 64, Mode::IP>(g, dim3(p->n_pad / 64, (int)ceil_div(m, 64), splits), s,
+                                     "innerproduct_f32<64,64>")));
+  if (splits > 1) {
+    const int64_t total = (int64_t)m * p->n_out;
+    NHIP_LAUNCH("ip_splitk_reduce", s, ip_splitk_reduce, dim3((unsigned)ceil_div(total, 256)), dim3(256), 0, s,
+                       static_cast<const float*>(ws), p->bias, out, m, p->n_out, p->n_pad,
+                       splits, p->act);
+    return check_launch("ip_splitk_reduce");
+  }
+  return ok();
+}
+
+}  // namespace nhip

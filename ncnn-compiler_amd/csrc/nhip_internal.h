@@ -1,0 +1,128 @@
+// Internal declarations shared by the runtime's translation units.
+// Device code targets gfx950 (CDNA4) only: wave64, fp32/int8 MFMA.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+
+#include "../../include/nhip.h"
+
+namespace nhip {
+
+// ---- status / error plumbing ---------------------------------------------
+int fail(int status, const std::string& message);
+int ok();
+int check_hip(hipError_t e, const char* what);
+int check_launch(const char* kernel);
+
+#define NHIP_TRY(expr)          \
+  do {                          \
+    int _st = (expr);           \
+    if (_st != NHIP_STATUS_SUCCESS) return _st; \
+  } while (0)
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+// Launch bracketing for nhip_timer_*: construct right before a launch on
+// stream `s`; the destructor records the closing event.  No-op when the
+// timer is off or the name does not match its filter.
+class LaunchTimer {
+ public:
+  LaunchTimer(const char* kernel, hipStream_t s);
+  ~LaunchTimer();
+  LaunchTimer(const LaunchTimer&) = delete;
+  LaunchTimer& operator=(const LaunchTimer&) = delete;
+
+ private:
+  hipEvent_t stop_ = nullptr;
+  hipStream_t stream_ = nullptr;
+};
+
+// Launch `kernel, grid, block, shmem, stream, args...` on `stream`, timed by
+// nhip_timer_* under `name` when the timer is on.
+#define NHIP_LAUNCH(name, stream, ...)            \
+  do {                                            \
+    ::nhip::LaunchTimer _nhip_timer(name, stream); \
+    hipLaunchKernelGGL(__VA_ARGS__);              \
+  } while (0)
+
+int cu_count();  // compute units of the current device (cached)
+
+inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+inline int64_t round_up(int64_t a, int64_t b) { return ceil_div(a, b) * b; }
+
+// ---- MFMA operand / accumulator types ---------------------------------------
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+
+// ---- plans ----------------------------------------------------------------
+enum class PlanKind { ConvF32, ConvInt8, DwConvF32 };
+
+struct ConvGeom {
+  int32_t c, k;             // input channels, num_output
+  int32_t kh, kw, sh, sw, dh, dw;
+  int32_t pt, pb, pl, pr;
+  int32_t act;              // NHIP_ACT_*
+};
+
+}  // namespace nhip
+
+// Opaque handle of nhip.h.  Device buffers are owned by the plan.
+struct nhip_conv_plan {
+  nhip::PlanKind kind;
+  nhip::ConvGeom g;
+  int32_t algorithm;        // resolved NHIP_CONV_ALGO_* (never AUTO)
+  int32_t has_bias;
+  // implicit GEMM fp32: weights [m_pad][kred_pad], k = (c, kh, kw) order;
+  // Winograd: weights U[36][m_pad][c_pad].
+  float* weight = nullptr;
+  float* bias = nullptr;      // [m_pad] zero-filled past k (always present)
+  int32_t m_pad = 0, kred = 0, kred_pad = 0, c_pad = 0;
+  // im2col gather table: one packed int per reduction index
+  // (c << 16 | dy << 8 | dx), dy/dx = kh*dil_h, kw*dil_w; sentinel past kred.
+  int32_t* ktab = nullptr;
+  // int8: weights int8 [m_pad][kh*kw*c_pad] (k = (kh, kw, c) order),
+  // reciprocal r[c] = ws==0 ? 0 : 1/(ws*is), bias, scales.
+  int8_t* weight_i8 = nullptr;
+  float* recip = nullptr;
+  float input_scale = 1.0f, output_scale = 1.0f;
+  int32_t scale_term = 0;
+};
+
+struct nhip_ip_plan {
+  int32_t n_out, k_in, act;
+  int32_t n_pad, k_pad;
+  float* weight = nullptr;  // [n_pad][k_pad]
+  float* bias = nullptr;    // [n_pad], zero past n_out
+};
+
+namespace nhip {
+// Kernel launchers (defined in the .hip files).
+int launch_conv_igemm_f32(const nhip_conv_plan* p, const float* in,
+                          const float* residual, float* out, int n, int h,
+                          int w, int oh, int ow, void* ws, uint64_t ws_bytes,
+                          hipStream_t s);
+uint64_t conv_igemm_f32_workspace(const nhip_conv_plan* p, int n, int oh,
+                                  int ow);
+int launch_conv_winograd_f32(const nhip_conv_plan* p, const float* in,
+                             const float* residual, float* out, int n, int h,
+                             int w, int oh, int ow, void* ws,
+                             uint64_t ws_bytes, hipStream_t s);
+uint64_t conv_winograd_f32_workspace(const nhip_conv_plan* p, int n, int oh,
+                                     int ow);
+int winograd_prepack_weights(nhip_conv_plan* p, const float* weight);
+int launch_conv_int8(const nhip_conv_plan* p, const void* in, int in_is_i8,
+                     void* out, int n, int h, int w, int oh, int ow, void* ws,
+                     uint64_t ws_bytes, hipStream_t s);
+uint64_t conv_int8_workspace(const nhip_conv_plan* p, int n, int h, int w);
+int launch_dwconv_f32(const nhip_conv_plan* p, const float* in, float* out,
+                      int n, int h, int w, int oh, int ow, hipStream_t s);
+int launch_innerproduct_f32(const nhip_ip_plan* p, const float* in,
+                            float* out, int m, void* ws, uint64_t ws_bytes,
+                            hipStream_t s);
+uint64_t innerproduct_workspace(const nhip_ip_plan* p, int m);
+}  // namespace nhip

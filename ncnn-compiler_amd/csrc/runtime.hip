@@ -1,0 +1,580 @@
+// Host side of the runtime: status/error plumbing, device and memory calls,
+// parameter validation (the checks the reference importer applies before a
+// layer reaches the hot path), weight prepacking, and forward dispatch.
+//
+// This file is compiled with -ffp-contract=off: the host-side constant weight
+// quantization and the dequantize reciprocals must be the same separately
+// rounded fp32 operations as the reference's compile-time folding.
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <limits>
+#include <mutex>
+#include <vector>
+
+#include "nhip_internal.h"
+
+namespace nhip {
+
+namespace {
+thread_local std::string g_last_error;
+
+struct DeviceInfo {
+  int cus = 0;
+};
+std::mutex g_dev_mutex;
+DeviceInfo g_dev[64];
+}  // namespace
+
+int fail(int status, const std::string& message) {
+  g_last_error = message;
+  return status;
+}
+
+int ok() {
+  g_last_error.clear();
+  return NHIP_STATUS_SUCCESS;
+}
+
+int check_hip(hipError_t e, const char* what) {
+  if (e == hipSuccess) return ok();
+  return fail(NHIP_STATUS_DEVICE_ERROR, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+int check_launch(const char* kernel) {
+  const hipError_t e = hipGetLastError();
+  if (e == hipSuccess) return ok();
+  return fail(NHIP_STATUS_DEVICE_ERROR, std::string("launch of ") + kernel + ": " + hipGetErrorString(e));
+}
+
+// ---- kernel timer -----------------------------------------------------------
+namespace {
+struct TimerState {
+  std::mutex mu;
+  bool on = false;
+  std::string filter;
+  std::vector<std::pair<hipEvent_t, hipEvent_t>> events;
+};
+TimerState& timer() {
+  static TimerState t;
+  return t;
+}
+}  // namespace
+
+LaunchTimer::LaunchTimer(const char* kernel, hipStream_t s) {
+  TimerState& t = timer();
+  std::lock_guard<std::mutex> lock(t.mu);
+  if (!t.on || (!t.filter.empty() && std::string(kernel).find(t.filter) == std::string::npos)) return;
+  hipEvent_t start = nullptr;
+  if (hipEventCreate(&start) != hipSuccess) return;
+  if (hipEventCreate(&stop_) != hipSuccess) {
+    (void)hipEventDestroy(start);
+    stop_ = nullptr;
+    return;
+  }
+  stream_ = s;
+  (void)hipEventRecord(start, s);
+  t.events.emplace_back(start, stop_);
+}
+
+LaunchTimer::~LaunchTimer() {
+  if (stop_) (void)hipEventRecord(stop_, stream_);
+}
+
+int cu_count() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  std::lock_guard<std::mutex> lock(g_dev_mutex);
+  if (g_dev[dev].cus == 0) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+      cus = 256;
+    g_dev[dev].cus = cus;
+  }
+  return g_dev[dev].cus;
+}
+
+namespace {
+
+// ---- validation mirrors lib/Graph/graph.cpp:219-301 and the importers -----
+int validate_common(const nhip_conv_desc* d) {
+  if (!d) return fail(NHIP_STATUS_NULL_POINTER, "conv: null descriptor");
+  if (d->input_channels <= 0 || d->num_output <= 0)
+    return fail(NHIP_STATUS_INVALID_SHAPE, "conv: channels must be positive");
+  if (d->kernel_w <= 0 || d->kernel_h <= 0)
+    return fail(NHIP_STATUS_INVALID_SHAPE, "convolution kernel dimensions must be positive");
+  if (d->dilation_w <= 0 || d->dilation_h <= 0)
+    return fail(NHIP_STATUS_INVALID_SHAPE, "convolution dilation must be positive");
+  if (d->stride_w <= 0 || d->stride_h <= 0)
+    return fail(NHIP_STATUS_INVALID_SHAPE, "convolution stride must be positive");
+  if (d->pad_left < 0 || d->pad_right < 0 || d->pad_top < 0 || d->pad_bottom < 0)
+    return fail(NHIP_STATUS_CONSTRAINT_VIOLATION,
+                "requires explicit non-negative padding; resolve SAME padding first");
+  if (d->bias_term != 0 && d->bias_term != 1)
+    return fail(NHIP_STATUS_CONSTRAINT_VIOLATION, "convolution bias_term must be 0 or 1");
+  const int t = d->int8_scale_term;
+  if (t != 0 && t != 1 && t != 2 && t != 101 && t != 102)
+    return fail(NHIP_STATUS_CONSTRAINT_VIOLATION,
+                "convolution int8_scale_term must be 0, 1, 2, 101, or 102");
+  // The gather tables pack dy/dx in 8 bits and the channel in 15.
+  if ((int64_t)(d->kernel_h - 1) * d->dilation_h > 255 || (int64_t)(d->kernel_w - 1) * d->dilation_w > 255 ||
+      d->input_channels > 32000)
+    return fail(NHIP_STATUS_UNSUPPORTED, "conv: kernel extent > 256 or more than 32000 channels");
+  return ok();
+}
+
+ConvGeom geom_of(const nhip_conv_desc* d) {
+  ConvGeom g;
+  g.c = d->input_channels;
+  g.k = d->num_output;
+  g.kh = d->kernel_h;
+  g.kw = d->kernel_w;
+  g.sh = d->stride_h;
+  g.sw = d->stride_w;
+  g.dh = d->dilation_h;
+  g.dw = d->dilation_w;
+  g.pt = d->pad_top;
+  g.pb = d->pad_bottom;
+  g.pl = d->pad_left;
+  g.pr = d->pad_right;
+  g.act = d->activation_type;
+  return g;
+}
+
+template <typename T>
+int upload(T** dst, const std::vector<T>& host, const char* what) {
+  NHIP_TRY(check_hip(hipMalloc(reinterpret_cast<void**>(dst), std::max<size_t>(host.size(), 1) * sizeof(T)), what));
+  return check_hip(hipMemcpy(*dst, host.data(), host.size() * sizeof(T), hipMemcpyHostToDevice), what);
+}
+
+int upload_bias(nhip_conv_plan* p, const float* bias, int count, int padded) {
+  std::vector<float> b((size_t)padded, 0.f);
+  if (bias) std::copy(bias, bias + count, b.begin());
+  return upload(&p->bias, b, "hipMalloc(bias)");
+}
+
+void free_plan(nhip_conv_plan* p) {
+  if (!p) return;
+  (void)hipFree(p->weight);
+  (void)hipFree(p->bias);
+  (void)hipFree(p->ktab);
+  (void)hipFree(p->weight_i8);
+  (void)hipFree(p->recip);
+  delete p;
+}
+
+// quantizeConstantToI8 (NCNNToTosa.cpp:234-301) for one value.
+int8_t quantize_host(float x, float scale) {
+#pragma clang fp contract(off)
+  const float s = x * scale;
+  if (s != s) return 0;
+  float r = (s >= 0.0f) ? std::floor(s + 0.5f) : std::ceil(s - 0.5f);
+  if (r > 127.0f) r = 127.0f;
+  if (r < -127.0f) r = -127.0f;
+  return (int8_t)(int)r;
+}
+
+int conv_out(const ConvGeom& g, int h, int w, int* oh, int* ow) {
+  const int64_t eh = (int64_t)(g.kh - 1) * g.dh + 1, ew = (int64_t)(g.kw - 1) * g.dw + 1;
+  const int64_t ph = (int64_t)h + g.pt + g.pb - eh, pw = (int64_t)w + g.pl + g.pr - ew;
+  if (ph < 0 || pw < 0) return fail(NHIP_STATUS_INVALID_SHAPE, "conv: input smaller than the kernel extent");
+  *oh = (int)(ph / g.sh + 1);
+  *ow = (int)(pw / g.sw + 1);
+  return ok();
+}
+
+// Checks shared by every forward call: pointers, positive extents, and that
+// per-batch element counts fit the kernels' 32-bit pixel indexing.
+int check_forward(const nhip_conv_plan* p, const void* in, const void* out, int n, int h, int w,
+                  int* oh, int* ow) {
+  if (!p) return fail(NHIP_STATUS_NULL_POINTER, "conv: null plan");
+  if (!in || !out) return fail(NHIP_STATUS_NULL_POINTER, "conv: null input or output");
+  if (n < 0 || h <= 0 || w <= 0) return fail(NHIP_STATUS_INVALID_SHAPE, "conv: invalid input extent");
+  NHIP_TRY(conv_out(p->g, h, w, oh, ow));
+  const int64_t lim = std::numeric_limits<int32_t>::max();
+  if ((int64_t)p->g.c * h * w > lim / 4 || (int64_t)p->g.k * *oh * *ow > lim / 4 ||
+      (int64_t)n * *oh * *ow > lim || (int64_t)n * h * w > lim)
+    return fail(NHIP_STATUS_SHAPE_ARITHMETIC_OVERFLOW, "conv: tensor too large for 32-bit pixel indexing");
+  return ok();
+}
+
+}  // namespace
+}  // namespace nhip
+
+using namespace nhip;
+
+extern "C" {
+
+const char* nhip_last_error(void) { return g_last_error.c_str(); }
+
+int nhip_init(int32_t device) {
+  int count = 0;
+  NHIP_TRY(check_hip(hipGetDeviceCount(&count), "hipGetDeviceCount"));
+  if (device < 0 || device >= count)
+    return fail(NHIP_STATUS_INVALID_SHAPE, "nhip_init: no such device " + std::to_string(device));
+  NHIP_TRY(check_hip(hipSetDevice(device), "hipSetDevice"));
+  NHIP_TRY(check_hip(hipFree(nullptr), "device initialisation"));
+  cu_count();
+  return ok();
+}
+
+int nhip_device_count(int32_t* count) {
+  if (!count) return fail(NHIP_STATUS_NULL_POINTER, "device_count: null pointer");
+  int c = 0;
+  NHIP_TRY(check_hip(hipGetDeviceCount(&c), "hipGetDeviceCount"));
+  *count = c;
+  return ok();
+}
+
+int nhip_malloc(void** ptr, uint64_t bytes) {
+  if (!ptr) return fail(NHIP_STATUS_NULL_POINTER, "malloc: null pointer");
+  *ptr = nullptr;
+  return check_hip(hipMalloc(ptr, bytes ? bytes : 1), "hipMalloc");
+}
+
+int nhip_free(void* ptr) { return check_hip(hipFree(ptr), "hipFree"); }
+
+int nhip_memcpy_h2d(void* dst, const void* src, uint64_t bytes, void* stream) {
+  if ((!dst || !src) && bytes) return fail(NHIP_STATUS_NULL_POINTER, "memcpy_h2d: null pointer");
+  return check_hip(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, as_stream(stream)), "hipMemcpyAsync(H2D)");
+}
+
+int nhip_memcpy_d2h(void* dst, const void* src, uint64_t bytes, void* stream) {
+  if ((!dst || !src) && bytes) return fail(NHIP_STATUS_NULL_POINTER, "memcpy_d2h: null pointer");
+  return check_hip(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, as_stream(stream)), "hipMemcpyAsync(D2H)");
+}
+
+int nhip_memcpy_d2d(void* dst, const void* src, uint64_t bytes, void* stream) {
+  if ((!dst || !src) && bytes) return fail(NHIP_STATUS_NULL_POINTER, "memcpy_d2d: null pointer");
+  return check_hip(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, as_stream(stream)), "hipMemcpyAsync(D2D)");
+}
+
+int nhip_stream_sync(void* stream) {
+  return check_hip(hipStreamSynchronize(as_stream(stream)), "hipStreamSynchronize");
+}
+
+int nhip_timer_start(const char* kernel_filter) {
+  TimerState& t = timer();
+  std::lock_guard<std::mutex> lock(t.mu);
+  for (auto& e : t.events) {
+    (void)hipEventDestroy(e.first);
+    (void)hipEventDestroy(e.second);
+  }
+  t.events.clear();
+  t.filter = kernel_filter ? kernel_filter : "";
+  t.on = true;
+  return ok();
+}
+
+int nhip_timer_stop(uint64_t* launches, double* total_ms) {
+  if (!launches || !total_ms) return fail(NHIP_STATUS_NULL_POINTER, "timer_stop: null pointer");
+  TimerState& t = timer();
+  std::lock_guard<std::mutex> lock(t.mu);
+  t.on = false;
+  double sum = 0.0;
+  int status = NHIP_STATUS_SUCCESS;
+  for (auto& e : t.events) {
+    float ms = 0.f;
+    if (status == NHIP_STATUS_SUCCESS) {
+      status = check_hip(hipEventSynchronize(e.second), "hipEventSynchronize(timer)");
+      if (status == NHIP_STATUS_SUCCESS)
+        status = check_hip(hipEventElapsedTime(&ms, e.first, e.second), "hipEventElapsedTime(timer)");
+    }
+    sum += ms;
+    (void)hipEventDestroy(e.first);
+    (void)hipEventDestroy(e.second);
+  }
+  *launches = t.events.size();
+  *total_ms = sum;
+  t.events.clear();
+  if (status != NHIP_STATUS_SUCCESS) return status;
+  return ok();
+}
+
+int nhip_conv_output_shape(const nhip_conv_desc* desc, int32_t h, int32_t w, int32_t* out_h, int32_t* out_w) {
+  NHIP_TRY(validate_common(desc));
+  if (!out_h || !out_w) return fail(NHIP_STATUS_NULL_POINTER, "conv_output_shape: null pointer");
+  if (h <= 0 || w <= 0) return fail(NHIP_STATUS_INVALID_SHAPE, "conv_output_shape: invalid input extent");
+  int oh = 0, ow = 0;
+  NHIP_TRY(conv_out(geom_of(desc), h, w, &oh, &ow));
+  *out_h = oh;
+  *out_w = ow;
+  return ok();
+}
+
+int nhip_conv2d_f32_create(const nhip_conv_desc* d, const float* weight, const float* bias,
+                           nhip_conv_t* plan) {
+  NHIP_TRY(validate_common(d));
+  if (!weight || !plan) return fail(NHIP_STATUS_NULL_POINTER, "conv2d_f32_create: null pointer");
+  if (d->bias_term && !bias) return fail(NHIP_STATUS_NULL_POINTER, "conv2d_f32_create: bias_term set but bias is null");
+  if (d->int8_scale_term != 0)
+    return fail(NHIP_STATUS_CONSTRAINT_VIOLATION, "conv2d_f32_create: int8_scale_term must be 0 (use conv2d_int8_create)");
+  if (d->group != 0 && d->group != 1)
+    return fail(NHIP_STATUS_UNSUPPORTED, "Convolution has no group parameter (ImportConvolution.cpp:55-56)");
+  const int act = d->activation_type;
+  if (act != NHIP_ACT_NONE && act != NHIP_ACT_RELU && act != NHIP_ACT_SIGMOID)
+    return fail(NHIP_STATUS_UNSUPPORTED, "unsupported fused activation");
+  *plan = nullptr;
+  auto* p = new nhip_conv_plan();
+  p->kind = PlanKind::ConvF32;
+  p->g = geom_of(d);
+  p->has_bias = d->bias_term;
+  const bool wino_shape = d->kernel_h == 3 && d->kernel_w == 3 && d->stride_h == 1 && d->stride_w == 1 &&
+                          d->dilation_h == 1 && d->dilation_w == 1;
+  int algo = d->algorithm;
+  if (algo == NHIP_CONV_ALGO_AUTO)
+    algo = (wino_shape && d->input_channels >= 16 && d->num_output >= 16) ? NHIP_CONV_ALGO_WINOGRAD
+                                                                         : NHIP_CONV_ALGO_IMPLICIT_GEMM;
+  if (algo == NHIP_CONV_ALGO_WINOGRAD && !wino_shape) {
+    free_plan(p);
+    return fail(NHIP_STATUS_UNSUPPORTED, "winograd needs a 3x3 stride-1 dilation-1 convolution");
+  }
+  if (algo != NHIP_CONV_ALGO_WINOGRAD && algo != NHIP_CONV_ALGO_IMPLICIT_GEMM) {
+    free_plan(p);
+    return fail(NHIP_STATUS_CONSTRAINT_VIOLATION, "unknown convolution algorithm");
+  }
+  p->algorithm = algo;
+  const int K = d->num_output, C = d->input_channels;
+  p->m_pad = (int)round_up(K, 64);
+  int st = NHIP_STATUS_SUCCESS;
+  if (algo == NHIP_CONV_ALGO_WINOGRAD) {
+    p->c_pad = (int)round_up(C, 16);
+    st = winograd_prepack_weights(p, weight);
+  } else {
+    const int khw = d->kernel_h * d->kernel_w;
+    p->kred = C * khw;
+    p->kred_pad = (int)round_up(p->kred, 16);
+    std::vector<float> wp((size_t)p->m_pad * p->kred_pad, 0.f);
+    for (int k = 0; k < K; ++k)
+      std::copy(weight + (size_t)k * p->kred, weight + (size_t)(k + 1) * p->kred, wp.begin() + (size_t)k * p->kred_pad);
+    std::vector<int32_t> kt((size_t)p->kred_pad, 0x7fff << 16);
+    for (int k = 0; k < p->kred; ++k) {
+      const int c = k / khw, r = k % khw, kh = r / d->kernel_w, kw = r % d->kernel_w;
+      kt[k] = (c << 16) | ((kh * d->dilation_h) << 8) | (kw * d->dilation_w);
+    }
+    st = upload(&p->weight, wp, "hipMalloc(conv weight)");
+    if (st == NHIP_STATUS_SUCCESS) st = upload(&p->ktab, kt, "hipMalloc(conv ktab)");
+  }
+  if (st == NHIP_STATUS_SUCCESS) st = upload_bias(p, d->bias_term ? bias : nullptr, K, p->m_pad);
+  if (st != NHIP_STATUS_SUCCESS) {
+    std::string msg = g_last_error;
+    free_plan(p);
+    return fail(st, msg);
+  }
+  *plan = p;
+  return ok();
+}
+
+int nhip_conv2d_workspace_size(nhip_conv_t p, int32_t n, int32_t h, int32_t w, uint64_t* bytes) {
+  if (!p || !bytes) return fail(NHIP_STATUS_NULL_POINTER, "workspace_size: null pointer");
+  int oh = 0, ow = 0;
+  if (n < 0 || h <= 0 || w <= 0) return fail(NHIP_STATUS_INVALID_SHAPE, "workspace_size: invalid extent");
+  NHIP_TRY(conv_out(p->g, h, w, &oh, &ow));
+  switch (p->kind) {
+    case PlanKind::ConvF32:
+      *bytes = p->algorithm == NHIP_CONV_ALGO_WINOGRAD ? conv_winograd_f32_workspace(p, n, oh, ow)
+                                                       : conv_igemm_f32_workspace(p, n, oh, ow);
+      break;
+    case PlanKind::ConvInt8:
+      *bytes = conv_int8_workspace(p, n, h, w);
+      break;
+    default:
+      *bytes = 0;
+  }
+  return ok();
+}
+
+int nhip_conv2d_f32_forward(nhip_conv_t p, const float* input, const float* residual, float* output,
+                            int32_t n, int32_t h, int32_t w, void* workspace, uint64_t workspace_bytes,
+                            void* stream) {
+  int oh = 0, ow = 0;
+  NHIP_TRY(check_forward(p, input, output, n, h, w, &oh, &ow));
+  if (p->kind != PlanKind::ConvF32) return fail(NHIP_STATUS_CONSTRAINT_VIOLATION, "conv2d_f32_forward: not an fp32 conv plan");
+  if (n == 0) return ok();
+  if (p->algorithm == NHIP_CONV_ALGO_WINOGRAD)
+    return launch_conv_winograd_f32(p, input, residual, output, n, h, w, oh, ow, workspace, workspace_bytes,
+                                    as_stream(stream));
+  return launch_conv_igemm_f32(p, input, residual, output, n, h, w, oh, ow, workspace, workspace_bytes,
+                               as_stream(stream));
+}
+
+int nhip_conv2d_int8_create(const nhip_conv_desc* d, const void* weight, int32_t weight_is_i8, const float* bias,
+                            const float* weight_scale, int32_t weight_scale_count, float input_scale,
+                            float output_scale, nhip_conv_t* plan) {
+  NHIP_TRY(validate_common(d));
+  if (!weight || !plan || !weight_scale) return fail(NHIP_STATUS_NULL_POINTER, "conv2d_int8_create: null pointer");
+  if (d->bias_term && !bias) return fail(NHIP_STATUS_NULL_POINTER, "conv2d_int8_create: bias_term set but bias is null");
+  if (d->int8_scale_term == 0)
+    return fail(NHIP_STATUS_CONSTRAINT_VIOLATION, "conv2d_int8_create: int8_scale_term must be nonzero");
+  if (d->group != 0 && d->group != 1)
+    return fail(NHIP_STATUS_UNSUPPORTED, "Convolution has no group parameter");
+  if (d->activation_type != NHIP_ACT_NONE && d->activation_type != NHIP_ACT_RELU)
+    return fail(NHIP_STATUS_UNSUPPORTED, "int8 convolution: activation must be 0 or 1");
+  if (weight_scale_count != 1 && weight_scale_count != d->num_output)
+    return fail(NHIP_STATUS_INVALID_SHAPE, "conv2d_int8_create: weight_scale count must be 1 or num_output");
+  *plan = nullptr;
+  auto* p = new nhip_conv_plan();
+  p->kind = PlanKind::ConvInt8;
+  p->g = geom_of(d);
+  p->algorithm = NHIP_CONV_ALGO_IMPLICIT_GEMM;
+  p->has_bias = d->bias_term;
+  p->scale_term = d->int8_scale_term;
+  p->input_scale = input_scale;
+  p->output_scale = output_scale;
+  const int K = d->num_output, C = d->input_channels, KH = d->kernel_h, KW = d->kernel_w;
+  p->m_pad = (int)round_up(K, 64);
+  p->c_pad = (int)round_up(C, 16);
+  p->kred = KH * KW * p->c_pad;
+  p->kred_pad = (int)round_up(p->kred, 64);
+  // Weights to int8 [m_pad][kh][kw][c_pad] (OHWI with channel padding).
+  std::vector<int8_t> wq((size_t)p->m_pad * p->kred_pad, 0);
+  for (int k = 0; k < K; ++k) {
+    const float ws = weight_scale[weight_scale_count == 1 ? 0 : k];
+    for (int c = 0; c < C; ++c)
+      for (int kh = 0; kh < KH; ++kh)
+        for (int kw = 0; kw < KW; ++kw) {
+          const size_t src = (((size_t)k * C + c) * KH + kh) * KW + kw;
+          const int8_t q = weight_is_i8 ? static_cast<const int8_t*>(weight)[src]
+                                        : quantize_host(static_cast<const float*>(weight)[src], ws);
+          wq[(size_t)k * p->kred_pad + (size_t)(kh * KW + kw) * p->c_pad + c] = q;
+        }
+  }
+  // dequantizeAccumulator reciprocals (NCNNToTosa.cpp:577-637).
+  std::vector<float> rc((size_t)p->m_pad, 0.f);
+  for (int k = 0; k < K; ++k) {
+#pragma clang fp contract(off)
+    const float ws = weight_scale[weight_scale_count == 1 ? 0 : k];
+    const float combined = ws * input_scale;
+    const float r = 1.0f / combined;
+    rc[k] = ws == 0.0f ? 0.0f : r;
+  }
+  std::vector<int32_t> kt((size_t)p->kred_pad / 16, 0x7fff << 16);
+  for (int q = 0; q < p->kred / 16; ++q) {
+    const int kidx = q * 16, r = kidx / p->c_pad, c0 = kidx % p->c_pad;
+    const int kh = r / KW, kw = r % KW;
+    kt[q] = (c0 << 16) | ((kh * d->dilation_h) << 8) | (kw * d->dilation_w);
+  }
+  int st = upload(&p->weight_i8, wq, "hipMalloc(int8 weight)");
+  if (st == NHIP_STATUS_SUCCESS) st = upload(&p->recip, rc, "hipMalloc(int8 reciprocal)");
+  if (st == NHIP_STATUS_SUCCESS) st = upload(&p->ktab, kt, "hipMalloc(int8 ktab)");
+  if (st == NHIP_STATUS_SUCCESS) st = upload_bias(p, d->bias_term ? bias : nullptr, K, p->m_pad);
+  if (st != NHIP_STATUS_SUCCESS) {
+    std::string msg = g_last_error;
+    free_plan(p);
+    return fail(st, msg);
+  }
+  *plan = p;
+  return ok();
+}
+
+int nhip_conv2d_int8_forward(nhip_conv_t p, const void* input, int32_t input_is_i8, void* output, int32_t n,
+                             int32_t h, int32_t w, void* workspace, uint64_t workspace_bytes, void* stream) {
+  int oh = 0, ow = 0;
+  NHIP_TRY(check_forward(p, input, output, n, h, w, &oh, &ow));
+  if (p->kind != PlanKind::ConvInt8) return fail(NHIP_STATUS_CONSTRAINT_VIOLATION, "conv2d_int8_forward: not an int8 conv plan");
+  if (n == 0) return ok();
+  return launch_conv_int8(p, input, input_is_i8 ? 1 : 0, output, n, h, w, oh, ow, workspace, workspace_bytes,
+                          as_stream(stream));
+}
+
+int nhip_dwconv2d_f32_create(const nhip_conv_desc* d, const float* weight, const float* bias, nhip_conv_t* plan) {
+  NHIP_TRY(validate_common(d));
+  if (!weight || !plan) return fail(NHIP_STATUS_NULL_POINTER, "dwconv2d_f32_create: null pointer");
+  if (d->bias_term && !bias) return fail(NHIP_STATUS_NULL_POINTER, "dwconv2d_f32_create: bias_term set but bias is null");
+  if (d->group != d->input_channels || d->num_output != d->input_channels)
+    return fail(NHIP_STATUS_CONSTRAINT_VIOLATION, "depthwise group must equal input channels");
+  if (d->int8_scale_term != 0)
+    return fail(NHIP_STATUS_UNSUPPORTED, "dwconv2d_f32_create: int8 depthwise is not in this build");
+  if (d->activation_type != NHIP_ACT_NONE && d->activation_type != NHIP_ACT_RELU)
+    return fail(NHIP_STATUS_UNSUPPORTED, "depthwise activation must be 0 or 1");
+  *plan = nullptr;
+  auto* p = new nhip_conv_plan();
+  p->kind = PlanKind::DwConvF32;
+  p->g = geom_of(d);
+  p->algorithm = NHIP_CONV_ALGO_IMPLICIT_GEMM;
+  p->has_bias = d->bias_term;
+  const size_t wcount = (size_t)d->num_output * d->kernel_h * d->kernel_w;
+  std::vector<float> wv(weight, weight + wcount);
+  int st = upload(&p->weight, wv, "hipMalloc(dw weight)");
+  if (st == NHIP_STATUS_SUCCESS) st = upload_bias(p, d->bias_term ? bias : nullptr, d->num_output, d->num_output);
+  if (st != NHIP_STATUS_SUCCESS) {
+    std::string msg = g_last_error;
+    free_plan(p);
+    return fail(st, msg);
+  }
+  *plan = p;
+  return ok();
+}
+
+int nhip_dwconv2d_f32_forward(nhip_conv_t p, const float* input, float* output, int32_t n, int32_t h, int32_t w,
+                              void* stream) {
+  int oh = 0, ow = 0;
+  NHIP_TRY(check_forward(p, input, output, n, h, w, &oh, &ow));
+  if (p->kind != PlanKind::DwConvF32) return fail(NHIP_STATUS_CONSTRAINT_VIOLATION, "dwconv2d_f32_forward: not a depthwise plan");
+  if (n == 0) return ok();
+  return launch_dwconv_f32(p, input, output, n, h, w, oh, ow, as_stream(stream));
+}
+
+int nhip_conv_destroy(nhip_conv_t p) {
+  free_plan(p);
+  return ok();
+}
+
+int nhip_innerproduct_f32_create(int32_t num_output, int32_t num_input, const float* weight, const float* bias,
+                                 int32_t activation_type, nhip_ip_t* plan) {
+  if (!weight || !plan) return fail(NHIP_STATUS_NULL_POINTER, "innerproduct_create: null pointer");
+  if (num_output <= 0 || num_input <= 0) return fail(NHIP_STATUS_INVALID_SHAPE, "innerproduct: sizes must be positive");
+  if (activation_type != NHIP_ACT_NONE && activation_type != NHIP_ACT_RELU)
+    return fail(NHIP_STATUS_UNSUPPORTED, "innerproduct activation must be 0 or 1");
+  *plan = nullptr;
+  auto* p = new nhip_ip_plan();
+  p->n_out = num_output;
+  p->k_in = num_input;
+  p->act = activation_type;
+  p->n_pad = (int)round_up(num_output, 64);
+  p->k_pad = (int)round_up(num_input, 16);
+  std::vector<float> wp((size_t)p->n_pad * p->k_pad, 0.f);
+  for (int j = 0; j < num_output; ++j)
+    std::copy(weight + (size_t)j * num_input, weight + (size_t)(j + 1) * num_input, wp.begin() + (size_t)j * p->k_pad);
+  std::vector<float> bv((size_t)p->n_pad, 0.f);
+  if (bias) std::copy(bias, bias + num_output, bv.begin());
+  int st = upload(&p->weight, wp, "hipMalloc(ip weight)");
+  if (st == NHIP_STATUS_SUCCESS) st = upload(&p->bias, bv, "hipMalloc(ip bias)");
+  if (st != NHIP_STATUS_SUCCESS) {
+    std::string msg = g_last_error;
+    (void)hipFree(p->weight);
+    (void)hipFree(p->bias);
+    delete p;
+    return fail(st, msg);
+  }
+  *plan = p;
+  return ok();
+}
+
+int nhip_innerproduct_workspace_size(nhip_ip_t p, int32_t m, uint64_t* bytes) {
+  if (!p || !bytes) return fail(NHIP_STATUS_NULL_POINTER, "innerproduct_workspace_size: null pointer");
+  if (m < 0) return fail(NHIP_STATUS_INVALID_SHAPE, "innerproduct: negative m");
+  *bytes = m == 0 ? 0 : innerproduct_workspace(p, m);
+  return ok();
+}
+
+int nhip_innerproduct_f32_forward(nhip_ip_t p, const float* input, float* output, int32_t m, void* workspace,
+                                  uint64_t workspace_bytes, void* stream) {
+  if (!p || !input || !output) return fail(NHIP_STATUS_NULL_POINTER, "innerproduct_forward: null pointer");
+  if (m < 0) return fail(NHIP_STATUS_INVALID_SHAPE, "innerproduct: negative m");
+  if ((int64_t)m * std::max(p->k_in, p->n_pad) > std::numeric_limits<int32_t>::max())
+    return fail(NHIP_STATUS_SHAPE_ARITHMETIC_OVERFLOW, "innerproduct: m too large");
+  if (m == 0) return ok();
+  return launch_innerproduct_f32(p, input, output, m, workspace, workspace_bytes, as_stream(stream));
+}
+
+int nhip_innerproduct_destroy(nhip_ip_t p) {
+  if (p) {
+    (void)hipFree(p->weight);
+    (void)hipFree(p->bias);
+    delete p;
+  }
+  return ok();
+}
+
+}  // extern "C"

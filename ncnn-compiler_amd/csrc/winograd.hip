@@ -1,0 +1,237 @@
+// Winograd F(4x4, 3x3) for 3x3, stride 1, dilation 1 Convolution.
+//
+// The reference has no Winograd: its 3x3 conv is the plain
+// linalg.conv_2d_nhwc_hwcf loop nest (NCNNToTosa.cpp:1485-1498,
+// NCNNPipelines.cpp:54-56).  This is the build's own algorithm choice with the
+// reference's result (bias + sum x*w, then activation), checked to a 1e-3
+// relative budget.
+//
+// Transform matrices: interpolation points 0, 1, -1, 2, -2 and infinity
+// (Lavin & Gray, "Fast Algorithms for Convolutional Neural Networks", 2016):
+//   Y = A^T [ (G g G^T) .* (B^T d B) ] A
+// with 6x6 input tiles d overlapping by 2, 4x4 output tiles Y.
+//
+// Three kernels, all launched on the caller's stream:
+//   1. input transform  x[N,C,H,W] -> V[36][c_pad][t_pad]  (HBM bound)
+//   2. 36 batched MFMA GEMMs M[xi] = U[xi] (m_pad x c_pad) * V[xi]
+//   3. output transform M -> out[N,K,OH,OW] with bias, residual add and the
+//      activation fused (HBM bound).
+// The weight transform U = G g G^T is done once on the host at plan creation.
+#include <vector>
+
+#include "nhip_internal.h"
+
+namespace nhip {
+int launch_wino_gemm(const float* U, const float* V, float* M, int m_pad,
+                     int c_pad, int t_pad, hipStream_t s);
+
+namespace {
+
+struct WinoShape {
+  int n, c, h, w, oh, ow, th, tw, t, t_pad, c_pad, m_pad;
+};
+
+WinoShape wino_shape(const nhip_conv_plan* p, int n, int h, int w, int oh, int ow) {
+  WinoShape s;
+  s.n = n;
+  s.c = p->g.c;
+  s.h = h;
+  s.w = w;
+  s.oh = oh;
+  s.ow = ow;
+  s.th = (int)ceil_div(oh, 4);
+  s.tw = (int)ceil_div(ow, 4);
+  s.t = n * s.th * s.tw;
+  s.t_pad = (int)round_up(s.t, 128);
+  s.c_pad = p->c_pad;
+  s.m_pad = p->m_pad;
+  return s;
+}
+
+// Thread (c, t): 6x6 zero-padded patch -> 36 transformed values.
+__global__ __launch_bounds__(256) void wino_input_transform(
+    const float* __restrict__ x, float* __restrict__ V, int C, int H, int W,
+    int th, int tw, int T, int t_pad, int c_pad, int pt, int pl) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (int64_t)c_pad * t_pad) return;
+  const int c = (int)(idx / t_pad);
+  const int t = (int)(idx - (int64_t)c * t_pad);
+  const int64_t plane_stride = (int64_t)c_pad * t_pad;
+  float* vout = V + (int64_t)c * t_pad + t;
+  if (c >= C || t >= T) {
+#pragma unroll
+    for (int xi = 0; xi < 36; ++xi) vout[xi * plane_stride] = 0.f;
+    return;
+  }
+  const int per_img = th * tw;
+  const int img = t / per_img;
+  const int r = t - img * per_img;
+  const int ty = r / tw, tx = r - (r / tw) * tw;
+  const int y0 = ty * 4 - pt, x0 = tx * 4 - pl;
+  const float* plane = x + ((int64_t)img * C + c) * H * W;
+
+  float d[6][6];
+#pragma unroll
+  for (int i = 0; i < 6; ++i) {
+    const int y = y0 + i;
+    const bool yok = (unsigned)y < (unsigned)H;
+#pragma unroll
+    for (int j = 0; j < 6; ++j) {
+      const int xx = x0 + j;
+      d[i][j] = (yok && (unsigned)xx < (unsigned)W) ? plane[(int64_t)y * W + xx] : 0.f;
+    }
+  }
+  // tmp = B^T d  (column-wise)
+  float tmp[6][6];
+#pragma unroll
+  for (int j = 0; j < 6; ++j) {
+    const float d0 = d[0][j], d1 = d[1][j], d2 = d[2][j], d3 = d[3][j], d4 = d[4][j], d5 = d[5][j];
+    tmp[0][j] = 4.f * d0 - 5.f * d2 + d4;
+    tmp[1][j] = -4.f * (d1 + d2) + d3 + d4;
+    tmp[2][j] = 4.f * (d1 - d2) - d3 + d4;
+    tmp[3][j] = -2.f * (d1 - d3) - d2 + d4;
+    tmp[4][j] = 2.f * (d1 - d3) - d2 + d4;
+    tmp[5][j] = 4.f * d1 - 5.f * d3 + d5;
+  }
+  // V = tmp B  (row-wise)
+#pragma unroll
+  for (int i = 0; i < 6; ++i) {
+    const float d0 = tmp[i][0], d1 = tmp[i][1], d2 = tmp[i][2], d3 = tmp[i][3], d4 = tmp[i][4], d5 = tmp[i][5];
+    float v[6];
+    v[0] = 4.f * d0 - 5.f * d2 + d4;
+    v[1] = -4.f * (d1 + d2) + d3 + d4;
+    v[2] = 4.f * (d1 - d2) - d3 + d4;
+    v[3] = -2.f * (d1 - d3) - d2 + d4;
+    v[4] = 2.f * (d1 - d3) - d2 + d4;
+    v[5] = 4.f * d1 - 5.f * d3 + d5;
+#pragma unroll
+    for (int j = 0; j < 6; ++j) vout[(i * 6 + j) * plane_stride] = v[j];
+  }
+}
+
+// Thread (k, t): 36 GEMM outputs -> 4x4 output tile, + bias (+ residual), act.
+__global__ __launch_bounds__(256) void wino_output_transform(
+    const float* __restrict__ M, const float* __restrict__ bias,
+    const float* __restrict__ residual, float* __restrict__ out, int K, int OH,
+    int OW, int th, int tw, int T, int t_pad, int m_pad, int act) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (int64_t)K * T) return;
+  const int k = (int)(idx / T);
+  const int t = (int)(idx - (int64_t)k * T);
+  const int64_t plane_stride = (int64_t)m_pad * t_pad;
+  const float* min = M + (int64_t)k * t_pad + t;
+  float m[6][6];
+#pragma unroll
+  for (int i = 0; i < 6; ++i)
+#pragma unroll
+    for (int j = 0; j < 6; ++j) m[i][j] = min[(i * 6 + j) * plane_stride];
+  // tmp = A^T m (4x6)
+  float tmp[4][6];
+#pragma unroll
+  for (int j = 0; j < 6; ++j) {
+    const float m0 = m[0][j], m1 = m[1][j], m2 = m[2][j], m3 = m[3][j], m4 = m[4][j], m5 = m[5][j];
+    const float s12 = m1 + m2, d12 = m1 - m2, s34 = m3 + m4, d34 = m3 - m4;
+    tmp[0][j] = m0 + s12 + s34;
+    tmp[1][j] = d12 + 2.f * d34;
+    tmp[2][j] = s12 + 4.f * s34;
+    tmp[3][j] = d12 + 8.f * d34 + m5;
+  }
+  const int per_img = th * tw;
+  const int img = t / per_img;
+  const int r = t - img * per_img;
+  const int ty = r / tw, tx = r - (r / tw) * tw;
+  const float b = bias[k];
+  const int64_t plane = ((int64_t)img * K + k) * OH * OW;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float m0 = tmp[i][0], m1 = tmp[i][1], m2 = tmp[i][2], m3 = tmp[i][3], m4 = tmp[i][4], m5 = tmp[i][5];
+    const float s12 = m1 + m2, d12 = m1 - m2, s34 = m3 + m4, d34 = m3 - m4;
+    float y[4];
+    y[0] = m0 + s12 + s34;
+    y[1] = d12 + 2.f * d34;
+    y[2] = s12 + 4.f * s34;
+    y[3] = d12 + 8.f * d34 + m5;
+    const int oy = ty * 4 + i;
+    if (oy >= OH) break;
+    const int64_t row = plane + (int64_t)oy * OW + tx * 4;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if (tx * 4 + j < OW) {
+        float v = y[j] + b;
+        if (residual) v += residual[row + j];
+        if (act == NHIP_ACT_RELU) v = v < 0.f ? 0.f : v;
+        else if (act == NHIP_ACT_SIGMOID) v = 1.0f / (1.0f + __expf(-v));
+        out[row + j] = v;
+      }
+    }
+  }
+}
+
+}  // namespace
+
+// U[xi][k][c] = (G g_kc G^T)[xi], computed in double, stored fp32 with zero
+// padding to [36][m_pad][c_pad].
+int winograd_prepack_weights(nhip_conv_plan* p, const float* weight) {
+  static const double G[6][3] = {
+      {1.0 / 4, 0, 0},
+      {-1.0 / 6, -1.0 / 6, -1.0 / 6},
+      {-1.0 / 6, 1.0 / 6, -1.0 / 6},
+      {1.0 / 24, 1.0 / 12, 1.0 / 6},
+      {1.0 / 24, -1.0 / 12, 1.0 / 6},
+      {0, 0, 1}};
+  const int K = p->g.k, C = p->g.c;
+  std::vector<float> U((size_t)36 * p->m_pad * p->c_pad, 0.f);
+  for (int k = 0; k < K; ++k)
+    for (int c = 0; c < C; ++c) {
+      const float* g = weight + ((size_t)k * C + c) * 9;
+      double tmp[6][3];
+      for (int i = 0; i < 6; ++i)
+        for (int j = 0; j < 3; ++j)
+          tmp[i][j] = G[i][0] * g[0 * 3 + j] + G[i][1] * g[1 * 3 + j] + G[i][2] * g[2 * 3 + j];
+      for (int i = 0; i < 6; ++i)
+        for (int j = 0; j < 6; ++j) {
+          const double u = tmp[i][0] * G[j][0] + tmp[i][1] * G[j][1] + tmp[i][2] * G[j][2];
+          U[((size_t)(i * 6 + j) * p->m_pad + k) * p->c_pad + c] = (float)u;
+        }
+    }
+  NHIP_TRY(check_hip(hipMalloc(&p->weight, U.size() * sizeof(float)), "hipMalloc(winograd U)"));
+  return check_hip(hipMemcpy(p->weight, U.data(), U.size() * sizeof(float), hipMemcpyHostToDevice),
+                   "hipMemcpy(winograd U)");
+}
+
+uint64_t conv_winograd_f32_workspace(const nhip_conv_plan* p, int n, int oh, int ow) {
+  const int th = (int)ceil_div(oh, 4), tw = (int)ceil_div(ow, 4);
+  const int64_t t_pad = round_up((int64_t)n * th * tw, 128);
+  return (uint64_t)36 * t_pad * (p->c_pad + p->m_pad) * sizeof(float);
+}
+
+int launch_conv_winograd_f32(const nhip_conv_plan* p, const float* in,
+                             const float* residual, float* out, int n, int h,
+                             int w, int oh, int ow, void* ws, uint64_t ws_bytes,
+                             hipStream_t s) {
+  const WinoShape ws_ = wino_shape(p, n, h, w, oh, ow);
+  const uint64_t need = conv_winograd_f32_workspace(p, n, oh, ow);
+  if (ws == nullptr || ws_bytes < need)
+    return fail(NHIP_STATUS_OUTPUT_CAPACITY_INSUFFICIENT,
+                "winograd conv: workspace of " + std::to_string(need) + " bytes required");
+  float* V = static_cast<float*>(ws);
+  float* M = V + (int64_t)36 * ws_.c_pad * ws_.t_pad;
+  {
+    const int64_t total = (int64_t)ws_.c_pad * ws_.t_pad;
+    NHIP_LAUNCH("wino_input_transform", s, wino_input_transform, dim3((unsigned)ceil_div(total, 256)), dim3(256), 0, s,
+                       in, V, ws_.c, h, w, ws_.th, ws_.tw, ws_.t, ws_.t_pad, ws_.c_pad,
+                       p->g.pt, p->g.pl);
+    NHIP_TRY(check_launch("wino_input_transform"));
+  }
+  NHIP_TRY(launch_wino_gemm(p->weight, V, M, ws_.m_pad, ws_.c_pad, ws_.t_pad, s));
+  {
+    const int64_t total = (int64_t)p->g.k * ws_.t;
+    NHIP_LAUNCH("wino_output_transform", s, wino_output_transform, dim3((unsigned)ceil_div(total, 256)), dim3(256), 0, s,
+                       M, p->bias, residual, out, p->g.k, oh, ow, ws_.th, ws_.tw, ws_.t,
+                       ws_.t_pad, ws_.m_pad, p->g.act);
+    NHIP_TRY(check_launch("wino_output_transform"));
+  }
+  return ok();
+}
+
+}  // namespace nhip

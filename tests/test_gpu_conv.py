@@ -1,0 +1,216 @@
+"""GPU parity: fp32 Convolution through the C ABI (implicit GEMM and
+Winograd F(4,3)) against the CPU oracle restating the reference's lowering
+(NCNNToTosa.cpp:1316-1529 + the importer's separate relu and the BinaryOp add).
+
+Budgets from the north star: max relative error <= 1e-4 for implicit GEMM,
+<= 1e-3 for Winograd (checked elementwise with a data-scaled absolute term,
+and normwise).
+"""
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+
+import nhip  # noqa: E402
+import workloads  # noqa: E402
+from numerics import assert_close, max_rel_err  # noqa: E402
+from oracle import refcpu  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+
+IGEMM_RTOL = 1e-4
+WINO_RTOL = 1e-3
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    assert torch.cuda.is_available(), "GPU tests need a HIP device"
+    nhip.init(0)
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def host(t):
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def oracle_conv(x, w, b, stride, dil, pad, act=0, residual=None):
+    n, c, h, wd = x.shape
+    k = w.shape[0]
+    g = refcpu.geom(n, c, h, wd, k, w.shape[2:], stride, dil, pad)
+    y = refcpu.conv2d_f32(g, x, w, b)
+    if residual is not None:
+        y = refcpu.add_f32(y, residual)
+    if act == nhip.ACT_RELU:
+        y = refcpu.relu_f32(y)
+    elif act == nhip.ACT_SIGMOID:
+        y = (1.0 / (1.0 + np.exp(-y.astype(np.float64)))).astype(np.float32)
+    return y
+
+
+RNG = np.random.default_rng(7)
+
+GENERAL_CASES = [
+    # (n, c, h, w, k, kernel, stride, dilation, pad(t,b,l,r))
+    (1, 1, 4, 4, 2, (3, 3), (1, 1), (1, 1), (1, 1, 1, 1)),
+    (2, 3, 7, 6, 5, (3, 3), (2, 2), (1, 1), (1, 1, 1, 1)),
+    (1, 4, 9, 8, 3, (3, 3), (1, 1), (2, 2), (2, 2, 2, 2)),
+    (1, 2, 6, 7, 3, (2, 3), (1, 2), (1, 1), (0, 1, 2, 0)),
+    (2, 8, 5, 5, 4, (1, 1), (1, 1), (1, 1), (0, 0, 0, 0)),
+    (1, 3, 11, 11, 8, (3, 3), (2, 2), (1, 1), (1, 1, 1, 1)),
+    (3, 70, 13, 9, 130, (3, 3), (1, 1), (1, 1), (1, 1, 1, 1)),
+    (2, 3, 32, 30, 32, (3, 3), (2, 2), (1, 1), (1, 1, 1, 1)),   # MobileNetV2 stem shape
+    (2, 96, 14, 14, 24, (1, 1), (1, 1), (1, 1), (0, 0, 0, 0)),  # 1x1 project
+    (1, 320, 7, 7, 1280, (1, 1), (1, 1), (1, 1), (0, 0, 0, 0)),  # 1x1 head
+    (1, 5, 10, 12, 6, (5, 5), (3, 2), (1, 2), (2, 1, 0, 3)),
+]
+
+
+@pytest.mark.parametrize("case", GENERAL_CASES, ids=lambda c: "x".join(map(str, c[:5])))
+@pytest.mark.parametrize("act", [nhip.ACT_NONE, nhip.ACT_RELU])
+def test_implicit_gemm_matches_oracle(case, act):
+    n, c, h, w, k, ker, st, dl, pad = case
+    x = RNG.uniform(-1, 1, (n, c, h, w)).astype(np.float32)
+    wt = workloads.he_normal(RNG, (k, c) + ker, c * ker[0] * ker[1])
+    b = RNG.normal(0, 0.05, k).astype(np.float32)
+    d = nhip.conv_desc(c, k, ker, st, dl, pad, bias=True, act=act, algorithm=nhip.ALGO_IMPLICIT_GEMM)
+    conv = nhip.Conv2dF32(d, wt, b)
+    got = host(conv.forward(dev(x)))
+    exp = oracle_conv(x, wt, b, st, dl, pad, act)
+    assert_close(got, exp, IGEMM_RTOL, f"igemm {case}")
+    assert max_rel_err(got, exp) <= IGEMM_RTOL
+
+
+def test_implicit_gemm_no_bias_sigmoid_and_residual():
+    n, c, h, w, k = 2, 24, 9, 11, 40
+    x = RNG.uniform(-1, 1, (n, c, h, w)).astype(np.float32)
+    wt = workloads.he_normal(RNG, (k, c, 3, 3), c * 9)
+    r = RNG.uniform(-1, 1, (n, k, h, w)).astype(np.float32)
+    d = nhip.conv_desc(c, k, bias=False, act=nhip.ACT_SIGMOID, algorithm=nhip.ALGO_IMPLICIT_GEMM)
+    got = host(nhip.Conv2dF32(d, wt).forward(dev(x)))
+    exp = oracle_conv(x, wt, None, (1, 1), (1, 1), (1, 1, 1, 1), nhip.ACT_SIGMOID)
+    assert_close(got, exp, IGEMM_RTOL, "sigmoid")
+    d = nhip.conv_desc(c, k, bias=False, act=nhip.ACT_RELU, algorithm=nhip.ALGO_IMPLICIT_GEMM)
+    got = host(nhip.Conv2dF32(d, wt).forward(dev(x), residual=dev(r)))
+    exp = oracle_conv(x, wt, None, (1, 1), (1, 1), (1, 1, 1, 1), nhip.ACT_RELU, residual=r)
+    assert_close(got, exp, IGEMM_RTOL, "residual")
+
+
+WINO_CASES = [
+    # (n, c, h, w, k, pad)
+    (1, 16, 4, 4, 16, (1, 1, 1, 1)),
+    (2, 20, 13, 10, 24, (1, 1, 1, 1)),      # ragged tiles, C not a multiple of 16
+    (2, 32, 9, 9, 48, (0, 0, 0, 0)),        # valid conv
+    (1, 17, 8, 12, 70, (2, 0, 1, 2)),       # asymmetric padding
+    (3, 64, 7, 7, 64, (1, 1, 1, 1)),
+    (1, 130, 6, 5, 200, (1, 1, 1, 1)),
+]
+
+
+@pytest.mark.parametrize("case", WINO_CASES, ids=lambda c: "x".join(map(str, c[:5])))
+def test_winograd_matches_oracle(case):
+    n, c, h, w, k, pad = case
+    x = RNG.uniform(-1, 1, (n, c, h, w)).astype(np.float32)
+    wt = workloads.he_normal(RNG, (k, c, 3, 3), c * 9)
+    b = RNG.normal(0, 0.05, k).astype(np.float32)
+    d = nhip.conv_desc(c, k, pad=pad, act=nhip.ACT_RELU, algorithm=nhip.ALGO_WINOGRAD)
+    got = host(nhip.Conv2dF32(d, wt, b).forward(dev(x)))
+    exp = oracle_conv(x, wt, b, (1, 1), (1, 1), pad, nhip.ACT_RELU)
+    assert_close(got, exp, WINO_RTOL, f"winograd {case}")
+    assert max_rel_err(got, exp) <= WINO_RTOL
+
+
+@pytest.mark.parametrize("algo", [nhip.ALGO_IMPLICIT_GEMM, nhip.ALGO_WINOGRAD])
+def test_config1_single_conv(algo):
+    x, wt, b = workloads.conv_single(seed=0)
+    d = nhip.conv_desc(64, 64, act=nhip.ACT_RELU, algorithm=algo)
+    got = host(nhip.Conv2dF32(d, wt, b).forward(dev(x)))
+    exp = oracle_conv(x, wt, b, (1, 1), (1, 1), (1, 1, 1, 1), nhip.ACT_RELU)
+    rtol = WINO_RTOL if algo == nhip.ALGO_WINOGRAD else IGEMM_RTOL
+    assert_close(got, exp, rtol, f"config1 algo {algo}")
+
+
+def run_stage(c, hw, n, algo, x, w1, b1, w2, b2):
+    """ResNet basic block: relu(conv1) -> relu(conv2 + x)."""
+    d1 = nhip.conv_desc(c, c, act=nhip.ACT_RELU, algorithm=algo)
+    d2 = nhip.conv_desc(c, c, act=nhip.ACT_RELU, algorithm=algo)
+    c1, c2 = nhip.Conv2dF32(d1, w1, b1), nhip.Conv2dF32(d2, w2, b2)
+    xd = dev(x)
+    y = c1.forward(xd)
+    return host(c2.forward(y, residual=xd))
+
+
+def oracle_stage(x, w1, b1, w2, b2):
+    p = (1, 1, 1, 1)
+    y = oracle_conv(x, w1, b1, (1, 1), (1, 1), p, nhip.ACT_RELU)
+    return oracle_conv(y, w2, b2, (1, 1), (1, 1), p, nhip.ACT_RELU, residual=x)
+
+
+@pytest.mark.parametrize("stage", workloads.RESNET18_STAGES, ids=lambda s: f"{s[0]}x{s[1]}")
+@pytest.mark.parametrize("algo", [nhip.ALGO_IMPLICIT_GEMM, nhip.ALGO_WINOGRAD])
+def test_resnet_stage_n2_matches_oracle(stage, algo):
+    c, hw = stage
+    x, w1, b1, w2, b2 = workloads.resnet_stage(c, hw, n=2, seed=0)
+    got = run_stage(c, hw, 2, algo, x, w1, b1, w2, b2)
+    exp = oracle_stage(x, w1, b1, w2, b2)
+    rtol = WINO_RTOL if algo == nhip.ALGO_WINOGRAD else IGEMM_RTOL
+    assert_close(got, exp, rtol, f"stage {stage} algo {algo}")
+
+
+@pytest.mark.parametrize("stage", workloads.RESNET18_STAGES, ids=lambda s: f"{s[0]}x{s[1]}")
+def test_resnet_stage_full_batch(stage):
+    """Batch 32 (the bench shape): images are independent ncnn blobs, so the
+    oracle is run on sampled images; Winograd and implicit GEMM must also
+    agree on every image."""
+    c, hw = stage
+    x, w1, b1, w2, b2 = workloads.resnet_stage(c, hw, n=32, seed=0)
+    wino = run_stage(c, hw, 32, nhip.ALGO_WINOGRAD, x, w1, b1, w2, b2)
+    igemm = run_stage(c, hw, 32, nhip.ALGO_IMPLICIT_GEMM, x, w1, b1, w2, b2)
+    assert_close(wino, igemm, WINO_RTOL, f"wino vs igemm {stage}")
+    for i in (0, 31):
+        exp = oracle_stage(x[i:i + 1], w1, b1, w2, b2)
+        assert_close(wino[i:i + 1], exp, WINO_RTOL, f"wino image {i}")
+        assert_close(igemm[i:i + 1], exp, IGEMM_RTOL, f"igemm image {i}")
+
+
+def test_batch_is_independent_images():
+    """The [N,C,H,W] batch equals N single-image calls (the reference ABI)."""
+    c, k = 32, 32
+    x = RNG.uniform(-1, 1, (4, c, 10, 10)).astype(np.float32)
+    wt = workloads.he_normal(RNG, (k, c, 3, 3), c * 9)
+    for algo in (nhip.ALGO_IMPLICIT_GEMM, nhip.ALGO_WINOGRAD):
+        conv = nhip.Conv2dF32(nhip.conv_desc(c, k, bias=False, algorithm=algo), wt)
+        whole = host(conv.forward(dev(x)))
+        for i in range(4):
+            one = host(conv.forward(dev(x[i:i + 1])))
+            np.testing.assert_array_equal(one, whole[i:i + 1])
+
+
+def test_empty_batch_and_workspace_errors():
+    c, k = 16, 16
+    wt = workloads.he_normal(RNG, (k, c, 3, 3), c * 9)
+    conv = nhip.Conv2dF32(nhip.conv_desc(c, k, bias=False, algorithm=nhip.ALGO_WINOGRAD), wt)
+    x = torch.empty((0, c, 8, 8), device="cuda")
+    assert conv.forward(x).shape == (0, k, 8, 8)
+    x = dev(RNG.uniform(-1, 1, (1, c, 8, 8)).astype(np.float32))
+    need = conv.workspace_size(1, 8, 8)
+    assert need > 0
+    small = torch.empty(need - 1, dtype=torch.uint8, device="cuda")
+    with pytest.raises(nhip.NhipError) as e:
+        conv.forward(x, workspace=small)
+    assert e.value.status == 5
+
+
+def test_kernel_timer_counts_launches():
+    c, k = 16, 16
+    wt = workloads.he_normal(RNG, (k, c, 3, 3), c * 9)
+    conv = nhip.Conv2dF32(nhip.conv_desc(c, k, bias=False, algorithm=nhip.ALGO_WINOGRAD), wt)
+    x = dev(RNG.uniform(-1, 1, (2, c, 8, 8)).astype(np.float32))
+    nhip.timer_start("wino_gemm")
+    for _ in range(3):
+        conv.forward(x)
+    n, ms = nhip.timer_stop()
+    assert n == 3 and ms > 0.0

@@ -1,0 +1,150 @@
+"""GPU parity: int8 Convolution with requantize, bit-exact against the CPU
+oracle's restatement of NCNNToTosa.cpp:1136-1315 (quantize :322-389,
+dequantizeAccumulator :577-637, bias add :1294-1300, requantize :1309-1312,
+relu after, ImportConvolution.cpp:236-241), plus the reference's own
+known-answer cases (test/Conversion/NCNNToTosa/quantized-contractions.mlir,
+test/Numerical/fixtures/generate_int8_bins.py)."""
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+
+import nhip  # noqa: E402
+import workloads  # noqa: E402
+from oracle import refcpu  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    assert torch.cuda.is_available(), "GPU tests need a HIP device"
+    nhip.init(0)
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def host(t):
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def run(desc, x, w, b, ws, is_, os_):
+    conv = nhip.Conv2dInt8(desc, w, b, ws, is_, os_)
+    return host(conv.forward(dev(x)))
+
+
+def oracle(desc, x, w_i8, b, ws, is_, os_):
+    n, c, h, wd = x.shape
+    g = refcpu.geom(n, c, h, wd, desc.num_output, (desc.kernel_h, desc.kernel_w),
+                    (desc.stride_h, desc.stride_w), (desc.dilation_h, desc.dilation_w),
+                    (desc.pad_top, desc.pad_bottom, desc.pad_left, desc.pad_right))
+    return refcpu.conv2d_int8(g, x, w_i8, b, ws, is_, os_, scale_term=desc.int8_scale_term,
+                              activation=desc.activation_type)
+
+
+def test_config4_batch2_bit_exact():
+    cfg = workloads.int8_conv(seed=0, n=2)
+    d = nhip.conv_desc(128, 128, act=nhip.ACT_RELU, int8_scale_term=101)
+    got = run(d, cfg["x"], cfg["w"], cfg["bias"], cfg["ws"], cfg["input_scale"], cfg["output_scale"])
+    exp = oracle(d, cfg["x"], cfg["w"], cfg["bias"], cfg["ws"], cfg["input_scale"], cfg["output_scale"])
+    assert got.dtype == np.int8
+    np.testing.assert_array_equal(got, exp)
+    # the case is not degenerate: many distinct levels, some saturation
+    assert len(np.unique(got)) > 64 and (got == 127).any() and (got == 0).any()
+
+
+def test_config4_full_batch_sampled_images_bit_exact():
+    cfg = workloads.int8_conv(seed=0, n=32)
+    d = nhip.conv_desc(128, 128, act=nhip.ACT_RELU, int8_scale_term=101)
+    got = run(d, cfg["x"], cfg["w"], cfg["bias"], cfg["ws"], 1.0, 1.0)
+    for i in (0, 13, 31):
+        exp = oracle(d, cfg["x"][i:i + 1], cfg["w"], cfg["bias"], cfg["ws"], 1.0, 1.0)
+        np.testing.assert_array_equal(got[i:i + 1], exp)
+
+
+def test_quantized_contractions_known_answers():
+    # quantized-contractions.mlir:3-8: ones weight [3,2,1,1], ws [2,4,8], is 2,
+    # bias [1,2,3], term 1: out = 3/(ws*2) + bias = 1.75, 2.375, 3.1875.
+    x = np.stack([np.full((3, 3), 1.0), np.full((3, 3), 0.25)]).astype(np.float32)[None]
+    w = np.ones((3, 2, 1, 1), np.int8)
+    d = nhip.conv_desc(2, 3, (1, 1), pad=(0, 0, 0, 0), int8_scale_term=1)
+    got = run(d, x, w, np.array([1, 2, 3], np.float32), np.array([2, 4, 8], np.float32), 2.0, 1.0)
+    assert got.dtype == np.float32
+    for ch, v in enumerate([1.75, 2.375, 3.1875]):
+        np.testing.assert_array_equal(got[0, ch], np.full((3, 3), v, np.float32))
+    # requantized_convolution: int8 input 3 and 5, os 4, term 101 -> 8, 4, 2
+    xi = np.stack([np.full((3, 3), 3), np.full((3, 3), 5)]).astype(np.int8)[None]
+    d = nhip.conv_desc(2, 3, (1, 1), pad=(0, 0, 0, 0), bias=False, int8_scale_term=101)
+    got = run(d, xi, w, None, np.array([2, 4, 8], np.float32), 2.0, 4.0)
+    np.testing.assert_array_equal(got[0, :, 0, 0], [8, 4, 2])
+    got = run(d, -xi, w, None, np.array([2, 4, 8], np.float32), 2.0, 4.0)
+    np.testing.assert_array_equal(got[0, :, 0, 0], [-8, -4, -2])
+
+
+def test_fixture_generator_weights_known_answer():
+    # generate_int8_bins.py:20-28 closed-form weights, convolution_int8_term101
+    w = np.array([((i * 7 + 3) % 15) - 7 for i in range(6)], np.int8).reshape(3, 2, 1, 1)
+    b = np.array([-0.125, 0.0, 0.125], np.float32)
+    ws = np.array([5.0, 6.5, 8.0], np.float32)
+    x = np.array([0.25, -0.5], np.float32).reshape(1, 2, 1, 1)
+    d = nhip.conv_desc(2, 3, (1, 1), pad=(0, 0, 0, 0), int8_scale_term=101)
+    got = run(d, x, w, b, ws, 8.0, 6.0)
+    np.testing.assert_array_equal(got[0, :, 0, 0], [-4, -2, -1])
+
+
+CASES = [
+    # (n, c, h, w, k, kernel, stride, dil, pad, term, act, weight fp32?, scalar ws?)
+    (2, 3, 11, 9, 70, (3, 3), (1, 1), (1, 1), (1, 1, 1, 1), 101, 1, False, False),
+    (1, 40, 14, 14, 64, (1, 1), (1, 1), (1, 1), (0, 0, 0, 0), 101, 0, True, False),
+    (2, 16, 15, 13, 20, (3, 3), (2, 2), (1, 1), (1, 1, 1, 1), 1, 1, True, True),
+    (1, 24, 12, 12, 130, (3, 3), (1, 1), (2, 2), (2, 2, 2, 2), 2, 0, False, True),
+    (3, 33, 8, 10, 48, (2, 3), (1, 2), (1, 1), (0, 1, 2, 0), 102, 1, True, False),
+]
+
+
+@pytest.mark.parametrize("case", CASES, ids=lambda c: "x".join(map(str, c[:5])) + f"-t{c[9]}")
+def test_int8_shapes_bit_exact(case):
+    n, c, h, w, k, ker, st, dl, pad, term, act, wf32, scalar = case
+    rng = np.random.default_rng(hash(case) % (2 ** 32))
+    x = rng.uniform(-1.5, 1.5, (n, c, h, w)).astype(np.float32)
+    ws = np.float32(rng.uniform(20, 200)) * np.ones(1 if scalar else k, np.float32)
+    if not scalar:
+        ws = rng.uniform(20, 200, k).astype(np.float32)
+    wfloat = rng.uniform(-0.6, 0.6, (k, c) + ker).astype(np.float32)
+    # oracle takes the already-quantized int8 weights
+    ws_full = np.broadcast_to(ws, (k,)) if ws.size == 1 else ws
+    w_i8 = np.stack([refcpu.quantize_f32_i8(wfloat[o], ws_full[o:o + 1]) for o in range(k)])
+    b = rng.normal(0, 0.3, k).astype(np.float32)
+    is_, os_ = 60.0, 25.0
+    d = nhip.conv_desc(c, k, ker, st, dl, pad, act=act, int8_scale_term=term)
+    got = run(d, x, wfloat if wf32 else w_i8, b, ws, is_, os_)
+    exp = oracle(d, x, w_i8, b, ws, is_, os_)
+    assert got.dtype == exp.dtype
+    np.testing.assert_array_equal(got, exp)
+
+
+def test_rounding_ties_and_saturation_on_device():
+    # x*is lands exactly on .5 and on the 0.49999997 trap; acc passes through
+    # a 1x1 identity so the output requantize sees the same values.
+    vals = np.array([0.5, -0.5, 1.5, -1.5, 2.5, -2.5, 0.49999997, -0.49999997,
+                     126.5, -126.5, 127.5, -127.5, 1e6, -1e6, 0.0, 3.0], np.float32)
+    x = vals.reshape(1, 1, 4, 4)
+    w = np.ones((1, 1, 1, 1), np.int8)
+    d = nhip.conv_desc(1, 1, (1, 1), pad=(0, 0, 0, 0), bias=False, int8_scale_term=101)
+    got = run(d, x, w, None, np.ones(1, np.float32), 1.0, 1.0)
+    exp = oracle(d, x, w, None, np.ones(1, np.float32), 1.0, 1.0)
+    np.testing.assert_array_equal(got, exp)
+    np.testing.assert_array_equal(got.ravel()[:8], [1, -1, 2, -2, 3, -3, 1, -1])
+    np.testing.assert_array_equal(got.ravel()[8:14], [127, -127, 127, -127, 127, -127])
+
+
+def test_zero_weight_scale_selects_zero():
+    x = np.ones((1, 2, 3, 3), np.float32)
+    w = np.ones((2, 2, 1, 1), np.int8)
+    d = nhip.conv_desc(2, 2, (1, 1), pad=(0, 0, 0, 0), int8_scale_term=1)
+    got = run(d, x, w, np.array([0.5, 0.25], np.float32), np.array([0.0, 2.0], np.float32), 1.0, 1.0)
+    np.testing.assert_array_equal(got[0, 0], np.full((3, 3), 0.5, np.float32))
+    np.testing.assert_array_equal(got[0, 1], np.full((3, 3), 2 * 0.5 + 0.25, np.float32))
