@@ -116,6 +116,9 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration-mib", type=int, default=0,
+                    help="first run a plain device copy of this many MiB (hipMemcpy D2D) so that "
+                         "rocprofv3 FETCH_SIZE/WRITE_SIZE can be scaled against known bytes")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -129,6 +132,14 @@ def main():
 
     torch.cuda.set_device(0)
     nhip.init(0)
+    if args.copy_calibration_mib:
+        nbytes = args.copy_calibration_mib << 20
+        src = torch.ones(nbytes // 4, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            nhip.check(nhip.load().nhip_memcpy_d2d(nhip._ptr(dst), nhip._ptr(src), nbytes, nhip._stream()))
+        torch.cuda.synchronize()
+        del src, dst
     stages = stage_stack(nhip, workloads, torch, BATCH)
     for _ in range(args.warmup):
         run_step(stages)

@@ -235,7 +235,7 @@ int launch_conv_int8(const nhip_conv_plan* p, const void* in, int in_is_i8,
     return fail(NHIP_STATUS_OUTPUT_CAPACITY_INSUFFICIENT,
                 "int8 conv: workspace of " + std::to_string(need) + " bytes required");
   int8_t* xq = static_cast<int8_t*>(ws);
-  NHIP_LAUNCH("quantize_nchw_to_nhwc", s, quantize_nchw_to_nhwc, dim3((unsigned)ceil_div((int64_t)h * w, 64), n), dim3(kThreads),
+  NHIP_LAUNCH("quantize_nchw_to_nhwc", quantize_nchw_to_nhwc, dim3((unsigned)ceil_div((int64_t)h * w, 64), n), dim3(kThreads),
                      0, s, in, in_is_i8, xq, p->g.c, h * w, p->c_pad, p->input_scale);
   NHIP_TRY(check_launch("quantize_nchw_to_nhwc"));
 
@@ -265,14 +265,14 @@ int launch_conv_int8(const nhip_conv_plan* p, const void* in, int in_is_i8,
   const int mt128 = (int)ceil_div(p->g.k, 128), mt64 = (int)ceil_div(p->g.k, 64);
   const int nt128 = (int)ceil_div(g.npix, 128), nt64 = (int)ceil_div(g.npix, 64);
   if (p->m_pad % 128 == 0 && (int64_t)mt128 * nt128 >= target) {
-    NHIP_LAUNCH("conv_int8<128,128>", s, (conv_int8_kernel<128, 128>), dim3(nt128, mt128), dim3(kThreads), 0, s, g);
+    NHIP_LAUNCH("conv_int8<128,128>", (conv_int8_kernel<128, 128>), dim3(nt128, mt128), dim3(kThreads), 0, s, g);
     return check_launch("conv_int8<128,128>");
   }
   if ((int64_t)mt64 * nt128 >= target) {
-    NHIP_LAUNCH("conv_int8<64,128>", s, (conv_int8_kernel<64, 128>), dim3(nt128, mt64), dim3(kThreads), 0, s, g);
+    NHIP_LAUNCH("conv_int8<64,128>", (conv_int8_kernel<64, 128>), dim3(nt128, mt64), dim3(kThreads), 0, s, g);
     return check_launch("conv_int8<64,128>");
   }
-  NHIP_LAUNCH("conv_int8<64,64>", s, (conv_int8_kernel<64, 64>), dim3(nt64, mt64), dim3(kThreads), 0, s, g);
+  NHIP_LAUNCH("conv_int8<64,64>", (conv_int8_kernel<64, 64>), dim3(nt64, mt64), dim3(kThreads), 0, s, g);
   return check_launch("conv_int8<64,64>");
 }
 

@@ -278,10 +278,10 @@ int launch_dwconv_f32(const nhip_conv_plan* p, const float* in, float* out,
   const int64_t blocks = ceil_div(a.planes, a.ppb) * a.bands;
   const bool fast = a.kh == 3 && a.kw == 3 && a.sh == 1 && a.sw == 1 && a.dh == 1 && a.dw == 1;
   if (fast) {
-    NHIP_LAUNCH("dwconv3x3s1_f32", s, dwconv3x3s1_f32_kernel, dim3((unsigned)blocks), dim3(256), (size_t)lds, s, a);
+    NHIP_LAUNCH("dwconv3x3s1_f32", dwconv3x3s1_f32_kernel, dim3((unsigned)blocks), dim3(256), (size_t)lds, s, a);
     return check_launch("dwconv3x3s1_f32");
   }
-  NHIP_LAUNCH("dwconv_f32", s, dwconv_f32_kernel, dim3((unsigned)blocks), dim3(256), (size_t)lds, s, a);
+  NHIP_LAUNCH("dwconv_f32", dwconv_f32_kernel, dim3((unsigned)blocks), dim3(256), (size_t)lds, s, a);
   return check_launch("dwconv_f32");
 }
 
@@ -295,7 +295,7 @@ int nhip_relu_f32(const float* input, float* output, int64_t count, void* stream
   if (!input || !output) return fail(NHIP_STATUS_NULL_POINTER, "relu: null pointer");
   if (count < 0) return fail(NHIP_STATUS_INVALID_SHAPE, "relu: negative count");
   if (count == 0) return ok();
-  NHIP_LAUNCH("relu_f32", as_stream(stream), relu_f32_kernel, dim3(grid_for(count)), dim3(256), 0, as_stream(stream), input,
+  NHIP_LAUNCH("relu_f32", relu_f32_kernel, dim3(grid_for(count)), dim3(256), 0, as_stream(stream), input,
                      output, count);
   return check_launch("relu_f32");
 }
@@ -304,7 +304,7 @@ int nhip_relu_i8(const int8_t* input, int8_t* output, int64_t count, void* strea
   if (!input || !output) return fail(NHIP_STATUS_NULL_POINTER, "relu_i8: null pointer");
   if (count < 0) return fail(NHIP_STATUS_INVALID_SHAPE, "relu_i8: negative count");
   if (count == 0) return ok();
-  NHIP_LAUNCH("relu_i8", as_stream(stream), relu_i8_kernel, dim3(grid_for(count)), dim3(256), 0, as_stream(stream), input,
+  NHIP_LAUNCH("relu_i8", relu_i8_kernel, dim3(grid_for(count)), dim3(256), 0, as_stream(stream), input,
                      output, count);
   return check_launch("relu_i8");
 }
@@ -314,7 +314,7 @@ int nhip_add_f32(const float* a, const float* b, float* output, int64_t count, i
   if (!a || !b || !output) return fail(NHIP_STATUS_NULL_POINTER, "add: null pointer");
   if (count < 0) return fail(NHIP_STATUS_INVALID_SHAPE, "add: negative count");
   if (count == 0) return ok();
-  NHIP_LAUNCH("add_f32", as_stream(stream), add_f32_kernel, dim3(grid_for(count)), dim3(256), 0, as_stream(stream), a, b,
+  NHIP_LAUNCH("add_f32", add_f32_kernel, dim3(grid_for(count)), dim3(256), 0, as_stream(stream), a, b,
                      output, count, relu ? 1 : 0);
   return check_launch("add_f32");
 }
@@ -326,7 +326,7 @@ int nhip_global_avgpool_f32(const float* input, float* output, int32_t n, int32_
     return fail(NHIP_STATUS_INVALID_SHAPE, "global_avgpool: invalid shape");
   if (n == 0) return ok();
   const int64_t planes = (int64_t)n * c;
-  NHIP_LAUNCH("global_avgpool_f32", as_stream(stream), gap_f32_kernel, dim3((unsigned)ceil_div(planes, 4)), dim3(256), 0,
+  NHIP_LAUNCH("global_avgpool_f32", gap_f32_kernel, dim3((unsigned)ceil_div(planes, 4)), dim3(256), 0,
                      as_stream(stream), input, output, planes, h * w);
   return check_launch("global_avgpool_f32");
 }
@@ -338,7 +338,7 @@ int nhip_quantize_f32_i8(const float* input, int8_t* output, int32_t n, int32_t 
     return fail(NHIP_STATUS_INVALID_SHAPE, "quantize: invalid shape or scale count");
   const int64_t count = (int64_t)n * c * plane;
   if (count == 0) return ok();
-  NHIP_LAUNCH("quantize_f32_i8", as_stream(stream), quantize_f32_i8_kernel, dim3(grid_for(count)), dim3(256), 0, as_stream(stream),
+  NHIP_LAUNCH("quantize_f32_i8", quantize_f32_i8_kernel, dim3(grid_for(count)), dim3(256), 0, as_stream(stream),
                      input, output, count, c, plane, scale, scale_count);
   return check_launch("quantize_f32_i8");
 }
@@ -355,7 +355,7 @@ int nhip_requantize_i32_i8(const int32_t* input, int8_t* output, int32_t n, int3
     return fail(NHIP_STATUS_INVALID_SHAPE, "requantize: invalid shape or scale count");
   const int64_t count = (int64_t)n * c * plane;
   if (count == 0) return ok();
-  NHIP_LAUNCH("requantize_i32_i8", as_stream(stream), requantize_kernel, dim3(grid_for(count)), dim3(256), 0, as_stream(stream),
+  NHIP_LAUNCH("requantize_i32_i8", requantize_kernel, dim3(grid_for(count)), dim3(256), 0, as_stream(stream),
                      input, output, count, c, plane, in_scale, in_scale_count, out_scale,
                      out_scale_count, bias, bias_count, activation);
   return check_launch("requantize_i32_i8");
@@ -370,7 +370,7 @@ int nhip_dequantize_i32_f32(const int32_t* input, float* output, int32_t n, int3
     return fail(NHIP_STATUS_INVALID_SHAPE, "dequantize: invalid shape or scale count");
   const int64_t count = (int64_t)n * c * plane;
   if (count == 0) return ok();
-  NHIP_LAUNCH("dequantize_i32_f32", as_stream(stream), dequantize_kernel, dim3(grid_for(count)), dim3(256), 0, as_stream(stream),
+  NHIP_LAUNCH("dequantize_i32_f32", dequantize_kernel, dim3(grid_for(count)), dim3(256), 0, as_stream(stream),
                      input, output, count, c, plane, scale, scale_count, bias, bias_count);
   return check_launch("dequantize_i32_f32");
 }

@@ -341,7 +341,7 @@ __global__ void ip_splitk_reduce(const float* part, const float* bias,
 
 template <int BM, int BN, Mode MODE>
 int launch(const GemmArgs& g, dim3 grid, hipStream_t s, const char* name) {
-  NHIP_LAUNCH(name, s, (gemm_f32_kernel<BM, BN, MODE>), grid, dim3(kThreads), 0, s, g);
+  NHIP_LAUNCH(name, (gemm_f32_kernel<BM, BN, MODE>), grid, dim3(kThreads), 0, s, g);
   return check_launch(name);
 }
 
@@ -464,7 +464,7 @@ int launch_innerproduct_f32(const nhip_ip_plan* p, const float* in,
                                      "innerproduct_f32<64,64>")));
   if (splits > 1) {
     const int64_t total = (int64_t)m * p->n_out;
-    NHIP_LAUNCH("ip_splitk_reduce", s, ip_splitk_reduce, dim3((unsigned)ceil_div(total, 256)), dim3(256), 0, s,
+    NHIP_LAUNCH("ip_splitk_reduce", ip_splitk_reduce, dim3((unsigned)ceil_div(total, 256)), dim3(256), 0, s,
                        static_cast<const float*>(ws), p->bias, out, m, p->n_out, p->n_pad,
                        splits, p->act);
     return check_launch("ip_splitk_reduce");

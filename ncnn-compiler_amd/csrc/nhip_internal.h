@@ -2,6 +2,7 @@
 // Device code targets gfx950 (CDNA4) only: wave64, fp32/int8 MFMA.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -25,27 +26,34 @@ int check_launch(const char* kernel);
 
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
-// Launch bracketing for nhip_timer_*: construct right before a launch on
-// stream `s`; the destructor records the closing event.  No-op when the
-// timer is off or the name does not match its filter.
+// Kernel timing for nhip_timer_*: when the timer is on and `kernel` matches
+// its filter, holds a start/stop event pair that hipExtLaunchKernelGGL
+// stamps from the kernel's own dispatch on its stream (no separate marker
+// packets around the launch).
 class LaunchTimer {
  public:
-  LaunchTimer(const char* kernel, hipStream_t s);
-  ~LaunchTimer();
+  explicit LaunchTimer(const char* kernel);
+  bool active() const { return start_ != nullptr; }
+  hipEvent_t start() const { return start_; }
+  hipEvent_t stop() const { return stop_; }
   LaunchTimer(const LaunchTimer&) = delete;
   LaunchTimer& operator=(const LaunchTimer&) = delete;
 
  private:
+  hipEvent_t start_ = nullptr;
   hipEvent_t stop_ = nullptr;
-  hipStream_t stream_ = nullptr;
 };
 
-// Launch `kernel, grid, block, shmem, stream, args...` on `stream`, timed by
-// nhip_timer_* under `name` when the timer is on.
-#define NHIP_LAUNCH(name, stream, ...)            \
-  do {                                            \
-    ::nhip::LaunchTimer _nhip_timer(name, stream); \
-    hipLaunchKernelGGL(__VA_ARGS__);              \
+// NHIP_LAUNCH(name, kernel, grid, block, shmem, stream, args...): launch,
+// timed under `name` while nhip_timer_start is in effect.
+#define NHIP_LAUNCH(name, kernel, grid, block, shmem, strm, ...)                                      \
+  do {                                                                                              \
+    ::nhip::LaunchTimer _nhip_timer(name);                                                          \
+    if (_nhip_timer.active())                                                                       \
+      hipExtLaunchKernelGGL(kernel, grid, block, shmem, strm, _nhip_timer.start(), _nhip_timer.stop(), \
+                            0, __VA_ARGS__);                                                        \
+    else                                                                                            \
+      hipLaunchKernelGGL(kernel, grid, block, shmem, strm, __VA_ARGS__);                            \
   } while (0)
 
 int cu_count();  // compute units of the current device (cached)

@@ -61,24 +61,20 @@ TimerState& timer() {
 }
 }  // namespace
 
-LaunchTimer::LaunchTimer(const char* kernel, hipStream_t s) {
+LaunchTimer::LaunchTimer(const char* kernel) {
   TimerState& t = timer();
   std::lock_guard<std::mutex> lock(t.mu);
   if (!t.on || (!t.filter.empty() && std::string(kernel).find(t.filter) == std::string::npos)) return;
-  hipEvent_t start = nullptr;
-  if (hipEventCreate(&start) != hipSuccess) return;
-  if (hipEventCreate(&stop_) != hipSuccess) {
-    (void)hipEventDestroy(start);
-    stop_ = nullptr;
+  if (hipEventCreate(&start_) != hipSuccess) {
+    start_ = nullptr;
     return;
   }
-  stream_ = s;
-  (void)hipEventRecord(start, s);
-  t.events.emplace_back(start, stop_);
-}
-
-LaunchTimer::~LaunchTimer() {
-  if (stop_) (void)hipEventRecord(stop_, stream_);
+  if (hipEventCreate(&stop_) != hipSuccess) {
+    (void)hipEventDestroy(start_);
+    start_ = stop_ = nullptr;
+    return;
+  }
+  t.events.emplace_back(start_, stop_);
 }
 
 int cu_count() {
@@ -188,8 +184,9 @@ int conv_out(const ConvGeom& g, int h, int w, int* oh, int* ow) {
 int check_forward(const nhip_conv_plan* p, const void* in, const void* out, int n, int h, int w,
                   int* oh, int* ow) {
   if (!p) return fail(NHIP_STATUS_NULL_POINTER, "conv: null plan");
-  if (!in || !out) return fail(NHIP_STATUS_NULL_POINTER, "conv: null input or output");
   if (n < 0 || h <= 0 || w <= 0) return fail(NHIP_STATUS_INVALID_SHAPE, "conv: invalid input extent");
+  // An empty batch has no elements to address: its buffers may be null.
+  if (n > 0 && (!in || !out)) return fail(NHIP_STATUS_NULL_POINTER, "conv: null input or output");
   NHIP_TRY(conv_out(p->g, h, w, oh, ow));
   const int64_t lim = std::numeric_limits<int32_t>::max();
   if ((int64_t)p->g.c * h * w > lim / 4 || (int64_t)p->g.k * *oh * *ow > lim / 4 ||
@@ -560,8 +557,9 @@ int nhip_innerproduct_workspace_size(nhip_ip_t p, int32_t m, uint64_t* bytes) {
 
 int nhip_innerproduct_f32_forward(nhip_ip_t p, const float* input, float* output, int32_t m, void* workspace,
                                   uint64_t workspace_bytes, void* stream) {
-  if (!p || !input || !output) return fail(NHIP_STATUS_NULL_POINTER, "innerproduct_forward: null pointer");
+  if (!p) return fail(NHIP_STATUS_NULL_POINTER, "innerproduct_forward: null plan");
   if (m < 0) return fail(NHIP_STATUS_INVALID_SHAPE, "innerproduct: negative m");
+  if (m > 0 && (!input || !output)) return fail(NHIP_STATUS_NULL_POINTER, "innerproduct_forward: null pointer");
   if ((int64_t)m * std::max(p->k_in, p->n_pad) > std::numeric_limits<int32_t>::max())
     return fail(NHIP_STATUS_SHAPE_ARITHMETIC_OVERFLOW, "innerproduct: m too large");
   if (m == 0) return ok();

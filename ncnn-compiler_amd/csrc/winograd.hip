@@ -218,7 +218,7 @@ int launch_conv_winograd_f32(const nhip_conv_plan* p, const float* in,
   float* M = V + (int64_t)36 * ws_.c_pad * ws_.t_pad;
   {
     const int64_t total = (int64_t)ws_.c_pad * ws_.t_pad;
-    NHIP_LAUNCH("wino_input_transform", s, wino_input_transform, dim3((unsigned)ceil_div(total, 256)), dim3(256), 0, s,
+    NHIP_LAUNCH("wino_input_transform", wino_input_transform, dim3((unsigned)ceil_div(total, 256)), dim3(256), 0, s,
                        in, V, ws_.c, h, w, ws_.th, ws_.tw, ws_.t, ws_.t_pad, ws_.c_pad,
                        p->g.pt, p->g.pl);
     NHIP_TRY(check_launch("wino_input_transform"));
@@ -226,7 +226,7 @@ int launch_conv_winograd_f32(const nhip_conv_plan* p, const float* in,
   NHIP_TRY(launch_wino_gemm(p->weight, V, M, ws_.m_pad, ws_.c_pad, ws_.t_pad, s));
   {
     const int64_t total = (int64_t)p->g.k * ws_.t;
-    NHIP_LAUNCH("wino_output_transform", s, wino_output_transform, dim3((unsigned)ceil_div(total, 256)), dim3(256), 0, s,
+    NHIP_LAUNCH("wino_output_transform", wino_output_transform, dim3((unsigned)ceil_div(total, 256)), dim3(256), 0, s,
                        M, p->bias, residual, out, p->g.k, oh, ow, ws_.th, ws_.tw, ws_.t,
                        ws_.t_pad, ws_.m_pad, p->g.act);
     NHIP_TRY(check_launch("wino_output_transform"));
