@@ -9,9 +9,10 @@ resident in HBM.
 
 value = direct-equivalent conv TFLOP/s (2*N*K*OH*OW*C*9 per conv, the same
 count for Winograd as for direct convolution).  roofline = the Winograd
-batched-GEMM kernel (the dominant kernel), its executed GEMM FLOPs per launch
-over its average duration from HIP events recorded around each of its
-launches on the launch stream inside the timed region.  cpu_baseline = the
+batched-GEMM kernel (36 fp32 MFMA GEMMs per conv, the dominant kernel): its
+work 2*36*T*C*K per launch (T = N*ceil(OH/4)*ceil(OW/4) tiles) over its
+average duration, from HIP events stamped by each of its dispatches on the
+launch stream inside the timed region.  cpu_baseline = the
 CPU oracle (restatement of the reference's lowered loops, compiled like the
 reference's .so: -O3, no -march, no FP contraction, OpenMP) on a bounded
 sample of the same stages.
@@ -145,7 +146,8 @@ def main():
         run_step(stages)
     torch.cuda.synchronize()
 
-    nhip.timer_start("wino_gemm")
+    fused = os.environ.get("NHIP_WINOGRAD_VARIANT", "") in ("2", "221", "114")
+    nhip.timer_start("wino_fused" if fused else "wino_gemm")
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):

@@ -83,6 +83,7 @@ struct Int8Args {
   int kred_pad;
   int m;               // num_output
   const int8_t* x;     // NHWC [N][H][W][c_pad]
+  uint32_t x_bytes;    // size of x (< 2^31)
   int H, W, c_pad, OW, OHW, sh, sw, pt, pl;
   int npix;            // N*OH*OW
   const int* ktab;     // per 16-byte k chunk: c0<<16 | dy<<8 | dx (sentinel past kred)
@@ -119,7 +120,9 @@ __global__ __launch_bounds__(kThreads) void conv_int8_kernel(Int8Args g) {
   const int rem = pp - img * g.OHW;
   const int oh = rem / g.OW, ow = rem - (rem / g.OW) * g.OW;
   const int iy0 = oh * g.sh - g.pt, ix0 = ow * g.sw - g.pl;
-  const int8_t* img_base = g.x + (int64_t)img * g.H * g.W * g.c_pad;
+  // the whole NHWC scratch image is one wave-uniform buffer resource
+  const __amdgpu_buffer_rsrc_t img_rs = make_rsrc(g.x, g.x_bytes);
+  const int img_pix0 = img * g.H;
 
   auto load = [&](int kt) {
 #pragma unroll
@@ -134,10 +137,8 @@ __global__ __launch_bounds__(kThreads) void conv_int8_kernel(Int8Args g) {
       const int t = g.ktab[chunk];  // wave-uniform
       const int c0 = t >> 16, dy = (t >> 8) & 255, dx = t & 255;
       const int y = iy0 + dy, x = ix0 + dx;
-      int4 v = make_int4(0, 0, 0, 0);
-      if (pix_ok && c0 < g.c_pad && (unsigned)y < (unsigned)g.H && (unsigned)x < (unsigned)g.W)
-        v = *reinterpret_cast<const int4*>(img_base + ((int64_t)y * g.W + x) * g.c_pad + c0);
-      rb[u] = v;
+      const bool in = pix_ok && c0 < g.c_pad && (unsigned)y < (unsigned)g.H && (unsigned)x < (unsigned)g.W;
+      rb[u] = buf_load_b128(img_rs, in ? (uint32_t)(((img_pix0 + y) * g.W + x) * g.c_pad + c0) : kBufOOB);
     }
   };
   auto store = [&](int buf) {
@@ -244,6 +245,7 @@ int launch_conv_int8(const nhip_conv_plan* p, const void* in, int in_is_i8,
   g.kred_pad = p->kred_pad;
   g.m = p->g.k;
   g.x = xq;
+  g.x_bytes = (uint32_t)need;
   g.H = h;
   g.W = w;
   g.c_pad = p->c_pad;

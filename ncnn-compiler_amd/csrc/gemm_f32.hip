@@ -40,6 +40,7 @@ struct GemmArgs {
   int n;                 // valid columns (pixels / tiles / IP outputs)
   int kdim;              // reduction length (multiple of kBK after padding)
   int k_valid;           // IP: valid input length (loads past it read 0)
+  uint32_t b_bytes;      // conv: size of the input tensor (< 2^31)
   // conv geometry
   const int* ktab;
   int C, H, W, OW, OHW, sh, sw, pt, pl;
@@ -144,8 +145,10 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_kernel(GemmArgs g) {
   // Conv per-thread pixel state (fixed for the whole block).
   const int jj = tid % BN;
   const int kg = __builtin_amdgcn_readfirstlane(tid / BN);
-  const float* img_base = nullptr;
-  int iy0 = 0, ix0 = 0;
+  // Conv: the whole input is one wave-uniform buffer resource (< 2^31 bytes);
+  // zero padding reads through kBufOOB offsets.
+  const __amdgpu_buffer_rsrc_t img_rs = make_rsrc(B, g.b_bytes);
+  int iy0 = 0, ix0 = 0, img_plane0 = 0;
   bool pix_ok = false;
   if constexpr (MODE == Mode::Conv) {
     const int p = j0 + jj;
@@ -157,7 +160,7 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_kernel(GemmArgs g) {
     const int ow = rem - oh * g.OW;
     iy0 = oh * g.sh - g.pt;
     ix0 = ow * g.sw - g.pl;
-    img_base = B + (int64_t)img * g.C * g.H * g.W;
+    img_plane0 = img * g.C;
   }
 
   auto load_b = [&](int kt) {
@@ -168,10 +171,9 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_kernel(GemmArgs g) {
         const int t = g.ktab[kbase + u];  // wave-uniform
         const int c = t >> 16, dy = (t >> 8) & 255, dx = t & 255;
         const int y = iy0 + dy, x = ix0 + dx;
-        float v = 0.f;
-        if (pix_ok && c < g.C && (unsigned)y < (unsigned)g.H && (unsigned)x < (unsigned)g.W)
-          v = img_base[((int64_t)c * g.H + y) * g.W + x];
-        rb[u] = v;
+        const bool in = pix_ok && c < g.C && (unsigned)y < (unsigned)g.H && (unsigned)x < (unsigned)g.W;
+        rb[u] = buf_load_f32(img_rs, in ? (uint32_t)((((img_plane0 + c) * g.H + y) * g.W + x) * (int)sizeof(float))
+                                        : kBufOOB);
       }
     } else if constexpr (MODE == Mode::Wino) {
 #pragma unroll
@@ -359,6 +361,7 @@ int launch_conv_igemm_f32(const nhip_conv_plan* p, const float* in,
   g.lda = p->kred_pad;
   g.m = p->g.k;
   g.b = in;
+  g.b_bytes = (uint32_t)((size_t)n * p->g.c * h * w * sizeof(float));
   g.n = n * oh * ow;
   g.kdim = p->kred_pad;
   g.ktab = p->ktab;

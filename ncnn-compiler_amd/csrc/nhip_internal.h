@@ -67,6 +67,25 @@ typedef float v16f __attribute__((ext_vector_type(16)));
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 
+// ---- raw buffer loads ---------------------------------------------------------
+// A raw buffer load whose byte offset is at or past the resource's size
+// returns 0 without touching memory.  Gathers with zero padding therefore pass
+// kBufOOB for out-of-image positions instead of branching around the load:
+// no per-load branch, so the compiler can issue all loads before waiting.
+// Resources here never exceed 2^31 bytes (checked on the host).
+constexpr uint32_t kBufOOB = 0x80000000u;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  // word 3 = 0x00020000: the gfx9-family (incl. gfx950) raw-buffer format
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ float buf_load_f32(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, byte_off, 0, 0));
+}
+__device__ __forceinline__ int4 buf_load_b128(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+  return __builtin_bit_cast(int4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 0));
+}
+
 // ---- plans ----------------------------------------------------------------
 enum class PlanKind { ConvF32, ConvInt8, DwConvF32 };
 

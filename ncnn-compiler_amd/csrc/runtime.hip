@@ -195,6 +195,17 @@ int check_forward(const nhip_conv_plan* p, const void* in, const void* out, int 
   return ok();
 }
 
+// Kernels address their input as one raw buffer resource with 32-bit byte
+// offsets, so a launch must keep every tensor below 2^31 bytes.  Larger
+// batches run as consecutive sub-batches of whole images on the same stream.
+template <typename F>
+int for_each_subbatch(int n, int64_t max_image_bytes, F&& run) {
+  const int64_t lim = (int64_t)1 << 31;
+  const int per = (int)std::max<int64_t>(1, (lim - 1) / std::max<int64_t>(max_image_bytes, 1));
+  for (int i0 = 0; i0 < n; i0 += per) NHIP_TRY(run(i0, std::min(per, n - i0)));
+  return ok();
+}
+
 }  // namespace
 }  // namespace nhip
 
@@ -388,11 +399,17 @@ int nhip_conv2d_f32_forward(nhip_conv_t p, const float* input, const float* resi
   NHIP_TRY(check_forward(p, input, output, n, h, w, &oh, &ow));
   if (p->kind != PlanKind::ConvF32) return fail(NHIP_STATUS_CONSTRAINT_VIOLATION, "conv2d_f32_forward: not an fp32 conv plan");
   if (n == 0) return ok();
-  if (p->algorithm == NHIP_CONV_ALGO_WINOGRAD)
-    return launch_conv_winograd_f32(p, input, residual, output, n, h, w, oh, ow, workspace, workspace_bytes,
-                                    as_stream(stream));
-  return launch_conv_igemm_f32(p, input, residual, output, n, h, w, oh, ow, workspace, workspace_bytes,
-                               as_stream(stream));
+  const int64_t in_img = (int64_t)p->g.c * h * w, out_img = (int64_t)p->g.k * oh * ow;
+  return for_each_subbatch(n, 4 * std::max(in_img, out_img), [&](int i0, int nb) {
+    const float* in = input + i0 * in_img;
+    const float* res = residual ? residual + i0 * out_img : nullptr;
+    float* out = output + i0 * out_img;
+    if (p->algorithm == NHIP_CONV_ALGO_WINOGRAD)
+      return launch_conv_winograd_f32(p, in, res, out, nb, h, w, oh, ow, workspace, workspace_bytes,
+                                      as_stream(stream));
+    return launch_conv_igemm_f32(p, in, res, out, nb, h, w, oh, ow, workspace, workspace_bytes,
+                                 as_stream(stream));
+  });
 }
 
 int nhip_conv2d_int8_create(const nhip_conv_desc* d, const void* weight, int32_t weight_is_i8, const float* bias,
@@ -470,8 +487,14 @@ int nhip_conv2d_int8_forward(nhip_conv_t p, const void* input, int32_t input_is_
   NHIP_TRY(check_forward(p, input, output, n, h, w, &oh, &ow));
   if (p->kind != PlanKind::ConvInt8) return fail(NHIP_STATUS_CONSTRAINT_VIOLATION, "conv2d_int8_forward: not an int8 conv plan");
   if (n == 0) return ok();
-  return launch_conv_int8(p, input, input_is_i8 ? 1 : 0, output, n, h, w, oh, ow, workspace, workspace_bytes,
-                          as_stream(stream));
+  const int64_t in_img = (int64_t)p->g.c * h * w, out_img = (int64_t)p->g.k * oh * ow;
+  const int in_es = input_is_i8 ? 1 : 4, out_es = p->scale_term > 100 ? 1 : 4;
+  const int64_t ws_img = (int64_t)h * w * p->c_pad;
+  return for_each_subbatch(n, std::max({in_es * in_img, out_es * out_img, ws_img}), [&](int i0, int nb) {
+    return launch_conv_int8(p, static_cast<const char*>(input) + i0 * in_img * in_es, input_is_i8 ? 1 : 0,
+                            static_cast<char*>(output) + i0 * out_img * out_es, nb, h, w, oh, ow, workspace,
+                            workspace_bytes, as_stream(stream));
+  });
 }
 
 int nhip_dwconv2d_f32_create(const nhip_conv_desc* d, const float* weight, const float* bias, nhip_conv_t* plan) {

@@ -110,8 +110,20 @@ WINO_CASES = [
 ]
 
 
+@pytest.fixture(params=["auto", "221", "114", "2"])
+def wino_variant(request, monkeypatch):
+    """Winograd implementations: the default three-kernel path (auto), the
+    fused kernel in its two workgroup shapes (221, 114) and with the fused
+    launcher's own shape choice (2)."""
+    if request.param == "auto":
+        monkeypatch.delenv("NHIP_WINOGRAD_VARIANT", raising=False)
+    else:
+        monkeypatch.setenv("NHIP_WINOGRAD_VARIANT", request.param)
+    return request.param
+
+
 @pytest.mark.parametrize("case", WINO_CASES, ids=lambda c: "x".join(map(str, c[:5])))
-def test_winograd_matches_oracle(case):
+def test_winograd_matches_oracle(case, wino_variant):
     n, c, h, w, k, pad = case
     x = RNG.uniform(-1, 1, (n, c, h, w)).astype(np.float32)
     wt = workloads.he_normal(RNG, (k, c, 3, 3), c * 9)
@@ -151,7 +163,9 @@ def oracle_stage(x, w1, b1, w2, b2):
 
 @pytest.mark.parametrize("stage", workloads.RESNET18_STAGES, ids=lambda s: f"{s[0]}x{s[1]}")
 @pytest.mark.parametrize("algo", [nhip.ALGO_IMPLICIT_GEMM, nhip.ALGO_WINOGRAD])
-def test_resnet_stage_n2_matches_oracle(stage, algo):
+def test_resnet_stage_n2_matches_oracle(stage, algo, wino_variant):
+    if algo == nhip.ALGO_IMPLICIT_GEMM and wino_variant != "auto":
+        pytest.skip("variant applies to Winograd only")
     c, hw = stage
     x, w1, b1, w2, b2 = workloads.resnet_stage(c, hw, n=2, seed=0)
     got = run_stage(c, hw, 2, algo, x, w1, b1, w2, b2)
@@ -176,8 +190,11 @@ def test_resnet_stage_full_batch(stage):
         assert_close(igemm[i:i + 1], exp, IGEMM_RTOL, f"igemm image {i}")
 
 
-def test_batch_is_independent_images():
-    """The [N,C,H,W] batch equals N single-image calls (the reference ABI)."""
+@pytest.mark.parametrize("variant", ["221", "114", "1"])
+def test_batch_is_independent_images(variant, monkeypatch):  # 1 = three-kernel path
+    """The [N,C,H,W] batch equals N single-image calls (the reference ABI),
+    bit for bit for a fixed kernel variant."""
+    monkeypatch.setenv("NHIP_WINOGRAD_VARIANT", variant)
     c, k = 32, 32
     x = RNG.uniform(-1, 1, (4, c, 10, 10)).astype(np.float32)
     wt = workloads.he_normal(RNG, (k, c, 3, 3), c * 9)
@@ -189,7 +206,8 @@ def test_batch_is_independent_images():
             np.testing.assert_array_equal(one, whole[i:i + 1])
 
 
-def test_empty_batch_and_workspace_errors():
+def test_empty_batch_and_workspace_errors(monkeypatch):
+    monkeypatch.delenv("NHIP_WINOGRAD_VARIANT", raising=False)  # default path needs a workspace
     c, k = 16, 16
     wt = workloads.he_normal(RNG, (k, c, 3, 3), c * 9)
     conv = nhip.Conv2dF32(nhip.conv_desc(c, k, bias=False, algorithm=nhip.ALGO_WINOGRAD), wt)
