@@ -2,6 +2,9 @@
 through the libnhip C ABI on one MI355X, plus the int8 requantized conv
 (config 4) as a secondary figure.
 
+Secondary figures in the same line: the int8 conv (config 4) and the
+MobileNetV2-shape graph at batch 32 (config 5).
+
 One step = the four ResNet-18 basic-block stages (64@56, 128@28, 256@14,
 512@7), each two 3x3 s1 p1 convs with folded-BN bias, ReLU and the residual
 add: 8 Winograd F(4,3) convolutions over 32 images whose inputs are already
@@ -111,6 +114,25 @@ def int8_secondary(nhip, workloads, torch, steps, warmup):
             "gemm_kernel_frac_int8_peak": ops / kavg / 1e12 / PEAK_INT8_TOPS}
 
 
+def mobilenetv2_secondary(torch, steps, warmup):
+    import graphs
+    layers = graphs.mobilenetv2_layers(seed=0)
+    g = graphs.DeviceGraph(layers)
+    x = torch.from_numpy(
+        __import__("numpy").random.default_rng(0).uniform(-1, 1, (BATCH, 3, 224, 224)).astype("float32")).cuda()
+    for _ in range(warmup):
+        g.forward(x)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        g.forward(x)
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / steps
+    flops = graphs.graph_flops(layers, BATCH, 224, 224)
+    return {"workload": "MobileNetV2-shape graph b32 224x224 fp32 (53 conv/dw layers, GAP, IP 1280->1000)",
+            "ms_per_step": dt * 1e3, "images_per_sec": BATCH / dt, "tflops": flops / dt / 1e12}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -166,6 +188,7 @@ def main():
     achieved = (wino_flops / gemm_launches_per_step) / avg_gemm_s / 1e12
 
     int8 = int8_secondary(nhip, workloads, torch, args.steps, args.warmup)
+    mbv2 = mobilenetv2_secondary(torch, args.steps, args.warmup)
     result = {
         "metric": METRIC,
         "value": round(value, 3),
@@ -187,6 +210,7 @@ def main():
             "frac_fp32_mfma_peak_direct_equivalent": round(value / PEAK_FP32_TFLOPS, 4),
             "winograd_executed_tflops": round(wino_flops / (ms_per_step / 1e3) / 1e12, 3),
             "int8": {k: (round(v, 4) if isinstance(v, float) else v) for k, v in int8.items()},
+            "mobilenetv2": {k: (round(v, 4) if isinstance(v, float) else v) for k, v in mbv2.items()},
         },
         "roofline": {
             "bound": "mfma",
