@@ -1,0 +1,168 @@
+"""GPU parity of models compiled by ncnn-compile: the generated lib<model>.so
+is loaded with ctypes and called through the reference's entry ABI (host
+buffers, one image per call, NCNN_STATUS_* returns), as the reference's own
+tests do (test/Numerical/support/numerical_test_support.hpp:82-..., ctypes in
+test/Native/check_ncnn_compile.py:338-380), and compared with the oracle."""
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+
+import graphs  # noqa: E402
+import ncnn_format  # noqa: E402
+import nhip  # noqa: E402
+import workloads  # noqa: E402
+from numerics import assert_close  # noqa: E402
+from oracle import refcpu  # noqa: E402
+from oracle_graphs import oracle_forward  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+TOOL = os.path.join(ROOT, "ncnn-compiler_amd", "bin", "ncnn-compile")
+RNG = np.random.default_rng(21)
+P = ctypes.c_void_p
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    assert torch.cuda.is_available(), "GPU tests need a HIP device"
+    nhip.init(0)
+
+
+def build(tmp_path, model, name, extra=()):
+    p, b = tmp_path / f"{name}.param", tmp_path / f"{name}.bin"
+    model.save(p, b)
+    out = tmp_path / name
+    r = subprocess.run([TOOL, str(p), "-o", str(out), *extra], capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr
+    return ctypes.CDLL(str(out / f"lib{name}.so"))
+
+
+def ptr(a):
+    return a.ctypes.data_as(P)
+
+
+def test_config1_conv_entry(tmp_path):
+    x, w, b = workloads.conv_single(seed=0)
+    m = ncnn_format.Model()
+    m.input("data", 64, 56, 56)
+    m.conv("conv", "data", "output", w, b, act=1)
+    lib = build(tmp_path, m, "conv")
+    lib.conv.argtypes = [P, P]
+    out = np.zeros((64, 56, 56), np.float32)
+    assert lib.conv(ptr(np.ascontiguousarray(x[0])), ptr(out)) == 0
+    exp = refcpu.relu_f32(refcpu.conv2d_f32(refcpu.geom(1, 64, 56, 56, 64), x, w, b))[0]
+    assert_close(out, exp, 1e-3, "compiled conv (Winograd)")
+    assert lib.conv(None, ptr(out)) == 1
+
+
+def test_config2_dynamic_m_innerproduct_entry(tmp_path):
+    x, w, b = workloads.innerproduct(seed=0)
+    m = ncnn_format.Model()
+    m.input("data", 0, 0, 0)
+    m.squeeze("squeeze", "data", "matrix", [0])
+    m.innerproduct("ip", "matrix", "output", w, b)
+    lib = build(tmp_path, m, "ip", ["--input-shape=1x?x2048"])
+    lib.ip.argtypes = [P, ctypes.POINTER(ctypes.c_int64), P, ctypes.c_uint64]
+    shape = (ctypes.c_int64 * 3)(1, 256, 2048)
+    out = np.zeros((256, 1000), np.float32)
+    assert lib.ip(ptr(x), shape, ptr(out), out.size) == 0
+    assert_close(out, refcpu.innerproduct_f32(x, w, b), 1e-4, "compiled dynamic-M InnerProduct")
+    assert lib.ip(ptr(x), shape, ptr(out), out.size - 1) == 5  # OUTPUT_CAPACITY_INSUFFICIENT
+    small = (ctypes.c_int64 * 3)(1, 3, 2048)
+    out3 = np.zeros((3, 1000), np.float32)
+    assert lib.ip(ptr(x[:3].copy()), small, ptr(out3), out3.size) == 0
+    assert_close(out3, refcpu.innerproduct_f32(x[:3], w, b), 1e-4, "M=3")
+
+
+def test_resnet_block_with_unfolded_batchnorm(tmp_path):
+    c, hw = 64, 14
+    x = RNG.uniform(-1, 1, (1, c, hw, hw)).astype(np.float32)
+    conv_w = [workloads.he_normal(RNG, (c, c, 3, 3), c * 9) for _ in range(2)]
+    conv_b = [RNG.normal(0, 0.01, c).astype(np.float32) for _ in range(2)]
+    bn = [(RNG.uniform(0.5, 1.5, c).astype(np.float32), RNG.normal(0, 0.1, c).astype(np.float32),
+           RNG.uniform(0.5, 2.0, c).astype(np.float32), RNG.normal(0, 0.1, c).astype(np.float32)) for _ in range(2)]
+    m = ncnn_format.Model()
+    m.input("data", c, hw, hw)
+    m.split("split", "data", ["d0", "d1"])
+    m.conv("conv0", "d0", "c0", conv_w[0], conv_b[0])
+    m.batchnorm("bn0", "c0", "n0", *bn[0])
+    m.relu("relu0", "n0", "r0")
+    m.conv("conv1", "r0", "c1", conv_w[1], conv_b[1])
+    m.batchnorm("bn1", "c1", "n1", *bn[1])
+    m.add("add", "n1", "d1", "sum", eltwise=True)
+    m.relu("relu1", "sum", "output")
+    lib = build(tmp_path, m, "block")
+    lib.block.argtypes = [P, P]
+    out = np.zeros((c, hw, hw), np.float32)
+    assert lib.block(ptr(x[0]), ptr(out)) == 0
+    # oracle: the reference folds each BatchNorm into its convolution
+    # (FoldNCNNBatchNorm.cpp:56-177), then conv, relu, conv, add, relu
+    g = refcpu.geom(1, c, hw, hw, c)
+    w0, b0 = refcpu.bn_fold(conv_w[0], conv_b[0], *bn[0], 1e-5)
+    w1, b1 = refcpu.bn_fold(conv_w[1], conv_b[1], *bn[1], 1e-5)
+    y = refcpu.relu_f32(refcpu.conv2d_f32(g, x, w0, b0))
+    exp = refcpu.relu_f32(refcpu.add_f32(refcpu.conv2d_f32(g, y, w1, b1), x))[0]
+    assert_close(out, exp, 1e-3, "compiled ResNet block")
+
+
+def test_int8_chain_bit_exact(tmp_path):
+    # int8_complete_chain.param without the depthwise stage: a term-101
+    # convolution (int8 out) feeding a term-1 convolution (int8 in, fp32 out)
+    c, k1, k2, hw = 16, 24, 8, 9
+    x = RNG.uniform(-1.5, 1.5, (1, c, hw, hw)).astype(np.float32)
+    w1 = RNG.integers(-127, 128, (k1, c, 3, 3)).astype(np.int8)
+    w2 = RNG.integers(-127, 128, (k2, k1, 1, 1)).astype(np.int8)
+    b1 = RNG.normal(0, 0.2, k1).astype(np.float32)
+    b2 = RNG.normal(0, 0.2, k2).astype(np.float32)
+    ws1 = RNG.uniform(50, 200, k1).astype(np.float32)
+    ws2 = RNG.uniform(50, 200, k2).astype(np.float32)
+    m = ncnn_format.Model()
+    m.input("data", c, hw, hw)
+    m.conv("conv_requant", "data", "q", w1, b1, act=1, int8=dict(term=101, ws=ws1, **{"is": 60.0, "os": 30.0}))
+    m.conv("conv_dequant", "q", "output", w2, b2, pad=0, int8=dict(term=1, ws=ws2, **{"is": 30.0}))
+    lib = build(tmp_path, m, "chain")
+    lib.chain.argtypes = [P, P]
+    out = np.zeros((k2, hw, hw), np.float32)
+    assert lib.chain(ptr(x[0]), ptr(out)) == 0
+    q = refcpu.conv2d_int8(refcpu.geom(1, c, hw, hw, k1), x, w1, b1, ws1, 60.0, 30.0, 101, 1)
+    exp = refcpu.conv2d_int8(refcpu.geom(1, k1, hw, hw, k2, (1, 1), pad=(0, 0, 0, 0)), q, w2, b2, ws2, 30.0,
+                             scale_term=1, activation=0)[0]
+    np.testing.assert_array_equal(out, exp)
+
+
+def test_mobilenetv2_entry_and_device_batch(tmp_path):
+    layers = graphs.mobilenetv2_layers(seed=0)
+    lib = build(tmp_path, ncnn_format.from_layer_list(layers), "mbv2")
+    lib.mbv2.argtypes = [P, P]
+    x = RNG.uniform(-1, 1, (2, 3, 224, 224)).astype(np.float32)
+    exp = oracle_forward(layers, x)["fc"]
+    for i in range(2):
+        out = np.zeros(1000, np.float32)
+        assert lib.mbv2(ptr(x[i]), ptr(out)) == 0
+        assert_close(out, exp[i], 1e-4, f"compiled MobileNetV2 image {i}")
+    # the batched device path of the same graph (nhip_graph_run)
+    L = nhip.load()
+    L.nhip_graph_load.argtypes = [ctypes.c_char_p, ctypes.c_uint64, P, ctypes.c_uint64,
+                                  ctypes.POINTER(ctypes.c_int64), ctypes.c_int32, ctypes.POINTER(P)]
+    L.nhip_graph_run.argtypes = [P, ctypes.c_int32, ctypes.POINTER(ctypes.c_int64), ctypes.POINTER(P),
+                                 ctypes.POINTER(P), P]
+    L.nhip_graph_destroy.argtypes = [P]
+    m = ncnn_format.from_layer_list(layers)
+    text, payload = m.param_text().encode(), bytes(m.payload)
+    g = P()
+    assert L.nhip_graph_load(text, len(text), payload, len(payload), None, 0, ctypes.byref(g)) == 0, \
+        L.nhip_last_error()
+    xd = torch.from_numpy(x).cuda()
+    yd = torch.empty((2, 1000), device="cuda")
+    ins = (P * 1)(xd.data_ptr())
+    outs = (P * 1)(yd.data_ptr())
+    st = L.nhip_graph_run(g, 2, None, ins, outs, P(torch.cuda.current_stream().cuda_stream))
+    assert st == 0, L.nhip_last_error()
+    torch.cuda.synchronize()
+    assert_close(yd.cpu().numpy(), exp, 1e-4, "nhip_graph_run batch")
+    L.nhip_graph_destroy(g)
