@@ -167,6 +167,22 @@ int nhip_dwconv2d_f32_forward(nhip_conv_t plan, const float* input,
                               float* output, int32_t n, int32_t h, int32_t w,
                               void* stream);
 
+/* a3 int8 — ConvolutionDepthWise with int8_scale_term (NCNNToTosa.cpp:
+ * 3257-3376).  weight: host [C][1][kh][kw], int8 when weight_is_i8 else fp32
+ * quantized per channel with weight_scale; weight_scale has C entries
+ * (terms 1/101) or 1 (terms 2/102, graph.cpp:1545-1548); input_scale and
+ * output_scale (term > 100) are scalars; bias fp32 or NULL.  Activation 0/1. */
+int nhip_dwconv2d_int8_create(const nhip_conv_desc* desc, const void* weight,
+                              int32_t weight_is_i8, const float* bias,
+                              const float* weight_scale,
+                              int32_t weight_scale_count, float input_scale,
+                              float output_scale, nhip_conv_t* plan);
+/* input fp32 (quantized by input_scale) or int8 (input_is_i8); output int8
+ * when int8_scale_term > 100, else fp32.  No workspace. */
+int nhip_dwconv2d_int8_forward(nhip_conv_t plan, const void* input,
+                               int32_t input_is_i8, void* output, int32_t n,
+                               int32_t h, int32_t w, void* stream);
+
 int nhip_conv_destroy(nhip_conv_t plan);
 
 /* a4 — fp32 InnerProduct (NCNNToTosa.cpp:5254-5392):
@@ -183,6 +199,22 @@ int nhip_innerproduct_workspace_size(nhip_ip_t plan, int32_t m,
 int nhip_innerproduct_f32_forward(nhip_ip_t plan, const float* input,
                                   float* output, int32_t m, void* workspace,
                                   uint64_t workspace_bytes, void* stream);
+/* a4 int8 — InnerProduct with int8_scale_term (NCNNToTosa.cpp:5300-5390):
+ * out = act((float)(sum_k q(x)*q(W)) * r[j] + bias[j]), fp32 output.
+ * weight: host [num_output][num_input], int8 when weight_is_i8 else fp32
+ * quantized per output row; weight_scale: num_output entries (graph.cpp:
+ * 1638-1678); input_scale scalar.  Forward: input [m][num_input] fp32 (or
+ * int8 when input_is_i8), output [m][num_output] fp32, workspace from
+ * nhip_innerproduct_workspace_size. */
+int nhip_innerproduct_int8_create(int32_t num_output, int32_t num_input,
+                                  const void* weight, int32_t weight_is_i8,
+                                  const float* bias, const float* weight_scale,
+                                  float input_scale, int32_t activation_type,
+                                  nhip_ip_t* plan);
+int nhip_innerproduct_int8_forward(nhip_ip_t plan, const void* input,
+                                   int32_t input_is_i8, float* output,
+                                   int32_t m, void* workspace,
+                                   uint64_t workspace_bytes, void* stream);
 int nhip_innerproduct_destroy(nhip_ip_t plan);
 
 /* ---------------------------------------------------------------------------

@@ -14,8 +14,8 @@
  *     (tools/ncnn-compile.cpp:915-932; GenerateCAPI.cpp:1460-1590): a
  *     generated library calls nhip_graph_run_host with the caller's buffers.
  *
- * Layer types: Input, Convolution (fp32, int8 terms 1/2/101/102),
- * ConvolutionDepthWise (fp32), InnerProduct (fp32), ReLU (slope 0),
+ * Layer types: Input, Convolution and ConvolutionDepthWise (fp32, int8 terms
+ * 1/2/101/102), InnerProduct (fp32, int8 terms 1/2), ReLU (slope 0),
  * BatchNorm (folded into the producing fp32 convolution), BinaryOp add and
  * Eltwise sum of equal shapes, Pooling global average, Quantize, Split,
  * Reshape/Flatten/Squeeze, Dropout/Noop.  Anything else is rejected with

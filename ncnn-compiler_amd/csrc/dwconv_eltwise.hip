@@ -141,6 +141,7 @@ __global__ __launch_bounds__(256) void dwconv3x3s1_f32_kernel(DwArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+
 __device__ __forceinline__ int8_t quantize_i8(float x, float scale) {
 #pragma clang fp contract(off)
   const float s = x * scale;
@@ -149,6 +150,77 @@ __device__ __forceinline__ int8_t quantize_i8(float x, float scale) {
   r = fminf(r, 127.0f);
   r = fmaxf(r, -127.0f);
   return (int8_t)(int)r;
+}
+
+// int8 ConvolutionDepthWise (NCNNToTosa.cpp:3257-3376): the input band is
+// quantized (fp32 input) or copied (int8 input) into LDS as int8, the window
+// sum is exact int32, and the epilogue is the int8 convolution's:
+// (float)acc * r[c], + bias[c], requantize when term > 100, relu last.
+struct DwI8Args {
+  const void* x;
+  void* y;
+  const int8_t* w;      // [C][kh*kw]
+  const float* bias;    // [C]
+  const float* recip;   // [C]: ws==0 ? 0 : 1/(ws*is)
+  float is, os;
+  int term, act, in_i8;
+  int C, H, W, OH, OW;
+  int kh, kw, sh, sw, dh, dw, pt, pl;
+  int planes, ppb, ob, bands, ir, lw;
+};
+
+__global__ __launch_bounds__(256) void dwconv_int8_kernel(DwI8Args a) {
+  extern __shared__ int8_t lds8[];
+  const int band = blockIdx.x % a.bands;
+  const int pgrp = blockIdx.x / a.bands;
+  const int plane0 = pgrp * a.ppb;
+  const int oy0 = band * a.ob;
+  const int iy0 = oy0 * a.sh - a.pt;
+  const int ix0 = -a.pl;
+  const int per_plane = a.ir * a.lw;
+  const int total_in = a.ppb * per_plane;
+  for (int e = threadIdx.x; e < total_in; e += blockDim.x) {
+    const int pi = e / per_plane;
+    const int r = e - pi * per_plane;
+    const int ry = r / a.lw, rx = r - (r / a.lw) * a.lw;
+    const int plane = plane0 + pi;
+    const int y = iy0 + ry, x = ix0 + rx;
+    int8_t v = 0;
+    if (plane < a.planes && (unsigned)y < (unsigned)a.H && (unsigned)x < (unsigned)a.W) {
+      const int64_t off = (int64_t)plane * a.H * a.W + (int64_t)y * a.W + x;
+      v = a.in_i8 ? static_cast<const int8_t*>(a.x)[off] : quantize_i8(static_cast<const float*>(a.x)[off], a.is);
+    }
+    lds8[e] = v;
+  }
+  __syncthreads();
+  const int rows = min(a.ob, a.OH - oy0);
+  const int per_out = rows * a.OW;
+  const int total_out = a.ppb * per_out;
+  for (int e = threadIdx.x; e < total_out; e += blockDim.x) {
+    const int pi = e / per_out;
+    const int r = e - pi * per_out;
+    const int oy = r / a.OW, ox = r - (r / a.OW) * a.OW;
+    const int plane = plane0 + pi;
+    if (plane >= a.planes) break;
+    const int c = plane % a.C;
+    const int8_t* wc = a.w + (int64_t)c * a.kh * a.kw;
+    const int8_t* src = lds8 + pi * per_plane + (oy * a.sh) * a.lw + ox * a.sw;
+    int acc = 0;
+    for (int i = 0; i < a.kh; ++i)
+      for (int j = 0; j < a.kw; ++j) acc += (int)src[i * a.dh * a.lw + j * a.dw] * (int)wc[i * a.kw + j];
+    const int64_t o = (int64_t)plane * a.OH * a.OW + (int64_t)(oy0 + oy) * a.OW + ox;
+    float f = (float)acc;
+    f = f * a.recip[c];
+    f = f + a.bias[c];
+    if (a.term > 100) {
+      int8_t q = quantize_i8(f, a.os);
+      if (a.act == NHIP_ACT_RELU && q < 0) q = 0;
+      static_cast<int8_t*>(a.y)[o] = q;
+    } else {
+      if (a.act == NHIP_ACT_RELU) f = f < 0.f ? 0.f : f;
+      static_cast<float*>(a.y)[o] = f;
+    }
+  }
 }
 
 __global__ void relu_f32_kernel(const float* x, float* y, int64_t n) {
@@ -232,6 +304,67 @@ unsigned grid_for(int64_t n) {
 
 }  // namespace
 
+// Band sizing shared by both depthwise kernels: about 1024 outputs per
+// workgroup, LDS staging within 32 KB (elem = bytes per staged element).
+static int dw_bands(int planes, int oh, int ow, int kh, int kw, int sh, int dh, int sw, int dw, int elem,
+                    int* ppb, int* ob, int* ir, int* lw, int* bands, int64_t* lds) {
+  *lw = (ow - 1) * sw + (kw - 1) * dw + 1;
+  const int plane_out = oh * ow;
+  if (plane_out >= 512) {
+    *ppb = 1;
+    *ob = std::max(1, std::min(oh, 1024 / ow));
+  } else {
+    *ppb = std::max(1, 1024 / plane_out);
+    *ob = oh;
+  }
+  *ir = (*ob - 1) * sh + (kh - 1) * dh + 1;
+  while (*ppb > 1 && (int64_t)*ppb * *ir * *lw * elem > 32768) *ppb /= 2;
+  while (*ob > 1 && (int64_t)*ppb * *ir * *lw * elem > 32768) {
+    *ob = (*ob + 1) / 2;
+    *ir = (*ob - 1) * sh + (kh - 1) * dh + 1;
+  }
+  *lds = (int64_t)*ppb * *ir * *lw * elem;
+  if (*lds > 65536) return fail(NHIP_STATUS_UNSUPPORTED, "depthwise: input rows too wide for LDS staging");
+  *bands = (int)ceil_div(oh, *ob);
+  (void)planes;
+  return ok();
+}
+
+int launch_dwconv_int8(const nhip_conv_plan* p, const void* in, int in_is_i8, void* out, int n, int h, int w,
+                       int oh, int ow, hipStream_t s) {
+  DwI8Args a{};
+  a.x = in;
+  a.y = out;
+  a.w = p->weight_i8;
+  a.bias = p->bias;
+  a.recip = p->recip;
+  a.is = p->input_scale;
+  a.os = p->output_scale;
+  a.term = p->scale_term;
+  a.act = p->g.act;
+  a.in_i8 = in_is_i8;
+  a.C = p->g.c;
+  a.H = h;
+  a.W = w;
+  a.OH = oh;
+  a.OW = ow;
+  a.kh = p->g.kh;
+  a.kw = p->g.kw;
+  a.sh = p->g.sh;
+  a.sw = p->g.sw;
+  a.dh = p->g.dh;
+  a.dw = p->g.dw;
+  a.pt = p->g.pt;
+  a.pl = p->g.pl;
+  a.planes = n * p->g.c;
+  int64_t lds = 0;
+  NHIP_TRY(dw_bands(a.planes, oh, ow, a.kh, a.kw, a.sh, a.dh, a.sw, a.dw, 1, &a.ppb, &a.ob, &a.ir, &a.lw, &a.bands,
+                    &lds));
+  const int64_t blocks = ceil_div(a.planes, a.ppb) * a.bands;
+  NHIP_LAUNCH("dwconv_int8", dwconv_int8_kernel, dim3((unsigned)blocks), dim3(256), (size_t)lds, s, a);
+  return check_launch("dwconv_int8");
+}
+
 int launch_dwconv_f32(const nhip_conv_plan* p, const float* in, float* out,
                       int n, int h, int w, int oh, int ow, hipStream_t s) {
   DwArgs a{};
@@ -254,27 +387,9 @@ int launch_dwconv_f32(const nhip_conv_plan* p, const float* in, float* out,
   a.pl = p->g.pl;
   a.planes = n * p->g.c;
   a.act = p->g.act;
-  a.lw = (ow - 1) * a.sw + (a.kw - 1) * a.dw + 1;
-  // Band sizing: about 1024 outputs per workgroup.
-  const int plane_out = oh * ow;
-  if (plane_out >= 512) {
-    a.ppb = 1;
-    a.ob = std::max(1, std::min(oh, 1024 / ow));
-  } else {
-    a.ppb = std::max(1, 1024 / plane_out);
-    a.ob = oh;
-  }
-  a.ir = (a.ob - 1) * a.sh + (a.kh - 1) * a.dh + 1;
-  // Keep the LDS footprint within 32 KB per workgroup.
-  while (a.ppb > 1 && (int64_t)a.ppb * a.ir * a.lw * 4 > 32768) a.ppb /= 2;
-  while (a.ob > 1 && (int64_t)a.ppb * a.ir * a.lw * 4 > 32768) {
-    a.ob = (a.ob + 1) / 2;
-    a.ir = (a.ob - 1) * a.sh + (a.kh - 1) * a.dh + 1;
-  }
-  const int64_t lds = (int64_t)a.ppb * a.ir * a.lw * 4;
-  if (lds > 65536)
-    return fail(NHIP_STATUS_UNSUPPORTED, "depthwise: input rows too wide for LDS staging");
-  a.bands = (int)ceil_div(oh, a.ob);
+  int64_t lds = 0;
+  NHIP_TRY(dw_bands(a.planes, oh, ow, a.kh, a.kw, a.sh, a.dh, a.sw, a.dw, 4, &a.ppb, &a.ob, &a.ir, &a.lw, &a.bands,
+                    &lds));
   const int64_t blocks = ceil_div(a.planes, a.ppb) * a.bands;
   const bool fast = a.kh == 3 && a.kw == 3 && a.sh == 1 && a.sw == 1 && a.dh == 1 && a.dw == 1;
   if (fast) {

@@ -438,7 +438,7 @@ void fuse_relu(std::vector<Layer>& layers) {
 }
 
 // ------------------------------------------------------------- call plan
-enum class OpKind { Input, ConvF32, ConvInt8, DwF32, IP, Relu, Add, Gap, Quantize, Alias };
+enum class OpKind { Input, ConvF32, ConvInt8, DwF32, DwInt8, IP, IPInt8, Relu, Add, Gap, Quantize, Alias };
 
 struct Shape {
   int rank = 0;
@@ -519,7 +519,8 @@ int infer_op(const nhip_graph& g, const Op& op, const std::vector<Shape>& sh, Sh
   switch (op.kind) {
     case OpKind::ConvF32:
     case OpKind::ConvInt8:
-    case OpKind::DwF32: {
+    case OpKind::DwF32:
+    case OpKind::DwInt8: {
       if (a.rank != 3) return fail(NHIP_STATUS_INVALID_SHAPE, op.name + ": convolution needs a [C,H,W] input");
       if (a.d[0] != op.desc.input_channels)
         return fail(NHIP_STATUS_INVALID_SHAPE, op.name + ": input has " + std::to_string(a.d[0]) +
@@ -538,7 +539,8 @@ int infer_op(const nhip_graph& g, const Op& op, const std::vector<Shape>& sh, Sh
       }
       return ok();
     }
-    case OpKind::IP: {
+    case OpKind::IP:
+    case OpKind::IPInt8: {
       int64_t k = 0;
       if (a.rank == 2) {
         k = a.d[1];
@@ -785,8 +787,18 @@ int build(nhip_graph& g, std::vector<Layer>& layers, const int64_t* input_shapes
       const float* bias = op.desc.bias_term ? L.weights[1].f.data() : nullptr;
       const size_t s0 = op.desc.bias_term ? 2 : 1;
       nhip_conv_desc d = op.desc;
-      if (ty == "ConvolutionDepthWise") {
-        if (term != 0) return fail(NHIP_STATUS_UNSUPPORTED, where(L) + "int8 depthwise is not in this build");
+      if (ty == "ConvolutionDepthWise" && term != 0) {
+        if (L.act != 0 && L.act != NHIP_ACT_RELU) return fail(NHIP_STATUS_UNSUPPORTED, where(L) + "int8 activation");
+        const Tensor& ws = L.weights[s0];
+        const float is = L.weights[s0 + 1].f[0];
+        const float os = term > 100 ? L.weights[s0 + 2].f[0] : 1.0f;
+        const bool wi8 = L.weights[0].dtype == NHIP_DTYPE_I8;
+        if (!dry)
+          TRY(nhip_dwconv2d_int8_create(&d, wi8 ? (const void*)L.weights[0].q.data() : (const void*)L.weights[0].f.data(),
+                                        wi8 ? 1 : 0, bias, ws.f.data(), (int32_t)ws.f.size(), is, os, &op.conv));
+        op.kind = OpKind::DwInt8;
+        op.out_dtype = term > 100 ? NHIP_DTYPE_I8 : NHIP_DTYPE_F32;
+      } else if (ty == "ConvolutionDepthWise") {
         if (L.weights[0].dtype != NHIP_DTYPE_F32) return fail(NHIP_STATUS_UNSUPPORTED, where(L) + "int8 weights without scale term");
         if (input_i8) return fail(NHIP_STATUS_UNSUPPORTED, where(L) + "int8 input to an fp32 depthwise convolution");
         if (!dry) TRY(nhip_dwconv2d_f32_create(&d, L.weights[0].f.data(), bias, &op.conv));
@@ -812,18 +824,31 @@ int build(nhip_graph& g, std::vector<Layer>& layers, const int64_t* input_shapes
         op.out_dtype = term > 100 ? NHIP_DTYPE_I8 : NHIP_DTYPE_F32;
       }
     } else if (ty == "InnerProduct") {
-      if (L.geti(8, 0) != 0) return fail(NHIP_STATUS_UNSUPPORTED, where(L) + "int8 InnerProduct is not in this build");
-      if (g.blobs[op.in[0]].dtype != NHIP_DTYPE_F32) return fail(NHIP_STATUS_UNSUPPORTED, where(L) + "int8 input");
       const int64_t n = L.geti(0, 0), count = L.geti(2, 0);
-      if (n <= 0 || count <= 0 || count % n != 0 || L.weights.empty() || L.weights[0].dtype != NHIP_DTYPE_F32)
+      const bool q = L.geti(8, 0) != 0;
+      if (n <= 0 || count <= 0 || count % n != 0 || L.weights.empty())
         return fail(NHIP_STATUS_INVALID_SHAPE, where(L) + "bad num_output / weight_data_size");
       if (L.act != 0 && L.act != NHIP_ACT_RELU) return fail(NHIP_STATUS_UNSUPPORTED, where(L) + "activation");
       op.ip_n = n;
       op.ip_k = count / n;
-      if (!dry)
-        TRY(nhip_innerproduct_f32_create((int32_t)n, (int32_t)op.ip_k, L.weights[0].f.data(),
-                                       L.geti(1, 0) ? L.weights[1].f.data() : nullptr, L.act, &op.ip));
-      op.kind = OpKind::IP;
+      const bool has_bias = L.geti(1, 0) != 0;
+      const float* bias = has_bias ? L.weights[1].f.data() : nullptr;
+      if (q) {
+        const size_t s0 = has_bias ? 2 : 1;
+        const bool wi8 = L.weights[0].dtype == NHIP_DTYPE_I8;
+        if (!dry)
+          TRY(nhip_innerproduct_int8_create((int32_t)n, (int32_t)op.ip_k,
+                                            wi8 ? (const void*)L.weights[0].q.data() : (const void*)L.weights[0].f.data(),
+                                            wi8 ? 1 : 0, bias, L.weights[s0].f.data(), L.weights[s0 + 1].f[0], L.act,
+                                            &op.ip));
+        op.kind = OpKind::IPInt8;
+      } else {
+        if (g.blobs[op.in[0]].dtype != NHIP_DTYPE_F32) return fail(NHIP_STATUS_UNSUPPORTED, where(L) + "int8 input");
+        if (L.weights[0].dtype != NHIP_DTYPE_F32)
+          return fail(NHIP_STATUS_CONSTRAINT_VIOLATION, where(L) + "int8 weights without scale term");
+        if (!dry) TRY(nhip_innerproduct_f32_create((int32_t)n, (int32_t)op.ip_k, L.weights[0].f.data(), bias, L.act, &op.ip));
+        op.kind = OpKind::IP;
+      }
     } else if (ty == "ReLU") {
       if (L.getf(0, 0.f) != 0.f) return fail(NHIP_STATUS_UNSUPPORTED, where(L) + "leaky slope");
       op.kind = OpKind::Relu;
@@ -933,7 +958,7 @@ int run_ops(nhip_graph& g, int n, const std::vector<Shape>& sh, const void* cons
     uint64_t w = 0;
     if (op.kind == OpKind::ConvF32 || op.kind == OpKind::ConvInt8)
       TRY(nhip_conv2d_workspace_size(op.conv, n, (int32_t)a.d[1], (int32_t)a.d[2], &w));
-    else if (op.kind == OpKind::IP)
+    else if (op.kind == OpKind::IP || op.kind == OpKind::IPInt8)
       TRY(nhip_innerproduct_workspace_size(op.ip, (int32_t)(a.rank == 2 ? n * a.d[0] : n), &w));
     ws_need = std::max(ws_need, w);
   }
@@ -960,6 +985,14 @@ int run_ops(nhip_graph& g, int n, const std::vector<Shape>& sh, const void* cons
         break;
       case OpKind::DwF32:
         TRY(nhip_dwconv2d_f32_forward(op.conv, (const float*)in, (float*)out, n, (int32_t)a.d[1], (int32_t)a.d[2], stream));
+        break;
+      case OpKind::DwInt8:
+        TRY(nhip_dwconv2d_int8_forward(op.conv, in, g.blobs[op.in[0]].dtype == NHIP_DTYPE_I8, out, n, (int32_t)a.d[1],
+                                       (int32_t)a.d[2], stream));
+        break;
+      case OpKind::IPInt8:
+        TRY(nhip_innerproduct_int8_forward(op.ip, in, g.blobs[op.in[0]].dtype == NHIP_DTYPE_I8, (float*)out,
+                                           (int32_t)(a.rank == 2 ? n * a.d[0] : n), g.ws, g.ws_cap, stream));
         break;
       case OpKind::IP:
         TRY(nhip_innerproduct_f32_forward(op.ip, (const float*)in, (float*)out, (int32_t)(a.rank == 2 ? n * a.d[0] : n),

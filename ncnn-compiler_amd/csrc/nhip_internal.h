@@ -87,7 +87,7 @@ __device__ __forceinline__ int4 buf_load_b128(__amdgpu_buffer_rsrc_t r, uint32_t
 }
 
 // ---- plans ----------------------------------------------------------------
-enum class PlanKind { ConvF32, ConvInt8, DwConvF32 };
+enum class PlanKind { ConvF32, ConvInt8, DwConvF32, DwConvInt8 };
 
 struct ConvGeom {
   int32_t c, k;             // input channels, num_output
@@ -125,6 +125,8 @@ struct nhip_ip_plan {
   int32_t n_pad, k_pad;
   float* weight = nullptr;  // [n_pad][k_pad]
   float* bias = nullptr;    // [n_pad], zero past n_out
+  // int8 InnerProduct: a 1x1 int8 convolution over m one-pixel images
+  nhip_conv_plan* q8 = nullptr;
 };
 
 namespace nhip {
@@ -148,6 +150,9 @@ int launch_conv_int8(const nhip_conv_plan* p, const void* in, int in_is_i8,
 uint64_t conv_int8_workspace(const nhip_conv_plan* p, int n, int h, int w);
 int launch_dwconv_f32(const nhip_conv_plan* p, const float* in, float* out,
                       int n, int h, int w, int oh, int ow, hipStream_t s);
+int launch_dwconv_int8(const nhip_conv_plan* p, const void* in, int in_is_i8,
+                       void* out, int n, int h, int w, int oh, int ow,
+                       hipStream_t s);
 int launch_innerproduct_f32(const nhip_ip_plan* p, const float* in,
                             float* out, int m, void* ws, uint64_t ws_bytes,
                             hipStream_t s);

@@ -535,6 +535,68 @@ int nhip_dwconv2d_f32_forward(nhip_conv_t p, const float* input, float* output, 
   return launch_dwconv_f32(p, input, output, n, h, w, oh, ow, as_stream(stream));
 }
 
+int nhip_dwconv2d_int8_create(const nhip_conv_desc* d, const void* weight, int32_t weight_is_i8, const float* bias,
+                              const float* weight_scale, int32_t weight_scale_count, float input_scale,
+                              float output_scale, nhip_conv_t* plan) {
+  NHIP_TRY(validate_common(d));
+  if (!weight || !plan || !weight_scale) return fail(NHIP_STATUS_NULL_POINTER, "dwconv2d_int8_create: null pointer");
+  if (d->bias_term && !bias) return fail(NHIP_STATUS_NULL_POINTER, "dwconv2d_int8_create: bias_term set but bias is null");
+  if (d->group != d->input_channels || d->num_output != d->input_channels)
+    return fail(NHIP_STATUS_CONSTRAINT_VIOLATION, "depthwise group must equal input channels");
+  if (d->int8_scale_term == 0)
+    return fail(NHIP_STATUS_CONSTRAINT_VIOLATION, "dwconv2d_int8_create: int8_scale_term must be nonzero");
+  if (d->activation_type != NHIP_ACT_NONE && d->activation_type != NHIP_ACT_RELU)
+    return fail(NHIP_STATUS_UNSUPPORTED, "depthwise activation must be 0 or 1");
+  const int C = d->input_channels, KHW = d->kernel_h * d->kernel_w;
+  if (weight_scale_count != 1 && weight_scale_count != C)
+    return fail(NHIP_STATUS_INVALID_SHAPE, "dwconv2d_int8_create: weight_scale count must be 1 or C");
+  *plan = nullptr;
+  auto* p = new nhip_conv_plan();
+  p->kind = PlanKind::DwConvInt8;
+  p->g = geom_of(d);
+  p->algorithm = NHIP_CONV_ALGO_IMPLICIT_GEMM;
+  p->has_bias = d->bias_term;
+  p->scale_term = d->int8_scale_term;
+  p->input_scale = input_scale;
+  p->output_scale = output_scale;
+  std::vector<int8_t> wq((size_t)C * KHW);
+  for (int c = 0; c < C; ++c) {
+    const float ws = weight_scale[weight_scale_count == 1 ? 0 : c];
+    for (int e = 0; e < KHW; ++e) {
+      const size_t i = (size_t)c * KHW + e;
+      wq[i] = weight_is_i8 ? static_cast<const int8_t*>(weight)[i] : quantize_host(static_cast<const float*>(weight)[i], ws);
+    }
+  }
+  std::vector<float> rc((size_t)C, 0.f);
+  for (int c = 0; c < C; ++c) {
+#pragma clang fp contract(off)
+    const float ws = weight_scale[weight_scale_count == 1 ? 0 : c];
+    const float combined = ws * input_scale;
+    const float r = 1.0f / combined;
+    rc[c] = ws == 0.0f ? 0.0f : r;
+  }
+  int st = upload(&p->weight_i8, wq, "hipMalloc(dw int8 weight)");
+  if (st == NHIP_STATUS_SUCCESS) st = upload(&p->recip, rc, "hipMalloc(dw int8 reciprocal)");
+  if (st == NHIP_STATUS_SUCCESS) st = upload_bias(p, d->bias_term ? bias : nullptr, C, C);
+  if (st != NHIP_STATUS_SUCCESS) {
+    std::string msg = g_last_error;
+    free_plan(p);
+    return fail(st, msg);
+  }
+  *plan = p;
+  return ok();
+}
+
+int nhip_dwconv2d_int8_forward(nhip_conv_t p, const void* input, int32_t input_is_i8, void* output, int32_t n,
+                               int32_t h, int32_t w, void* stream) {
+  int oh = 0, ow = 0;
+  NHIP_TRY(check_forward(p, input, output, n, h, w, &oh, &ow));
+  if (p->kind != PlanKind::DwConvInt8)
+    return fail(NHIP_STATUS_CONSTRAINT_VIOLATION, "dwconv2d_int8_forward: not an int8 depthwise plan");
+  if (n == 0) return ok();
+  return launch_dwconv_int8(p, input, input_is_i8 ? 1 : 0, output, n, h, w, oh, ow, as_stream(stream));
+}
+
 int nhip_conv_destroy(nhip_conv_t p) {
   free_plan(p);
   return ok();
@@ -574,13 +636,54 @@ int nhip_innerproduct_f32_create(int32_t num_output, int32_t num_input, const fl
 int nhip_innerproduct_workspace_size(nhip_ip_t p, int32_t m, uint64_t* bytes) {
   if (!p || !bytes) return fail(NHIP_STATUS_NULL_POINTER, "innerproduct_workspace_size: null pointer");
   if (m < 0) return fail(NHIP_STATUS_INVALID_SHAPE, "innerproduct: negative m");
+  if (p->q8) return nhip_conv2d_workspace_size(p->q8, m, 1, 1, bytes);
   *bytes = m == 0 ? 0 : innerproduct_workspace(p, m);
   return ok();
+}
+
+int nhip_innerproduct_int8_create(int32_t num_output, int32_t num_input, const void* weight, int32_t weight_is_i8,
+                                  const float* bias, const float* weight_scale, float input_scale,
+                                  int32_t activation_type, nhip_ip_t* plan) {
+  if (!weight || !plan || !weight_scale) return fail(NHIP_STATUS_NULL_POINTER, "innerproduct_int8_create: null pointer");
+  if (num_output <= 0 || num_input <= 0) return fail(NHIP_STATUS_INVALID_SHAPE, "innerproduct: sizes must be positive");
+  if (activation_type != NHIP_ACT_NONE && activation_type != NHIP_ACT_RELU)
+    return fail(NHIP_STATUS_UNSUPPORTED, "innerproduct activation must be 0 or 1");
+  *plan = nullptr;
+  // A 1x1 int8 convolution with fp32 output over m one-pixel "images" is
+  // exactly the quantized matmul + dequantize + bias of the InnerProduct.
+  nhip_conv_desc d{};
+  d.input_channels = num_input;
+  d.num_output = num_output;
+  d.kernel_w = d.kernel_h = 1;
+  d.dilation_w = d.dilation_h = 1;
+  d.stride_w = d.stride_h = 1;
+  d.bias_term = bias ? 1 : 0;
+  d.int8_scale_term = 2;
+  d.activation_type = activation_type;
+  d.group = 1;
+  nhip_conv_t c = nullptr;
+  NHIP_TRY(nhip_conv2d_int8_create(&d, weight, weight_is_i8, bias, weight_scale, num_output, input_scale, 1.0f, &c));
+  auto* p = new nhip_ip_plan();
+  p->n_out = num_output;
+  p->k_in = num_input;
+  p->act = activation_type;
+  p->q8 = c;
+  *plan = p;
+  return ok();
+}
+
+int nhip_innerproduct_int8_forward(nhip_ip_t p, const void* input, int32_t input_is_i8, float* output, int32_t m,
+                                   void* workspace, uint64_t workspace_bytes, void* stream) {
+  if (!p) return fail(NHIP_STATUS_NULL_POINTER, "innerproduct_int8_forward: null plan");
+  if (!p->q8) return fail(NHIP_STATUS_CONSTRAINT_VIOLATION, "innerproduct_int8_forward: not an int8 plan");
+  if (m < 0) return fail(NHIP_STATUS_INVALID_SHAPE, "innerproduct: negative m");
+  return nhip_conv2d_int8_forward(p->q8, input, input_is_i8, output, m, 1, 1, workspace, workspace_bytes, stream);
 }
 
 int nhip_innerproduct_f32_forward(nhip_ip_t p, const float* input, float* output, int32_t m, void* workspace,
                                   uint64_t workspace_bytes, void* stream) {
   if (!p) return fail(NHIP_STATUS_NULL_POINTER, "innerproduct_forward: null plan");
+  if (p->q8) return fail(NHIP_STATUS_CONSTRAINT_VIOLATION, "innerproduct_f32_forward: int8 plan");
   if (m < 0) return fail(NHIP_STATUS_INVALID_SHAPE, "innerproduct: negative m");
   if (m > 0 && (!input || !output)) return fail(NHIP_STATUS_NULL_POINTER, "innerproduct_forward: null pointer");
   if ((int64_t)m * std::max(p->k_in, p->n_pad) > std::numeric_limits<int32_t>::max())
@@ -591,6 +694,7 @@ int nhip_innerproduct_f32_forward(nhip_ip_t p, const float* input, float* output
 
 int nhip_innerproduct_destroy(nhip_ip_t p) {
   if (p) {
+    if (p->q8) free_plan(p->q8);
     (void)hipFree(p->weight);
     (void)hipFree(p->bias);
     delete p;

@@ -39,7 +39,9 @@ EXPORTS = (
     "nhip_conv2d_workspace_size", "nhip_conv2d_f32_forward",
     "nhip_conv2d_int8_create", "nhip_conv2d_int8_forward",
     "nhip_dwconv2d_f32_create", "nhip_dwconv2d_f32_forward",
+    "nhip_dwconv2d_int8_create", "nhip_dwconv2d_int8_forward",
     "nhip_conv_destroy", "nhip_innerproduct_f32_create",
+    "nhip_innerproduct_int8_create", "nhip_innerproduct_int8_forward",
     "nhip_innerproduct_workspace_size", "nhip_innerproduct_f32_forward",
     "nhip_innerproduct_destroy", "nhip_relu_f32", "nhip_relu_i8",
     "nhip_add_f32", "nhip_global_avgpool_f32", "nhip_quantize_f32_i8",
@@ -100,6 +102,10 @@ def load():
         "nhip_conv2d_int8_forward": [_P, _P, i32, _P, i32, i32, i32, _P, u64, _P],
         "nhip_dwconv2d_f32_create": [D, _P, _P, ctypes.POINTER(_P)],
         "nhip_dwconv2d_f32_forward": [_P, _P, _P, i32, i32, i32, _P],
+        "nhip_dwconv2d_int8_create": [D, _P, i32, _P, _P, i32, f32, f32, ctypes.POINTER(_P)],
+        "nhip_dwconv2d_int8_forward": [_P, _P, i32, _P, i32, i32, i32, _P],
+        "nhip_innerproduct_int8_create": [i32, i32, _P, i32, _P, _P, f32, i32, ctypes.POINTER(_P)],
+        "nhip_innerproduct_int8_forward": [_P, _P, i32, _P, i32, _P, u64, _P],
         "nhip_conv_destroy": [_P],
         "nhip_innerproduct_f32_create": [i32, i32, _P, _P, i32, ctypes.POINTER(_P)],
         "nhip_innerproduct_workspace_size": [_P, i32, ctypes.POINTER(u64)],
@@ -319,6 +325,75 @@ class DwConv2dF32(_Plan):
         if out is None:
             out = torch.empty((n, self.desc.num_output, oh, ow), dtype=torch.float32, device=x.device)
         check(load().nhip_dwconv2d_f32_forward(self.handle, _ptr(x), _ptr(out), n, h, w, _stream(stream)))
+        return out
+
+
+class DwConv2dInt8(_Plan):
+    """ncnn ConvolutionDepthWise with int8_scale_term."""
+
+    def __init__(self, desc: ConvDesc, weight, bias, weight_scale, input_scale, output_scale=1.0):
+        super().__init__()
+        self.desc = desc
+        w = np.ascontiguousarray(weight)
+        self._w = w if w.dtype == np.int8 else np.ascontiguousarray(w, dtype=np.float32)
+        self._b = None if bias is None else np.ascontiguousarray(bias, dtype=np.float32)
+        self._ws = np.ascontiguousarray(np.atleast_1d(weight_scale), dtype=np.float32)
+        check(load().nhip_dwconv2d_int8_create(
+            ctypes.byref(desc), _np_ptr(self._w), 1 if self._w.dtype == np.int8 else 0, _np_ptr(self._b),
+            _np_ptr(self._ws), self._ws.size, ctypes.c_float(input_scale), ctypes.c_float(output_scale),
+            ctypes.byref(self.handle)))
+
+    def forward(self, x, out=None, stream=None):
+        torch = _torch()
+        if not x.is_cuda or x.dtype not in (torch.float32, torch.int8):
+            raise TypeError("int8 depthwise input must be a float32 or int8 device tensor")
+        x = x.contiguous()
+        n, c, h, w = x.shape
+        oh, ow = output_shape(self.desc, h, w)
+        odt = torch.int8 if self.desc.int8_scale_term > 100 else torch.float32
+        if out is None:
+            out = torch.empty((n, c, oh, ow), dtype=odt, device=x.device)
+        check(load().nhip_dwconv2d_int8_forward(self.handle, _ptr(x), 1 if x.dtype == torch.int8 else 0, _ptr(out),
+                                                n, h, w, _stream(stream)))
+        return out
+
+
+class InnerProductInt8(_Plan):
+    """ncnn InnerProduct with int8_scale_term (fp32 output)."""
+    _destroy = "nhip_innerproduct_destroy"
+
+    def __init__(self, weight, bias, weight_scale, input_scale, activation=ACT_NONE):
+        super().__init__()
+        w = np.ascontiguousarray(weight)
+        self._w = w if w.dtype == np.int8 else np.ascontiguousarray(w, dtype=np.float32)
+        self.num_output, self.num_input = self._w.shape
+        self._b = None if bias is None else np.ascontiguousarray(bias, dtype=np.float32)
+        self._ws = np.ascontiguousarray(np.broadcast_to(np.atleast_1d(weight_scale), (self.num_output,)),
+                                        dtype=np.float32)
+        check(load().nhip_innerproduct_int8_create(
+            self.num_output, self.num_input, _np_ptr(self._w), 1 if self._w.dtype == np.int8 else 0,
+            _np_ptr(self._b), _np_ptr(self._ws), ctypes.c_float(input_scale), activation,
+            ctypes.byref(self.handle)))
+
+    def workspace_size(self, m) -> int:
+        b = ctypes.c_uint64()
+        check(load().nhip_innerproduct_workspace_size(self.handle, m, ctypes.byref(b)))
+        return b.value
+
+    def forward(self, x, out=None, workspace=None, stream=None):
+        torch = _torch()
+        if not x.is_cuda or x.dtype not in (torch.float32, torch.int8):
+            raise TypeError("int8 InnerProduct input must be a float32 or int8 device tensor")
+        x = x.contiguous()
+        m = x.shape[0]
+        if out is None:
+            out = torch.empty((m, self.num_output), dtype=torch.float32, device=x.device)
+        if workspace is None:
+            workspace, nbytes = _workspace(self.workspace_size(m), x.device)
+        else:
+            nbytes = workspace.numel()
+        check(load().nhip_innerproduct_int8_forward(self.handle, _ptr(x), 1 if x.dtype == torch.int8 else 0,
+                                                    _ptr(out), m, _ptr(workspace), nbytes, _stream(stream)))
         return out
 
 

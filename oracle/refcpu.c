@@ -374,3 +374,96 @@ void ref_same_padding(int32_t input, int32_t kernel, int32_t stride,
   *before = (int32_t)b;
   *after = (int32_t)(total - b);
 }
+
+/* Shared int8 epilogue: (float)acc * r, + bias, then either requantize by
+ * os (term > 100) with relu on int8, or relu on fp32 (NCNNToTosa.cpp:577-637,
+ * :1292-1312, ConvertRelu :1532-1578). */
+static void int8_epilogue(int64_t acc, float r, const float* bias, int c,
+                          float os, int32_t term, int32_t act, void* out,
+                          int64_t i) {
+  float f = (float)(int32_t)acc;
+  f = f * r;
+  if (bias) f = f + bias[c];
+  if (term > 100) {
+    int8_t v = ref_quantize_one(f, os);
+    if (act == 1 && v < 0) v = 0;
+    ((int8_t*)out)[i] = v;
+  } else {
+    if (act == 1) f = f < 0.0f ? 0.0f : f;
+    ((float*)out)[i] = f;
+  }
+}
+
+void ref_dwconv2d_int8(const ref_conv_geom* g, const void* input,
+                       int32_t input_is_i8, const int8_t* weight,
+                       const float* bias, const float* weight_scale,
+                       int32_t weight_scale_count, float input_scale,
+                       float output_scale, int32_t scale_term,
+                       int32_t activation, void* output, int threads) {
+  const int oh_n = ref_conv_out_h(g), ow_n = ref_conv_out_w(g);
+  const int C = g->c, H = g->h, W = g->w, KH = g->kernel_h, KW = g->kernel_w;
+  const int64_t in_count = (int64_t)g->n * C * H * W;
+  int8_t* q = (int8_t*)malloc((size_t)in_count);
+  float* recip = (float*)malloc((size_t)C * sizeof(float));
+  if (input_is_i8) {
+    memcpy(q, input, (size_t)in_count);
+  } else {
+    ref_quantize_f32_i8(in_count, (const float*)input, &input_scale, 1, 1, q);
+  }
+  for (int c = 0; c < C; ++c) {
+    float ws = weight_scale[weight_scale_count == 1 ? 0 : c];
+    ref_dequant_reciprocal(1, &ws, input_scale, &recip[c]);
+  }
+#pragma omp parallel for collapse(2) num_threads(pick_threads(threads)) schedule(static)
+  for (int n = 0; n < g->n; ++n) {
+    for (int c = 0; c < C; ++c) {
+      const int8_t* plane = q + ((int64_t)n * C + c) * H * W;
+      const int8_t* wc = weight + (int64_t)c * KH * KW;
+      for (int oh = 0; oh < oh_n; ++oh) {
+        for (int ow = 0; ow < ow_n; ++ow) {
+          int64_t s = 0;
+          for (int kh = 0; kh < KH; ++kh) {
+            const int y = oh * g->stride_h - g->pad_top + kh * g->dilation_h;
+            if (y < 0 || y >= H) continue;
+            for (int kw = 0; kw < KW; ++kw) {
+              const int x = ow * g->stride_w - g->pad_left + kw * g->dilation_w;
+              if (x < 0 || x >= W) continue;
+              s += (int64_t)plane[(int64_t)y * W + x] * (int64_t)wc[kh * KW + kw];
+            }
+          }
+          const int64_t i = (((int64_t)n * C + c) * oh_n + oh) * ow_n + ow;
+          int8_epilogue(s, recip[c], bias, c, output_scale, scale_term, activation, output, i);
+        }
+      }
+    }
+  }
+  free(q);
+  free(recip);
+}
+
+void ref_innerproduct_int8(int32_t m, int32_t k, int32_t n, const void* input,
+                           int32_t input_is_i8, const int8_t* weight,
+                           const float* bias, const float* weight_scale,
+                           float input_scale, int32_t activation,
+                           float* output, int threads) {
+  const int64_t in_count = (int64_t)m * k;
+  int8_t* q = (int8_t*)malloc((size_t)in_count);
+  float* recip = (float*)malloc((size_t)n * sizeof(float));
+  if (input_is_i8) {
+    memcpy(q, input, (size_t)in_count);
+  } else {
+    ref_quantize_f32_i8(in_count, (const float*)input, &input_scale, 1, 1, q);
+  }
+  ref_dequant_reciprocal(n, weight_scale, input_scale, recip);
+#pragma omp parallel for collapse(2) num_threads(pick_threads(threads)) schedule(static)
+  for (int i = 0; i < m; ++i) {
+    for (int j = 0; j < n; ++j) {
+      int64_t s = 0;
+      for (int t = 0; t < k; ++t)
+        s += (int64_t)q[(int64_t)i * k + t] * (int64_t)weight[(int64_t)j * k + t];
+      int8_epilogue(s, recip[j], bias, j, 1.0f, 1, activation, output, (int64_t)i * n + j);
+    }
+  }
+  free(q);
+  free(recip);
+}

@@ -79,6 +79,28 @@ void ref_conv2d_int8(const ref_conv_geom* g, const void* input,
                      float output_scale, int32_t scale_term,
                      int32_t activation, void* output, int threads);
 
+/* a3 int8 — ConvolutionDepthWise with int8_scale_term (NCNNToTosa.cpp:3257-3376):
+ * quantize input by input_scale (no-op for int8 input), int32 depthwise sum
+ * with the already-quantized weights [C][kh][kw], dequantize with
+ * r[c] = 1/(ws[c]*is) (ws count = C or 1), + bias, requantize by output_scale
+ * when scale_term > 100, then the separate relu when activation == 1. */
+void ref_dwconv2d_int8(const ref_conv_geom* g, const void* input,
+                       int32_t input_is_i8, const int8_t* weight,
+                       const float* bias, const float* weight_scale,
+                       int32_t weight_scale_count, float input_scale,
+                       float output_scale, int32_t scale_term,
+                       int32_t activation, void* output, int threads);
+
+/* a4 int8 — InnerProduct with int8_scale_term (NCNNToTosa.cpp:5300-5390):
+ * quantize input by input_scale, int32 matmul with int8 weights [N][K],
+ * dequantize with r[j] = 1/(ws[j]*is), + bias; fp32 output, then the
+ * separate relu when activation == 1. */
+void ref_innerproduct_int8(int32_t m, int32_t k, int32_t n, const void* input,
+                           int32_t input_is_i8, const int8_t* weight,
+                           const float* bias, const float* weight_scale,
+                           float input_scale, int32_t activation,
+                           float* output, int threads);
+
 /* Integer-only accumulator of the int8 convolution (int64, for brute-force
  * pinning: exact for any reduction order). */
 void ref_conv2d_i8_acc(const ref_conv_geom* g, const int8_t* input,

@@ -136,6 +136,37 @@ def conv2d_int8(g: ConvGeom, x, w_i8, b, weight_scale, input_scale,
     return out
 
 
+def dwconv2d_int8(g: ConvGeom, x, w_i8, b, weight_scale, input_scale,
+                  output_scale=1.0, scale_term=101, activation=1, threads=0):
+    """x: float32 (quantized by input_scale) or int8; w_i8 [C][1][kh][kw]."""
+    is_i8 = x.dtype == np.int8
+    x = np.ascontiguousarray(x) if is_i8 else _f32(x)
+    w_i8 = np.ascontiguousarray(w_i8, dtype=np.int8)
+    ws = _f32(np.atleast_1d(weight_scale))
+    oh, ow = out_hw(g)
+    out = np.empty((g.n, g.k, oh, ow), np.int8 if scale_term > 100 else np.float32)
+    lib().ref_dwconv2d_int8(ctypes.byref(g), _p(x), ctypes.c_int32(int(is_i8)), _p(w_i8), _p(_f32(b)), _p(ws),
+                            ctypes.c_int32(ws.size), ctypes.c_float(input_scale), ctypes.c_float(output_scale),
+                            ctypes.c_int32(scale_term), ctypes.c_int32(activation), _p(out), ctypes.c_int(threads))
+    return out
+
+
+def innerproduct_int8(x, w_i8, b, weight_scale, input_scale, activation=0, threads=0):
+    """x [M][K] float32 or int8, w_i8 [N][K] -> float32 [M][N]."""
+    is_i8 = x.dtype == np.int8
+    x = np.ascontiguousarray(x) if is_i8 else _f32(x)
+    w_i8 = np.ascontiguousarray(w_i8, dtype=np.int8)
+    m, k = x.shape
+    n = w_i8.shape[0]
+    ws = _f32(np.broadcast_to(np.atleast_1d(weight_scale), (n,)))
+    out = np.empty((m, n), np.float32)
+    lib().ref_innerproduct_int8(ctypes.c_int32(m), ctypes.c_int32(k), ctypes.c_int32(n), _p(x),
+                                ctypes.c_int32(int(is_i8)), _p(w_i8), _p(_f32(b)), _p(ws),
+                                ctypes.c_float(input_scale), ctypes.c_int32(activation), _p(out),
+                                ctypes.c_int(threads))
+    return out
+
+
 def conv2d_i8_acc(g: ConvGeom, x_i8, w_i8, threads=0):
     x_i8 = np.ascontiguousarray(x_i8, dtype=np.int8)
     w_i8 = np.ascontiguousarray(w_i8, dtype=np.int8)

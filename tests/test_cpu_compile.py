@@ -142,7 +142,7 @@ def test_int8_chain_io_types():
     ("magic", 3, "magic"),
     ("truncated", 3, "truncated"),
     ("omitted", 2, "omitted"),
-    ("int8_dw", 7, "int8 depthwise"),
+    ("int8_dw_f32_input_relu6", 7, "activation"),
     ("channels", 2, "channels"),
 ])
 def test_rejections(case, status, needle):
@@ -151,11 +151,11 @@ def test_rejections(case, status, needle):
         m.layer("Softmax", "prob", ["output"], ["prob"])
     if case == "omitted":
         m = ip_dynamic_model()
-    if case == "int8_dw":
+    if case == "int8_dw_f32_input_relu6":
         m = ncnn_format.Model()
         m.input("data", 4, 6, 6)
         m.conv("dw", "data", "out", RNG.integers(-9, 9, (4, 1, 3, 3)).astype(np.int8), None, depthwise=True,
-               int8=dict(term=1, ws=np.ones(4, np.float32), **{"is": 1.0}))
+               act=2, int8=dict(term=1, ws=np.ones(4, np.float32), **{"is": 1.0}))
     if case == "channels":
         m = ncnn_format.Model()
         m.input("data", 3, 6, 6)

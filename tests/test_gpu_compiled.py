@@ -135,6 +135,45 @@ def test_int8_chain_bit_exact(tmp_path):
     np.testing.assert_array_equal(out, exp)
 
 
+def test_int8_complete_chain_fixture(tmp_path):
+    # test/Numerical/fixtures/int8_complete_chain.param: conv (term 101) ->
+    # depthwise (term 101) -> conv (term 1), with the closed-form weights of
+    # generate_int8_bins.py (convolution(101, 2, 3) + depthwise(101, 3) +
+    # convolution(1, 3, 2)), on a 2x5x4 input.
+    def conv_w(cin, cout):
+        return np.array([((i * 7 + 3) % 15) - 7 for i in range(cin * cout)], np.int8).reshape(cout, cin, 1, 1)
+
+    def conv_b(cout):
+        return np.array([0.125 * (i - 1) for i in range(cout)], np.float32)
+
+    def conv_ws(cout):
+        return np.array([5.0 + i * 1.5 for i in range(cout)], np.float32)
+
+    dw_w = np.array([((i * 5 + 1) % 11) - 5 for i in range(3)], np.int8).reshape(3, 1, 1, 1)
+    dw_b = np.array([0.1 * (i - 1) for i in range(3)], np.float32)
+    dw_ws = np.array([4.0 + i for i in range(3)], np.float32)
+    m = ncnn_format.Model()
+    m.input("data", 2, 5, 4)
+    m.conv("conv_requant", "data", "conv_i8", conv_w(2, 3), conv_b(3), pad=0,
+           int8=dict(term=101, ws=conv_ws(3), **{"is": 8.0, "os": 6.0}))
+    m.conv("dw_requant", "conv_i8", "dw_i8", dw_w, dw_b, pad=0, depthwise=True,
+           int8=dict(term=101, ws=dw_ws, **{"is": 7.0, "os": 5.0}))
+    m.conv("conv_dequant", "dw_i8", "output", conv_w(3, 2), conv_b(2), pad=0,
+           int8=dict(term=1, ws=conv_ws(2), **{"is": 8.0}))
+    lib = build(tmp_path, m, "chain8")
+    lib.chain8.argtypes = [P, P]
+    x = RNG.uniform(-1.5, 1.5, (1, 2, 5, 4)).astype(np.float32)
+    out = np.zeros((2, 5, 4), np.float32)
+    assert lib.chain8(ptr(x[0]), ptr(out)) == 0
+    g1 = refcpu.geom(1, 2, 5, 4, 3, (1, 1), pad=(0, 0, 0, 0))
+    q1 = refcpu.conv2d_int8(g1, x, conv_w(2, 3), conv_b(3), conv_ws(3), 8.0, 6.0, 101, 0)
+    g2 = refcpu.geom(1, 3, 5, 4, 3, (1, 1), pad=(0, 0, 0, 0))
+    q2 = refcpu.dwconv2d_int8(g2, q1, dw_w, dw_b, dw_ws, 7.0, 5.0, 101, 0)
+    g3 = refcpu.geom(1, 3, 5, 4, 2, (1, 1), pad=(0, 0, 0, 0))
+    exp = refcpu.conv2d_int8(g3, q2, conv_w(3, 2), conv_b(2), conv_ws(2), 8.0, 1.0, 1, 0)[0]
+    np.testing.assert_array_equal(out, exp)
+
+
 def test_mobilenetv2_entry_and_device_batch(tmp_path):
     layers = graphs.mobilenetv2_layers(seed=0)
     lib = build(tmp_path, ncnn_format.from_layer_list(layers), "mbv2")

@@ -148,3 +148,69 @@ def test_zero_weight_scale_selects_zero():
     got = run(d, x, w, np.array([0.5, 0.25], np.float32), np.array([0.0, 2.0], np.float32), 1.0, 1.0)
     np.testing.assert_array_equal(got[0, 0], np.full((3, 3), 0.5, np.float32))
     np.testing.assert_array_equal(got[0, 1], np.full((3, 3), 2 * 0.5 + 0.25, np.float32))
+
+
+# ---- int8 ConvolutionDepthWise (NCNNToTosa.cpp:3257-3376) ----
+DW_CASES = [
+    # (n, c, h, w, kernel, stride, dil, pad, term, act, fp32 weights?, int8 input?)
+    (2, 32, 28, 28, (3, 3), (1, 1), (1, 1), (1, 1, 1, 1), 101, 1, False, False),
+    (2, 96, 28, 28, (3, 3), (2, 2), (1, 1), (1, 1, 1, 1), 1, 1, True, False),
+    (1, 24, 13, 17, (3, 3), (1, 1), (1, 1), (1, 1, 1, 1), 2, 0, False, True),
+    (3, 8, 11, 9, (5, 5), (2, 1), (2, 1), (3, 1, 0, 2), 102, 0, True, True),
+    (1, 960, 7, 7, (3, 3), (1, 1), (1, 1), (1, 1, 1, 1), 101, 1, False, False),
+]
+
+
+@pytest.mark.parametrize("case", DW_CASES, ids=lambda c: "x".join(map(str, c[:4])) + f"-t{c[8]}")
+def test_int8_depthwise_bit_exact(case):
+    n, c, h, w, ker, st, dl, pad, term, act, wf32, in_i8 = case
+    rng = np.random.default_rng(hash(case) % (2 ** 32))
+    x = (rng.integers(-127, 128, (n, c, h, w)).astype(np.int8) if in_i8
+         else rng.uniform(-1.5, 1.5, (n, c, h, w)).astype(np.float32))
+    scalar = term in (2, 102)
+    ws = rng.uniform(20, 200, 1 if scalar else c).astype(np.float32)
+    wfloat = rng.uniform(-0.6, 0.6, (c, 1) + ker).astype(np.float32)
+    ws_full = np.broadcast_to(ws, (c,))
+    w_i8 = np.stack([refcpu.quantize_f32_i8(wfloat[o], ws_full[o:o + 1]) for o in range(c)])
+    b = rng.normal(0, 0.3, c).astype(np.float32)
+    d = nhip.conv_desc(c, c, ker, st, dl, pad, act=act, int8_scale_term=term, group=c)
+    conv = nhip.DwConv2dInt8(d, wfloat if wf32 else w_i8, b, ws, 60.0, 25.0)
+    got = host(conv.forward(dev(x)))
+    g = refcpu.geom(n, c, h, w, c, ker, st, dl, pad)
+    exp = refcpu.dwconv2d_int8(g, x, w_i8, b, ws, 60.0, 25.0, term, act)
+    assert got.dtype == exp.dtype
+    np.testing.assert_array_equal(got, exp)
+
+
+def test_int8_depthwise_fixture_known_answer_on_device():
+    w = np.array([-4, 1, -5], np.int8).reshape(3, 1, 1, 1)
+    b = np.array([-0.1, 0.0, 0.1], np.float32)
+    x = np.array([0.5, -0.25, 1.0], np.float32).reshape(1, 3, 1, 1)
+    d = nhip.conv_desc(3, 3, (1, 1), pad=(0, 0, 0, 0), int8_scale_term=101, group=3)
+    got = host(nhip.DwConv2dInt8(d, w, b, np.array([4.0, 5.0, 6.0], np.float32), 7.0, 5.0).forward(dev(x)))
+    np.testing.assert_array_equal(got[0, :, 0, 0], [-3, 0, -4])
+
+
+# ---- int8 InnerProduct (NCNNToTosa.cpp:5300-5390) ----
+@pytest.mark.parametrize("m,k,n,act,wf32,in_i8", [
+    (1, 4, 3, 0, False, False), (256, 2048, 1000, 0, False, False), (7, 130, 65, 1, True, False),
+    (33, 1280, 1000, 1, False, True), (2, 17, 5, 0, True, True)])
+def test_int8_innerproduct_bit_exact(m, k, n, act, wf32, in_i8):
+    rng = np.random.default_rng(m * 1000 + k + n)
+    x = rng.integers(-127, 128, (m, k)).astype(np.int8) if in_i8 else rng.uniform(-1.5, 1.5, (m, k)).astype(np.float32)
+    ws = rng.uniform(20, 200, n).astype(np.float32)
+    wfloat = rng.uniform(-0.6, 0.6, (n, k)).astype(np.float32)
+    w_i8 = np.stack([refcpu.quantize_f32_i8(wfloat[j], ws[j:j + 1]) for j in range(n)])
+    b = rng.normal(0, 0.3, n).astype(np.float32)
+    ip = nhip.InnerProductInt8(wfloat if wf32 else w_i8, b, ws, 60.0, act)
+    got = host(ip.forward(dev(x)))
+    exp = refcpu.innerproduct_int8(x, w_i8, b, ws, 60.0, act)
+    np.testing.assert_array_equal(got, exp)
+
+
+def test_int8_innerproduct_fixture_known_answer_on_device():
+    w = np.array([3, -2, 1, 4, -4, 2, 5, -1, 2, 3, -3, 1], np.int8).reshape(3, 4)
+    ip = nhip.InnerProductInt8(w, np.array([0.25, -0.5, 0.125], np.float32), np.array([4.0, 6.0, 8.0], np.float32), 9.0)
+    got = host(ip.forward(dev(np.array([[1.0, 0.5, -1.0, 0.25]], np.float32))))
+    exp = np.array([16 / 36 + 0.25, -73 / 54 - 0.5, 62 / 72 + 0.125], np.float32)
+    np.testing.assert_allclose(got[0], exp, rtol=1e-6)

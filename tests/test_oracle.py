@@ -342,3 +342,58 @@ def test_same_padding_upper_lower():
     assert refcpu.same_padding(5, 3, 2, 1, -233) == (1, 1)
     assert refcpu.same_padding(7, 3, 1, 2, -233) == (2, 2)
     assert refcpu.same_padding(8, 1, 1, 1, -233) == (0, 0)
+
+
+# ---- int8 depthwise / InnerProduct (NCNNToTosa.cpp:3257-3376, 5300-5390) ----
+
+def test_int8_depthwise_known_answer_fixture_generator():
+    # generate_int8_bins.py depthwise(101, 3): weights ((i*5+1)%11)-5 = [-4, 1, -5],
+    # bias 0.1*(i-1), ws 4+i, is 7, os 5; 1x1 kernel.
+    w = np.array([((i * 5 + 1) % 11) - 5 for i in range(3)], np.int8).reshape(3, 1, 1, 1)
+    np.testing.assert_array_equal(w.ravel(), [-4, 1, -5])
+    b = np.array([0.1 * (i - 1) for i in range(3)], np.float32)
+    ws = np.array([4.0, 5.0, 6.0], np.float32)
+    x = np.array([0.5, -0.25, 1.0], np.float32).reshape(1, 3, 1, 1)
+    g = refcpu.geom(1, 3, 1, 1, 3, (1, 1), pad=(0, 0, 0, 0))
+    f = refcpu.dwconv2d_int8(g, x, w, b, ws, 7.0, scale_term=1, activation=0)[0, :, 0, 0]
+    # q = round(3.5)=4, round(-1.75)=-2, 7 ; acc = -16, -2, -35
+    # f = -16/28 - 0.1 ; -2/35 + 0 ; -35/42 + 0.1
+    np.testing.assert_allclose(f, [-16 / 28 - 0.1, -2 / 35, -35 / 42 + 0.1], rtol=1e-6)
+    q = refcpu.dwconv2d_int8(g, x, w, b, ws, 7.0, 5.0, scale_term=101, activation=0)[0, :, 0, 0]
+    # *5: -3.357 -> -3 ; -0.2857 -> 0 ; -3.6667 -> -4
+    np.testing.assert_array_equal(q, [-3, 0, -4])
+    relu = refcpu.dwconv2d_int8(g, x, w, b, ws, 7.0, 5.0, scale_term=101, activation=1)[0, :, 0, 0]
+    np.testing.assert_array_equal(relu, [0, 0, 0])
+    # scalar weight scale (terms 2 / 102): ws count 1 applies to every channel
+    s = refcpu.dwconv2d_int8(g, x, w, b, np.array([4.0], np.float32), 7.0, scale_term=2, activation=0)[0, :, 0, 0]
+    np.testing.assert_allclose(s, [-16 / 28 - 0.1, -2 / 28, -35 / 28 + 0.1], rtol=1e-6)
+
+
+def test_int8_depthwise_accumulator_bruteforce():
+    rng = np.random.default_rng(5)
+    x = rng.integers(-127, 128, (2, 4, 7, 6)).astype(np.int8)
+    w = rng.integers(-127, 128, (4, 1, 3, 3)).astype(np.int8)
+    g = refcpu.geom(2, 4, 7, 6, 4, (3, 3), (2, 1))
+    # ws = 1, is = 1 and a huge fp32 output keep the accumulator exact in fp32
+    out = refcpu.dwconv2d_int8(g, x, w, None, np.ones(4, np.float32), 1.0, scale_term=1, activation=0)
+    exp = conv_f64(x.astype(np.float64), w.astype(np.float64), None, (2, 1), groups=4)
+    np.testing.assert_array_equal(out, exp.astype(np.float32))
+
+
+def test_int8_innerproduct_known_answer_fixture_generator():
+    # generate_int8_bins.py inner_product(): weights [3,-2,1,4 | -4,2,5,-1 | 2,3,-3,1],
+    # bias [0.25,-0.5,0.125], ws [4,6,8], is 9
+    w = np.array([3, -2, 1, 4, -4, 2, 5, -1, 2, 3, -3, 1], np.int8).reshape(3, 4)
+    b = np.array([0.25, -0.5, 0.125], np.float32)
+    ws = np.array([4.0, 6.0, 8.0], np.float32)
+    x = np.array([[1.0, 0.5, -1.0, 0.25]], np.float32)
+    out = refcpu.innerproduct_int8(x, w, b, ws, 9.0)
+    # q = [9, round(4.5)=5, -9, round(2.25)=2]; acc = 27-10-9+8 = 16, -36+10-45-2 = -73, 18+15+27+2 = 62
+    np.testing.assert_allclose(out[0], [16 / 36 + 0.25, -73 / 54 - 0.5, 62 / 72 + 0.125], rtol=1e-6)
+    relu = refcpu.innerproduct_int8(x, w, b, ws, 9.0, activation=1)
+    assert relu[0, 1] == 0.0 and relu[0, 0] == out[0, 0]
+    rng = np.random.default_rng(6)
+    xi = rng.integers(-127, 128, (5, 33)).astype(np.int8)
+    wi = rng.integers(-127, 128, (7, 33)).astype(np.int8)
+    acc = refcpu.innerproduct_int8(xi, wi, None, np.ones(7, np.float32), 1.0)
+    np.testing.assert_array_equal(acc, (xi.astype(np.int64) @ wi.T.astype(np.int64)).astype(np.float32))
