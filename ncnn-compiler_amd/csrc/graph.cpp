@@ -897,19 +897,11 @@ int build(nhip_graph& g, std::vector<Layer>& layers, const int64_t* input_shapes
     if (op.kind != OpKind::Alias || op.view != Op::View::Same) {
       if (L.tops.size() != 1) return fail(NHIP_STATUS_UNSUPPORTED, where(L) + "one output expected");
     }
-    // outputs (Split fans one blob out to several aliases)
-    const int first_out = blob(L.tops[0]);
+    // outputs (Split fans its input out to several aliases of it, so that
+    // each top can also be a graph output)
     for (size_t t = 0; t < L.tops.size(); ++t) {
       Op o = op;
       o.out = blob(L.tops[t]);
-      if (t > 0) {
-        o.conv = nullptr;
-        o.ip = nullptr;
-        o.scale_dev = nullptr;
-        o.kind = OpKind::Alias;
-        o.view = Op::View::Same;
-        o.in = {first_out};
-      }
       Blob& ob = g.blobs[o.out];
       ob.dtype = o.kind == OpKind::Alias ? g.blobs[o.in[0]].dtype : o.out_dtype;
       if (o.kind == OpKind::Alias) ob.alias_of = o.in[0];

@@ -48,6 +48,14 @@ EXPORTS = (
     "nhip_requantize_i32_i8", "nhip_dequantize_i32_f32",
 )
 
+# Every symbol include/nhip_graph.h declares.
+GRAPH_EXPORTS = (
+    "nhip_graph_load", "nhip_graph_describe", "nhip_graph_num_io",
+    "nhip_graph_io_info", "nhip_graph_infer_shapes", "nhip_graph_run",
+    "nhip_graph_run_host", "nhip_graph_destroy",
+)
+DTYPE_F32, DTYPE_I8 = 0, 1
+
 
 class NhipError(RuntimeError):
     def __init__(self, status: int, message: str):
@@ -119,6 +127,17 @@ def load():
         "nhip_requantize_i32_i8": [_P, _P, i32, i32, i64, _P, i32, _P, i32, _P, i32, i32, _P],
         "nhip_dequantize_i32_f32": [_P, _P, i32, i32, i64, _P, i32, _P, i32, _P],
     }
+    i64p, i32p, vpp = ctypes.POINTER(i64), ctypes.POINTER(i32), ctypes.POINTER(_P)
+    sig.update({
+        "nhip_graph_load": [ctypes.c_char_p, u64, _P, u64, i64p, i32, vpp],
+        "nhip_graph_describe": [ctypes.c_char_p, u64, _P, u64, i64p, i32, vpp],
+        "nhip_graph_num_io": [_P, i32p, i32p],
+        "nhip_graph_io_info": [_P, i32, i32, i32p, i64p, i32p, ctypes.POINTER(ctypes.c_char_p)],
+        "nhip_graph_infer_shapes": [_P, i64p, i64p, i32p],
+        "nhip_graph_run": [_P, i32, i64p, vpp, vpp, _P],
+        "nhip_graph_run_host": [_P, i64p, vpp, vpp, ctypes.POINTER(u64)],
+        "nhip_graph_destroy": [_P],
+    })
     for name, args in sig.items():
         fn = getattr(L, name)
         fn.argtypes = args
@@ -502,3 +521,107 @@ def dequantize(x, scale, bias=None, stream=None):
     check(load().nhip_dequantize_i32_f32(_ptr(x), _ptr(out), n, c, plane, _ptr(s), s.numel(), _ptr(b),
                                          0 if b is None else b.numel(), _stream(stream)))
     return out
+
+
+class Graph:
+    """An ncnn model (.param text + .bin payload) lowered onto libnhip
+    (include/nhip_graph.h), the device counterpart of the reference's
+    compiled model: Graph::load (lib/Graph/graph.cpp:2129-2333) + the
+    generated entry (tools/ncnn-compile.cpp:915-932).
+
+    input_shapes: None, or one CHW triple per Input layer (-1 = given at run
+    time, the reference's "?" of --input-shape).  describe_only=True parses,
+    validates and lowers without any device work (what a compiler on a host
+    without a GPU needs); running such a graph is a constraint violation.
+    """
+
+    def __init__(self, param_text, bin_bytes=b"", input_shapes=None, describe_only=False):
+        L = load()
+        param = param_text.encode() if isinstance(param_text, str) else bytes(param_text)
+        self._bin = bytes(bin_bytes)
+        arr, count = None, 0
+        if input_shapes is not None:
+            flat = [int(v) for s in input_shapes for v in s]
+            arr = (ctypes.c_int64 * max(len(flat), 1))(*flat)
+            count = len(input_shapes)
+        self.handle = _P()
+        fn = L.nhip_graph_describe if describe_only else L.nhip_graph_load
+        check(fn(param, len(param), self._bin or None, len(self._bin), arr, count, ctypes.byref(self.handle)))
+        ni, no = ctypes.c_int32(), ctypes.c_int32()
+        check(L.nhip_graph_num_io(self.handle, ctypes.byref(ni), ctypes.byref(no)))
+        self.inputs = [self._io(0, i) for i in range(ni.value)]
+        self.outputs = [self._io(1, i) for i in range(no.value)]
+
+    def _io(self, is_output, index):
+        rank, dtype, name = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_char_p()
+        dims = (ctypes.c_int64 * 4)()
+        check(load().nhip_graph_io_info(self.handle, is_output, index, ctypes.byref(rank), dims,
+                                        ctypes.byref(dtype), ctypes.byref(name)))
+        return dict(name=name.value.decode(), shape=tuple(dims[:rank.value]),
+                    dtype=np.int8 if dtype.value == DTYPE_I8 else np.float32)
+
+    @staticmethod
+    def _shape_arg(shapes):
+        if shapes is None:
+            return None
+        flat = [int(v) for s in shapes for v in s]
+        return (ctypes.c_int64 * len(flat))(*flat)
+
+    def infer_shapes(self, input_shapes=None):
+        """-> list of output shapes for concrete CHW input shapes."""
+        n = len(self.outputs)
+        out = (ctypes.c_int64 * (4 * n))()
+        ranks = (ctypes.c_int32 * n)()
+        check(load().nhip_graph_infer_shapes(self.handle, self._shape_arg(input_shapes), out, ranks))
+        return [tuple(out[4 * j:4 * j + ranks[j]]) for j in range(n)]
+
+    def run_host(self, *arrays, capacity=None):
+        """The reference entry semantics: one image per input (host numpy
+        arrays), returns the list of outputs as numpy arrays."""
+        xs = [np.ascontiguousarray(a, dtype=io["dtype"]) for a, io in zip(arrays, self.inputs)]
+        if len(xs) != len(self.inputs):
+            raise ValueError(f"expected {len(self.inputs)} inputs")
+        shapes = [a.shape if a.ndim == 3 else (1,) * (3 - a.ndim) + a.shape for a in xs]
+        dyn = any(d < 0 for io in self.inputs for d in io["shape"])
+        arg = self._shape_arg(shapes) if dyn else None
+        oshapes = self.infer_shapes(shapes if dyn else None)
+        outs = [np.empty(s, io["dtype"]) for s, io in zip(oshapes, self.outputs)]
+        ins = (_P * len(xs))(*[a.ctypes.data for a in xs])
+        ops = (_P * len(outs))(*[o.ctypes.data for o in outs])
+        cap = None
+        if capacity is not None:
+            cap = (ctypes.c_uint64 * len(outs))(*capacity)
+        check(load().nhip_graph_run_host(self.handle, arg, ins, ops, cap))
+        return outs
+
+    def run(self, *tensors, stream=None):
+        """Batch execution: each input a [N, ...] device tensor of N blobs;
+        returns device tensors [N, ...] per output."""
+        torch = _torch()
+        if len(tensors) != len(self.inputs):
+            raise ValueError(f"expected {len(self.inputs)} inputs")
+        n = int(tensors[0].shape[0])
+        xs = [_dev(t, torch.int8 if io["dtype"] == np.int8 else torch.float32)
+              for t, io in zip(tensors, self.inputs)]
+        shapes = [tuple(t.shape[1:]) if t.dim() == 4 else (1,) * (4 - t.dim()) + tuple(t.shape[1:])
+                  for t in xs]
+        dyn = any(d < 0 for io in self.inputs for d in io["shape"])
+        oshapes = self.infer_shapes(shapes if dyn else None)
+        outs = [torch.empty((n,) + s, dtype=torch.int8 if io["dtype"] == np.int8 else torch.float32,
+                            device=xs[0].device) for s, io in zip(oshapes, self.outputs)]
+        ins = (_P * len(xs))(*[t.data_ptr() for t in xs])
+        ops = (_P * len(outs))(*[o.data_ptr() for o in outs])
+        check(load().nhip_graph_run(self.handle, n, self._shape_arg(shapes) if dyn else None, ins, ops,
+                                    _stream(stream)))
+        return outs
+
+    def close(self):
+        if self.handle:
+            load().nhip_graph_destroy(self.handle)
+            self.handle = _P()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

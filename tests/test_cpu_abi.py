@@ -13,19 +13,20 @@ import nhip
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 
-def header_functions():
-    text = open(os.path.join(ROOT, "include", "nhip.h")).read()
+def header_functions(header="nhip.h"):
+    text = open(os.path.join(ROOT, "include", header)).read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
     return sorted(set(re.findall(r"\b(nhip_\w+)\s*\(", text)))
 
 
 def test_header_declares_exactly_the_binding_exports():
     assert header_functions() == sorted(nhip.EXPORTS)
+    assert header_functions("nhip_graph.h") == sorted(nhip.GRAPH_EXPORTS)
 
 
 def test_library_exports_every_header_symbol():
     lib = nhip.load()
-    for name in header_functions():
+    for name in header_functions() + header_functions("nhip_graph.h"):
         assert hasattr(lib, name), name
     # and nothing reference-reserved (tools/ncnn-compile.cpp:2189-2196)
     syms = os.popen(f"nm -D --defined-only {nhip.LIB_PATH}").read()
