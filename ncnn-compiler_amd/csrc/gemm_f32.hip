@@ -1,14 +1,14 @@
-// fp32 MFMA GEMM core (v_mfma_f32_32x32x2_f32, wave64) and the three
-// contractions that use it:
+// fp32 MFMA GEMM core (v_mfma_f32_32x32x2_f32, wave64) and the two
+// contractions that use it (the Winograd batched GEMM has its own kernel in
+// wino_gemm.hip):
 //   - implicit-GEMM Convolution over NCHW blobs (reference ConvertConvolution
 //     fp32 path, NCNNToTosa.cpp:1316-1529, lowered upstream to
 //     linalg.conv_2d_nhwc_hwcf: out = bias + sum_{kh,kw,c} x*w);
-//   - the 36 batched GEMMs of Winograd F(4,3) (M[xi] = U[xi] * V[xi]);
 //   - InnerProduct (NCNNToTosa.cpp:5254-5392: zero-init matmul, then bias).
 //
 // GEMM view: D[i][j] = sum_k A[i][k] * B[k][j].  A rows i are output channels
-// (conv, Winograd) or input rows m (InnerProduct); B columns j are output
-// pixels, Winograd tiles, or InnerProduct outputs.  One workgroup = 4 waves
+// (conv) or input rows m (InnerProduct); B columns j are output pixels or
+// InnerProduct outputs.  One workgroup = 4 waves
 // (2x2) computes a BM x BN tile; each wave a (BM/2) x (BN/2) tile built from
 // 32x32 MFMA blocks.  K advances in chunks of 16 through double-buffered LDS.
 //
@@ -22,31 +22,29 @@ namespace nhip {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kBK = 16;
+constexpr int kBK = 16;      // K chunk of the MFMA k mapping; tiles use BK = 16 or 32
 constexpr int kRowPad = 4;  // LDS row padding (floats): conflict-free b128 reads
+constexpr int kXcds = 8;    // accelerator complex dies on MI355X
 
-enum class Mode { Conv, Wino, IP };
+enum class Mode { Conv, IP };
 
 struct GemmArgs {
   // A operand
-  const float* a;        // conv/wino: weights [m_pad][lda]; IP: input [M][lda]
-  int64_t a_batch;       // elements between Winograd batches (xi)
+  const float* a;        // conv: weights [m_pad][lda]; IP: input [M][lda]
   int lda;
   int m;                 // valid rows of the problem (out channels / IP rows)
   // B operand
-  const float* b;        // conv: input NCHW; wino: V [36][c_pad][ldb]; IP: W [n_pad][ldb]
-  int64_t b_batch;
+  const float* b;        // conv: input NCHW; IP: W [n_pad][ldb]
   int ldb;
-  int n;                 // valid columns (pixels / tiles / IP outputs)
-  int kdim;              // reduction length (multiple of kBK after padding)
+  int n;                 // valid columns (pixels / IP outputs)
+  int kdim;              // reduction length (multiple of BK after padding)
   int k_valid;           // IP: valid input length (loads past it read 0)
   uint32_t b_bytes;      // conv: size of the input tensor (< 2^31)
   // conv geometry
   const int* ktab;
   int C, H, W, OW, OHW, sh, sw, pt, pl;
   // epilogue
-  float* d;              // conv: out NCHW; wino: M [36][m_pad][ldd]; IP: out [M][ldd]
-  int64_t d_batch;
+  float* d;              // conv: out NCHW; IP: out [M][ldd]
   int ldd;
   const float* bias;
   const float* residual;
@@ -61,14 +59,13 @@ __device__ __forceinline__ float apply_act(float v, int act) {
   return v;
 }
 
-template <int BM, int BN, Mode MODE>
+template <int BM, int BN, int BK, Mode MODE>
 __global__ __launch_bounds__(kThreads) void gemm_f32_kernel(GemmArgs g) {
+  static_assert(BK % kBK == 0, "BK is a multiple of the 16-wide MFMA k chunk");
   constexpr int TM = BM / 64;  // 32x32 blocks per wave along i
   constexpr int TN = BN / 64;  // along j
-  constexpr int AS = kBK + kRowPad;                 // As[BM][AS]
-  constexpr bool B_KJ = (MODE == Mode::Wino);       // Bs[kBK][BN+pad] else Bs[BN][AS]
-  constexpr int BS_ROW = B_KJ ? (BN + kRowPad) : AS;
-  constexpr int B_ELEMS = B_KJ ? kBK * BS_ROW : BN * AS;
+  constexpr int AS = BK + kRowPad;                  // As[BM][AS], Bs[BN][AS]
+  constexpr int B_ELEMS = BN * AS;
   __shared__ __attribute__((aligned(16))) float As[2][BM * AS];
   __shared__ __attribute__((aligned(16))) float Bs[2][B_ELEMS];
 
@@ -78,39 +75,54 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_kernel(GemmArgs g) {
   const int wm = wave >> 1, wn = wave & 1;
   const int li = lane & 31, lh = lane >> 5;
 
-  const int j0 = blockIdx.x * BN;
-  const int i0 = blockIdx.y * BM;
-  int batch = 0, split = 0;
-  if constexpr (MODE == Mode::Wino) batch = blockIdx.z;
-  if constexpr (MODE == Mode::IP) split = blockIdx.z;
+  // Workgroups are dispatched round-robin over the XCDs (8 on MI355X, each
+  // with its own L2): hardware id L runs on XCD L % 8.  Renumber so that each
+  // XCD gets a contiguous range of logical tiles; tiles that share an A row
+  // block (same i) then run on the same XCD and share its L2.
+  int bx, by, bz;
+  {
+    const int nbx = gridDim.x, nby = gridDim.y;
+    const int total = nbx * nby * gridDim.z;
+    const int L = blockIdx.x + nbx * (blockIdx.y + nby * blockIdx.z);
+    const int x = L % kXcds, q = L / kXcds;
+    const int logical = x * (total / kXcds) + min(x, total % kXcds) + q;
+    bx = logical % nbx;
+    by = (logical / nbx) % nby;
+    bz = logical / (nbx * nby);
+  }
+  const int j0 = bx * BN;
+  const int i0 = by * BM;
+  int split = 0;
+  if constexpr (MODE == Mode::IP) split = bz;
 
-  const float* A = g.a + (int64_t)batch * g.a_batch;
-  const float* B = g.b + (int64_t)batch * g.b_batch;
+  const float* A = g.a;
+  const float* B = g.b;
 
-  const int nk_total = g.kdim / kBK;
+  const int nk_total = g.kdim / BK;
   int kt_begin = 0, kt_end = nk_total;
-  if constexpr (MODE == Mode::IP) {
+  if constexpr (MODE != Mode::Conv) {
     const int per = (nk_total + g.splits - 1) / g.splits;
     kt_begin = split * per;
     kt_end = min(nk_total, kt_begin + per);
   }
 
-  // ---- A loader: BM x 16 floats = BM*4 float4, (BM*4)/256 per thread.
-  constexpr int A_LD = BM * 4 / kThreads;
-  float4 ra[A_LD];
+  // ---- A loader: BM x BK floats = BM*BK/4 float4, BM*BK/1024 per thread.
+  constexpr int A_Q = BK / 4;  // float4 per A row chunk
+  constexpr int A_LD = BM * A_Q / kThreads;
+  v4f ra[A_LD];  // native vectors: HIP's float4 struct copies would stay in scratch
   auto load_a = [&](int kt) {
 #pragma unroll
     for (int u = 0; u < A_LD; ++u) {
       const int q = tid + u * kThreads;
-      const int row = q >> 2, kq = (q & 3) * 4;
-      const int k = kt * kBK + kq;
+      const int row = q / A_Q, kq = (q % A_Q) * 4;
+      const int k = kt * BK + kq;
       if constexpr (MODE == Mode::IP) {
         const int r = i0 + row;
-        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        v4f v = {0.f, 0.f, 0.f, 0.f};
         if (r < g.m) {
           const float* src = A + (int64_t)r * g.lda;
           if (g.a_vec4) {
-            if (k < g.k_valid) v = *reinterpret_cast<const float4*>(src + k);
+            if (k < g.k_valid) v = *reinterpret_cast<const v4f*>(src + k);
           } else {
             v.x = (k + 0 < g.k_valid) ? src[k + 0] : 0.f;
             v.y = (k + 1 < g.k_valid) ? src[k + 1] : 0.f;
@@ -120,7 +132,7 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_kernel(GemmArgs g) {
         }
         ra[u] = v;
       } else {
-        ra[u] = *reinterpret_cast<const float4*>(A + (int64_t)(i0 + row) * g.lda + k);
+        ra[u] = *reinterpret_cast<const v4f*>(A + (int64_t)(i0 + row) * g.lda + k);
       }
     }
   };
@@ -128,19 +140,18 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_kernel(GemmArgs g) {
 #pragma unroll
     for (int u = 0; u < A_LD; ++u) {
       const int q = tid + u * kThreads;
-      const int row = q >> 2, kq = (q & 3) * 4;
-      *reinterpret_cast<float4*>(&As[buf][row * AS + kq]) = ra[u];
+      const int row = q / A_Q, kq = (q % A_Q) * 4;
+      *reinterpret_cast<v4f*>(&As[buf][row * AS + kq]) = ra[u];
     }
   };
 
   // ---- B loader.
   // Conv: im2col gather; thread owns pixel column jj = tid % BN and KPT
-  // consecutive k (KPT = 16*BN/256).  Wino: V rows [k][j] are contiguous in j
-  // -> float4 loads.  IP: W [j][k] rows, like A.
-  constexpr int KPT = kBK * BN / kThreads;
-  constexpr int B_LD4 = BN * 4 / kThreads;  // float4 per thread (Wino / IP)
+  // consecutive k (KPT = BK*BN/256).  IP: W [j][k] rows, like A.
+  constexpr int KPT = BK * BN / kThreads;
+  constexpr int B_LD4 = BN * A_Q / kThreads;  // float4 per thread (IP)
   float rb[(MODE == Mode::Conv) ? KPT : 1];
-  float4 rb4[(MODE == Mode::Conv) ? 1 : B_LD4];
+  v4f rb4[(MODE == Mode::Conv) ? 1 : B_LD4];
 
   // Conv per-thread pixel state (fixed for the whole block).
   const int jj = tid % BN;
@@ -165,7 +176,7 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_kernel(GemmArgs g) {
 
   auto load_b = [&](int kt) {
     if constexpr (MODE == Mode::Conv) {
-      const int kbase = kt * kBK + kg * KPT;
+      const int kbase = kt * BK + kg * KPT;
 #pragma unroll
       for (int u = 0; u < KPT; ++u) {
         const int t = g.ktab[kbase + u];  // wave-uniform
@@ -175,21 +186,12 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_kernel(GemmArgs g) {
         rb[u] = buf_load_f32(img_rs, in ? (uint32_t)((((img_plane0 + c) * g.H + y) * g.W + x) * (int)sizeof(float))
                                         : kBufOOB);
       }
-    } else if constexpr (MODE == Mode::Wino) {
-#pragma unroll
-      for (int u = 0; u < B_LD4; ++u) {
-        const int q = tid + u * kThreads;
-        const int row = q / (BN / 4), jq = (q % (BN / 4)) * 4;
-        rb4[u] = *reinterpret_cast<const float4*>(
-            B + (int64_t)(kt * kBK + row) * g.ldb + j0 + jq);
-      }
     } else {
 #pragma unroll
       for (int u = 0; u < B_LD4; ++u) {
         const int q = tid + u * kThreads;
-        const int row = q >> 2, kq = (q & 3) * 4;
-        rb4[u] = *reinterpret_cast<const float4*>(
-            B + (int64_t)(j0 + row) * g.ldb + kt * kBK + kq);
+        const int row = q / A_Q, kq = (q % A_Q) * 4;
+        rb4[u] = *reinterpret_cast<const v4f*>(B + (int64_t)(j0 + row) * g.ldb + kt * BK + kq);
       }
     }
   };
@@ -197,21 +199,13 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_kernel(GemmArgs g) {
     if constexpr (MODE == Mode::Conv) {
 #pragma unroll
       for (int u = 0; u < KPT; u += 4)
-        *reinterpret_cast<float4*>(&Bs[buf][jj * AS + kg * KPT + u]) =
-            make_float4(rb[u], rb[u + 1], rb[u + 2], rb[u + 3]);
-    } else if constexpr (MODE == Mode::Wino) {
-#pragma unroll
-      for (int u = 0; u < B_LD4; ++u) {
-        const int q = tid + u * kThreads;
-        const int row = q / (BN / 4), jq = (q % (BN / 4)) * 4;
-        *reinterpret_cast<float4*>(&Bs[buf][row * BS_ROW + jq]) = rb4[u];
-      }
+        *reinterpret_cast<v4f*>(&Bs[buf][jj * AS + kg * KPT + u]) = v4f{rb[u], rb[u + 1], rb[u + 2], rb[u + 3]};
     } else {
 #pragma unroll
       for (int u = 0; u < B_LD4; ++u) {
         const int q = tid + u * kThreads;
-        const int row = q >> 2, kq = (q & 3) * 4;
-        *reinterpret_cast<float4*>(&Bs[buf][row * AS + kq]) = rb4[u];
+        const int row = q / A_Q, kq = (q % A_Q) * 4;
+        *reinterpret_cast<v4f*>(&Bs[buf][row * AS + kq]) = rb4[u];
       }
     }
   };
@@ -225,36 +219,34 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_kernel(GemmArgs g) {
       for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.f;
 
   auto compute = [&](int buf) {
-    float af[TM][8], bf[TN][8];
 #pragma unroll
-    for (int a = 0; a < TM; ++a) {
-      const float* pa = &As[buf][(wm * (BM / 2) + a * 32 + li) * AS + lh * 8];
-      const float4 x0 = *reinterpret_cast<const float4*>(pa);
-      const float4 x1 = *reinterpret_cast<const float4*>(pa + 4);
-      af[a][0] = x0.x; af[a][1] = x0.y; af[a][2] = x0.z; af[a][3] = x0.w;
-      af[a][4] = x1.x; af[a][5] = x1.y; af[a][6] = x1.z; af[a][7] = x1.w;
-    }
+    for (int kc = 0; kc < BK; kc += kBK) {
+      float af[TM][8], bf[TN][8];
 #pragma unroll
-    for (int b = 0; b < TN; ++b) {
-      const int col = wn * (BN / 2) + b * 32 + li;
-      if constexpr (B_KJ) {
+      for (int a = 0; a < TM; ++a) {
+        const float* pa = &As[buf][(wm * (BM / 2) + a * 32 + li) * AS + kc + lh * 8];
+        const v4f x0 = *reinterpret_cast<const v4f*>(pa);
+        const v4f x1 = *reinterpret_cast<const v4f*>(pa + 4);
+        af[a][0] = x0.x; af[a][1] = x0.y; af[a][2] = x0.z; af[a][3] = x0.w;
+        af[a][4] = x1.x; af[a][5] = x1.y; af[a][6] = x1.z; af[a][7] = x1.w;
+      }
 #pragma unroll
-        for (int s = 0; s < 8; ++s) bf[b][s] = Bs[buf][(lh * 8 + s) * BS_ROW + col];
-      } else {
-        const float* pb = &Bs[buf][col * AS + lh * 8];
-        const float4 y0 = *reinterpret_cast<const float4*>(pb);
-        const float4 y1 = *reinterpret_cast<const float4*>(pb + 4);
+      for (int b = 0; b < TN; ++b) {
+        const int col = wn * (BN / 2) + b * 32 + li;
+        const float* pb = &Bs[buf][col * AS + kc + lh * 8];
+        const v4f y0 = *reinterpret_cast<const v4f*>(pb);
+        const v4f y1 = *reinterpret_cast<const v4f*>(pb + 4);
         bf[b][0] = y0.x; bf[b][1] = y0.y; bf[b][2] = y0.z; bf[b][3] = y0.w;
         bf[b][4] = y1.x; bf[b][5] = y1.y; bf[b][6] = y1.z; bf[b][7] = y1.w;
       }
+#pragma unroll
+      for (int s = 0; s < 8; ++s)
+#pragma unroll
+        for (int a = 0; a < TM; ++a)
+#pragma unroll
+          for (int b = 0; b < TN; ++b)
+            acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[a][s], bf[b][s], acc[a][b], 0, 0, 0);
     }
-#pragma unroll
-    for (int s = 0; s < 8; ++s)
-#pragma unroll
-      for (int a = 0; a < TM; ++a)
-#pragma unroll
-        for (int b = 0; b < TN; ++b)
-          acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[a][s], bf[b][s], acc[a][b], 0, 0, 0);
   };
 
   if (kt_begin < kt_end) {
@@ -301,15 +293,6 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_kernel(GemmArgs g) {
             g.d[o] = apply_act(v, g.act);
           }
         }
-    } else if constexpr (MODE == Mode::Wino) {
-      float* D = g.d + (int64_t)batch * g.d_batch;
-#pragma unroll
-      for (int a = 0; a < TM; ++a)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int i = i0 + wm * (BM / 2) + a * 32 + (r & 3) + 8 * (r >> 2) + 4 * lh;
-          D[(int64_t)i * g.ldd + j] = acc[a][b][r];
-        }
     } else {
       if (j >= g.n) continue;
 #pragma unroll
@@ -341,9 +324,9 @@ __global__ void ip_splitk_reduce(const float* part, const float* bias,
   out[idx] = apply_act(s + bias[j], act);
 }
 
-template <int BM, int BN, Mode MODE>
+template <int BM, int BN, Mode MODE, int BK = kBK>
 int launch(const GemmArgs& g, dim3 grid, hipStream_t s, const char* name) {
-  NHIP_LAUNCH(name, (gemm_f32_kernel<BM, BN, MODE>), grid, dim3(kThreads), 0, s, g);
+  NHIP_LAUNCH(name, (gemm_f32_kernel<BM, BN, BK, MODE>), grid, dim3(kThreads), 0, s, g);
   return check_launch(name);
 }
 
@@ -390,31 +373,6 @@ int launch_conv_igemm_f32(const nhip_conv_plan* p, const float* in,
   if ((int64_t)mt64 * nt128 >= target)
     return launch<64, 128, Mode::Conv>(g, dim3(nt128, mt64), s, "conv_igemm_f32<64,128>");
   return launch<64, 64, Mode::Conv>(g, dim3(nt64, mt64), s, "conv_igemm_f32<64,64>");
-}
-
-// Winograd batched GEMM: M[xi][m_pad][t_pad] = U[xi][m_pad][c_pad] * V[xi][c_pad][t_pad].
-int launch_wino_gemm(const float* U, const float* V, float* M, int m_pad,
-                     int c_pad, int t_pad, hipStream_t s) {
-  GemmArgs g{};
-  g.a = U;
-  g.a_batch = (int64_t)m_pad * c_pad;
-  g.lda = c_pad;
-  g.m = m_pad;
-  g.b = V;
-  g.b_batch = (int64_t)c_pad * t_pad;
-  g.ldb = t_pad;
-  g.n = t_pad;
-  g.kdim = c_pad;
-  g.d = M;
-  g.d_batch = (int64_t)m_pad * t_pad;
-  g.ldd = t_pad;
-  g.splits = 1;
-  const int64_t target = 2LL * cu_count();
-  if (m_pad % 128 == 0 && 36LL * (m_pad / 128) * (t_pad / 128) >= target)
-    return launch<128, 128, Mode::Wino>(g, dim3(t_pad / 128, m_pad / 128, 36), s, "wino_gemm<128,128>");
-  if (36LL * (m_pad / 64) * (t_pad / 128) >= target)
-    return launch<64, 128, Mode::Wino>(g, dim3(t_pad / 128, m_pad / 64, 36), s, "wino_gemm<64,128>");
-  return launch<64, 64, Mode::Wino>(g, dim3(t_pad / 64, m_pad / 64, 36), s, "wino_gemm<64,64>");
 }
 
 // ------------------------------- InnerProduct -----------------------------

@@ -144,6 +144,14 @@ int launch_conv_winograd_f32(const nhip_conv_plan* p, const float* in,
 uint64_t conv_winograd_f32_workspace(const nhip_conv_plan* p, int n, int oh,
                                      int ow);
 int winograd_prepack_weights(nhip_conv_plan* p, const float* weight);
+
+// Tile shape and K split of the Winograd batched GEMM (gemm_f32.hip).
+struct WinoGemmCfg {
+  int bm, bn, bk, splits;
+};
+WinoGemmCfg wino_gemm_config(int m_pad, int c_pad, int t_pad);
+int launch_wino_gemm(const float* U, const float* V, float* M, int m_pad, int c_pad, int t_pad,
+                     const WinoGemmCfg& cfg, hipStream_t s);
 int launch_conv_int8(const nhip_conv_plan* p, const void* in, int in_is_i8,
                      void* out, int n, int h, int w, int oh, int ow, void* ws,
                      uint64_t ws_bytes, hipStream_t s);

@@ -23,8 +23,6 @@
 #include "nhip_internal.h"
 
 namespace nhip {
-int launch_wino_gemm(const float* U, const float* V, float* M, int m_pad,
-                     int c_pad, int t_pad, hipStream_t s);
 int launch_conv_winograd_fused(const nhip_conv_plan* p, const float* in, const float* residual,
                                float* out, int n, int h, int w, int oh, int ow, hipStream_t s);
 
@@ -128,9 +126,11 @@ __global__ __launch_bounds__(256) void wino_input_transform(
   }
 }
 
-// Thread (k, t): 36 GEMM outputs -> 4x4 output tile, + bias (+ residual), act.
+// Thread (k, t): 36 GEMM outputs (the sum of S K-partial buffers) -> 4x4
+// output tile, + bias (+ residual), act.
+template <int S>
 __global__ __launch_bounds__(256) void wino_output_transform(
-    const float* __restrict__ M, const float* __restrict__ bias,
+    const float* __restrict__ M, int64_t split_stride, const float* __restrict__ bias,
     const float* __restrict__ residual, float* __restrict__ out, int K, int OH,
     int OW, int th, int tw, int T, int t_pad, int m_pad, int act) {
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -143,7 +143,12 @@ __global__ __launch_bounds__(256) void wino_output_transform(
 #pragma unroll
   for (int i = 0; i < 6; ++i)
 #pragma unroll
-    for (int j = 0; j < 6; ++j) m[i][j] = min[(i * 6 + j) * plane_stride];
+    for (int j = 0; j < 6; ++j) {
+      float v = min[(i * 6 + j) * plane_stride];
+#pragma unroll
+      for (int sp = 1; sp < S; ++sp) v += min[sp * split_stride + (i * 6 + j) * plane_stride];
+      m[i][j] = v;
+    }
   // tmp = A^T m (4x6)
   float tmp[4][6];
 #pragma unroll
@@ -222,7 +227,8 @@ uint64_t conv_winograd_f32_workspace(const nhip_conv_plan* p, int n, int oh, int
   if (!unfused_requested()) return 0;
   const int th = (int)ceil_div(oh, 4), tw = (int)ceil_div(ow, 4);
   const int64_t t_pad = round_up((int64_t)n * th * tw, 128);
-  return (uint64_t)36 * t_pad * (p->c_pad + p->m_pad) * sizeof(float);
+  const WinoGemmCfg cfg = wino_gemm_config(p->m_pad, p->c_pad, (int)t_pad);
+  return (uint64_t)36 * t_pad * (p->c_pad + (int64_t)cfg.splits * p->m_pad) * sizeof(float);
 }
 
 int launch_conv_winograd_f32(const nhip_conv_plan* p, const float* in,
@@ -245,12 +251,25 @@ int launch_conv_winograd_f32(const nhip_conv_plan* p, const float* in,
                        p->g.pt, p->g.pl);
     NHIP_TRY(check_launch("wino_input_transform"));
   }
-  NHIP_TRY(launch_wino_gemm(p->weight, V, M, ws_.m_pad, ws_.c_pad, ws_.t_pad, s));
+  const WinoGemmCfg cfg = wino_gemm_config(ws_.m_pad, ws_.c_pad, ws_.t_pad);
+  NHIP_TRY(launch_wino_gemm(p->weight, V, M, ws_.m_pad, ws_.c_pad, ws_.t_pad, cfg, s));
   {
     const int64_t total = (int64_t)p->g.k * ws_.t;
-    NHIP_LAUNCH("wino_output_transform", wino_output_transform, dim3((unsigned)ceil_div(total, 256)), dim3(256), 0, s,
-                       M, p->bias, residual, out, p->g.k, oh, ow, ws_.th, ws_.tw, ws_.t,
-                       ws_.t_pad, ws_.m_pad, p->g.act);
+    const int64_t split_stride = (int64_t)36 * ws_.m_pad * ws_.t_pad;
+    const dim3 grid((unsigned)ceil_div(total, 256));
+#define NHIP_WINO_OUT(S_)                                                                                    \
+  case S_:                                                                                                   \
+    NHIP_LAUNCH("wino_output_transform", wino_output_transform<S_>, grid, dim3(256), 0, s, M, split_stride, \
+                p->bias, residual, out, p->g.k, oh, ow, ws_.th, ws_.tw, ws_.t, ws_.t_pad, ws_.m_pad, p->g.act); \
+    break;
+    switch (cfg.splits) {
+      NHIP_WINO_OUT(1)
+      NHIP_WINO_OUT(2)
+      NHIP_WINO_OUT(4)
+      default:
+        return fail(NHIP_STATUS_CONSTRAINT_VIOLATION, "winograd conv: unsupported split count");
+    }
+#undef NHIP_WINO_OUT
     NHIP_TRY(check_launch("wino_output_transform"));
   }
   return ok();
