@@ -21,6 +21,8 @@
 // (kh, kw, c) — the OHWI order the reference itself transposes the weights
 // to (NCNNToTosa.cpp:1168-1176).
 #include <cmath>
+#include <cstdio>
+#include <cstdlib>
 #include <vector>
 
 #include "nhip_internal.h"
@@ -29,8 +31,7 @@ namespace nhip {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kBK = 64;       // bytes of k per LDS stage = 2 MFMA steps
-constexpr int kRow = kBK + 16;  // LDS row stride (bytes), keeps b128 reads conflict-free
+constexpr int kRow = 64 + 16;  // quantize tile row stride (bytes)
 
 __device__ __forceinline__ int8_t quantize_i8(float x, float scale) {
 #pragma clang fp contract(off)
@@ -43,39 +44,47 @@ __device__ __forceinline__ int8_t quantize_i8(float x, float scale) {
 }
 
 // x [N][C][HW] (fp32 or int8) -> y [N][HW][c_pad] int8, zero channel padding.
-// Block: 64 pixels of one image; loops over 64-channel slabs through LDS.
+// Workgroup = 64 pixels x one 64-channel slab of one image (grid x: pixel
+// blocks, y: slabs, z: images); each thread issues its 16 loads before any
+// LDS write, then the slab leaves as 16-byte rows.
 __global__ __launch_bounds__(kThreads) void quantize_nchw_to_nhwc(
     const void* __restrict__ x, int in_is_i8, int8_t* __restrict__ y, int C,
     int HW, int c_pad, float scale) {
   __shared__ __attribute__((aligned(16))) int8_t tile[64 * kRow];
-  const int img = blockIdx.y;
+  const int img = blockIdx.z;
   const int p0 = blockIdx.x * 64;
+  const int c0 = blockIdx.y * 64;
   const int tid = threadIdx.x;
   const int px = tid & 63, cc = tid >> 6;
   const int p = p0 + px;
   const float* xf = static_cast<const float*>(x) + (int64_t)img * C * HW;
   const int8_t* xi = static_cast<const int8_t*>(x) + (int64_t)img * C * HW;
-  for (int c0 = 0; c0 < c_pad; c0 += 64) {
-#pragma unroll 4
+  int8_t v[16];
+  if (in_is_i8) {
+#pragma unroll
     for (int u = 0; u < 16; ++u) {
-      const int cl = cc + 4 * u;
-      const int c = c0 + cl;
-      int8_t v = 0;
-      if (c < C && p < HW) {
-        const int64_t off = (int64_t)c * HW + p;
-        v = in_is_i8 ? xi[off] : quantize_i8(xf[off], scale);
-      }
-      tile[px * kRow + cl] = v;
+      const int c = c0 + cc + 4 * u;
+      v[u] = (c < C && p < HW) ? xi[(int64_t)c * HW + p] : (int8_t)0;
     }
-    __syncthreads();
-    const int wp = tid >> 2, chunk = tid & 3;
-    const int pw = p0 + wp;
-    const int cw = c0 + chunk * 16;
-    if (pw < HW && cw < c_pad)
-      *reinterpret_cast<int4*>(y + ((int64_t)img * HW + pw) * c_pad + cw) =
-          *reinterpret_cast<const int4*>(&tile[wp * kRow + chunk * 16]);
-    __syncthreads();
+  } else {
+    float f[16];
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      const int c = c0 + cc + 4 * u;
+      f[u] = (c < C && p < HW) ? xf[(int64_t)c * HW + p] : 0.0f;
+    }
+#pragma unroll
+    for (int u = 0; u < 16; ++u) v[u] = quantize_i8(f[u], scale);
   }
+#pragma unroll
+  for (int u = 0; u < 16; ++u) tile[px * kRow + cc + 4 * u] = v[u];
+  __syncthreads();
+  const int wp = tid >> 2, chunk = tid & 3;
+  const int pw = p0 + wp;
+  const int cw = c0 + chunk * 16;
+  if (pw < HW && cw < c_pad)
+    *reinterpret_cast<int4*>(y + ((int64_t)img * HW + pw) * c_pad + cw) =
+        *reinterpret_cast<const int4*>(&tile[wp * kRow + chunk * 16]);
 }
 
 struct Int8Args {
@@ -95,62 +104,84 @@ struct Int8Args {
 };
 
 // D[i = out channel][j = pixel] over the (kh, kw, c) reduction.
-template <int BM, int BN>
+// One workgroup = 4 waves (2x2), each a (BM/2) x (BN/2) tile of 32x32 blocks
+// with v_mfma_i32_32x32x32_i8.  K advances BK bytes per stage through two LDS
+// buffers; global loads run two stages ahead (stage k multiplies while stage
+// k+1 waits in registers and stage k+2 is in flight), and the loop body is
+// straight-line so the accumulators stay in one register range.
+template <int BM, int BN, int BK>
 __global__ __launch_bounds__(kThreads) void conv_int8_kernel(Int8Args g) {
   constexpr int TM = BM / 64, TN = BN / 64;
-  __shared__ __attribute__((aligned(16))) int8_t As[2][BM * kRow];
-  __shared__ __attribute__((aligned(16))) int8_t Bs[2][BN * kRow];
+  constexpr int ROW = BK + 16;              // LDS row stride (bytes): conflict-free b128 reads
+  constexpr int CH = BK / 16;               // 16-byte chunks per row per stage
+  constexpr int A_LD = BM * CH / kThreads;  // 16-byte loads per thread per stage
+  constexpr int B_LD = BN * CH / kThreads;
+  static_assert(A_LD >= 1 && B_LD >= 1, "tile too small for the workgroup");
+  constexpr int ES = BN + 16;  // LDS row stride of the staged epilogue tile (elements)
+  constexpr int OPER = 2 * (BM + BN) * ROW;
+  constexpr int EPI = BM * ES * 4;
+  __shared__ __attribute__((aligned(16))) int8_t smem[OPER > EPI ? OPER : EPI];
+  // operand buffers: A[buf] = smem + buf*BM*ROW, B[buf] = smem + 2*BM*ROW + buf*BN*ROW
+  auto As = [&](int buf) { return smem + buf * BM * ROW; };
+  auto Bs = [&](int buf) { return smem + 2 * BM * ROW + buf * BN * ROW; };
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
   const int li = lane & 31, lh = lane >> 5;
   const int j0 = blockIdx.x * BN, i0 = blockIdx.y * BM;
 
-  // A: BM rows x 4 chunks of 16B.
-  constexpr int A_LD = BM * 4 / kThreads;
-  int4 ra[A_LD];
-  // B: BN pixels x 4 chunks; CPT chunks per thread.
-  constexpr int CPT = 4 * BN / kThreads;
-  int4 rb[CPT];
-  const int jj = tid % BN;
-  const int kg = __builtin_amdgcn_readfirstlane(tid / BN);
-  const int p = j0 + jj;
-  const bool pix_ok = p < g.npix;
-  const int pp = pix_ok ? p : 0;
-  const int img = pp / g.OHW;
-  const int rem = pp - img * g.OHW;
-  const int oh = rem / g.OW, ow = rem - (rem / g.OW) * g.OW;
-  const int iy0 = oh * g.sh - g.pt, ix0 = ow * g.sw - g.pl;
+  // B gather: load u of a thread covers pixel jj[u] = (tid + u*256) / CH and
+  // 16-byte chunk tid % CH of the stage, so CH consecutive lanes read one
+  // pixel's contiguous channel run (one cache line per CH lanes, not one per
+  // lane).  The pixel geometry of each load is fixed for the whole K loop.
+  const int chl = tid % CH;
+  int iy0[B_LD], ix0[B_LD], ipix0[B_LD];
+  bool pok[B_LD];
+#pragma unroll
+  for (int u = 0; u < B_LD; ++u) {
+    const int p = j0 + (tid + u * kThreads) / CH;
+    pok[u] = p < g.npix;
+    const int pp = pok[u] ? p : 0;
+    const int img = pp / g.OHW;
+    const int rem = pp - img * g.OHW;
+    const int oh = rem / g.OW, ow = rem - oh * g.OW;
+    iy0[u] = oh * g.sh - g.pt;
+    ix0[u] = ow * g.sw - g.pl;
+    ipix0[u] = img * g.H;
+  }
   // the whole NHWC scratch image is one wave-uniform buffer resource
   const __amdgpu_buffer_rsrc_t img_rs = make_rsrc(g.x, g.x_bytes);
-  const int img_pix0 = img * g.H;
 
-  auto load = [&](int kt) {
+  struct Stage {
+    v4i a[A_LD];
+    v4i b[B_LD];
+  };
+  auto gload = [&](Stage& st, int kt) {
 #pragma unroll
     for (int u = 0; u < A_LD; ++u) {
       const int q = tid + u * kThreads;
-      const int row = q >> 2, ch = q & 3;
-      ra[u] = *reinterpret_cast<const int4*>(g.w + (int64_t)(i0 + row) * g.kred_pad + kt * kBK + ch * 16);
+      const int row = q / CH, ch = q % CH;
+      st.a[u] = *reinterpret_cast<const v4i*>(g.w + (int64_t)(i0 + row) * g.kred_pad + kt * BK + ch * 16);
     }
+    const int t = g.ktab[kt * CH + chl];
+    const int c0 = t >> 16, dy = (t >> 8) & 255, dx = t & 255;
 #pragma unroll
-    for (int u = 0; u < CPT; ++u) {
-      const int chunk = kt * 4 + kg * CPT + u;
-      const int t = g.ktab[chunk];  // wave-uniform
-      const int c0 = t >> 16, dy = (t >> 8) & 255, dx = t & 255;
-      const int y = iy0 + dy, x = ix0 + dx;
-      const bool in = pix_ok && c0 < g.c_pad && (unsigned)y < (unsigned)g.H && (unsigned)x < (unsigned)g.W;
-      rb[u] = buf_load_b128(img_rs, in ? (uint32_t)(((img_pix0 + y) * g.W + x) * g.c_pad + c0) : kBufOOB);
+    for (int u = 0; u < B_LD; ++u) {
+      const int y = iy0[u] + dy, x = ix0[u] + dx;
+      const bool in = pok[u] && c0 < g.c_pad && (unsigned)y < (unsigned)g.H && (unsigned)x < (unsigned)g.W;
+      st.b[u] = __builtin_bit_cast(
+          v4i, buf_load_b128(img_rs, in ? (uint32_t)(((ipix0[u] + y) * g.W + x) * g.c_pad + c0) : kBufOOB));
     }
   };
-  auto store = [&](int buf) {
+  auto lstore = [&](const Stage& st, int buf) {
 #pragma unroll
     for (int u = 0; u < A_LD; ++u) {
       const int q = tid + u * kThreads;
-      const int row = q >> 2, ch = q & 3;
-      *reinterpret_cast<int4*>(&As[buf][row * kRow + ch * 16]) = ra[u];
+      const int row = q / CH, ch = q % CH;
+      *reinterpret_cast<v4i*>(As(buf) + row * ROW + ch * 16) = st.a[u];
     }
 #pragma unroll
-    for (int u = 0; u < CPT; ++u)
-      *reinterpret_cast<int4*>(&Bs[buf][jj * kRow + (kg * CPT + u) * 16]) = rb[u];
+    for (int u = 0; u < B_LD; ++u)
+      *reinterpret_cast<v4i*>(Bs(buf) + ((tid + u * kThreads) / CH) * ROW + chl * 16) = st.b[u];
   };
 
   v16i acc[TM][TN];
@@ -161,48 +192,64 @@ __global__ __launch_bounds__(kThreads) void conv_int8_kernel(Int8Args g) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[a][b][r] = 0;
 
-  const int nk = g.kred_pad / kBK;
-  load(0);
-  store(0);
-  __syncthreads();
-  for (int kt = 0; kt < nk; ++kt) {
-    const int buf = kt & 1;
-    const bool more = kt + 1 < nk;
-    if (more) load(kt + 1);
+  auto compute = [&](int buf) {
 #pragma unroll
-    for (int s = 0; s < 2; ++s) {
+    for (int s = 0; s < BK / 32; ++s) {
       v4i af[TM], bf[TN];
 #pragma unroll
       for (int a = 0; a < TM; ++a)
-        af[a] = *reinterpret_cast<const v4i*>(&As[buf][(wm * (BM / 2) + a * 32 + li) * kRow + s * 32 + lh * 16]);
+        af[a] = *reinterpret_cast<const v4i*>(As(buf) + (wm * (BM / 2) + a * 32 + li) * ROW + s * 32 + lh * 16);
 #pragma unroll
       for (int b = 0; b < TN; ++b)
-        bf[b] = *reinterpret_cast<const v4i*>(&Bs[buf][(wn * (BN / 2) + b * 32 + li) * kRow + s * 32 + lh * 16]);
+        bf[b] = *reinterpret_cast<const v4i*>(Bs(buf) + (wn * (BN / 2) + b * 32 + li) * ROW + s * 32 + lh * 16);
 #pragma unroll
       for (int a = 0; a < TM; ++a)
 #pragma unroll
         for (int b = 0; b < TN; ++b)
           acc[a][b] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[a], bf[b], acc[a][b], 0, 0, 0);
     }
-    if (more) store(buf ^ 1);
+  };
+
+  const int n = g.kred_pad / BK;
+  {
+    Stage s0, s1;
+    gload(s0, 0);
+    if (n > 1) gload(s1, 1);
+    lstore(s0, 0);
     __syncthreads();
+    int i = 0;
+    for (; i + 1 < n; i += 2) {
+      if (i + 2 < n) gload(s0, i + 2);
+      compute(0);
+      lstore(s1, 1);
+      __syncthreads();
+      if (i + 3 < n) gload(s1, i + 3);
+      compute(1);
+      if (i + 2 < n) lstore(s0, 0);
+      __syncthreads();
+    }
+    if (i < n) compute(0);
   }
 
-  // Epilogue: register r of lane l holds row (r%4)+8*(r/4)+4*(l/32), column l%32.
+  // Epilogue.  Register r of lane l holds row (r%4)+8*(r/4)+4*(l/32), column
+  // l%32.  The exact fp32 sequence runs per element, the results are staged
+  // in LDS as [i][j] (over the operand buffers, free after the barrier),
+  // and each thread then writes 16 consecutive pixels of one output channel
+  // with one vector store (bytes or floats), falling back to element stores
+  // where the run crosses an image or the tile edge or is misaligned.
+  __syncthreads();
+  const bool q8 = g.term > 100;
+  float* tf = reinterpret_cast<float*>(smem);
+  int8_t* tq = smem;
 #pragma unroll
   for (int b = 0; b < TN; ++b) {
-    const int j = j0 + wn * (BN / 2) + b * 32 + li;
-    if (j >= g.npix) continue;
-    const int im = j / g.OHW;
-    const int rm = j - im * g.OHW;
-    const int64_t obase = (int64_t)im * g.m * g.OHW + rm;
+    const int jl = wn * (BN / 2) + b * 32 + li;
 #pragma unroll
     for (int a = 0; a < TM; ++a)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int i = i0 + wm * (BM / 2) + a * 32 + (r & 3) + 8 * (r >> 2) + 4 * lh;
-        if (i >= g.m) continue;
-        const int64_t o = obase + (int64_t)i * g.OHW;
+        const int il = wm * (BM / 2) + a * 32 + (r & 3) + 8 * (r >> 2) + 4 * lh;
+        const int i = i0 + il;
         float f;
         {
 #pragma clang fp contract(off)
@@ -210,15 +257,48 @@ __global__ __launch_bounds__(kThreads) void conv_int8_kernel(Int8Args g) {
           f = f * g.recip[i];
           f = f + g.bias[i];
         }
-        if (g.term > 100) {
+        if (q8) {
           int8_t q = quantize_i8(f, g.os);
           if (g.act == NHIP_ACT_RELU && q < 0) q = 0;
-          static_cast<int8_t*>(g.out)[o] = q;
+          tq[il * ES + jl] = q;
         } else {
           if (g.act == NHIP_ACT_RELU) f = f < 0.0f ? 0.0f : f;
-          static_cast<float*>(g.out)[o] = f;
+          tf[il * ES + jl] = f;
         }
       }
+  }
+  __syncthreads();
+  constexpr int RUNS = BN / 16;  // 16-pixel runs per row
+  for (int q = tid; q < BM * RUNS; q += kThreads) {
+    const int il = q / RUNS, jl = (q % RUNS) * 16;
+    const int i = i0 + il, j = j0 + jl;
+    if (i >= g.m || j >= g.npix) continue;
+    const int im = j / g.OHW, rm = j - im * g.OHW;
+    const int64_t o = ((int64_t)im * g.m + i) * g.OHW + rm;
+    const bool whole = j + 16 <= g.npix && rm + 16 <= g.OHW && (o & 15) == 0;
+    if (q8) {
+      int8_t* dst = static_cast<int8_t*>(g.out);
+      if (whole) {
+        *reinterpret_cast<v4i*>(dst + o) = *reinterpret_cast<const v4i*>(&tq[il * ES + jl]);
+      } else {
+        for (int e = 0; e < 16 && j + e < g.npix; ++e) {
+          const int je = j + e, ie = je / g.OHW;
+          dst[((int64_t)ie * g.m + i) * g.OHW + (je - ie * g.OHW)] = tq[il * ES + jl + e];
+        }
+      }
+    } else {
+      float* dst = static_cast<float*>(g.out);
+      if (whole) {
+#pragma unroll
+        for (int e = 0; e < 16; e += 4)
+          *reinterpret_cast<v4f*>(dst + o + e) = *reinterpret_cast<const v4f*>(&tf[il * ES + jl + e]);
+      } else {
+        for (int e = 0; e < 16 && j + e < g.npix; ++e) {
+          const int je = j + e, ie = je / g.OHW;
+          dst[((int64_t)ie * g.m + i) * g.OHW + (je - ie * g.OHW)] = tf[il * ES + jl + e];
+        }
+      }
+    }
   }
 }
 
@@ -236,8 +316,9 @@ int launch_conv_int8(const nhip_conv_plan* p, const void* in, int in_is_i8,
     return fail(NHIP_STATUS_OUTPUT_CAPACITY_INSUFFICIENT,
                 "int8 conv: workspace of " + std::to_string(need) + " bytes required");
   int8_t* xq = static_cast<int8_t*>(ws);
-  NHIP_LAUNCH("quantize_nchw_to_nhwc", quantize_nchw_to_nhwc, dim3((unsigned)ceil_div((int64_t)h * w, 64), n), dim3(kThreads),
-                     0, s, in, in_is_i8, xq, p->g.c, h * w, p->c_pad, p->input_scale);
+  NHIP_LAUNCH("quantize_nchw_to_nhwc", quantize_nchw_to_nhwc,
+              dim3((unsigned)ceil_div((int64_t)h * w, 64), (unsigned)ceil_div(p->c_pad, 64), n), dim3(kThreads), 0, s,
+              in, in_is_i8, xq, p->g.c, h * w, p->c_pad, p->input_scale);
   NHIP_TRY(check_launch("quantize_nchw_to_nhwc"));
 
   Int8Args g{};
@@ -263,19 +344,34 @@ int launch_conv_int8(const nhip_conv_plan* p, const void* in, int in_is_i8,
   g.term = p->scale_term;
   g.act = p->g.act;
   g.out = out;
-  const int64_t target = 2LL * cu_count();
-  const int mt128 = (int)ceil_div(p->g.k, 128), mt64 = (int)ceil_div(p->g.k, 64);
-  const int nt128 = (int)ceil_div(g.npix, 128), nt64 = (int)ceil_div(g.npix, 64);
-  if (p->m_pad % 128 == 0 && (int64_t)mt128 * nt128 >= target) {
-    NHIP_LAUNCH("conv_int8<128,128>", (conv_int8_kernel<128, 128>), dim3(nt128, mt128), dim3(kThreads), 0, s, g);
-    return check_launch("conv_int8<128,128>");
+  // Tile shape: NHIP_INT8_TILE="bm,bn,bk" overrides (tuning switch, ignored
+  // when not valid for the plan).
+  int bm = p->m_pad % 128 == 0 ? 128 : 64, bn = 64, bk = 128;
+  if (const char* env = std::getenv("NHIP_INT8_TILE")) {
+    int a = 0, b = 0, c = 0;
+    if (std::sscanf(env, "%d,%d,%d", &a, &b, &c) == 3 && (a == 64 || a == 128) && (b == 64 || b == 128) &&
+        (c == 128 || c == 256) && p->m_pad % a == 0 && p->kred_pad % c == 0) {
+      bm = a;
+      bn = b;
+      bk = c;
+    }
   }
-  if ((int64_t)mt64 * nt128 >= target) {
-    NHIP_LAUNCH("conv_int8<64,128>", (conv_int8_kernel<64, 128>), dim3(nt128, mt64), dim3(kThreads), 0, s, g);
-    return check_launch("conv_int8<64,128>");
+  const dim3 grid((unsigned)ceil_div(g.npix, bn), (unsigned)(p->m_pad / bm));
+#define NHIP_INT8_CASE(BM_, BN_, BK_)                                                                     \
+  if (bm == BM_ && bn == BN_ && bk == BK_) {                                                              \
+    NHIP_LAUNCH("conv_int8<" #BM_ "," #BN_ "," #BK_ ">", (conv_int8_kernel<BM_, BN_, BK_>), grid, dim3(kThreads), \
+                0, s, g);                                                                                 \
+    return check_launch("conv_int8");                                                                     \
   }
-  NHIP_LAUNCH("conv_int8<64,64>", (conv_int8_kernel<64, 64>), dim3(nt64, mt64), dim3(kThreads), 0, s, g);
-  return check_launch("conv_int8<64,64>");
+  NHIP_INT8_CASE(64, 64, 128)
+  NHIP_INT8_CASE(128, 64, 128)
+  NHIP_INT8_CASE(64, 128, 128)
+  NHIP_INT8_CASE(128, 128, 128)
+  NHIP_INT8_CASE(64, 64, 256)
+  NHIP_INT8_CASE(128, 64, 256)
+  NHIP_INT8_CASE(64, 128, 256)
+#undef NHIP_INT8_CASE
+  return fail(NHIP_STATUS_CONSTRAINT_VIOLATION, "int8 conv: bad tile config");
 }
 
 }  // namespace nhip

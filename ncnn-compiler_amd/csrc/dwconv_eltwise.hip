@@ -140,6 +140,93 @@ __global__ __launch_bounds__(256) void dwconv3x3s1_f32_kernel(DwArgs a) {
   }
 }
 
+// 3x3 depthwise, stride S (1 or 2), dilation 1, straight from global memory:
+// thread = 4 consecutive outputs of R rows of one plane.  Its input window
+// ((R-1)*S+3 rows x 3S+3 columns) comes in through raw buffer loads, the zero
+// halo through out-of-range offsets (no load waits on a branch); the overlap
+// between neighbouring windows is served by the caches.  VEC (W and OW
+// multiples of 4): each window row is one or two aligned 16-byte loads plus
+// halo words and the four outputs leave as one 16-byte store.  Summation
+// order of the CPU loop nest: acc = 0, += x*w over (kh, kw), then + bias.
+template <int S, int R, bool VEC>
+__global__ __launch_bounds__(256) void dw3x3_f32_kernel(DwArgs a, uint32_t x_bytes) {
+  constexpr int IR = (R - 1) * S + 3;  // input rows per thread
+  constexpr int IC = 3 * S + 3;        // input columns for 4 outputs
+  const int quads = (a.OW + 3) >> 2;
+  const int rblocks = (a.OH + R - 1) / R;
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int q = (int)(idx % quads);
+  const int64_t t2 = idx / quads;
+  const int rb = (int)(t2 % rblocks);
+  const int plane = (int)(t2 / rblocks);
+  if (plane >= a.planes) return;
+  const int c = plane % a.C;
+  float w[9];
+#pragma unroll
+  for (int t = 0; t < 9; ++t) w[t] = a.w[c * 9 + t];
+  const float b = a.bias[c];
+  const int ox0 = q * 4, oy0 = rb * R;
+  const int x0 = ox0 * S - a.pl, y0 = oy0 * S - a.pt;
+  const __amdgpu_buffer_rsrc_t rs = make_rsrc(a.x, x_bytes);
+  const int base = plane * a.H * a.W;  // < 2^31 elements (checked on the host)
+  float in[IR][IC];
+#pragma unroll
+  for (int i = 0; i < IR; ++i) {
+    const int y = y0 + i;
+    const bool yok = (unsigned)y < (unsigned)a.H;
+    if constexpr (VEC) {
+      // columns x0 .. x0+IC-1 = (4qS - 1) .. : word x0, then aligned vectors from x0+1
+      const int row = base + y * a.W;
+      const bool lok = yok && x0 >= 0;
+      in[i][0] = buf_load_f32(rs, lok ? (uint32_t)((row + x0) * 4) : kBufOOB);
+#pragma unroll
+      for (int v = 0; v < S; ++v) {
+        const v4f t = __builtin_bit_cast(v4f, buf_load_b128(rs, yok ? (uint32_t)((row + x0 + 1 + 4 * v) * 4) : kBufOOB));
+        in[i][1 + 4 * v] = t.x;
+        in[i][2 + 4 * v] = t.y;
+        in[i][3 + 4 * v] = t.z;
+        in[i][4 + 4 * v] = t.w;
+      }
+      if constexpr (S == 1) {
+        const bool rok = yok && x0 + 5 < a.W;
+        in[i][5] = buf_load_f32(rs, rok ? (uint32_t)((row + x0 + 5) * 4) : kBufOOB);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < IC; ++j) {
+        const int x = x0 + j;
+        const bool ok = yok && (unsigned)x < (unsigned)a.W;
+        in[i][j] = buf_load_f32(rs, ok ? (uint32_t)((base + y * a.W + x) * (int)sizeof(float)) : kBufOOB);
+      }
+    }
+  }
+  float* yp = a.y + (int64_t)plane * a.OH * a.OW;
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int oy = oy0 + r;
+    if (oy >= a.OH) break;
+    float o[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      float acc = 0.f;
+#pragma unroll
+      for (int i = 0; i < 3; ++i)
+#pragma unroll
+        for (int j = 0; j < 3; ++j) acc = acc + in[r * S + i][u * S + j] * w[i * 3 + j];
+      acc = acc + b;
+      if (a.act == NHIP_ACT_RELU) acc = acc < 0.f ? 0.f : acc;
+      o[u] = acc;
+    }
+    if constexpr (VEC) {
+      *reinterpret_cast<v4f*>(yp + oy * a.OW + ox0) = v4f{o[0], o[1], o[2], o[3]};
+    } else {
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        if (ox0 + u < a.OW) yp[oy * a.OW + ox0 + u] = o[u];
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------
 
 __device__ __forceinline__ int8_t quantize_i8(float x, float scale) {
@@ -387,6 +474,25 @@ int launch_dwconv_f32(const nhip_conv_plan* p, const float* in, float* out,
   a.pl = p->g.pl;
   a.planes = n * p->g.c;
   a.act = p->g.act;
+  const bool k3 = a.kh == 3 && a.kw == 3 && a.dh == 1 && a.dw == 1 && a.sh == a.sw && (a.sh == 1 || a.sh == 2);
+  const uint64_t x_bytes = (uint64_t)a.planes * h * w * sizeof(float);
+  if (k3 && x_bytes < (1ull << 31)) {
+    // VEC needs aligned rows and the left pad of 1 that the vector offsets assume
+    const bool vec = w % 4 == 0 && ow % 4 == 0 && a.pl == 1;
+    const int R = a.sh == 1 ? 4 : 2;
+    const int64_t threads = (int64_t)a.planes * ceil_div(oh, R) * ((ow + 3) / 4);
+    const dim3 grid((unsigned)ceil_div(threads, 256));
+#define NHIP_DW3(S_, R_, V_)                                                                            \
+  if (a.sh == S_ && vec == V_) {                                                                        \
+    NHIP_LAUNCH("dw3x3s" #S_ "_f32", (dw3x3_f32_kernel<S_, R_, V_>), grid, dim3(256), 0, s, a, (uint32_t)x_bytes); \
+    return check_launch("dw3x3_f32");                                                                   \
+  }
+    NHIP_DW3(1, 4, true)
+    NHIP_DW3(1, 4, false)
+    NHIP_DW3(2, 2, true)
+    NHIP_DW3(2, 2, false)
+#undef NHIP_DW3
+  }
   int64_t lds = 0;
   NHIP_TRY(dw_bands(a.planes, oh, ow, a.kh, a.kw, a.sh, a.dh, a.sw, a.dw, 4, &a.ppb, &a.ob, &a.ir, &a.lw, &a.bands,
                     &lds));
