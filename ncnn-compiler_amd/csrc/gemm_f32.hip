@@ -66,8 +66,13 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_kernel(GemmArgs g) {
   constexpr int TN = BN / 64;  // along j
   constexpr int AS = BK + kRowPad;                  // As[BM][AS], Bs[BN][AS]
   constexpr int B_ELEMS = BN * AS;
-  __shared__ __attribute__((aligned(16))) float As[2][BM * AS];
-  __shared__ __attribute__((aligned(16))) float Bs[2][B_ELEMS];
+  // One LDS array: two A and two B operand buffers, reused by the conv
+  // epilogue for a 64 x (BN+4) staging slab.
+  constexpr int OPER = 2 * (BM * AS + B_ELEMS);
+  constexpr int SLAB = (MODE == Mode::Conv) ? 64 * (BN + 4) : 0;
+  __shared__ __attribute__((aligned(16))) float smem[OPER > SLAB ? OPER : SLAB];
+  auto As = [&](int buf) { return smem + buf * BM * AS; };
+  auto Bs = [&](int buf) { return smem + 2 * BM * AS + buf * B_ELEMS; };
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -92,66 +97,29 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_kernel(GemmArgs g) {
   }
   const int j0 = bx * BN;
   const int i0 = by * BM;
-  int split = 0;
-  if constexpr (MODE == Mode::IP) split = bz;
+  const int split = bz;  // K split (grid z)
 
   const float* A = g.a;
   const float* B = g.b;
 
   const int nk_total = g.kdim / BK;
-  int kt_begin = 0, kt_end = nk_total;
-  if constexpr (MODE != Mode::Conv) {
-    const int per = (nk_total + g.splits - 1) / g.splits;
-    kt_begin = split * per;
-    kt_end = min(nk_total, kt_begin + per);
-  }
+  const int per = (nk_total + g.splits - 1) / g.splits;
+  const int kt_begin = min(nk_total, split * per);
+  const int kt_end = min(nk_total, kt_begin + per);
 
-  // ---- A loader: BM x BK floats = BM*BK/4 float4, BM*BK/1024 per thread.
+  // ---- operand stages.  A: BM x BK floats as float4 rows.  B (Conv): im2col
+  // gather, thread owns pixel column jj = tid % BN and KPT consecutive k
+  // (KPT = BK*BN/256).  B (IP): W [j][k] rows, like A.
   constexpr int A_Q = BK / 4;  // float4 per A row chunk
   constexpr int A_LD = BM * A_Q / kThreads;
-  v4f ra[A_LD];  // native vectors: HIP's float4 struct copies would stay in scratch
-  auto load_a = [&](int kt) {
-#pragma unroll
-    for (int u = 0; u < A_LD; ++u) {
-      const int q = tid + u * kThreads;
-      const int row = q / A_Q, kq = (q % A_Q) * 4;
-      const int k = kt * BK + kq;
-      if constexpr (MODE == Mode::IP) {
-        const int r = i0 + row;
-        v4f v = {0.f, 0.f, 0.f, 0.f};
-        if (r < g.m) {
-          const float* src = A + (int64_t)r * g.lda;
-          if (g.a_vec4) {
-            if (k < g.k_valid) v = *reinterpret_cast<const v4f*>(src + k);
-          } else {
-            v.x = (k + 0 < g.k_valid) ? src[k + 0] : 0.f;
-            v.y = (k + 1 < g.k_valid) ? src[k + 1] : 0.f;
-            v.z = (k + 2 < g.k_valid) ? src[k + 2] : 0.f;
-            v.w = (k + 3 < g.k_valid) ? src[k + 3] : 0.f;
-          }
-        }
-        ra[u] = v;
-      } else {
-        ra[u] = *reinterpret_cast<const v4f*>(A + (int64_t)(i0 + row) * g.lda + k);
-      }
-    }
-  };
-  auto store_a = [&](int buf) {
-#pragma unroll
-    for (int u = 0; u < A_LD; ++u) {
-      const int q = tid + u * kThreads;
-      const int row = q / A_Q, kq = (q % A_Q) * 4;
-      *reinterpret_cast<v4f*>(&As[buf][row * AS + kq]) = ra[u];
-    }
-  };
-
-  // ---- B loader.
-  // Conv: im2col gather; thread owns pixel column jj = tid % BN and KPT
-  // consecutive k (KPT = BK*BN/256).  IP: W [j][k] rows, like A.
   constexpr int KPT = BK * BN / kThreads;
-  constexpr int B_LD4 = BN * A_Q / kThreads;  // float4 per thread (IP)
-  float rb[(MODE == Mode::Conv) ? KPT : 1];
-  v4f rb4[(MODE == Mode::Conv) ? 1 : B_LD4];
+  constexpr int B_LD4 = BN * A_Q / kThreads;
+  // Native vectors: HIP's float4 struct copies would keep a stage in scratch.
+  struct Stage {
+    v4f a[A_LD];
+    float b[(MODE == Mode::Conv) ? KPT : 1];
+    v4f b4[(MODE == Mode::Conv) ? 1 : B_LD4];
+  };
 
   // Conv per-thread pixel state (fixed for the whole block).
   const int jj = tid % BN;
@@ -174,7 +142,31 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_kernel(GemmArgs g) {
     img_plane0 = img * g.C;
   }
 
-  auto load_b = [&](int kt) {
+  auto gload = [&](Stage& st, int kt) {
+#pragma unroll
+    for (int u = 0; u < A_LD; ++u) {
+      const int q = tid + u * kThreads;
+      const int row = q / A_Q, kq = (q % A_Q) * 4;
+      const int k = kt * BK + kq;
+      if constexpr (MODE == Mode::IP) {
+        const int r = i0 + row;
+        v4f v = {0.f, 0.f, 0.f, 0.f};
+        if (r < g.m) {
+          const float* src = A + (int64_t)r * g.lda;
+          if (g.a_vec4) {
+            if (k < g.k_valid) v = *reinterpret_cast<const v4f*>(src + k);
+          } else {
+            v.x = (k + 0 < g.k_valid) ? src[k + 0] : 0.f;
+            v.y = (k + 1 < g.k_valid) ? src[k + 1] : 0.f;
+            v.z = (k + 2 < g.k_valid) ? src[k + 2] : 0.f;
+            v.w = (k + 3 < g.k_valid) ? src[k + 3] : 0.f;
+          }
+        }
+        st.a[u] = v;
+      } else {
+        st.a[u] = *reinterpret_cast<const v4f*>(A + (int64_t)(i0 + row) * g.lda + k);
+      }
+    }
     if constexpr (MODE == Mode::Conv) {
       const int kbase = kt * BK + kg * KPT;
 #pragma unroll
@@ -183,29 +175,35 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_kernel(GemmArgs g) {
         const int c = t >> 16, dy = (t >> 8) & 255, dx = t & 255;
         const int y = iy0 + dy, x = ix0 + dx;
         const bool in = pix_ok && c < g.C && (unsigned)y < (unsigned)g.H && (unsigned)x < (unsigned)g.W;
-        rb[u] = buf_load_f32(img_rs, in ? (uint32_t)((((img_plane0 + c) * g.H + y) * g.W + x) * (int)sizeof(float))
-                                        : kBufOOB);
+        st.b[u] = buf_load_f32(img_rs, in ? (uint32_t)((((img_plane0 + c) * g.H + y) * g.W + x) * (int)sizeof(float))
+                                          : kBufOOB);
       }
     } else {
 #pragma unroll
       for (int u = 0; u < B_LD4; ++u) {
         const int q = tid + u * kThreads;
         const int row = q / A_Q, kq = (q % A_Q) * 4;
-        rb4[u] = *reinterpret_cast<const v4f*>(B + (int64_t)(j0 + row) * g.ldb + kt * BK + kq);
+        st.b4[u] = *reinterpret_cast<const v4f*>(B + (int64_t)(j0 + row) * g.ldb + kt * BK + kq);
       }
     }
   };
-  auto store_b = [&](int buf) {
+  auto lstore = [&](const Stage& st, int buf) {
+#pragma unroll
+    for (int u = 0; u < A_LD; ++u) {
+      const int q = tid + u * kThreads;
+      const int row = q / A_Q, kq = (q % A_Q) * 4;
+      *reinterpret_cast<v4f*>(&As(buf)[row * AS + kq]) = st.a[u];
+    }
     if constexpr (MODE == Mode::Conv) {
 #pragma unroll
       for (int u = 0; u < KPT; u += 4)
-        *reinterpret_cast<v4f*>(&Bs[buf][jj * AS + kg * KPT + u]) = v4f{rb[u], rb[u + 1], rb[u + 2], rb[u + 3]};
+        *reinterpret_cast<v4f*>(&Bs(buf)[jj * AS + kg * KPT + u]) = v4f{st.b[u], st.b[u + 1], st.b[u + 2], st.b[u + 3]};
     } else {
 #pragma unroll
       for (int u = 0; u < B_LD4; ++u) {
         const int q = tid + u * kThreads;
         const int row = q / A_Q, kq = (q % A_Q) * 4;
-        *reinterpret_cast<v4f*>(&Bs[buf][row * AS + kq]) = rb4[u];
+        *reinterpret_cast<v4f*>(&Bs(buf)[row * AS + kq]) = st.b4[u];
       }
     }
   };
@@ -221,23 +219,18 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_kernel(GemmArgs g) {
   auto compute = [&](int buf) {
 #pragma unroll
     for (int kc = 0; kc < BK; kc += kBK) {
-      float af[TM][8], bf[TN][8];
+      v4f af[TM][2], bf[TN][2];
 #pragma unroll
       for (int a = 0; a < TM; ++a) {
-        const float* pa = &As[buf][(wm * (BM / 2) + a * 32 + li) * AS + kc + lh * 8];
-        const v4f x0 = *reinterpret_cast<const v4f*>(pa);
-        const v4f x1 = *reinterpret_cast<const v4f*>(pa + 4);
-        af[a][0] = x0.x; af[a][1] = x0.y; af[a][2] = x0.z; af[a][3] = x0.w;
-        af[a][4] = x1.x; af[a][5] = x1.y; af[a][6] = x1.z; af[a][7] = x1.w;
+        const float* pa = &As(buf)[(wm * (BM / 2) + a * 32 + li) * AS + kc + lh * 8];
+        af[a][0] = *reinterpret_cast<const v4f*>(pa);
+        af[a][1] = *reinterpret_cast<const v4f*>(pa + 4);
       }
 #pragma unroll
       for (int b = 0; b < TN; ++b) {
-        const int col = wn * (BN / 2) + b * 32 + li;
-        const float* pb = &Bs[buf][col * AS + kc + lh * 8];
-        const v4f y0 = *reinterpret_cast<const v4f*>(pb);
-        const v4f y1 = *reinterpret_cast<const v4f*>(pb + 4);
-        bf[b][0] = y0.x; bf[b][1] = y0.y; bf[b][2] = y0.z; bf[b][3] = y0.w;
-        bf[b][4] = y1.x; bf[b][5] = y1.y; bf[b][6] = y1.z; bf[b][7] = y1.w;
+        const float* pb = &Bs(buf)[(wn * (BN / 2) + b * 32 + li) * AS + kc + lh * 8];
+        bf[b][0] = *reinterpret_cast<const v4f*>(pb);
+        bf[b][1] = *reinterpret_cast<const v4f*>(pb + 4);
       }
 #pragma unroll
       for (int s = 0; s < 8; ++s)
@@ -245,39 +238,104 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_kernel(GemmArgs g) {
         for (int a = 0; a < TM; ++a)
 #pragma unroll
           for (int b = 0; b < TN; ++b)
-            acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[a][s], bf[b][s], acc[a][b], 0, 0, 0);
+            acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[a][s >> 2][s & 3], bf[b][s >> 2][s & 3], acc[a][b],
+                                                             0, 0, 0);
     }
   };
 
-  if (kt_begin < kt_end) {
-    load_a(kt_begin);
-    load_b(kt_begin);
-    store_a(0);
-    store_b(0);
+  // Two LDS buffers, global loads two stages ahead; the loop body is
+  // straight-line (two stages per trip, odd tail peeled) so the accumulators
+  // keep one register range.
+  const int n = kt_end - kt_begin;
+  if (n > 0) {
+    Stage s0, s1;
+    gload(s0, kt_begin);
+    if (n > 1) gload(s1, kt_begin + 1);
+    lstore(s0, 0);
     __syncthreads();
-    for (int kt = kt_begin; kt < kt_end; ++kt) {
-      const int buf = (kt - kt_begin) & 1;
-      const bool more = kt + 1 < kt_end;
-      if (more) {
-        load_a(kt + 1);
-        load_b(kt + 1);
-      }
-      compute(buf);
-      if (more) {
-        store_a(buf ^ 1);
-        store_b(buf ^ 1);
-      }
+    int i = 0;
+    for (; i + 1 < n; i += 2) {
+      if (i + 2 < n) gload(s0, kt_begin + i + 2);
+      compute(0);
+      lstore(s1, 1);
+      __syncthreads();
+      if (i + 3 < n) gload(s1, kt_begin + i + 3);
+      compute(1);
+      if (i + 2 < n) lstore(s0, 0);
       __syncthreads();
     }
+    if (i < n) compute(0);
   }
 
   // ---- epilogue.  32x32 accumulator layout: register r of lane l holds
   // row (r%4) + 8*(r/4) + 4*(l/32), column l%32.
+  if constexpr (MODE == Mode::Conv) {
+    if (g.splits == 1) {
+      // Staged through LDS one 64-row slab (a) at a time: each thread then
+      // writes runs of 4 pixels of one output channel with 16-byte accesses
+      // (bias once per run, residual read as a vector), 32-bit offsets (a
+      // launch's tensors stay below 2^31 bytes).  Same order as the direct
+      // epilogue: acc + bias, + residual, then the activation.
+      constexpr int TS = BN + 4;  // staged row stride (floats)
+      float* tile = smem;
+      const int ohw = g.OHW;
+      const bool vec = (ohw & 3) == 0;
+#pragma unroll
+      for (int a = 0; a < TM; ++a) {
+        __syncthreads();
+#pragma unroll
+        for (int b = 0; b < TN; ++b)
+#pragma unroll
+          for (int r = 0; r < 16; ++r)
+            tile[(wm * 32 + (r & 3) + 8 * (r >> 2) + 4 * lh) * TS + wn * (BN / 2) + b * 32 + li] = acc[a][b][r];
+        __syncthreads();
+        for (int q = tid; q < 64 * (BN / 4); q += kThreads) {
+          const int lr = q / (BN / 4), lc = (q % (BN / 4)) * 4;
+          const int i = i0 + (lr >> 5) * (BM / 2) + a * 32 + (lr & 31);
+          const int j = j0 + lc;
+          if (i >= g.m || j >= g.n) continue;
+          const float bi = g.bias[i];
+          const int img = j / ohw, rem = j - img * ohw;
+          const int o = (img * g.m + i) * ohw + rem;
+          const v4f t = *reinterpret_cast<const v4f*>(&tile[lr * TS + lc]);
+          if (vec && j + 4 <= g.n) {  // a 4-run never crosses an image when ohw % 4 == 0
+            v4f v = t + bi;
+            if (g.residual) v += *reinterpret_cast<const v4f*>(g.residual + o);
+            v.x = apply_act(v.x, g.act);
+            v.y = apply_act(v.y, g.act);
+            v.z = apply_act(v.z, g.act);
+            v.w = apply_act(v.w, g.act);
+            *reinterpret_cast<v4f*>(g.d + o) = v;
+          } else {
+            for (int e = 0; e < 4 && j + e < g.n; ++e) {
+              const int je = j + e, ie = je / ohw;
+              const int oe = (ie * g.m + i) * ohw + (je - ie * ohw);
+              float v = t[e] + bi;
+              if (g.residual) v += g.residual[oe];
+              g.d[oe] = apply_act(v, g.act);
+            }
+          }
+        }
+      }
+      return;
+    }
+  }
 #pragma unroll
   for (int b = 0; b < TN; ++b) {
     const int j = j0 + wn * (BN / 2) + b * 32 + li;
     if constexpr (MODE == Mode::Conv) {
       if (j >= g.n) continue;
+      if (g.splits > 1) {  // raw partial sums [split][m][n]; bias etc. in conv_splitk_reduce
+        float* P = g.d + (int64_t)split * g.m * g.n;
+#pragma unroll
+        for (int a = 0; a < TM; ++a)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int i = i0 + wm * (BM / 2) + a * 32 + (r & 3) + 8 * (r >> 2) + 4 * lh;
+            if (i < g.m) P[(int64_t)i * g.n + j] = acc[a][b][r];
+          }
+        continue;
+      }
       const int img = j / g.OHW;
       const int rem = j - img * g.OHW;
       const int64_t obase = (int64_t)img * g.m * g.OHW + rem;
@@ -312,6 +370,24 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_kernel(GemmArgs g) {
   }
 }
 
+// Split-K reduction for the implicit-GEMM convolution: part [S][m][npix] ->
+// out NCHW = act(sum_s part + bias (+ residual)), the order of the unsplit
+// epilogue.
+__global__ void conv_splitk_reduce(const float* __restrict__ part, int splits, int m, int npix, int ohw,
+                                   const float* __restrict__ bias, const float* __restrict__ residual,
+                                   float* __restrict__ out, int act) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (int64_t)m * npix) return;
+  const int i = (int)(idx / npix), j = (int)(idx - (int64_t)i * npix);
+  float acc = part[idx];
+  for (int s = 1; s < splits; ++s) acc += part[(int64_t)s * m * npix + idx];
+  const int img = j / ohw, rem = j - img * ohw;
+  const int64_t o = ((int64_t)img * m + i) * ohw + rem;
+  float v = acc + bias[i];
+  if (residual) v += residual[o];
+  out[o] = apply_act(v, act);
+}
+
 // Split-K reduction for InnerProduct: out = act((sum_s part[s]) + bias).
 __global__ void ip_splitk_reduce(const float* part, const float* bias,
                                  float* out, int m, int n, int ldp,
@@ -333,11 +409,36 @@ int launch(const GemmArgs& g, dim3 grid, hipStream_t s, const char* name) {
 }  // namespace
 
 // ------------------------------- Convolution ------------------------------
-uint64_t conv_igemm_f32_workspace(const nhip_conv_plan*, int, int, int) { return 0; }
+namespace {
+struct IgemmCfg {
+  int bm, bn, splits;
+};
+// Tile: the largest that still gives about two workgroups per CU (64x64
+// otherwise).  K split: when even that leaves the CUs short of work and K is
+// long, split K so that each workgroup keeps at least 4 chunks.
+IgemmCfg igemm_config(const nhip_conv_plan* p, int64_t npix) {
+  const int64_t target = 2LL * cu_count();
+  const int64_t mt128 = ceil_div(p->g.k, 128), mt64 = ceil_div(p->g.k, 64);
+  const int64_t nt128 = ceil_div(npix, 128), nt64 = ceil_div(npix, 64);
+  IgemmCfg c{64, 64, 1};
+  if (p->m_pad % 128 == 0 && mt128 * nt128 >= target) c = {128, 128, 1};
+  else if (mt64 * nt128 >= target) c = {64, 128, 1};
+  const int64_t tiles = ceil_div(p->g.k, c.bm) * ceil_div(npix, c.bn);
+  const int nk = p->kred_pad / kBK;
+  while (c.splits < 16 && tiles * c.splits < cu_count() && nk / (c.splits * 2) >= 4) c.splits *= 2;
+  return c;
+}
+}  // namespace
+
+uint64_t conv_igemm_f32_workspace(const nhip_conv_plan* p, int n, int oh, int ow) {
+  const int64_t npix = (int64_t)n * oh * ow;
+  const IgemmCfg c = igemm_config(p, npix);
+  return c.splits > 1 ? (uint64_t)c.splits * p->g.k * npix * sizeof(float) : 0;
+}
 
 int launch_conv_igemm_f32(const nhip_conv_plan* p, const float* in,
                           const float* residual, float* out, int n, int h,
-                          int w, int oh, int ow, void*, uint64_t,
+                          int w, int oh, int ow, void* ws, uint64_t ws_bytes,
                           hipStream_t s) {
   GemmArgs g{};
   g.a = p->weight;
@@ -361,18 +462,29 @@ int launch_conv_igemm_f32(const nhip_conv_plan* p, const float* in,
   g.bias = p->bias;
   g.residual = residual;
   g.act = p->g.act;
-  g.splits = 1;
-  // Tile choice: the largest tile that still gives about two workgroups per
-  // CU; 64x64 otherwise.
-  const int64_t target = 2LL * cu_count();
-  const int mt128 = (int)ceil_div(p->g.k, 128), mt64 = (int)ceil_div(p->g.k, 64);
-  const int nt128 = (int)ceil_div(g.n, 128), nt64 = (int)ceil_div(g.n, 64);
-  const bool m_is_128 = p->m_pad % 128 == 0;
-  if (m_is_128 && (int64_t)mt128 * nt128 >= target)
-    return launch<128, 128, Mode::Conv>(g, dim3(nt128, mt128), s, "conv_igemm_f32<128,128>");
-  if ((int64_t)mt64 * nt128 >= target)
-    return launch<64, 128, Mode::Conv>(g, dim3(nt128, mt64), s, "conv_igemm_f32<64,128>");
-  return launch<64, 64, Mode::Conv>(g, dim3(nt64, mt64), s, "conv_igemm_f32<64,64>");
+  const IgemmCfg c = igemm_config(p, g.n);
+  g.splits = c.splits;
+  if (c.splits > 1) {
+    const uint64_t need = conv_igemm_f32_workspace(p, n, oh, ow);
+    if (ws == nullptr || ws_bytes < need)
+      return fail(NHIP_STATUS_OUTPUT_CAPACITY_INSUFFICIENT,
+                  "implicit-GEMM conv: workspace of " + std::to_string(need) + " bytes required");
+    g.d = static_cast<float*>(ws);
+  }
+  const dim3 grid((unsigned)ceil_div(g.n, c.bn), (unsigned)ceil_div(p->g.k, c.bm), (unsigned)c.splits);
+  if (c.bm == 128)
+    NHIP_TRY((launch<128, 128, Mode::Conv>(g, grid, s, "conv_igemm_f32<128,128>")));
+  else if (c.bn == 128)
+    NHIP_TRY((launch<64, 128, Mode::Conv>(g, grid, s, "conv_igemm_f32<64,128>")));
+  else
+    NHIP_TRY((launch<64, 64, Mode::Conv>(g, grid, s, "conv_igemm_f32<64,64>")));
+  if (c.splits > 1) {
+    const int64_t total = (int64_t)p->g.k * g.n;
+    NHIP_LAUNCH("conv_splitk_reduce", conv_splitk_reduce, dim3((unsigned)ceil_div(total, 256)), dim3(256), 0, s,
+                static_cast<const float*>(ws), c.splits, p->g.k, g.n, g.OHW, p->bias, residual, out, p->g.act);
+    return check_launch("conv_splitk_reduce");
+  }
+  return ok();
 }
 
 // ------------------------------- InnerProduct -----------------------------
