@@ -15,7 +15,9 @@ count for Winograd as for direct convolution).  roofline = the Winograd
 batched-GEMM kernel (36 fp32 MFMA GEMMs per conv, the dominant kernel): its
 work 2*36*T*C*K per launch (T = N*ceil(OH/4)*ceil(OW/4) tiles) over its
 average duration, from HIP events stamped by each of its dispatches on the
-launch stream inside the timed region.  cpu_baseline = the
+launch stream inside the timed region; traffic = its HBM bytes per launch
+from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary
+(profiles/wino_gemm_traffic.json).  cpu_baseline = the
 CPU oracle (restatement of the reference's lowered loops, compiled like the
 reference's .so: -O3, no -march, no FP contraction, OpenMP) on a bounded
 sample of the same stages.
@@ -133,6 +135,21 @@ def mobilenetv2_secondary(torch, steps, warmup):
             "ms_per_step": dt * 1e3, "images_per_sec": BATCH / dt, "tflops": flops / dt / 1e12}
 
 
+def measured_traffic(fused):
+    """HBM bytes per launch of the Winograd GEMM, from the committed
+    rocprofv3 FETCH_SIZE / WRITE_SIZE summary (profiles/wino_gemm_traffic.json,
+    averaged over the four stage shapes, copy-calibrated); None for the fused
+    variant, which that summary does not cover."""
+    if fused:
+        return None
+    try:
+        with open(os.path.join(ROOT, "profiles", "wino_gemm_traffic.json")) as f:
+            d = json.load(f)
+        return int(d["bytes_per_launch"]) if d.get("kernel") == "wino_gemm" else None
+    except (OSError, ValueError, KeyError):
+        return None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -219,7 +236,7 @@ def main():
             "peak": PEAK_FP32_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(achieved / PEAK_FP32_TFLOPS, 4),
-            "traffic": None,
+            "traffic": measured_traffic(fused),
             "avg_launch_us": round(avg_gemm_s * 1e6, 2),
             "launches_timed": launches,
         },
