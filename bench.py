@@ -199,8 +199,9 @@ def main():
     direct_flops = sum(2 * workloads.conv_flops(BATCH, c, c, hw, hw) for c, hw in workloads.RESNET18_STAGES)
     wino_flops = sum(2 * workloads.winograd_flops(BATCH, c, c, hw, hw) for c, hw in workloads.RESNET18_STAGES)
     value = direct_flops / (ms_per_step / 1e3) / 1e12
-    gemm_launches_per_step = 8
-    assert launches == gemm_launches_per_step * args.steps, (launches, args.steps)
+    # 8 convs per step; each runs as one or two batch parts (one GEMM launch each)
+    gemm_launches_per_step = launches // args.steps
+    assert launches % args.steps == 0 and gemm_launches_per_step in (8, 16), (launches, args.steps)
     avg_gemm_s = gemm_ms / launches / 1e3
     achieved = (wino_flops / gemm_launches_per_step) / avg_gemm_s / 1e12
 

@@ -226,7 +226,8 @@ def test_kernel_timer_counts_launches():
     c, k = 16, 16
     wt = workloads.he_normal(RNG, (k, c, 3, 3), c * 9)
     conv = nhip.Conv2dF32(nhip.conv_desc(c, k, bias=False, algorithm=nhip.ALGO_WINOGRAD), wt)
-    x = dev(RNG.uniform(-1, 1, (2, c, 8, 8)).astype(np.float32))
+    # one image: a single Winograd part, one GEMM launch per forward
+    x = dev(RNG.uniform(-1, 1, (1, c, 8, 8)).astype(np.float32))
     nhip.timer_start("wino_gemm")
     for _ in range(3):
         conv.forward(x)
