@@ -20,6 +20,7 @@
 // then gathers 16-byte channel vectors per (pixel, kh, kw), reduction order
 // (kh, kw, c) — the OHWI order the reference itself transposes the weights
 // to (NCNNToTosa.cpp:1168-1176).
+#include <algorithm>
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
@@ -101,6 +102,10 @@ struct Int8Args {
   float os;
   int term, act;
   void* out;           // int8 or fp32 NCHW
+  // footprint kernel only
+  int OH, R;           // output rows per workgroup
+  int FH, FW, FS;      // input footprint rows / columns / LDS bytes per pixel
+  int fp_bytes;        // LDS bytes of the footprint (multiple of 16)
 };
 
 // D[i = out channel][j = pixel] over the (kh, kw, c) reduction.
@@ -302,6 +307,198 @@ __global__ __launch_bounds__(kThreads) void conv_int8_kernel(Int8Args g) {
   }
 }
 
+// Footprint variant.  A workgroup owns R whole output rows of one image (at
+// most 128 pixels, padded to 128 MFMA columns) and BM output channels.  The
+// input rows those outputs read (a (R-1)*sh+(kh-1)*dh+1 by
+// (OW-1)*sw+(kw-1)*dw+1 window of the NHWC int8 scratch image, zero halo) are
+// copied into LDS once, with coalesced 16-byte loads; every tap's B fragment
+// is then read straight from that window, so only the weights stream through
+// the two-stage K pipeline (they are shared by all workgroups and stay in
+// L2).  Same MFMA mapping, accumulation and epilogue as conv_int8_kernel.
+template <int BM>
+__global__ __launch_bounds__(kThreads) void conv_int8_fp_kernel(Int8Args g) {
+  constexpr int BN = 128, BK = 128;
+  constexpr int TM = BM / 64, TN = BN / 64;
+  constexpr int ROW = BK + 16;
+  constexpr int CH = BK / 16;
+  constexpr int A_LD = BM * CH / kThreads;
+  constexpr int ES = BN + 16;
+  extern __shared__ __attribute__((aligned(16))) int8_t dsm[];
+  int8_t* foot = dsm;
+  auto As = [&](int buf) { return dsm + g.fp_bytes + buf * BM * ROW; };
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int li = lane & 31, lh = lane >> 5;
+  const int rgs = (g.OH + g.R - 1) / g.R;
+  const int img = blockIdx.x / rgs, oy0 = (blockIdx.x % rgs) * g.R;
+  const int i0 = blockIdx.y * BM;
+  const int npx = min(g.R, g.OH - oy0) * g.OW;  // valid pixels of this workgroup
+
+  // ---- footprint -> LDS, four 16-byte loads in flight per thread
+  {
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(g.x, g.x_bytes);
+    const int cpp = g.c_pad / 16;
+    const int total = g.FH * g.FW * cpp;
+    const int iy_base = oy0 * g.sh - g.pt;
+    for (int base = 0; base < total; base += 4 * kThreads) {
+      v4i v[4];
+      int dst[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int e = base + q * kThreads + tid;
+        const int pix = e / cpp, ch = e - pix * cpp;
+        const int fy = pix / g.FW, fx = pix - fy * g.FW;
+        const int iy = iy_base + fy, ix = fx - g.pl;
+        const bool in = e < total && (unsigned)iy < (unsigned)g.H && (unsigned)ix < (unsigned)g.W;
+        v[q] = __builtin_bit_cast(
+            v4i, buf_load_b128(rs, in ? (uint32_t)(((img * g.H + iy) * g.W + ix) * g.c_pad + ch * 16) : kBufOOB));
+        dst[q] = e < total ? pix * g.FS + ch * 16 : -1;
+      }
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        if (dst[q] >= 0) *reinterpret_cast<v4i*>(foot + dst[q]) = v[q];
+    }
+  }
+
+  // per-lane window origin (bytes) of each of the wave's pixel columns
+  int fbase[TN];
+#pragma unroll
+  for (int b = 0; b < TN; ++b) {
+    const int pc = min(wn * (BN / 2) + b * 32 + li, npx - 1);
+    const int py = pc / g.OW, px = pc - py * g.OW;
+    fbase[b] = (py * g.sh * g.FW + px * g.sw) * g.FS;
+  }
+
+  struct Stage {
+    v4i a[A_LD];
+  };
+  auto gload = [&](Stage& st, int kt) {
+#pragma unroll
+    for (int u = 0; u < A_LD; ++u) {
+      const int q = tid + u * kThreads;
+      const int row = q / CH, ch = q % CH;
+      st.a[u] = *reinterpret_cast<const v4i*>(g.w + (int64_t)(i0 + row) * g.kred_pad + kt * BK + ch * 16);
+    }
+  };
+  auto lstore = [&](const Stage& st, int buf) {
+#pragma unroll
+    for (int u = 0; u < A_LD; ++u) {
+      const int q = tid + u * kThreads;
+      const int row = q / CH, ch = q % CH;
+      *reinterpret_cast<v4i*>(As(buf) + row * ROW + ch * 16) = st.a[u];
+    }
+  };
+
+  v16i acc[TM][TN];
+#pragma unroll
+  for (int a = 0; a < TM; ++a)
+#pragma unroll
+    for (int b = 0; b < TN; ++b)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[a][b][r] = 0;
+
+  auto compute = [&](int buf, int kt) {
+#pragma unroll
+    for (int s = 0; s < BK / 32; ++s) {
+      const int t = g.ktab[kt * CH + s * 2 + lh];  // this lane's 16-byte k chunk
+      int c0 = t >> 16;
+      const int dy = (t >> 8) & 255, dx = t & 255;
+      if (c0 >= g.c_pad) c0 = 0;  // K padding: the weights there are zero
+      const int koff = (dy * g.FW + dx) * g.FS + c0;
+      v4i af[TM], bf[TN];
+#pragma unroll
+      for (int a = 0; a < TM; ++a)
+        af[a] = *reinterpret_cast<const v4i*>(As(buf) + (wm * (BM / 2) + a * 32 + li) * ROW + s * 32 + lh * 16);
+#pragma unroll
+      for (int b = 0; b < TN; ++b) bf[b] = *reinterpret_cast<const v4i*>(foot + fbase[b] + koff);
+#pragma unroll
+      for (int a = 0; a < TM; ++a)
+#pragma unroll
+        for (int b = 0; b < TN; ++b)
+          acc[a][b] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[a], bf[b], acc[a][b], 0, 0, 0);
+    }
+  };
+
+  const int n = g.kred_pad / BK;
+  {
+    Stage s0, s1;
+    gload(s0, 0);
+    if (n > 1) gload(s1, 1);
+    lstore(s0, 0);
+    __syncthreads();  // footprint and first A stage visible
+    int i = 0;
+    for (; i + 1 < n; i += 2) {
+      if (i + 2 < n) gload(s0, i + 2);
+      compute(0, i);
+      lstore(s1, 1);
+      __syncthreads();
+      if (i + 3 < n) gload(s1, i + 3);
+      compute(1, i + 1);
+      if (i + 2 < n) lstore(s0, 0);
+      __syncthreads();
+    }
+    if (i < n) compute(0, i);
+  }
+
+  // ---- epilogue (as conv_int8_kernel), staged in LDS over the footprint
+  __syncthreads();
+  const bool q8 = g.term > 100;
+  float* tf = reinterpret_cast<float*>(dsm);
+  int8_t* tq = dsm;
+#pragma unroll
+  for (int b = 0; b < TN; ++b) {
+    const int jl = wn * (BN / 2) + b * 32 + li;
+#pragma unroll
+    for (int a = 0; a < TM; ++a)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int il = wm * (BM / 2) + a * 32 + (r & 3) + 8 * (r >> 2) + 4 * lh;
+        const int i = i0 + il;
+        float f;
+        {
+#pragma clang fp contract(off)
+          f = (float)acc[a][b][r];
+          f = f * g.recip[i];
+          f = f + g.bias[i];
+        }
+        if (q8) {
+          int8_t q = quantize_i8(f, g.os);
+          if (g.act == NHIP_ACT_RELU && q < 0) q = 0;
+          tq[il * ES + jl] = q;
+        } else {
+          if (g.act == NHIP_ACT_RELU) f = f < 0.0f ? 0.0f : f;
+          tf[il * ES + jl] = f;
+        }
+      }
+  }
+  __syncthreads();
+  constexpr int RUNS = BN / 16;
+  for (int q = tid; q < BM * RUNS; q += kThreads) {
+    const int il = q / RUNS, jl = (q % RUNS) * 16;
+    const int i = i0 + il;
+    if (i >= g.m || jl >= npx) continue;
+    const int64_t o = ((int64_t)img * g.m + i) * g.OHW + (int64_t)oy0 * g.OW + jl;
+    const bool whole = jl + 16 <= npx && (o & 15) == 0;
+    if (q8) {
+      int8_t* dst = static_cast<int8_t*>(g.out);
+      if (whole) {
+        *reinterpret_cast<v4i*>(dst + o) = *reinterpret_cast<const v4i*>(&tq[il * ES + jl]);
+      } else {
+        for (int e = 0; e < 16 && jl + e < npx; ++e) dst[o + e] = tq[il * ES + jl + e];
+      }
+    } else {
+      float* dst = static_cast<float*>(g.out);
+      if (whole) {
+#pragma unroll
+        for (int e = 0; e < 16; e += 4)
+          *reinterpret_cast<v4f*>(dst + o + e) = *reinterpret_cast<const v4f*>(&tf[il * ES + jl + e]);
+      } else {
+        for (int e = 0; e < 16 && jl + e < npx; ++e) dst[o + e] = tf[il * ES + jl + e];
+      }
+    }
+  }
+}
+
 }  // namespace
 
 uint64_t conv_int8_workspace(const nhip_conv_plan* p, int n, int h, int w) {
@@ -344,6 +541,36 @@ int launch_conv_int8(const nhip_conv_plan* p, const void* in, int in_is_i8,
   g.term = p->scale_term;
   g.act = p->g.act;
   g.out = out;
+  // Footprint kernel when a workgroup's input window fits in LDS (whole rows
+  // of at most 128 output pixels); NHIP_INT8_FOOTPRINT=0 turns it off (a
+  // tuning and comparison switch).
+  {
+    const char* env = std::getenv("NHIP_INT8_FOOTPRINT");
+    const bool allowed = !(env && std::atoi(env) == 0);
+    const int R = ow > 0 ? 128 / ow : 0;
+    const int max_dy = (p->g.kh - 1) * p->g.dh, max_dx = (p->g.kw - 1) * p->g.dw;
+    if (allowed && R >= 1 && p->kred_pad % 128 == 0) {
+      g.OH = oh;
+      g.R = std::min(R, oh);
+      g.FH = (g.R - 1) * p->g.sh + max_dy + 1;
+      g.FW = (ow - 1) * p->g.sw + max_dx + 1;
+      g.FS = p->c_pad + 16;
+      g.fp_bytes = (int)round_up((int64_t)g.FH * g.FW * g.FS, 16);
+      const int bm = p->m_pad % 128 == 0 && p->m_pad >= 256 ? 128 : 64;
+      const int64_t lds_oper = (int64_t)g.fp_bytes + 2LL * bm * (128 + 16);
+      const int64_t lds_epi = (int64_t)bm * (128 + 16) * 4;
+      const int64_t lds = std::max(lds_oper, lds_epi);
+      if (lds <= 64 * 1024) {
+        const dim3 grid((unsigned)(n * ceil_div(oh, g.R)), (unsigned)(p->m_pad / bm));
+        if (bm == 128) {
+          NHIP_LAUNCH("conv_int8_fp<128>", conv_int8_fp_kernel<128>, grid, dim3(kThreads), (unsigned)lds, s, g);
+        } else {
+          NHIP_LAUNCH("conv_int8_fp<64>", conv_int8_fp_kernel<64>, grid, dim3(kThreads), (unsigned)lds, s, g);
+        }
+        return check_launch("conv_int8_fp");
+      }
+    }
+  }
   // Tile shape: NHIP_INT8_TILE="bm,bn,bk" overrides (tuning switch, ignored
   // when not valid for the plan).
   int bm = p->m_pad % 128 == 0 ? 128 : 64, bn = 64, bk = 128;
