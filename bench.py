@@ -100,7 +100,7 @@ def int8_secondary(nhip, workloads, torch, steps, warmup):
     for _ in range(warmup):
         conv.forward(x, out=out, workspace=ws)
     torch.cuda.synchronize()
-    nhip.timer_start("conv_int8<")
+    nhip.timer_start("conv_int8")
     t0 = time.perf_counter()
     for _ in range(steps):
         conv.forward(x, out=out, workspace=ws)
