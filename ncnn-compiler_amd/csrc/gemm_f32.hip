@@ -16,6 +16,9 @@
 // for both operands, so each lane reads 8 consecutive k of its A row (two
 // ds_read_b128) instead of 16 scattered words.  Any permutation of k is valid
 // for a dot product as long as A and B use the same one.
+#include <cstdio>
+#include <cstdlib>
+
 #include "nhip_internal.h"
 
 namespace nhip {
@@ -421,8 +424,19 @@ IgemmCfg igemm_config(const nhip_conv_plan* p, int64_t npix) {
   const int64_t mt128 = ceil_div(p->g.k, 128), mt64 = ceil_div(p->g.k, 64);
   const int64_t nt128 = ceil_div(npix, 128), nt64 = ceil_div(npix, 64);
   IgemmCfg c{64, 64, 1};
-  if (p->m_pad % 128 == 0 && mt128 * nt128 >= target) c = {128, 128, 1};
-  else if (mt64 * nt128 >= target) c = {64, 128, 1};
+  // Short reductions (1x1 and stem convolutions, K <= 256) are bandwidth-bound:
+  // the 64x64 tile gives the most workgroups and measures fastest there.
+  if (p->kred_pad > 256) {
+    if (p->m_pad % 128 == 0 && mt128 * nt128 >= target) c = {128, 128, 1};
+    else if (mt64 * nt128 >= target) c = {64, 128, 1};
+  }
+  // Tuning override NHIP_IGEMM_TILE="bm,bn" (64x64, 64x128, 128x128).
+  if (const char* env = std::getenv("NHIP_IGEMM_TILE")) {
+    int bm = 0, bn = 0;
+    if (std::sscanf(env, "%d,%d", &bm, &bn) == 2 && (bm == 64 || (bm == 128 && p->m_pad % 128 == 0)) &&
+        (bn == 64 || bn == 128) && !(bm == 128 && bn == 64))
+      c = {bm, bn, 1};
+  }
   const int64_t tiles = ceil_div(p->g.k, c.bm) * ceil_div(npix, c.bn);
   const int nk = p->kred_pad / kBK;
   while (c.splits < 16 && tiles * c.splits < cu_count() && nk / (c.splits * 2) >= 4) c.splits *= 2;
