@@ -185,7 +185,7 @@ def main():
         run_step(stages)
     torch.cuda.synchronize()
 
-    fused = os.environ.get("NHIP_WINOGRAD_VARIANT", "") in ("2", "221", "114")
+    fused = os.environ.get("NHIP_WINOGRAD_VARIANT", "") == "2"
     nhip.timer_start("wino_fused" if fused else "wino_gemm")
     torch.cuda.synchronize()
     t0 = time.perf_counter()

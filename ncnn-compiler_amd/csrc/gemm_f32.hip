@@ -422,7 +422,7 @@ struct IgemmCfg {
 IgemmCfg igemm_config(const nhip_conv_plan* p, int64_t npix) {
   const int64_t target = 2LL * cu_count();
   const int64_t mt128 = ceil_div(p->g.k, 128), mt64 = ceil_div(p->g.k, 64);
-  const int64_t nt128 = ceil_div(npix, 128), nt64 = ceil_div(npix, 64);
+  const int64_t nt128 = ceil_div(npix, 128);
   IgemmCfg c{64, 64, 1};
   // Short reductions (1x1 and stem convolutions, K <= 256) are bandwidth-bound:
   // the 64x64 tile gives the most workgroups and measures fastest there.

@@ -107,6 +107,10 @@ struct nhip_conv_plan {
   // implicit GEMM fp32: weights [m_pad][kred_pad], k = (c, kh, kw) order;
   // Winograd: weights U[36][m_pad][c_pad].
   float* weight = nullptr;
+  // Winograd, fused kernel: the same U blocked by 8 channels in channel
+  // pairs, [c_pad/8][36][4][m_pad][2], so one chunk's slice for 32 output
+  // channels is four contiguous 256-byte runs per transform point.
+  float* weight_fused = nullptr;
   float* bias = nullptr;      // [m_pad] zero-filled past k (always present)
   int32_t m_pad = 0, kred = 0, kred_pad = 0, c_pad = 0;
   // im2col gather table: one packed int per reduction index

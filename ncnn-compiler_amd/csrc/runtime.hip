@@ -152,6 +152,7 @@ int upload_bias(nhip_conv_plan* p, const float* bias, int count, int padded) {
 void free_plan(nhip_conv_plan* p) {
   if (!p) return;
   (void)hipFree(p->weight);
+  (void)hipFree(p->weight_fused);
   (void)hipFree(p->bias);
   (void)hipFree(p->ktab);
   (void)hipFree(p->weight_i8);

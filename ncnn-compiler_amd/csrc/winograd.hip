@@ -23,20 +23,28 @@
 #include "nhip_internal.h"
 
 namespace nhip {
-int launch_conv_winograd_fused(const nhip_conv_plan* p, const float* in, const float* residual,
-                               float* out, int n, int h, int w, int oh, int ow, hipStream_t s);
+// winograd_fused.hip: the batched GEMM with the output transform fused.
+int launch_wino_gemm_out(const nhip_conv_plan* p, const float* V, int t_pad, const float* residual, float* out,
+                         int n, int oh, int ow, float* parts, hipStream_t s);
+uint64_t wino_gemm_out_parts_bytes(const nhip_conv_plan* p, int n, int oh, int ow);
 
-// Path selection.  The three-kernel path of this file (transforms through
-// HBM) is the default: on MI355X it measures at least as fast as the fused
-// kernel on every ResNet-18 stage shape (the fused kernel is bound by its two
-// memory round trips and barriers per channel chunk).  NHIP_WINOGRAD_VARIANT
-// = 221 or 114 selects the fused kernel in that workgroup shape, 2 lets the
-// fused launcher pick; a tuning and comparison switch.
-static bool unfused_requested() {
+// Path selection: input transform + GEMM with the output transform fused
+// (winograd_fused.hip), or the three-kernel path (M through HBM).
+// NHIP_WINOGRAD_VARIANT = 1 forces the three-kernel path, 2 the fused GEMM
+// (where its limits allow); unset or 0 chooses by shape.
+static int variant_requested() {
   const char* env = std::getenv("NHIP_WINOGRAD_VARIANT");
-  if (!env || !*env) return true;
-  const int v = std::atoi(env);
-  return v == 0 || v == 1;
+  return (env && *env) ? std::atoi(env) : 0;
+}
+
+static bool fused_selected(const nhip_conv_plan* p, int n, int oh, int ow) {
+  // The fused GEMM's limit: V (32-bit buffer offsets) below 2 GiB.
+  const int64_t t_pad = round_up((int64_t)n * ceil_div(oh, 4) * ceil_div(ow, 4), 128);
+  if ((int64_t)36 * p->c_pad * t_pad * (int64_t)sizeof(float) >= (int64_t(1) << 31)) return false;
+  const int v = variant_requested();
+  if (v == 1) return false;
+  if (v == 2) return true;
+  return false;
 }
 
 namespace {
@@ -62,67 +70,81 @@ WinoShape wino_shape(const nhip_conv_plan* p, int n, int h, int w, int oh, int o
   return s;
 }
 
-// Thread (c, t): 6x6 zero-padded patch -> 36 transformed values.
+// Thread (c, t): 6x6 zero-padded patch -> 36 transformed values, V[xi][c][t].
+// PAIRS: thread (channel pair cp, t) transforms channels 2cp and 2cp + 1 and
+// writes V[xi][cp][t][2] (the layout the fused GEMM reads), one 8-byte store
+// per transform point.
+template <bool PAIRS>
 __global__ __launch_bounds__(256) void wino_input_transform(
     const float* __restrict__ x, uint32_t x_bytes, float* __restrict__ V, int C, int H, int W,
     int th, int tw, int T, int t_pad, int c_pad, int pt, int pl) {
+  constexpr int CPT = PAIRS ? 2 : 1;  // channels per thread
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= (int64_t)c_pad * t_pad) return;
-  const int c = (int)(idx / t_pad);
-  const int t = (int)(idx - (int64_t)c * t_pad);
+  if (idx >= (int64_t)(c_pad / CPT) * t_pad) return;
+  const int cg = (int)(idx / t_pad);
+  const int t = (int)(idx - (int64_t)cg * t_pad);
   const int64_t plane_stride = (int64_t)c_pad * t_pad;
-  float* vout = V + (int64_t)c * t_pad + t;
-  if (c >= C || t >= T) {
-#pragma unroll
-    for (int xi = 0; xi < 36; ++xi) vout[xi * plane_stride] = 0.f;
-    return;
-  }
+  float* vout = V + ((int64_t)cg * t_pad + t) * CPT;
   const int per_img = th * tw;
-  const int img = t / per_img;
-  const int r = t - img * per_img;
+  const bool t_ok = t < T;
+  const int tt = t_ok ? t : 0;
+  const int img = tt / per_img;
+  const int r = tt - img * per_img;
   const int ty = r / tw, tx = r - (r / tw) * tw;
   const int y0 = ty * 4 - pt, x0 = tx * 4 - pl;
   const __amdgpu_buffer_rsrc_t rs = make_rsrc(x, x_bytes);  // whole input, < 2^31 bytes
-  const int plane = (img * C + c) * H;
 
-  float d[6][6];
+  float v[CPT][36];
 #pragma unroll
-  for (int i = 0; i < 6; ++i) {
-    const int y = y0 + i;
-    const bool yok = (unsigned)y < (unsigned)H;
+  for (int e = 0; e < CPT; ++e) {
+    const int c = cg * CPT + e;
+    const bool ok = t_ok && c < C;  // padding tiles / channels transform a zero patch
+    const int plane = (img * C + c) * H;
+    float d[6][6];
+#pragma unroll
+    for (int i = 0; i < 6; ++i) {
+      const int y = y0 + i;
+      const bool yok = ok && (unsigned)y < (unsigned)H;
+#pragma unroll
+      for (int j = 0; j < 6; ++j) {
+        const int xx = x0 + j;
+        const uint32_t off =
+            (yok && (unsigned)xx < (unsigned)W) ? (uint32_t)(((plane + y) * W + xx) * (int)sizeof(float)) : kBufOOB;
+        d[i][j] = buf_load_f32(rs, off);
+      }
+    }
+    // tmp = B^T d  (column-wise)
+    float tmp[6][6];
 #pragma unroll
     for (int j = 0; j < 6; ++j) {
-      const int xx = x0 + j;
-      const uint32_t off =
-          (yok && (unsigned)xx < (unsigned)W) ? (uint32_t)(((plane + y) * W + xx) * (int)sizeof(float)) : kBufOOB;
-      d[i][j] = buf_load_f32(rs, off);
+      const float d0 = d[0][j], d1 = d[1][j], d2 = d[2][j], d3 = d[3][j], d4 = d[4][j], d5 = d[5][j];
+      tmp[0][j] = 4.f * d0 - 5.f * d2 + d4;
+      tmp[1][j] = -4.f * (d1 + d2) + d3 + d4;
+      tmp[2][j] = 4.f * (d1 - d2) - d3 + d4;
+      tmp[3][j] = -2.f * (d1 - d3) - d2 + d4;
+      tmp[4][j] = 2.f * (d1 - d3) - d2 + d4;
+      tmp[5][j] = 4.f * d1 - 5.f * d3 + d5;
+    }
+    // V = tmp B  (row-wise)
+#pragma unroll
+    for (int i = 0; i < 6; ++i) {
+      const float d0 = tmp[i][0], d1 = tmp[i][1], d2 = tmp[i][2], d3 = tmp[i][3], d4 = tmp[i][4], d5 = tmp[i][5];
+      v[e][i * 6 + 0] = 4.f * d0 - 5.f * d2 + d4;
+      v[e][i * 6 + 1] = -4.f * (d1 + d2) + d3 + d4;
+      v[e][i * 6 + 2] = 4.f * (d1 - d2) - d3 + d4;
+      v[e][i * 6 + 3] = -2.f * (d1 - d3) - d2 + d4;
+      v[e][i * 6 + 4] = 2.f * (d1 - d3) - d2 + d4;
+      v[e][i * 6 + 5] = 4.f * d1 - 5.f * d3 + d5;
     }
   }
-  // tmp = B^T d  (column-wise)
-  float tmp[6][6];
 #pragma unroll
-  for (int j = 0; j < 6; ++j) {
-    const float d0 = d[0][j], d1 = d[1][j], d2 = d[2][j], d3 = d[3][j], d4 = d[4][j], d5 = d[5][j];
-    tmp[0][j] = 4.f * d0 - 5.f * d2 + d4;
-    tmp[1][j] = -4.f * (d1 + d2) + d3 + d4;
-    tmp[2][j] = 4.f * (d1 - d2) - d3 + d4;
-    tmp[3][j] = -2.f * (d1 - d3) - d2 + d4;
-    tmp[4][j] = 2.f * (d1 - d3) - d2 + d4;
-    tmp[5][j] = 4.f * d1 - 5.f * d3 + d5;
-  }
-  // V = tmp B  (row-wise)
-#pragma unroll
-  for (int i = 0; i < 6; ++i) {
-    const float d0 = tmp[i][0], d1 = tmp[i][1], d2 = tmp[i][2], d3 = tmp[i][3], d4 = tmp[i][4], d5 = tmp[i][5];
-    float v[6];
-    v[0] = 4.f * d0 - 5.f * d2 + d4;
-    v[1] = -4.f * (d1 + d2) + d3 + d4;
-    v[2] = 4.f * (d1 - d2) - d3 + d4;
-    v[3] = -2.f * (d1 - d3) - d2 + d4;
-    v[4] = 2.f * (d1 - d3) - d2 + d4;
-    v[5] = 4.f * d1 - 5.f * d3 + d5;
-#pragma unroll
-    for (int j = 0; j < 6; ++j) vout[(i * 6 + j) * plane_stride] = v[j];
+  for (int xi = 0; xi < 36; ++xi) {
+    if constexpr (PAIRS) {
+      typedef float v2f_t __attribute__((ext_vector_type(2)));
+      *reinterpret_cast<v2f_t*>(vout + xi * plane_stride) = v2f_t{v[0][xi], v[1][xi]};
+    } else {
+      vout[xi * plane_stride] = v[0][xi];
+    }
   }
 }
 
@@ -194,7 +216,8 @@ __global__ __launch_bounds__(256) void wino_output_transform(
 }  // namespace
 
 // U[xi][k][c] = (G g_kc G^T)[xi], computed in double, stored fp32 with zero
-// padding to [36][m_pad][c_pad].
+// padding to [36][m_pad][c_pad], and again blocked for the fused kernel as
+// [c_pad/8][36][4][m_pad][2] (channel c = 8*chunk + 2*pair + s).
 int winograd_prepack_weights(nhip_conv_plan* p, const float* weight) {
   static const double G[6][3] = {
       {1.0 / 4, 0, 0},
@@ -218,15 +241,25 @@ int winograd_prepack_weights(nhip_conv_plan* p, const float* weight) {
           U[((size_t)(i * 6 + j) * p->m_pad + k) * p->c_pad + c] = (float)u;
         }
     }
+  std::vector<float> Uf(U.size());
+  for (int xi = 0; xi < 36; ++xi)
+    for (int k = 0; k < p->m_pad; ++k)
+      for (int c = 0; c < p->c_pad; ++c)
+        Uf[((((size_t)(c / 8) * 36 + xi) * 4 + (c % 8) / 2) * p->m_pad + k) * 2 + c % 2] =
+            U[((size_t)xi * p->m_pad + k) * p->c_pad + c];
+  NHIP_TRY(check_hip(hipMalloc(&p->weight_fused, Uf.size() * sizeof(float)), "hipMalloc(winograd U, blocked)"));
+  NHIP_TRY(check_hip(hipMemcpy(p->weight_fused, Uf.data(), Uf.size() * sizeof(float), hipMemcpyHostToDevice),
+                     "hipMemcpy(winograd U, blocked)"));
   NHIP_TRY(check_hip(hipMalloc(&p->weight, U.size() * sizeof(float)), "hipMalloc(winograd U)"));
   return check_hip(hipMemcpy(p->weight, U.data(), U.size() * sizeof(float), hipMemcpyHostToDevice),
                    "hipMemcpy(winograd U)");
 }
 
 uint64_t conv_winograd_f32_workspace(const nhip_conv_plan* p, int n, int oh, int ow) {
-  if (!unfused_requested()) return 0;
   const int th = (int)ceil_div(oh, 4), tw = (int)ceil_div(ow, 4);
   const int64_t t_pad = round_up((int64_t)n * th * tw, 128);
+  if (fused_selected(p, n, oh, ow))  // V, then the GEMM's partial sums
+    return (uint64_t)36 * t_pad * p->c_pad * sizeof(float) + wino_gemm_out_parts_bytes(p, n, oh, ow);
   const WinoGemmCfg cfg = wino_gemm_config(p->m_pad, p->c_pad, (int)t_pad);
   return (uint64_t)36 * t_pad * (p->c_pad + (int64_t)cfg.splits * p->m_pad) * sizeof(float);
 }
@@ -235,22 +268,27 @@ int launch_conv_winograd_f32(const nhip_conv_plan* p, const float* in,
                              const float* residual, float* out, int n, int h,
                              int w, int oh, int ow, void* ws, uint64_t ws_bytes,
                              hipStream_t s) {
-  if (!unfused_requested()) return launch_conv_winograd_fused(p, in, residual, out, n, h, w, oh, ow, s);
   const WinoShape ws_ = wino_shape(p, n, h, w, oh, ow);
   const uint64_t need = conv_winograd_f32_workspace(p, n, oh, ow);
   if (ws == nullptr || ws_bytes < need)
     return fail(NHIP_STATUS_OUTPUT_CAPACITY_INSUFFICIENT,
                 "winograd conv: workspace of " + std::to_string(need) + " bytes required");
+  const bool fused = fused_selected(p, n, oh, ow);
   float* V = static_cast<float*>(ws);
   float* M = V + (int64_t)36 * ws_.c_pad * ws_.t_pad;
   {
-    const int64_t total = (int64_t)ws_.c_pad * ws_.t_pad;
-    NHIP_LAUNCH("wino_input_transform", wino_input_transform, dim3((unsigned)ceil_div(total, 256)), dim3(256), 0, s,
-                       in, (uint32_t)((size_t)n * ws_.c * h * w * sizeof(float)), V, ws_.c, h, w,
-                       ws_.th, ws_.tw, ws_.t, ws_.t_pad, ws_.c_pad,
-                       p->g.pt, p->g.pl);
+    const uint32_t x_bytes = (uint32_t)((size_t)n * ws_.c * h * w * sizeof(float));
+    const int64_t total = (int64_t)(fused ? ws_.c_pad / 2 : ws_.c_pad) * ws_.t_pad;
+    const dim3 grid((unsigned)ceil_div(total, 256));
+    if (fused)
+      NHIP_LAUNCH("wino_input_transform", wino_input_transform<true>, grid, dim3(256), 0, s, in, x_bytes, V, ws_.c,
+                  h, w, ws_.th, ws_.tw, ws_.t, ws_.t_pad, ws_.c_pad, p->g.pt, p->g.pl);
+    else
+      NHIP_LAUNCH("wino_input_transform", wino_input_transform<false>, grid, dim3(256), 0, s, in, x_bytes, V, ws_.c,
+                  h, w, ws_.th, ws_.tw, ws_.t, ws_.t_pad, ws_.c_pad, p->g.pt, p->g.pl);
     NHIP_TRY(check_launch("wino_input_transform"));
   }
+  if (fused) return launch_wino_gemm_out(p, V, ws_.t_pad, residual, out, n, oh, ow, M, s);
   const WinoGemmCfg cfg = wino_gemm_config(ws_.m_pad, ws_.c_pad, ws_.t_pad);
   NHIP_TRY(launch_wino_gemm(p->weight, V, M, ws_.m_pad, ws_.c_pad, ws_.t_pad, cfg, s));
   {

@@ -1,25 +1,36 @@
-// Fused Winograd F(4x4, 3x3): input transform, the 36 point-wise products and
-// the output transform in one kernel, so the transformed input V and the
-// products M never leave the CU (the unfused path in winograd.hip writes and
-// re-reads both through HBM).
+// Winograd F(4x4, 3x3) batched GEMM with the output transform fused: the
+// 36 point-wise products M[xi] = U[xi] V[xi] and Y = A^T M A in one kernel,
+// so M never leaves the CU (the three-kernel path in winograd.hip writes and
+// re-reads M through HBM).  V comes from wino_input_transform<true>
+// (winograd.hip) in the channel-pair layout [36][c_pad/2][t_pad][2].
 //
-// Work decomposition.  A wave owns a 16 (output channel) x 16 (tile) block for
-// all 36 transform points xi and accumulates it with v_mfma_f32_16x16x4_f32:
-// 36 x 4 accumulator registers per lane.  In the 16x16 MFMA result layout
-// register r of lane l holds (row 4*(l/16)+r, column l%16) for every xi, so a
-// lane owns all 36 values of four (k, t) pairs and the output transform
-// A^T M A runs in registers.
+// The input transform stays a separate, HBM-bound kernel on purpose: on
+// gfx950 the fp32 MFMA and fp32 VALU work of the waves on one SIMD do not
+// overlap (measured: time(MFMA + VALU) ~ time(MFMA) + time(VALU)), so
+// transforming patches inside the GEMM costs MFMA time, at 32 output
+// channels per workgroup about 0.7 x the MFMA work of a chunk.
 //
-// A workgroup is 4 waves arranged WK x WT x WC: WK*16 output channels, WT*16
-// tiles, and the channel reduction split WC ways across waves (reduced
-// through LDS at the end) for layers with few tiles.  Per chunk of CB input
-// channels the workgroup
-//   1. loads the 6x6 input patches of its tiles and transforms them
-//      (V = B^T d B) into LDS, one (tile, channel) pair per thread;
-//   2. copies U[xi][k][c] (transformed weights, prepacked on the host) into LDS;
-//   3. runs 36 * CB/(4*WC) MFMAs per wave.
-// Two workgroups fit per CU (73.7 KB LDS each), so one's load/transform
-// phase overlaps the other's MFMA phase.
+// Work decomposition.  A workgroup owns 32 tiles x 32 output channels for
+// all 36 transform points xi and runs 8 waves in two roles:
+//   * 4 load waves copy, for a chunk of 8 input channels, the V slice
+//     (36 x 8 x 32 floats) and the U slice (36 x 32 x 8, transformed
+//     weights prepacked on the host) from HBM into LDS, prefetching two
+//     chunks ahead in registers;
+//   * 4 MFMA waves, a 2 x 2 grid of 16 (channel) x 16 (tile) blocks, each
+//     accumulate their block for all 36 xi with v_mfma_f32_16x16x4_f32
+//     (36 x 4 accumulator registers per lane).
+// LDS holds two chunk slots (2 x 72 KB): while the MFMA waves consume chunk
+// i from one slot, the load waves fill the other with chunk i + 1; one
+// workgroup barrier per chunk hands the slots over.
+//
+// In the 16x16 MFMA result layout register r of lane l holds (row
+// 4*(l/16)+r, column l%16) for every xi, so an MFMA lane owns all 36 values
+// of four (k, t) pairs and the output transform A^T M A runs in registers.
+//
+// Layers with few tiles split the input channels over `splits` workgroups
+// (grid), each writing its partial output transform (linear in M) to a
+// workspace; wino_fused_reduce sums the parts and applies bias, residual and
+// activation.
 #include <cstdlib>
 #include <cstring>
 
@@ -28,206 +39,220 @@
 namespace nhip {
 namespace {
 
-constexpr int kThreads = 256;
+constexpr int kThreads = 512;                 // 4 MFMA waves + 4 load waves
+constexpr int kTB = 32;                       // tiles per workgroup
+constexpr int kKB = 32;                       // output channels per workgroup
+constexpr int kCB = 8;                        // input channels per chunk
+constexpr int kVElems = 36 * kTB * kCB;       // V chunk [36][kCB/2][kTB][2]
+constexpr int kUElems = 36 * kKB * kCB;       // U chunk [36][kCB/2][kKB][2]
+constexpr int kSlotElems = kVElems + kUElems;
+constexpr int kLdsBytes = 2 * kSlotElems * (int)sizeof(float);  // 147456
+constexpr int kProducers = 256;               // load threads
+constexpr int kULoads = kUElems / 4 / kProducers;  // 16-byte U loads per thread and chunk
+constexpr int kVLoads = kVElems / 4 / kProducers;  // 16-byte V loads per thread and chunk
+constexpr int kXcds = 8;                      // MI355X: workgroup L runs on XCD L % 8
+static_assert(kUElems % (4 * kProducers) == 0 && kVElems % (4 * kProducers) == 0,
+              "whole 16-byte loads per thread");
+static_assert(kTB == 32 && kKB == 32 && kCB == 8, "the load mappings below assume 32 x 32 x 8");
+
+typedef float v2f __attribute__((ext_vector_type(2)));
 
 struct FusedArgs {
-  const float* x;       // [N][C][H][W]
-  const float* U;       // [36][m_pad][c_pad]
+  const float* V;       // [36][c_pad/2][t_pad][2]
+  const float* U;       // [c_pad/8][36][4][m_pad][2]
   const float* bias;    // [m_pad]
   const float* residual;
-  float* out;           // [N][K][OH][OW]
-  int C, H, W, K, OH, OW, th, tw, T, m_pad, c_pad, pt, pl, act;
-  uint32_t x_bytes;     // size of x (< 2^31)
+  float* out;           // [N][K][OH][OW]; with splits > 1 the parts [splits][N][K][OH][OW]
+  int K, OH, OW, th, tw, T, t_pad, m_pad, c_pad;
+  int nt, nk, splits, per;  // tile blocks, channel blocks, channel splits, chunks per split
+  // Tile blocks (mode = 0, 1, 2):
+  //   0  whole images, R = (32 / tw) / th * th tile rows (th <= 32 / tw): a
+  //      block's outputs for one image are one contiguous run over its 32
+  //      channels;
+  //   1  up to R = 32 / tw tile rows of one image (th > 32 / tw), blocks
+  //      restarting at each image (bpi per image): one contiguous run per
+  //      channel;
+  //   2  32-tile pieces of a tile row (tw > 32), bpr per row.
+  // G = N * th tile rows.
+  int mode, R, bpi, bpr, G;
+  uint32_t v_bytes;     // size of V (< 2^31)
+  uint32_t u_bytes;     // size of U (< 2^31)
 };
 
-// LDS layout of one chunk, for both V (rows = tiles) and U (rows = output
-// channels): [xi][c / S][row][S].  An MFMA operand read by a wave is then
-// rows 0..15 x 4 lane groups of S consecutive floats, and each half-wave
-// reads one contiguous 256-byte span: no bank conflicts.
-template <int WK, int WT, int WC, int S>
-struct FusedCfg {
-  static constexpr int KB = 16 * WK;          // output channels per workgroup
-  static constexpr int TB = 16 * WT;          // tiles per workgroup
-  static constexpr int CB = 4 * S * WC;       // input channels per chunk
-  static constexpr int V_ELEMS = 36 * TB * CB;
-  static constexpr int U_ELEMS = 36 * KB * CB;
-  static_assert(WK * WT * WC == 4, "4 waves per workgroup");
-  static_assert(TB * CB == kThreads, "one (tile, channel) pair per thread and chunk");
-};
-
-template <int ROWS, int CB, int S>
-__device__ __forceinline__ int lds_index(int xi, int c, int row) {
-  return ((xi * (CB / S) + c / S) * ROWS + row) * S + (c % S);
+template <int ACT>
+__device__ __forceinline__ float activate(float v) {
+  if constexpr (ACT == NHIP_ACT_RELU) return v < 0.f ? 0.f : v;
+  if constexpr (ACT == NHIP_ACT_SIGMOID) return __frcp_rn(1.0f + __expf(-v));
+  return v;
 }
 
-// V = B^T d B; each transformed row is handed to `store(xi, value)` as soon
-// as it is computed, so the 36 outputs never need to be live together.
-template <class Store>
-__device__ __forceinline__ void input_transform(float d[6][6], Store store) {
-#pragma unroll
-  for (int j = 0; j < 6; ++j) {  // columns: d <- B^T d, in place
-    const float d0 = d[0][j], d1 = d[1][j], d2 = d[2][j], d3 = d[3][j], d4 = d[4][j], d5 = d[5][j];
-    d[0][j] = 4.f * d0 - 5.f * d2 + d4;
-    d[1][j] = -4.f * (d1 + d2) + d3 + d4;
-    d[2][j] = 4.f * (d1 - d2) - d3 + d4;
-    d[3][j] = -2.f * (d1 - d3) - d2 + d4;
-    d[4][j] = 2.f * (d1 - d3) - d2 + d4;
-    d[5][j] = 4.f * d1 - 5.f * d3 + d5;
-  }
-#pragma unroll
-  for (int i = 0; i < 6; ++i) {  // rows: (B^T d) B
-    const float d0 = d[i][0], d1 = d[i][1], d2 = d[i][2], d3 = d[i][3], d4 = d[i][4], d5 = d[i][5];
-    store(i * 6 + 0, 4.f * d0 - 5.f * d2 + d4);
-    store(i * 6 + 1, -4.f * (d1 + d2) + d3 + d4);
-    store(i * 6 + 2, 4.f * (d1 - d2) - d3 + d4);
-    store(i * 6 + 3, -2.f * (d1 - d3) - d2 + d4);
-    store(i * 6 + 4, 2.f * (d1 - d3) - d2 + d4);
-    store(i * 6 + 5, 4.f * d1 - 5.f * d3 + d5);
-  }
-}
+// The load waves: copy the V and U slices of chunks ch_begin ..
+// ch_begin + n - 1 into LDS, chunk i into slot i & 1 in iteration i, one
+// workgroup barrier per iteration (n + 1 in all).  Both operands sit in LDS
+// as [xi][channel pair][row][2], so the MFMA lanes' 8-byte reads of 16
+// consecutive rows hit 32 distinct banks; in HBM both are stored so that a
+// chunk's slice for one (xi, channel pair) is one contiguous 256-byte run
+// (32 rows x 2 channels).  Element e4 = it*256 + p (16-byte units) of a slice
+// is xi = e4 / 64, pair (e4 % 64) / 16, rows 2*(e4 % 16) and +1, and lands at
+// slot + e4*4.  Consecutive it are 4 transform points apart: a wave-uniform
+// byte stride, passed as the scalar offset (which the range check excludes;
+// an offset of 2^31 >= the buffer size reads as 0).
+__device__ __forceinline__ void load_role(const FusedArgs& a, float* lds, int p, int t0, int k0, int ch_begin,
+                                          int n) {
+  const __amdgpu_buffer_rsrc_t vr = make_rsrc(a.V, a.v_bytes);
+  const __amdgpu_buffer_rsrc_t ur = make_rsrc(a.U, a.u_bytes);
+  const int xi0 = p >> 6, cp = (p & 63) >> 4, r2 = 2 * (p & 15);
+  // V[xi][c/2][t][2]: pair planes of t_pad x 2 floats, xi planes of c_pad/2 pairs
+  const uint32_t v_lane = (uint32_t)(((xi0 * (a.c_pad / 2) + cp) * a.t_pad + t0 + r2) * 2 * 4);
+  const uint32_t v_it = (uint32_t)(4 * (a.c_pad / 2) * a.t_pad * 2 * 4);
+  const uint32_t v_ch = (uint32_t)(4 * a.t_pad * 2 * 4);
+  // U[c/8][xi][pair][k][2]
+  const uint32_t u_lane = (uint32_t)((((xi0 * 4 + cp) * a.m_pad + k0 + r2) * 2) * 4);
+  const uint32_t u_it = (uint32_t)(4 * 4 * a.m_pad * 2 * 4);
+  const uint32_t u_ch = (uint32_t)(36 * 4 * a.m_pad * 2 * 4);
 
-template <int WK, int WT, int WC, int S>
-__global__ __launch_bounds__(kThreads, 2) void wino_fused_kernel(FusedArgs a) {
-  using Cfg = FusedCfg<WK, WT, WC, S>;
-  constexpr int KB = Cfg::KB, TB = Cfg::TB, CB = Cfg::CB;
-  extern __shared__ __attribute__((aligned(16))) float lds[];
-  float* Vs = lds;                    // [36][CB/S][TB][S]
-  float* Us = lds + Cfg::V_ELEMS;     // [36][CB/S][KB][S]
-
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wc = wave % WC, wt = (wave / WC) % WT, wk = wave / (WC * WT);
-  const int li = lane & 15, lg = lane >> 4;
-  const int t0 = blockIdx.x * TB, k0 = blockIdx.y * KB;
-
-  // This thread's (tile, channel) pair for the input transform: consecutive
-  // lanes take consecutive tiles (coalesced patch rows, conflict-free V writes).
-  const int pt_local = tid % TB, pc_local = tid / TB;
-  const int t = t0 + pt_local;
-  const bool t_ok = t < a.T;
-  int y0 = 0, x0 = 0, im = 0;
-  {
-    const int per_img = a.th * a.tw;
-    const int tt = t_ok ? t : 0;
-    im = tt / per_img;
-    const int r = tt - im * per_img;
-    const int ty = r / a.tw, tx = r - (r / a.tw) * a.tw;
-    y0 = ty * 4 - a.pt;
-    x0 = tx * 4 - a.pl;
-  }
-  // The whole input is one (wave-uniform) buffer resource, < 2^31 bytes;
-  // padding and out-of-range tiles or channels read as 0 via kBufOOB.
-  const __amdgpu_buffer_rsrc_t rs = make_rsrc(a.x, a.x_bytes);
-  float d[6][6];
-  auto load_patch = [&](int c0) {
-    const int c = c0 + pc_local;
-    const bool ok = t_ok && c < a.C;
-    const int plane = (im * a.C + c) * a.H;
+  // Two chunks in flight.  Loads are issued unconditionally (past this
+  // workgroup's last chunk they are pointed out of range and return 0): a
+  // conditional load would make the compiler copy the loaded registers at
+  // the join, which waits for the loads there and defeats the prefetch.
+  v4f vA[kVLoads], vB[kVLoads], uA[kULoads], uB[kULoads];
+  auto load = [&](int ch, bool live, v4f (&v)[kVLoads], v4f (&u)[kULoads]) {
+    const uint32_t vo = live ? v_lane + (uint32_t)ch * v_ch : 0x80000000u;
+    const uint32_t uo = live ? u_lane + (uint32_t)ch * u_ch : 0x80000000u;
 #pragma unroll
-    for (int i = 0; i < 6; ++i) {
-      const int y = y0 + i;
-      const bool yok = ok && (unsigned)y < (unsigned)a.H;
+    for (int it = 0; it < kVLoads; ++it)
+      v[it] = __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(vr, vo, it * v_it, 0));
 #pragma unroll
-      for (int j = 0; j < 6; ++j) {
-        const int x = x0 + j;
-        const uint32_t off = (yok && (unsigned)x < (unsigned)a.W)
-                                 ? (uint32_t)(((plane + y) * a.W + x) * (int)sizeof(float))
-                                 : kBufOOB;
-        d[i][j] = buf_load_f32(rs, off);
-      }
-    }
+    for (int it = 0; it < kULoads; ++it)
+      u[it] = __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(ur, uo, it * u_it, 0));
   };
+  auto fill = [&](int slot_idx, v4f (&v)[kVLoads], v4f (&u)[kULoads]) {
+    float* slot = lds + slot_idx * kSlotElems;
+#pragma unroll
+    for (int it = 0; it < kVLoads; ++it) *reinterpret_cast<v4f*>(slot + (it * kProducers + p) * 4) = v[it];
+#pragma unroll
+    for (int it = 0; it < kULoads; ++it)
+      *reinterpret_cast<v4f*>(slot + kVElems + (it * kProducers + p) * 4) = u[it];
+  };
+
+  load(ch_begin, n > 0, vA, uA);
+  load(ch_begin + 1, n > 1, vB, uB);
+  // Iteration i: chunk i (if any) into slot i & 1, then the barrier.
+  for (int i = 0; i <= n; i += 2) {
+    if (i < n) fill(0, vA, uA);
+    load(ch_begin + i + 2, i + 2 < n, vA, uA);
+    __syncthreads();  // slot 0 full; slot 1 consumed
+    if (i + 1 < n) fill(1, vB, uB);
+    load(ch_begin + i + 3, i + 3 < n, vB, uB);
+    if (i + 1 <= n) __syncthreads();  // slot 1 full; slot 0 consumed
+  }
+}
+
+// FINAL: write act(Y + bias (+ residual)) with activation ACT; otherwise
+// the raw part of channel split cs for wino_fused_reduce.
+template <int ACT, bool FINAL>
+__global__ __launch_bounds__(kThreads, 1) void wino_fused_kernel(FusedArgs a) {
+  extern __shared__ __attribute__((aligned(16))) float lds[];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+
+  // XCD-contiguous renumbering: each XCD gets a contiguous range of logical
+  // blocks, ordered (tile block, split, channel block) with the channel
+  // block fastest, so the workgroups that read the same input patches share
+  // an L2.
+  int tb, kb, cs;
+  {
+    const int total = a.nt * a.nk * a.splits;
+    const int L = blockIdx.x;
+    const int x = L % kXcds, q = L / kXcds;
+    const int logical = x * (total / kXcds) + min(x, total % kXcds) + q;
+    kb = logical % a.nk;
+    const int rest = logical / a.nk;
+    cs = rest % a.splits;
+    tb = rest / a.splits;
+  }
+  const int k0 = kb * kKB;
+  int g0, nrows, tx_a, t0, ntiles;
+  if (a.mode == 0) {
+    g0 = tb * a.R;
+    nrows = min(a.R, a.G - g0);
+    tx_a = 0;
+  } else if (a.mode == 1) {
+    const int im = tb / a.bpi, ty0 = (tb - im * a.bpi) * a.R;
+    g0 = im * a.th + ty0;
+    nrows = min(a.R, a.th - ty0);
+    tx_a = 0;
+  } else {
+    g0 = tb / a.bpr;
+    nrows = 1;
+    tx_a = (tb - g0 * a.bpr) * kTB;
+  }
+  t0 = g0 * a.tw + tx_a;
+  ntiles = a.mode == 2 ? min(kTB, a.tw - tx_a) : nrows * a.tw;
+  const int nch = a.c_pad / kCB;
+  const int ch_begin = cs * a.per;
+  const int n = max(0, min(nch, ch_begin + a.per) - ch_begin);
+  float* dst = a.out + (FINAL ? 0 : (int64_t)cs * (a.G / a.th) * a.K * a.OH * a.OW);
+  constexpr int kYS = 20;  // LDS row of one (k, tile) output tile: 16 values + 4 pad (conflict-free)
+
+  if (wave >= 4) {
+    load_role(a, lds, tid - 4 * 64, t0, k0, ch_begin, n);
+  } else {
+  // ---- MFMA waves ------------------------------------------------------------
+  const int li = lane & 15, q = lane >> 4;
+  const int wk = wave & 1, wt = wave >> 1;
+  // Lane (li, q) supplies reduction index q at MFMA step s as channel 2q + s
+  // of the chunk, for both operands: A = U[k = wk*16 + li], B = V[t = wt*16 + li].
+  const int ua_off = kVElems + (q * kKB + wk * 16 + li) * 2;
+  const int vb_off = (q * kTB + wt * 16 + li) * 2;
 
   v4f acc[36];
 #pragma unroll
   for (int xi = 0; xi < 36; ++xi) acc[xi] = v4f{0.f, 0.f, 0.f, 0.f};
 
-  const int nchunks = a.c_pad / CB;
-  for (int ch = 0; ch < nchunks; ++ch) {
-    const int c0 = ch * CB;
-    // 36 independent buffer loads in flight at once; the other workgroup on
-    // the CU runs its MFMAs meanwhile.
-    load_patch(c0);
-    __syncthreads();  // previous chunk's MFMA reads of Vs/Us are done
-    {
-      // 1. input patch -> V
-      float* vrow = Vs + lds_index<TB, CB, S>(0, pc_local, pt_local);
-      input_transform(d, [&](int xi, float v) { vrow[xi * TB * CB] = v; });
-    }
-    {
-      // 2. U[xi][k0..k0+KB)[c0..c0+CB) -> LDS, float2 granules
-      constexpr int PAIRS = 36 * KB * CB / 2;
-      static_assert(PAIRS % kThreads == 0, "whole float2 granules per thread");
+  // Operands are read in groups of kG transform points, one group ahead of
+  // the MFMAs that use them; a scheduling fence per group keeps the compiler
+  // from hoisting all 72 reads (which would not fit in registers beside the
+  // 144 accumulators).
+  constexpr int kG = 4, kGroups = 36 / kG;
+  for (int i = 0; i <= n; ++i) {
+    if (i > 0) {
+      const float* slot = lds + ((i - 1) & 1) * kSlotElems;
+      const float* ua = slot + ua_off;
+      const float* vb = slot + vb_off;
+      v2f av[2][kG], bv[2][kG];
+      auto read_group = [&](int g, int buf) {
 #pragma unroll
-      for (int it = 0; it < PAIRS / kThreads; ++it) {
-        const int q = tid + it * kThreads;
-        const int xi = q / (KB * CB / 2);
-        const int rem = q - xi * (KB * CB / 2);
-        const int kk = rem / (CB / 2), c2 = (rem - (rem / (CB / 2)) * (CB / 2)) * 2;
-        const float2 u = *reinterpret_cast<const float2*>(
-            a.U + ((int64_t)xi * a.m_pad + k0 + kk) * a.c_pad + c0 + c2);
-        Us[lds_index<KB, CB, S>(xi, c2, kk)] = u.x;
-        Us[lds_index<KB, CB, S>(xi, c2 + 1, kk)] = u.y;
+        for (int j = 0; j < kG; ++j) {
+          av[buf][j] = *reinterpret_cast<const v2f*>(ua + (g * kG + j) * kKB * kCB);
+          bv[buf][j] = *reinterpret_cast<const v2f*>(vb + (g * kG + j) * kTB * kCB);
+        }
+      };
+      read_group(0, 0);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int g = 0; g < kGroups; ++g) {
+        if (g + 1 < kGroups) read_group(g + 1, (g + 1) & 1);
+#pragma unroll
+        for (int s = 0; s < 2; ++s)
+#pragma unroll
+          for (int j = 0; j < kG; ++j)
+            acc[g * kG + j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[g & 1][j][s], bv[g & 1][j][s],
+                                                                  acc[g * kG + j], 0, 0, 0);
+        // order within the group: the next group's LDS reads, then this
+        // group's MFMAs
+        if (g + 1 < kGroups) __builtin_amdgcn_sched_group_barrier(0x100, kG, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 2 * kG, 0);
+        __builtin_amdgcn_sched_barrier(0);
       }
     }
-    __syncthreads();
-    // 3. MFMAs: lane group lg supplies channel wc*4S + S*lg + s at step s.
-    const int cw = wc * 4 * S + S * lg;
-    const float* ua = Us + lds_index<KB, CB, S>(0, cw, wk * 16 + li);
-    const float* vb = Vs + lds_index<TB, CB, S>(0, cw, wt * 16 + li);
-#pragma unroll
-    for (int xi = 0; xi < 36; ++xi) {
-      if constexpr (S == 2) {
-        const float2 av = *reinterpret_cast<const float2*>(ua + xi * KB * CB);
-        const float2 bv = *reinterpret_cast<const float2*>(vb + xi * TB * CB);
-        acc[xi] = __builtin_amdgcn_mfma_f32_16x16x4f32(av.x, bv.x, acc[xi], 0, 0, 0);
-        acc[xi] = __builtin_amdgcn_mfma_f32_16x16x4f32(av.y, bv.y, acc[xi], 0, 0, 0);
-      } else {
-        acc[xi] = __builtin_amdgcn_mfma_f32_16x16x4f32(ua[xi * KB * CB], vb[xi * TB * CB], acc[xi], 0, 0, 0);
-      }
-    }
+    __syncthreads();  // matches the transform waves' barrier of iteration i
   }
 
-  // Reduce the WC channel splits through LDS, 12 transform points at a time.
-  if constexpr (WC > 1) {
-    constexpr int XS = 12;
-#pragma unroll
-    for (int xs = 0; xs < 36; xs += XS) {
-#pragma unroll
-      for (int half = WC / 2; half >= 1; half /= 2) {
-        __syncthreads();
-        const int group = wk * WT + wt;
-        if (wc >= half && wc < 2 * half) {
-          float* slot = lds + (size_t)((group * half + (wc - half)) * XS * 4) * 64;
-#pragma unroll
-          for (int xi = 0; xi < XS; ++xi)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) slot[(xi * 4 + r) * 64 + lane] = acc[xs + xi][r];
-        }
-        __syncthreads();
-        if (wc < half) {
-          const float* slot = lds + (size_t)((group * half + wc) * XS * 4) * 64;
-#pragma unroll
-          for (int xi = 0; xi < XS; ++xi)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) acc[xs + xi][r] += slot[(xi * 4 + r) * 64 + lane];
-        }
-      }
-    }
-    if (wc != 0) return;
-  }
-
-  // Output transform Y = A^T M A, + bias (+ residual), activation.
-  const int tt = t0 + wt * 16 + li;
-  if (tt >= a.T) return;
-  const int per_img = a.th * a.tw;
-  const int oim = tt / per_img;
-  const int rr = tt - oim * per_img;
-  const int ty = rr / a.tw, tx = rr - (rr / a.tw) * a.tw;
-  const bool vec4 = (a.OW % 4 == 0);
+  // ---- output transform Y = A^T M A, into LDS as Ys[k][tile][kYS] ------------
+  // (both slots are free: every wave has passed the last chunk's barrier)
+  const int tl = wt * 16 + li;
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
-    const int k = k0 + wk * 16 + 4 * lg + r;
-    if (k >= a.K) continue;
     float tmp[4][6];
 #pragma unroll
     for (int j = 0; j < 6; ++j) {
@@ -239,101 +264,314 @@ __global__ __launch_bounds__(kThreads, 2) void wino_fused_kernel(FusedArgs a) {
       tmp[2][j] = s12 + 4.f * s34;
       tmp[3][j] = d12 + 8.f * d34 + m5;
     }
-    const float b = a.bias[k];
-    const int64_t plane = ((int64_t)oim * a.K + k) * a.OH * a.OW;
+    float* yrow = lds + ((wk * 16 + 4 * q + r) * kTB + tl) * kYS;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int oy = ty * 4 + i;
-      if (oy >= a.OH) break;
       const float m0 = tmp[i][0], m1 = tmp[i][1], m2 = tmp[i][2], m3 = tmp[i][3], m4 = tmp[i][4], m5 = tmp[i][5];
       const float s12 = m1 + m2, d12 = m1 - m2, s34 = m3 + m4, d34 = m3 - m4;
-      float y[4];
-      y[0] = m0 + s12 + s34;
-      y[1] = d12 + 2.f * d34;
-      y[2] = s12 + 4.f * s34;
-      y[3] = d12 + 8.f * d34 + m5;
-      const int64_t row = plane + (int64_t)oy * a.OW + tx * 4;
-      if (vec4) {
-        float4 res = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (a.residual) res = *reinterpret_cast<const float4*>(a.residual + row);
-        float o[4] = {y[0] + b + res.x, y[1] + b + res.y, y[2] + b + res.z, y[3] + b + res.w};
+      *reinterpret_cast<v4f*>(yrow + i * 4) =
+          v4f{m0 + s12 + s34, d12 + 2.f * d34, s12 + 4.f * s34, d12 + 8.f * d34 + m5};
+    }
+  }
+  }  // MFMA waves
+  __syncthreads();
+
+  // ---- write-out by all 8 waves: wave w takes channels w, w+8, w+16, w+24 ------
+  // Outputs are written in memory order.  All residual loads of a wave are
+  // issued before its first store: vmcnt counts loads and stores in issue
+  // order, so a load issued after a store would make its wait include the
+  // store.
+  const int OHW = a.OH * a.OW;
+  float bias4[4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          if (a.act == NHIP_ACT_RELU) o[j] = o[j] < 0.f ? 0.f : o[j];
-          else if (a.act == NHIP_ACT_SIGMOID) o[j] = __frcp_rn(1.0f + __expf(-o[j]));
+  for (int j = 0; j < 4; ++j) {
+    const int k = k0 + wave + 8 * j;
+    bias4[j] = (FINAL && k < a.K) ? a.bias[k] : 0.f;
+  }
+  if (a.mode == 0) {
+    // Whole images: per (image, channel) plane P = OH*OW <= 16 * 32 floats; a
+    // lane's pixels p = lane + 64m (m < 8) and their LDS offsets are
+    // computed once.  Wave w writes planes (image, channel) = (il, w + 8j).
+    int yoff[8];
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+      const int pix = lane + 64 * m;
+      const int oy = pix / a.OW, ox = pix - (pix / a.OW) * a.OW;
+      yoff[m] = pix < OHW ? ((oy >> 2) * a.tw + (ox >> 2)) * kYS + (oy & 3) * 4 + (ox & 3) : -1;
+    }
+    const int nimg = nrows / a.th;
+    const int im0 = g0 / a.th;
+    for (int il = 0; il < nimg; ++il) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int kk = wave + 8 * j, k = k0 + kk;
+        if (k >= a.K) break;
+        const float* ys = lds + (kk * kTB + il * a.th * a.tw) * kYS;
+        const int64_t base = ((int64_t)(im0 + il) * a.K + k) * OHW;
+        float res[8];
+#pragma unroll
+        for (int m = 0; m < 8; ++m)
+          res[m] = (FINAL && a.residual && yoff[m] >= 0) ? a.residual[base + lane + 64 * m] : 0.f;
+#pragma unroll
+        for (int m = 0; m < 8; ++m)
+          if (yoff[m] >= 0) dst[base + lane + 64 * m] = activate<ACT>(ys[yoff[m]] + bias4[j] + res[m]);
+      }
+    }
+    return;
+  }
+  if (a.mode == 1) {
+    // One contiguous run of count = orows x OW floats per channel; the
+    // wave's 4 runs hold <= 4 x 512 floats, so a lane has at most 8 float4
+    // (or 32 float) slots E = lane*VW + 64*VW*u over the concatenated runs.
+    const int im = g0 / a.th, ty0 = g0 - im * a.th;
+    const int orows = min(4 * nrows, a.OH - 4 * ty0);
+    const int count = orows * a.OW;
+    const int64_t row0 = (int64_t)4 * ty0 * a.OW;
+    const int nk_w = min(4, max(0, (a.K - k0 - wave + 7) / 8));  // this wave's channels
+    auto slot = [&](int E, int& j, int64_t& o, int& yo) {
+      j = E / count;
+      const int e = E - j * count;
+      const int i = e / a.OW, x = e - i * a.OW;
+      const int kk = wave + 8 * j;
+      o = ((int64_t)im * a.K + k0 + kk) * OHW + row0 + e;
+      yo = (kk * kTB + (i >> 2) * a.tw + (x >> 2)) * kYS + (i & 3) * 4 + (x & 3);
+    };
+    if (a.OW % 4 == 0) {
+      v4f res[8];
+      int64_t o[8];
+      int yo[8], jj[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int E = lane * 4 + 256 * u;
+        res[u] = v4f{0.f, 0.f, 0.f, 0.f};
+        jj[u] = -1;
+        if (E < nk_w * count) {
+          slot(E, jj[u], o[u], yo[u]);
+          if (FINAL && a.residual) res[u] = *reinterpret_cast<const v4f*>(a.residual + o[u]);
         }
-        *reinterpret_cast<float4*>(a.out + row) = make_float4(o[0], o[1], o[2], o[3]);
-      } else {
+      }
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          if (tx * 4 + j < a.OW) {
-            float v = y[j] + b;
-            if (a.residual) v += a.residual[row + j];
-            if (a.act == NHIP_ACT_RELU) v = v < 0.f ? 0.f : v;
-            else if (a.act == NHIP_ACT_SIGMOID) v = __frcp_rn(1.0f + __expf(-v));
-            a.out[row + j] = v;
-          }
+      for (int u = 0; u < 8; ++u) {
+        if (jj[u] < 0) continue;
+        const v4f y = *reinterpret_cast<const v4f*>(lds + yo[u]);
+        const float b = jj[u] == 0 ? bias4[0] : jj[u] == 1 ? bias4[1] : jj[u] == 2 ? bias4[2] : bias4[3];
+        v4f v;
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4) v[q4] = activate<ACT>(y[q4] + b + res[u][q4]);
+        *reinterpret_cast<v4f*>(dst + o[u]) = v;
+      }
+    } else {
+      float res[32];
+      int64_t o[32];
+      int yo[32], jj[32];
+#pragma unroll
+      for (int u = 0; u < 32; ++u) {
+        const int E = lane + 64 * u;
+        res[u] = 0.f;
+        jj[u] = -1;
+        if (E < nk_w * count) {
+          slot(E, jj[u], o[u], yo[u]);
+          if (FINAL && a.residual) res[u] = a.residual[o[u]];
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < 32; ++u) {
+        if (jj[u] < 0) continue;
+        const float b = jj[u] == 0 ? bias4[0] : jj[u] == 1 ? bias4[1] : jj[u] == 2 ? bias4[2] : bias4[3];
+        dst[o[u]] = activate<ACT>(lds[yo[u]] + b + res[u]);
+      }
+    }
+    return;
+  }
+  // mode 2: a cut tile row, written one pixel row at a time per channel.
+  {
+    const int im = g0 / a.th, ty = g0 - im * a.th;
+    const int rows = min(4, a.OH - 4 * ty);
+    const int x_base = 4 * tx_a;
+    const int cols = min(4 * ntiles, a.OW - x_base);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int kk = wave + 8 * j, k = k0 + kk;
+      if (k >= a.K) break;
+      const float* ys = lds + kk * kTB * kYS;
+      for (int i = 0; i < rows; ++i) {
+        const int64_t base = (((int64_t)im * a.K + k) * a.OH + 4 * ty + i) * a.OW + x_base;
+        for (int x = lane; x < cols; x += 64) {
+          const float r = (FINAL && a.residual) ? a.residual[base + x] : 0.f;
+          dst[base + x] = activate<ACT>(ys[(x >> 2) * kYS + i * 4 + (x & 3)] + bias4[j] + r);
         }
       }
     }
   }
 }
 
-template <int WK, int WT, int WC, int S>
-int launch_cfg(const FusedArgs& a, hipStream_t s, const char* name) {
-  using Cfg = FusedCfg<WK, WT, WC, S>;
-  const size_t lds = (size_t)(Cfg::V_ELEMS + Cfg::U_ELEMS) * sizeof(float);
-  const dim3 grid((unsigned)ceil_div(a.T, Cfg::TB), (unsigned)ceil_div(a.K, Cfg::KB));
+// out = act(sum_s part[s] + bias[k] (+ residual)), parts [splits][N][K][OH][OW];
+// VEC = 4 when OH*OW % 4 == 0 (a float4 never crosses a channel plane).
+template <int VEC, int ACT>
+__global__ void wino_fused_reduce(const float* __restrict__ part, int splits, int64_t total, int ohw, int K,
+                                  const float* __restrict__ bias, const float* __restrict__ residual,
+                                  float* __restrict__ out) {
+  const int64_t idx = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * VEC;
+  if (idx >= total) return;
+  const float b = bias[(int)((idx / ohw) % K)];
+  if constexpr (VEC == 4) {
+    v4f s = *reinterpret_cast<const v4f*>(part + idx);
+    for (int z = 1; z < splits; ++z) s += *reinterpret_cast<const v4f*>(part + (int64_t)z * total + idx);
+    v4f r = v4f{0.f, 0.f, 0.f, 0.f};
+    if (residual) r = *reinterpret_cast<const v4f*>(residual + idx);
+    v4f o;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) o[j] = activate<ACT>(s[j] + b + r[j]);
+    *reinterpret_cast<v4f*>(out + idx) = o;
+  } else {
+    float s = part[idx];
+    for (int z = 1; z < splits; ++z) s += part[(int64_t)z * total + idx];
+    float v = s + b;
+    if (residual) v += residual[idx];
+    out[idx] = activate<ACT>(v);
+  }
+}
+
+template <int ACT, bool FINAL>
+int launch_kernel(const FusedArgs& a, int64_t blocks, hipStream_t s) {
   static bool attr_set = false;  // dynamic LDS above 64 KB needs the attribute
   if (!attr_set) {
-    NHIP_TRY(check_hip(hipFuncSetAttribute(reinterpret_cast<const void*>(&wino_fused_kernel<WK, WT, WC, S>),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
+    NHIP_TRY(check_hip(hipFuncSetAttribute(reinterpret_cast<const void*>(&wino_fused_kernel<ACT, FINAL>),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes),
                        "hipFuncSetAttribute(wino_fused)"));
     attr_set = true;
   }
-  NHIP_LAUNCH(name, (wino_fused_kernel<WK, WT, WC, S>), grid, dim3(kThreads), lds, s, a);
-  return check_launch(name);
+  NHIP_LAUNCH("wino_fused", (wino_fused_kernel<ACT, FINAL>), dim3((unsigned)blocks), dim3(kThreads), kLdsBytes, s,
+              a);
+  return check_launch("wino_fused");
+}
+
+template <int VEC, int ACT>
+int launch_reduce(const float* parts, int splits, int64_t total, int ohw, int K, const float* bias,
+                  const float* residual, float* out, hipStream_t s) {
+  NHIP_LAUNCH("wino_fused_reduce", (wino_fused_reduce<VEC, ACT>), dim3((unsigned)ceil_div(total / VEC, 256)),
+              dim3(256), 0, s, parts, splits, total, ohw, K, bias, residual, out);
+  return check_launch("wino_fused_reduce");
+}
+
+struct FusedShape {
+  int th, tw, G, mode, R, bpi, bpr, nt, nk, nch, splits, per;
+};
+
+// Tile blocks (whole tile rows, or 32-tile pieces of wider rows); channel
+// splits: the fewest that minimise (rounds of one workgroup per CU) x
+// (chunks per workgroup), each split keeping at least 4 chunks.
+FusedShape fused_shape(const nhip_conv_plan* p, int n, int oh, int ow) {
+  FusedShape f;
+  f.th = (int)ceil_div(oh, 4);
+  f.tw = (int)ceil_div(ow, 4);
+  f.G = n * f.th;
+  f.bpi = f.bpr = 0;
+  if (f.tw <= kTB && f.th <= kTB / f.tw) {
+    f.mode = 0;
+    f.R = kTB / f.tw / f.th * f.th;
+    f.nt = (int)ceil_div(f.G, f.R);
+  } else if (f.tw <= kTB) {
+    f.mode = 1;
+    f.R = kTB / f.tw;
+    f.bpi = (int)ceil_div(f.th, f.R);
+    f.nt = n * f.bpi;
+  } else {
+    f.mode = 2;
+    f.R = 1;
+    f.bpr = (int)ceil_div(f.tw, kTB);
+    f.nt = f.G * f.bpr;
+  }
+  f.nk = (int)ceil_div(p->g.k, kKB);
+  f.nch = p->c_pad / kCB;
+  const int64_t cus = cu_count();
+  const int64_t blocks = (int64_t)f.nt * f.nk;
+  f.splits = 1;
+  int64_t best = ceil_div(blocks, cus) * f.nch;
+  for (int s = 2; s <= 8 && ceil_div(f.nch, s) >= 4; s *= 2) {
+    const int64_t cost = ceil_div(blocks * s, cus) * ceil_div(f.nch, s);
+    if (cost < best) {
+      best = cost;
+      f.splits = s;
+    }
+  }
+  f.per = (int)ceil_div(f.nch, f.splits);
+  return f;
 }
 
 }  // namespace
 
-// Workgroup shape: 2x2x1 (32 channels x 32 tiles per workgroup, full channel
-// reduction per wave) when that alone gives at least one workgroup per CU;
-// otherwise 1x1x4 (16 x 16 per workgroup, channel reduction split over the
-// four waves).  NHIP_WINOGRAD_VARIANT=221|114 forces one.
-int launch_conv_winograd_fused(const nhip_conv_plan* p, const float* in, const float* residual,
-                               float* out, int n, int h, int w, int oh, int ow, hipStream_t s) {
+uint64_t wino_gemm_out_parts_bytes(const nhip_conv_plan* p, int n, int oh, int ow) {
+  const FusedShape f = fused_shape(p, n, oh, ow);
+  return f.splits > 1 ? (uint64_t)f.splits * n * p->g.k * oh * ow * sizeof(float) : 0;
+}
+
+int launch_wino_gemm_out(const nhip_conv_plan* p, const float* V, int t_pad, const float* residual, float* out,
+                         int n, int oh, int ow, float* parts, hipStream_t s) {
+  const size_t v_bytes = (size_t)36 * p->c_pad * t_pad * sizeof(float);
+  const size_t u_bytes = (size_t)36 * p->m_pad * p->c_pad * sizeof(float);
+  if (v_bytes >= (size_t(1) << 31) || u_bytes >= (size_t(1) << 31))
+    return fail(NHIP_STATUS_CONSTRAINT_VIOLATION, "winograd GEMM: transformed input or weights above 2 GiB");
+  if (p->c_pad % kCB != 0 || p->m_pad % kKB != 0 || t_pad % kTB != 0)
+    return fail(NHIP_STATUS_CONSTRAINT_VIOLATION, "winograd GEMM: padding mismatch");
+  if ((reinterpret_cast<uintptr_t>(out) & 15) || (residual && (reinterpret_cast<uintptr_t>(residual) & 15)) ||
+      (reinterpret_cast<uintptr_t>(parts) & 15) || (reinterpret_cast<uintptr_t>(V) & 15))
+    return fail(NHIP_STATUS_CONSTRAINT_VIOLATION, "winograd: buffers must be 16-byte aligned");
+  const FusedShape f = fused_shape(p, n, oh, ow);
+  if (f.splits > 1 && parts == nullptr)
+    return fail(NHIP_STATUS_NULL_POINTER, "winograd GEMM: partial-sum workspace missing");
   FusedArgs a{};
-  a.x = in;
-  a.x_bytes = (uint32_t)((size_t)n * p->g.c * h * w * sizeof(float));
-  a.U = p->weight;
+  a.V = V;
+  a.v_bytes = (uint32_t)v_bytes;
+  a.U = p->weight_fused;
+  a.u_bytes = (uint32_t)u_bytes;
   a.bias = p->bias;
   a.residual = residual;
-  a.out = out;
-  a.C = p->g.c;
-  a.H = h;
-  a.W = w;
+  a.out = f.splits > 1 ? parts : out;
   a.K = p->g.k;
   a.OH = oh;
   a.OW = ow;
-  a.th = (int)ceil_div(oh, 4);
-  a.tw = (int)ceil_div(ow, 4);
-  a.T = n * a.th * a.tw;
+  a.th = f.th;
+  a.tw = f.tw;
+  a.T = n * f.th * f.tw;
+  a.mode = f.mode;
+  a.R = f.R;
+  a.bpi = f.bpi;
+  a.bpr = f.bpr;
+  a.G = f.G;
+  a.t_pad = t_pad;
   a.m_pad = p->m_pad;
   a.c_pad = p->c_pad;
-  a.pt = p->g.pt;
-  a.pl = p->g.pl;
-  a.act = p->g.act;
-  if ((reinterpret_cast<uintptr_t>(out) & 15) || (residual && (reinterpret_cast<uintptr_t>(residual) & 15)))
-    return fail(NHIP_STATUS_CONSTRAINT_VIOLATION, "winograd: output/residual must be 16-byte aligned");
-  int variant = 0;
-  if (const char* env = std::getenv("NHIP_WINOGRAD_VARIANT")) variant = std::atoi(env);
-  if (variant != 221 && variant != 114) {
-    const int64_t blocks221 = ceil_div(a.T, 32) * ceil_div(a.K, 32);
-    variant = blocks221 >= cu_count() ? 221 : 114;
+  a.nt = f.nt;
+  a.nk = f.nk;
+  a.splits = f.splits;
+  a.per = f.per;
+  const int64_t blocks = (int64_t)f.nt * f.nk * f.splits;
+  if (f.splits == 1) {
+    switch (p->g.act) {
+      case NHIP_ACT_NONE: return launch_kernel<NHIP_ACT_NONE, true>(a, blocks, s);
+      case NHIP_ACT_RELU: return launch_kernel<NHIP_ACT_RELU, true>(a, blocks, s);
+      case NHIP_ACT_SIGMOID: return launch_kernel<NHIP_ACT_SIGMOID, true>(a, blocks, s);
+      default: return fail(NHIP_STATUS_UNSUPPORTED, "winograd GEMM: unsupported activation");
+    }
   }
-  if (variant == 221) return launch_cfg<2, 2, 1, 2>(a, s, "wino_fused<2,2,1>");
-  return launch_cfg<1, 1, 4, 1>(a, s, "wino_fused<1,1,4>");
+  NHIP_TRY((launch_kernel<NHIP_ACT_NONE, false>(a, blocks, s)));
+  const int64_t total = (int64_t)n * p->g.k * oh * ow;
+  const int ohw = oh * ow;
+#define NHIP_REDUCE(V_)                                                                                       \
+  switch (p->g.act) {                                                                                         \
+    case NHIP_ACT_RELU: return launch_reduce<V_, NHIP_ACT_RELU>(parts, f.splits, total, ohw, p->g.k, p->bias, \
+                                                                residual, out, s);                            \
+    case NHIP_ACT_SIGMOID:                                                                                    \
+      return launch_reduce<V_, NHIP_ACT_SIGMOID>(parts, f.splits, total, ohw, p->g.k, p->bias, residual, out, s); \
+    default: return launch_reduce<V_, NHIP_ACT_NONE>(parts, f.splits, total, ohw, p->g.k, p->bias, residual, out, s); \
+  }
+  if (ohw % 4 == 0) {
+    NHIP_REDUCE(4)
+  } else {
+    NHIP_REDUCE(1)
+  }
+#undef NHIP_REDUCE
 }
 
 }  // namespace nhip
