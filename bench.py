@@ -11,13 +11,15 @@ add: 8 Winograd F(4,3) convolutions over 32 images whose inputs are already
 resident in HBM.
 
 value = direct-equivalent conv TFLOP/s (2*N*K*OH*OW*C*9 per conv, the same
-count for Winograd as for direct convolution).  roofline = the Winograd
-batched-GEMM kernel (36 fp32 MFMA GEMMs per conv, the dominant kernel): its
+count for Winograd as for direct convolution).  roofline = the dominant
+kernel, the Winograd GEMM with the output transform fused (wino_fused: 36
+fp32 MFMA GEMMs and the output transform per conv; it runs the three stages
+with at least 256 tiles, the 512@7 stage takes the three-kernel path): its
 work 2*36*T*C*K per launch (T = N*ceil(OH/4)*ceil(OW/4) tiles) over its
-average duration, from HIP events stamped by each of its dispatches on the
-launch stream inside the timed region; traffic = its HBM bytes per launch
-from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary
-(profiles/wino_gemm_traffic.json).  cpu_baseline = the
+duration, from HIP events stamped by each of its dispatches on the launch
+stream inside the timed region; traffic = its HBM bytes per launch from the
+committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary
+(profiles/wino_fused_traffic.json).  cpu_baseline = the
 CPU oracle (restatement of the reference's lowered loops, compiled like the
 reference's .so: -O3, no -march, no FP contraction, OpenMP) on a bounded
 sample of the same stages.
@@ -135,19 +137,23 @@ def mobilenetv2_secondary(torch, steps, warmup):
             "ms_per_step": dt * 1e3, "images_per_sec": BATCH / dt, "tflops": flops / dt / 1e12}
 
 
-def measured_traffic(fused):
-    """HBM bytes per launch of the Winograd GEMM, from the committed
-    rocprofv3 FETCH_SIZE / WRITE_SIZE summary (profiles/wino_gemm_traffic.json,
-    averaged over the four stage shapes, copy-calibrated); None for the fused
-    variant, which that summary does not cover."""
-    if fused:
-        return None
+def measured_traffic(kernel):
+    """HBM bytes per launch of `kernel`, from the committed rocprofv3
+    FETCH_SIZE / WRITE_SIZE summary (profiles/<kernel>_traffic.json, averaged
+    over the stage shapes it runs, copy-calibrated); None if absent."""
     try:
-        with open(os.path.join(ROOT, "profiles", "wino_gemm_traffic.json")) as f:
+        with open(os.path.join(ROOT, "profiles", f"{kernel}_traffic.json")) as f:
             d = json.load(f)
-        return int(d["bytes_per_launch"]) if d.get("kernel") == "wino_gemm" else None
+        return int(d["bytes_per_launch"]) if d.get("kernel") == kernel else None
     except (OSError, ValueError, KeyError):
         return None
+
+
+def fused_stage(c, hw):
+    """The library's default Winograd path choice: the fused GEMM from 256
+    tiles up (winograd.hip, fused_selected)."""
+    t = -(-hw // 4)
+    return BATCH * t * t >= 256
 
 
 def main():
@@ -185,26 +191,31 @@ def main():
         run_step(stages)
     torch.cuda.synchronize()
 
-    fused = os.environ.get("NHIP_WINOGRAD_VARIANT", "") == "2"
-    nhip.timer_start("wino_fused" if fused else "wino_gemm")
+    variant = os.environ.get("NHIP_WINOGRAD_VARIANT", "")
+    fused_convs = [(c, hw) for c, hw in workloads.RESNET18_STAGES
+                   if variant == "2" or (variant != "1" and fused_stage(c, hw))]
+    kernel = "wino_fused" if fused_convs else "wino_gemm"
+    kernel_convs = fused_convs or list(workloads.RESNET18_STAGES)
+    nhip.timer_start(kernel)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
         run_step(stages)
     torch.cuda.synchronize()
     t1 = time.perf_counter()
-    launches, gemm_ms = nhip.timer_stop()
+    launches, kernel_ms = nhip.timer_stop()
 
     ms_per_step = (t1 - t0) * 1e3 / args.steps
     direct_flops = sum(2 * workloads.conv_flops(BATCH, c, c, hw, hw) for c, hw in workloads.RESNET18_STAGES)
     wino_flops = sum(2 * workloads.winograd_flops(BATCH, c, c, hw, hw) for c, hw in workloads.RESNET18_STAGES)
+    kernel_flops = sum(2 * workloads.winograd_flops(BATCH, c, c, hw, hw) for c, hw in kernel_convs)
     value = direct_flops / (ms_per_step / 1e3) / 1e12
-    # 8 convs per step; each runs as one or two batch parts (one GEMM launch each)
-    gemm_launches_per_step = launches // args.steps
-    assert launches % args.steps == 0 and gemm_launches_per_step in (8, 16), (launches, args.steps)
-    avg_gemm_s = gemm_ms / launches / 1e3
-    achieved = (wino_flops / gemm_launches_per_step) / avg_gemm_s / 1e12
-
+    # two convs per stage; each runs as one or two batch parts (one kernel launch each)
+    per_step = launches // args.steps
+    assert launches % args.steps == 0 and per_step in (2 * len(kernel_convs), 4 * len(kernel_convs)), \
+        (launches, args.steps, kernel_convs)
+    kernel_s_per_step = kernel_ms / args.steps / 1e3
+    achieved = kernel_flops / kernel_s_per_step / 1e12
     int8 = int8_secondary(nhip, workloads, torch, args.steps, args.warmup)
     mbv2 = mobilenetv2_secondary(torch, args.steps, args.warmup)
     result = {
@@ -232,13 +243,15 @@ def main():
         },
         "roofline": {
             "bound": "mfma",
-            "kernel": "wino_gemm (36 batched fp32 MFMA GEMMs per conv)",
+            "kernel": ("wino_fused (36 batched fp32 MFMA GEMMs + output transform per conv; stages "
+                       + ", ".join(f"{c}@{hw}" for c, hw in kernel_convs) + ")") if kernel == "wino_fused"
+                      else "wino_gemm (36 batched fp32 MFMA GEMMs per conv)",
             "achieved": round(achieved, 3),
             "peak": PEAK_FP32_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(achieved / PEAK_FP32_TFLOPS, 4),
-            "traffic": measured_traffic(fused),
-            "avg_launch_us": round(avg_gemm_s * 1e6, 2),
+            "traffic": measured_traffic(kernel),
+            "avg_launch_us": round(kernel_s_per_step / per_step * 1e6, 2),
             "launches_timed": launches,
         },
     }

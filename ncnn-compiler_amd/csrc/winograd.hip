@@ -31,7 +31,9 @@ uint64_t wino_gemm_out_parts_bytes(const nhip_conv_plan* p, int n, int oh, int o
 // Path selection: input transform + GEMM with the output transform fused
 // (winograd_fused.hip), or the three-kernel path (M through HBM).
 // NHIP_WINOGRAD_VARIANT = 1 forces the three-kernel path, 2 the fused GEMM
-// (where its limits allow); unset or 0 chooses by shape.
+// (where its limits allow); unset or 0 chooses by shape: the fused GEMM from
+// 256 tiles up (on MI355X it measures faster there; with fewer tiles its
+// channel-split partial sums cost more than the M round trip saves).
 static int variant_requested() {
   const char* env = std::getenv("NHIP_WINOGRAD_VARIANT");
   return (env && *env) ? std::atoi(env) : 0;
@@ -44,7 +46,7 @@ static bool fused_selected(const nhip_conv_plan* p, int n, int oh, int ow) {
   const int v = variant_requested();
   if (v == 1) return false;
   if (v == 2) return true;
-  return false;
+  return (int64_t)n * ceil_div(oh, 4) * ceil_div(ow, 4) >= 256;
 }
 
 namespace {

@@ -51,6 +51,7 @@ constexpr int kProducers = 256;               // load threads
 constexpr int kULoads = kUElems / 4 / kProducers;  // 16-byte U loads per thread and chunk
 constexpr int kVLoads = kVElems / 4 / kProducers;  // 16-byte V loads per thread and chunk
 constexpr int kXcds = 8;                      // MI355X: workgroup L runs on XCD L % 8
+static_assert(kLdsBytes >= kKB * kTB * 16 * (int)sizeof(float), "the staged output tiles fit in the chunk slots");
 static_assert(kUElems % (4 * kProducers) == 0 && kVElems % (4 * kProducers) == 0,
               "whole 16-byte loads per thread");
 static_assert(kTB == 32 && kKB == 32 && kCB == 8, "the load mappings below assume 32 x 32 x 8");
@@ -148,108 +149,61 @@ __device__ __forceinline__ void load_role(const FusedArgs& a, float* lds, int p,
   }
 }
 
-// FINAL: write act(Y + bias (+ residual)) with activation ACT; otherwise
-// the raw part of channel split cs for wino_fused_reduce.
-template <int ACT, bool FINAL>
-__global__ __launch_bounds__(kThreads, 1) void wino_fused_kernel(FusedArgs a) {
-  extern __shared__ __attribute__((aligned(16))) float lds[];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+// A workgroup's share of the work: tile block tb (mode 0/1/2 above), output
+// channels k0 .. k0 + 31, and chunks ch_begin .. ch_begin + n - 1 of channel
+// split cs (chunks of `cb` input channels).
+struct Block {
+  int tb, kb, cs, k0, g0, nrows, tx_a, t0, ntiles, ch_begin, n;
+};
 
+__device__ __forceinline__ Block block_of(const FusedArgs& a, int cb) {
+  Block b;
   // XCD-contiguous renumbering: each XCD gets a contiguous range of logical
   // blocks, ordered (tile block, split, channel block) with the channel
-  // block fastest, so the workgroups that read the same input patches share
-  // an L2.
-  int tb, kb, cs;
+  // block fastest, so the workgroups that read the same V slices share an L2.
   {
     const int total = a.nt * a.nk * a.splits;
     const int L = blockIdx.x;
     const int x = L % kXcds, q = L / kXcds;
     const int logical = x * (total / kXcds) + min(x, total % kXcds) + q;
-    kb = logical % a.nk;
+    b.kb = logical % a.nk;
     const int rest = logical / a.nk;
-    cs = rest % a.splits;
-    tb = rest / a.splits;
+    b.cs = rest % a.splits;
+    b.tb = rest / a.splits;
   }
-  const int k0 = kb * kKB;
-  int g0, nrows, tx_a, t0, ntiles;
+  b.k0 = b.kb * kKB;
   if (a.mode == 0) {
-    g0 = tb * a.R;
-    nrows = min(a.R, a.G - g0);
-    tx_a = 0;
+    b.g0 = b.tb * a.R;
+    b.nrows = min(a.R, a.G - b.g0);
+    b.tx_a = 0;
   } else if (a.mode == 1) {
-    const int im = tb / a.bpi, ty0 = (tb - im * a.bpi) * a.R;
-    g0 = im * a.th + ty0;
-    nrows = min(a.R, a.th - ty0);
-    tx_a = 0;
+    const int im = b.tb / a.bpi, ty0 = (b.tb - im * a.bpi) * a.R;
+    b.g0 = im * a.th + ty0;
+    b.nrows = min(a.R, a.th - ty0);
+    b.tx_a = 0;
   } else {
-    g0 = tb / a.bpr;
-    nrows = 1;
-    tx_a = (tb - g0 * a.bpr) * kTB;
+    b.g0 = b.tb / a.bpr;
+    b.nrows = 1;
+    b.tx_a = (b.tb - b.g0 * a.bpr) * kTB;
   }
-  t0 = g0 * a.tw + tx_a;
-  ntiles = a.mode == 2 ? min(kTB, a.tw - tx_a) : nrows * a.tw;
-  const int nch = a.c_pad / kCB;
-  const int ch_begin = cs * a.per;
-  const int n = max(0, min(nch, ch_begin + a.per) - ch_begin);
-  float* dst = a.out + (FINAL ? 0 : (int64_t)cs * (a.G / a.th) * a.K * a.OH * a.OW);
-  constexpr int kYS = 20;  // LDS row of one (k, tile) output tile: 16 values + 4 pad (conflict-free)
+  b.t0 = b.g0 * a.tw + b.tx_a;
+  b.ntiles = a.mode == 2 ? min(kTB, a.tw - b.tx_a) : b.nrows * a.tw;
+  const int nch = a.c_pad / cb;
+  b.ch_begin = b.cs * a.per;
+  b.n = max(0, min(nch, b.ch_begin + a.per) - b.ch_begin);
+  return b;
+}
 
-  if (wave >= 4) {
-    load_role(a, lds, tid - 4 * 64, t0, k0, ch_begin, n);
-  } else {
-  // ---- MFMA waves ------------------------------------------------------------
-  const int li = lane & 15, q = lane >> 4;
-  const int wk = wave & 1, wt = wave >> 1;
-  // Lane (li, q) supplies reduction index q at MFMA step s as channel 2q + s
-  // of the chunk, for both operands: A = U[k = wk*16 + li], B = V[t = wt*16 + li].
-  const int ua_off = kVElems + (q * kKB + wk * 16 + li) * 2;
-  const int vb_off = (q * kTB + wt * 16 + li) * 2;
+// Output tiles staged in LDS: Ys[k][tile][16] (64 KB for 32 x 32), the four
+// 4-float rows of a tile rotated by the tile index so that the MFMA lanes'
+// 16-byte writes of consecutive tiles spread over the banks.
+__device__ __forceinline__ int ys_off(int kk, int tl, int i) {
+  return (kk * kTB + tl) * 16 + ((i ^ tl) & 3) * 4;
+}
 
-  v4f acc[36];
-#pragma unroll
-  for (int xi = 0; xi < 36; ++xi) acc[xi] = v4f{0.f, 0.f, 0.f, 0.f};
-
-  // Operands are read in groups of kG transform points, one group ahead of
-  // the MFMAs that use them; a scheduling fence per group keeps the compiler
-  // from hoisting all 72 reads (which would not fit in registers beside the
-  // 144 accumulators).
-  constexpr int kG = 4, kGroups = 36 / kG;
-  for (int i = 0; i <= n; ++i) {
-    if (i > 0) {
-      const float* slot = lds + ((i - 1) & 1) * kSlotElems;
-      const float* ua = slot + ua_off;
-      const float* vb = slot + vb_off;
-      v2f av[2][kG], bv[2][kG];
-      auto read_group = [&](int g, int buf) {
-#pragma unroll
-        for (int j = 0; j < kG; ++j) {
-          av[buf][j] = *reinterpret_cast<const v2f*>(ua + (g * kG + j) * kKB * kCB);
-          bv[buf][j] = *reinterpret_cast<const v2f*>(vb + (g * kG + j) * kTB * kCB);
-        }
-      };
-      read_group(0, 0);
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int g = 0; g < kGroups; ++g) {
-        if (g + 1 < kGroups) read_group(g + 1, (g + 1) & 1);
-#pragma unroll
-        for (int s = 0; s < 2; ++s)
-#pragma unroll
-          for (int j = 0; j < kG; ++j)
-            acc[g * kG + j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[g & 1][j][s], bv[g & 1][j][s],
-                                                                  acc[g * kG + j], 0, 0, 0);
-        // order within the group: the next group's LDS reads, then this
-        // group's MFMAs
-        if (g + 1 < kGroups) __builtin_amdgcn_sched_group_barrier(0x100, kG, 0);
-        __builtin_amdgcn_sched_group_barrier(0x008, 2 * kG, 0);
-        __builtin_amdgcn_sched_barrier(0);
-      }
-    }
-    __syncthreads();  // matches the transform waves' barrier of iteration i
-  }
-
-  // ---- output transform Y = A^T M A, into LDS as Ys[k][tile][kYS] ------------
-  // (both slots are free: every wave has passed the last chunk's barrier)
+// Y = A^T M A for the lane's four (k, tile) pairs of the 16x16 MFMA layout
+// (wave (wk, wt), lane (li, q)), into Ys.
+__device__ __forceinline__ void y_to_lds(const v4f (&acc)[36], float* lds, int wk, int wt, int li, int q) {
   const int tl = wt * 16 + li;
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
@@ -264,145 +218,236 @@ __global__ __launch_bounds__(kThreads, 1) void wino_fused_kernel(FusedArgs a) {
       tmp[2][j] = s12 + 4.f * s34;
       tmp[3][j] = d12 + 8.f * d34 + m5;
     }
-    float* yrow = lds + ((wk * 16 + 4 * q + r) * kTB + tl) * kYS;
+    const int kk = wk * 16 + 4 * q + r;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const float m0 = tmp[i][0], m1 = tmp[i][1], m2 = tmp[i][2], m3 = tmp[i][3], m4 = tmp[i][4], m5 = tmp[i][5];
       const float s12 = m1 + m2, d12 = m1 - m2, s34 = m3 + m4, d34 = m3 - m4;
-      *reinterpret_cast<v4f*>(yrow + i * 4) =
+      *reinterpret_cast<v4f*>(lds + ys_off(kk, tl, i)) =
           v4f{m0 + s12 + s34, d12 + 2.f * d34, s12 + 4.f * s34, d12 + 8.f * d34 + m5};
     }
   }
-  }  // MFMA waves
-  __syncthreads();
+}
 
-  // ---- write-out by all 8 waves: wave w takes channels w, w+8, w+16, w+24 ------
-  // Outputs are written in memory order.  All residual loads of a wave are
-  // issued before its first store: vmcnt counts loads and stores in issue
-  // order, so a load issued after a store would make its wait include the
-  // store.
+// Write-out of the staged tiles by NW waves, wave w taking channels w + NW*j.
+// Outputs are written in memory order.  All residual loads of a group of
+// four channels are issued before its first store: vmcnt counts loads and
+// stores in issue order, so a load issued after a store would make its wait
+// include the store.  FINAL: act(Y + bias (+ residual)); otherwise the raw
+// part of channel split b.cs for wino_fused_reduce.
+template <int NW, int ACT, bool FINAL>
+__device__ __forceinline__ void write_out(const FusedArgs& a, const Block& bk, const float* lds, int lane,
+                                          int wave) {
+  constexpr int JW = kKB / NW;  // channels per wave
+  float* dst = a.out + (FINAL ? 0 : (int64_t)bk.cs * (a.G / a.th) * a.K * a.OH * a.OW);
   const int OHW = a.OH * a.OW;
-  float bias4[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int k = k0 + wave + 8 * j;
-    bias4[j] = (FINAL && k < a.K) ? a.bias[k] : 0.f;
-  }
+  const int k0 = bk.k0;
   if (a.mode == 0) {
     // Whole images: per (image, channel) plane P = OH*OW <= 16 * 32 floats; a
-    // lane's pixels p = lane + 64m (m < 8) and their LDS offsets are
-    // computed once.  Wave w writes planes (image, channel) = (il, w + 8j).
-    int yoff[8];
+    // lane's pixels p = lane + 64m (m < 8) and their (tile, row, column)
+    // within the image are computed once, packed as tile*16 + row*4 + column.
+    int tij[8];
 #pragma unroll
     for (int m = 0; m < 8; ++m) {
       const int pix = lane + 64 * m;
       const int oy = pix / a.OW, ox = pix - (pix / a.OW) * a.OW;
-      yoff[m] = pix < OHW ? ((oy >> 2) * a.tw + (ox >> 2)) * kYS + (oy & 3) * 4 + (ox & 3) : -1;
+      tij[m] = pix < OHW ? ((oy >> 2) * a.tw + (ox >> 2)) * 16 + (oy & 3) * 4 + (ox & 3) : -1;
     }
-    const int nimg = nrows / a.th;
-    const int im0 = g0 / a.th;
+    const int nimg = bk.nrows / a.th;
+    const int im0 = bk.g0 / a.th;
+    const int img_tiles = a.th * a.tw;
     for (int il = 0; il < nimg; ++il) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int kk = wave + 8 * j, k = k0 + kk;
+      for (int j = 0; j < JW; ++j) {
+        const int kk = wave + NW * j, k = k0 + kk;
         if (k >= a.K) break;
-        const float* ys = lds + (kk * kTB + il * a.th * a.tw) * kYS;
+        const float b = FINAL ? a.bias[k] : 0.f;
         const int64_t base = ((int64_t)(im0 + il) * a.K + k) * OHW;
         float res[8];
 #pragma unroll
         for (int m = 0; m < 8; ++m)
-          res[m] = (FINAL && a.residual && yoff[m] >= 0) ? a.residual[base + lane + 64 * m] : 0.f;
+          res[m] = (FINAL && a.residual && tij[m] >= 0) ? a.residual[base + lane + 64 * m] : 0.f;
 #pragma unroll
         for (int m = 0; m < 8; ++m)
-          if (yoff[m] >= 0) dst[base + lane + 64 * m] = activate<ACT>(ys[yoff[m]] + bias4[j] + res[m]);
+          if (tij[m] >= 0) {
+            const int tl = il * img_tiles + (tij[m] >> 4);
+            const float y = lds[ys_off(kk, tl, (tij[m] >> 2) & 3) + (tij[m] & 3)];
+            dst[base + lane + 64 * m] = activate<ACT>(y + b + res[m]);
+          }
       }
     }
     return;
   }
   if (a.mode == 1) {
-    // One contiguous run of count = orows x OW floats per channel; the
-    // wave's 4 runs hold <= 4 x 512 floats, so a lane has at most 8 float4
-    // (or 32 float) slots E = lane*VW + 64*VW*u over the concatenated runs.
-    const int im = g0 / a.th, ty0 = g0 - im * a.th;
-    const int orows = min(4 * nrows, a.OH - 4 * ty0);
+    // One contiguous run of count = orows x OW floats per channel; a group
+    // of 4 channels holds <= 4 x 512 floats, i.e. <= 8 float4 (32 float)
+    // slots per lane, E = lane*VW + 64*VW*u over the group's runs.
+    const int im = bk.g0 / a.th, ty0 = bk.g0 - im * a.th;
+    const int orows = min(4 * bk.nrows, a.OH - 4 * ty0);
     const int count = orows * a.OW;
     const int64_t row0 = (int64_t)4 * ty0 * a.OW;
-    const int nk_w = min(4, max(0, (a.K - k0 - wave + 7) / 8));  // this wave's channels
-    auto slot = [&](int E, int& j, int64_t& o, int& yo) {
-      j = E / count;
-      const int e = E - j * count;
-      const int i = e / a.OW, x = e - i * a.OW;
-      const int kk = wave + 8 * j;
-      o = ((int64_t)im * a.K + k0 + kk) * OHW + row0 + e;
-      yo = (kk * kTB + (i >> 2) * a.tw + (x >> 2)) * kYS + (i & 3) * 4 + (x & 3);
-    };
-    if (a.OW % 4 == 0) {
-      v4f res[8];
-      int64_t o[8];
-      int yo[8], jj[8];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const int E = lane * 4 + 256 * u;
-        res[u] = v4f{0.f, 0.f, 0.f, 0.f};
-        jj[u] = -1;
-        if (E < nk_w * count) {
-          slot(E, jj[u], o[u], yo[u]);
-          if (FINAL && a.residual) res[u] = *reinterpret_cast<const v4f*>(a.residual + o[u]);
+    for (int jg = 0; jg < JW; jg += 4) {
+      // channels kk = wave + NW*(jg + j), j < 4
+      int nk_g = 0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) nk_g += (k0 + wave + NW * (jg + j) < a.K) ? 1 : 0;
+      float bias4[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int k = k0 + wave + NW * (jg + j);
+        bias4[j] = (FINAL && k < a.K) ? a.bias[k] : 0.f;
+      }
+      auto slot = [&](int E, int& j, int64_t& o, int& yo) {
+        j = E / count;
+        const int e = E - j * count;
+        const int i = e / a.OW, x = e - i * a.OW;
+        const int kk = wave + NW * (jg + j);
+        o = ((int64_t)im * a.K + k0 + kk) * OHW + row0 + e;
+        yo = ys_off(kk, (i >> 2) * a.tw + (x >> 2), i & 3) + (x & 3);
+      };
+      if (a.OW % 4 == 0) {
+        v4f res[8];
+        int64_t o[8];
+        int yo[8], jj[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const int E = lane * 4 + 256 * u;
+          res[u] = v4f{0.f, 0.f, 0.f, 0.f};
+          jj[u] = -1;
+          if (E < nk_g * count) {
+            slot(E, jj[u], o[u], yo[u]);
+            if (FINAL && a.residual) res[u] = *reinterpret_cast<const v4f*>(a.residual + o[u]);
+          }
         }
-      }
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        if (jj[u] < 0) continue;
-        const v4f y = *reinterpret_cast<const v4f*>(lds + yo[u]);
-        const float b = jj[u] == 0 ? bias4[0] : jj[u] == 1 ? bias4[1] : jj[u] == 2 ? bias4[2] : bias4[3];
-        v4f v;
+        for (int u = 0; u < 8; ++u) {
+          if (jj[u] < 0) continue;
+          const v4f y = *reinterpret_cast<const v4f*>(lds + yo[u]);
+          const float b = jj[u] == 0 ? bias4[0] : jj[u] == 1 ? bias4[1] : jj[u] == 2 ? bias4[2] : bias4[3];
+          v4f v;
 #pragma unroll
-        for (int q4 = 0; q4 < 4; ++q4) v[q4] = activate<ACT>(y[q4] + b + res[u][q4]);
-        *reinterpret_cast<v4f*>(dst + o[u]) = v;
-      }
-    } else {
-      float res[32];
-      int64_t o[32];
-      int yo[32], jj[32];
-#pragma unroll
-      for (int u = 0; u < 32; ++u) {
-        const int E = lane + 64 * u;
-        res[u] = 0.f;
-        jj[u] = -1;
-        if (E < nk_w * count) {
-          slot(E, jj[u], o[u], yo[u]);
-          if (FINAL && a.residual) res[u] = a.residual[o[u]];
+          for (int q4 = 0; q4 < 4; ++q4) v[q4] = activate<ACT>(y[q4] + b + res[u][q4]);
+          *reinterpret_cast<v4f*>(dst + o[u]) = v;
         }
-      }
+      } else {
+        float res[32];
+        int64_t o[32];
+        int yo[32], jj[32];
 #pragma unroll
-      for (int u = 0; u < 32; ++u) {
-        if (jj[u] < 0) continue;
-        const float b = jj[u] == 0 ? bias4[0] : jj[u] == 1 ? bias4[1] : jj[u] == 2 ? bias4[2] : bias4[3];
-        dst[o[u]] = activate<ACT>(lds[yo[u]] + b + res[u]);
+        for (int u = 0; u < 32; ++u) {
+          const int E = lane + 64 * u;
+          res[u] = 0.f;
+          jj[u] = -1;
+          if (E < nk_g * count) {
+            slot(E, jj[u], o[u], yo[u]);
+            if (FINAL && a.residual) res[u] = a.residual[o[u]];
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < 32; ++u) {
+          if (jj[u] < 0) continue;
+          const float b = jj[u] == 0 ? bias4[0] : jj[u] == 1 ? bias4[1] : jj[u] == 2 ? bias4[2] : bias4[3];
+          dst[o[u]] = activate<ACT>(lds[yo[u]] + b + res[u]);
+        }
       }
     }
     return;
   }
   // mode 2: a cut tile row, written one pixel row at a time per channel.
-  {
-    const int im = g0 / a.th, ty = g0 - im * a.th;
-    const int rows = min(4, a.OH - 4 * ty);
-    const int x_base = 4 * tx_a;
-    const int cols = min(4 * ntiles, a.OW - x_base);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int kk = wave + 8 * j, k = k0 + kk;
-      if (k >= a.K) break;
-      const float* ys = lds + kk * kTB * kYS;
-      for (int i = 0; i < rows; ++i) {
-        const int64_t base = (((int64_t)im * a.K + k) * a.OH + 4 * ty + i) * a.OW + x_base;
-        for (int x = lane; x < cols; x += 64) {
-          const float r = (FINAL && a.residual) ? a.residual[base + x] : 0.f;
-          dst[base + x] = activate<ACT>(ys[(x >> 2) * kYS + i * 4 + (x & 3)] + bias4[j] + r);
-        }
+  const int im = bk.g0 / a.th, ty = bk.g0 - im * a.th;
+  const int rows = min(4, a.OH - 4 * ty);
+  const int x_base = 4 * bk.tx_a;
+  const int cols = min(4 * bk.ntiles, a.OW - x_base);
+  for (int j = 0; j < JW; ++j) {
+    const int kk = wave + NW * j, k = k0 + kk;
+    if (k >= a.K) break;
+    const float b = FINAL ? a.bias[k] : 0.f;
+    for (int i = 0; i < rows; ++i) {
+      const int64_t base = (((int64_t)im * a.K + k) * a.OH + 4 * ty + i) * a.OW + x_base;
+      for (int x = lane; x < cols; x += 64) {
+        const float r = (FINAL && a.residual) ? a.residual[base + x] : 0.f;
+        dst[base + x] = activate<ACT>(lds[ys_off(kk, x >> 2, i) + (x & 3)] + b + r);
       }
     }
   }
+}
+
+// 8 waves, 4 load + 4 MFMA, chunks of 8 channels in 2 x 72 KB of LDS (one
+// workgroup per CU).  FINAL: write act(Y + bias (+ residual)) with
+// activation ACT; otherwise the raw part of channel split cs.
+template <int ACT, bool FINAL>
+__global__ __launch_bounds__(kThreads, 1) void wino_fused_kernel(FusedArgs a) {
+  extern __shared__ __attribute__((aligned(16))) float lds[];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const Block bk = block_of(a, kCB);
+
+  if (wave >= 4) {
+    load_role(a, lds, tid - 4 * 64, bk.t0, bk.k0, bk.ch_begin, bk.n);
+  } else {
+    // ---- MFMA waves ----------------------------------------------------------
+    const int li = lane & 15, q = lane >> 4;
+    const int wk = wave & 1, wt = wave >> 1;
+    // Lane (li, q) supplies reduction index q at MFMA step s as channel
+    // 2q + s of the chunk, for both operands: A = U[k = wk*16 + li],
+    // B = V[t = wt*16 + li].
+    const int ua_off = kVElems + (q * kKB + wk * 16 + li) * 2;
+    const int vb_off = (q * kTB + wt * 16 + li) * 2;
+
+    v4f acc[36];
+#pragma unroll
+    for (int xi = 0; xi < 36; ++xi) acc[xi] = v4f{0.f, 0.f, 0.f, 0.f};
+
+    // Operands are read in groups of kG transform points, one group ahead
+    // of the MFMAs that use them; a scheduling fence per group keeps the
+    // compiler from hoisting all 72 reads (which would not fit in registers
+    // beside the 144 accumulators).  The chunk barrier sits before the last
+    // group's MFMAs: by then every read of the chunk's slot has completed, so
+    // the barrier can release the slot, and the next chunk's first group is
+    // read while the last MFMAs run.  kGroups is even, so a chunk's first
+    // group always lands in register buffer 0.
+    constexpr int kG = 6, kGroups = 36 / kG;
+    static_assert(kGroups % 2 == 0, "static register buffer parity across chunks");
+    v2f av[2][kG], bv[2][kG];
+    auto read_group = [&](const float* slot, int g, int buf) {
+#pragma unroll
+      for (int j = 0; j < kG; ++j) {
+        av[buf][j] = *reinterpret_cast<const v2f*>(slot + ua_off + (g * kG + j) * kKB * kCB);
+        bv[buf][j] = *reinterpret_cast<const v2f*>(slot + vb_off + (g * kG + j) * kTB * kCB);
+      }
+    };
+    __syncthreads();  // barrier 0: chunk 0 in slot 0
+    read_group(lds, 0, 0);
+    for (int i = 1; i <= bk.n; ++i) {  // consume chunk i - 1; barrier i inside
+      const float* slot = lds + ((i - 1) & 1) * kSlotElems;
+      const float* next = lds + (i & 1) * kSlotElems;
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int g = 0; g < kGroups; ++g) {
+        if (g + 1 < kGroups) {
+          read_group(slot, g + 1, (g + 1) & 1);
+        } else {
+          __syncthreads();  // barrier i: chunk i - 1 read, chunk i in the other slot
+          if (i < bk.n) read_group(next, 0, 0);
+        }
+#pragma unroll
+        for (int s = 0; s < 2; ++s)
+#pragma unroll
+          for (int j = 0; j < kG; ++j)
+            acc[g * kG + j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[g & 1][j][s], bv[g & 1][j][s],
+                                                                  acc[g * kG + j], 0, 0, 0);
+        // order within the group: the next group's LDS reads, then this
+        // group's MFMAs
+        __builtin_amdgcn_sched_group_barrier(0x100, kG, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 2 * kG, 0);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    // n + 1 barriers in all, as the load waves
+    // both slots are free: every wave has passed the last chunk's barrier
+    y_to_lds(acc, lds, wk, wt, li, q);
+  }
+  __syncthreads();
+  write_out<8, ACT, FINAL>(a, bk, lds, lane, wave);
 }
 
 // out = act(sum_s part[s] + bias[k] (+ residual)), parts [splits][N][K][OH][OW];
@@ -449,9 +494,9 @@ int launch_kernel(const FusedArgs& a, int64_t blocks, hipStream_t s) {
 template <int VEC, int ACT>
 int launch_reduce(const float* parts, int splits, int64_t total, int ohw, int K, const float* bias,
                   const float* residual, float* out, hipStream_t s) {
-  NHIP_LAUNCH("wino_fused_reduce", (wino_fused_reduce<VEC, ACT>), dim3((unsigned)ceil_div(total / VEC, 256)),
+  NHIP_LAUNCH("wino_split_reduce", (wino_fused_reduce<VEC, ACT>), dim3((unsigned)ceil_div(total / VEC, 256)),
               dim3(256), 0, s, parts, splits, total, ohw, K, bias, residual, out);
-  return check_launch("wino_fused_reduce");
+  return check_launch("wino_split_reduce");
 }
 
 struct FusedShape {

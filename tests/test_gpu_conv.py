@@ -117,7 +117,7 @@ WINO_CASES = [
 @pytest.fixture(params=["auto", "1", "2"])
 def wino_variant(request, monkeypatch):
     """Winograd implementations: the default per-shape choice (auto), the
-    three-kernel path (1) and the fused kernel (2)."""
+    three-kernel path (1) and the GEMM with the output transform fused (2)."""
     if request.param == "auto":
         monkeypatch.delenv("NHIP_WINOGRAD_VARIANT", raising=False)
     else:
