@@ -75,8 +75,10 @@ WinoShape wino_shape(const nhip_conv_plan* p, int n, int h, int w, int oh, int o
 // Thread (c, t): 6x6 zero-padded patch -> 36 transformed values, V[xi][c][t].
 // PAIRS: thread (channel pair cp, t) transforms channels 2cp and 2cp + 1 and
 // writes V[xi][cp][t][2] (the layout the fused GEMM reads), one 8-byte store
-// per transform point.
-template <bool PAIRS>
+// per transform point.  VEC (left padding 1, W % 4 == 0, 16-byte aligned
+// input): columns 1..4 of a patch row are the aligned run x = 4*tx .. +3,
+// wholly inside the row or wholly past its end, loaded as one 16-byte vector.
+template <bool PAIRS, bool VEC>
 __global__ __launch_bounds__(256) void wino_input_transform(
     const float* __restrict__ x, uint32_t x_bytes, float* __restrict__ V, int C, int H, int W,
     int th, int tw, int T, int t_pad, int c_pad, int pt, int pl) {
@@ -107,12 +109,23 @@ __global__ __launch_bounds__(256) void wino_input_transform(
     for (int i = 0; i < 6; ++i) {
       const int y = y0 + i;
       const bool yok = ok && (unsigned)y < (unsigned)H;
+      if constexpr (VEC) {
+        const uint32_t rb = (uint32_t)((plane + y) * W * (int)sizeof(float));
+        d[i][0] = buf_load_f32(rs, (yok && x0 >= 0) ? rb + (uint32_t)(x0 * 4) : kBufOOB);
+        const int4 m = buf_load_b128(rs, (yok && x0 + 1 < W) ? rb + (uint32_t)((x0 + 1) * 4) : kBufOOB);
+        d[i][1] = __builtin_bit_cast(float, m.x);
+        d[i][2] = __builtin_bit_cast(float, m.y);
+        d[i][3] = __builtin_bit_cast(float, m.z);
+        d[i][4] = __builtin_bit_cast(float, m.w);
+        d[i][5] = buf_load_f32(rs, (yok && x0 + 5 < W) ? rb + (uint32_t)((x0 + 5) * 4) : kBufOOB);
+      } else {
 #pragma unroll
-      for (int j = 0; j < 6; ++j) {
-        const int xx = x0 + j;
-        const uint32_t off =
-            (yok && (unsigned)xx < (unsigned)W) ? (uint32_t)(((plane + y) * W + xx) * (int)sizeof(float)) : kBufOOB;
-        d[i][j] = buf_load_f32(rs, off);
+        for (int j = 0; j < 6; ++j) {
+          const int xx = x0 + j;
+          const uint32_t off =
+              (yok && (unsigned)xx < (unsigned)W) ? (uint32_t)(((plane + y) * W + xx) * (int)sizeof(float)) : kBufOOB;
+          d[i][j] = buf_load_f32(rs, off);
+        }
       }
     }
     // tmp = B^T d  (column-wise)
@@ -282,12 +295,15 @@ int launch_conv_winograd_f32(const nhip_conv_plan* p, const float* in,
     const uint32_t x_bytes = (uint32_t)((size_t)n * ws_.c * h * w * sizeof(float));
     const int64_t total = (int64_t)(fused ? ws_.c_pad / 2 : ws_.c_pad) * ws_.t_pad;
     const dim3 grid((unsigned)ceil_div(total, 256));
-    if (fused)
-      NHIP_LAUNCH("wino_input_transform", wino_input_transform<true>, grid, dim3(256), 0, s, in, x_bytes, V, ws_.c,
-                  h, w, ws_.th, ws_.tw, ws_.t, ws_.t_pad, ws_.c_pad, p->g.pt, p->g.pl);
-    else
-      NHIP_LAUNCH("wino_input_transform", wino_input_transform<false>, grid, dim3(256), 0, s, in, x_bytes, V, ws_.c,
-                  h, w, ws_.th, ws_.tw, ws_.t, ws_.t_pad, ws_.c_pad, p->g.pt, p->g.pl);
+    const bool vec = p->g.pl == 1 && w % 4 == 0 && (reinterpret_cast<uintptr_t>(in) & 15) == 0;
+#define NHIP_WINO_IN(P_, V_)                                                                                  \
+  NHIP_LAUNCH("wino_input_transform", (wino_input_transform<P_, V_>), grid, dim3(256), 0, s, in, x_bytes, V, \
+              ws_.c, h, w, ws_.th, ws_.tw, ws_.t, ws_.t_pad, ws_.c_pad, p->g.pt, p->g.pl)
+    if (fused && vec) NHIP_WINO_IN(true, true);
+    else if (fused) NHIP_WINO_IN(true, false);
+    else if (vec) NHIP_WINO_IN(false, true);
+    else NHIP_WINO_IN(false, false);
+#undef NHIP_WINO_IN
     NHIP_TRY(check_launch("wino_input_transform"));
   }
   if (fused) return launch_wino_gemm_out(p, V, ws_.t_pad, residual, out, n, oh, ow, M, s);
