@@ -39,6 +39,7 @@ template <int BM, int BN, int BK>
 __global__ __launch_bounds__(kThreads) void wino_gemm_kernel(WinoArgs g) {
   constexpr int TM = BM / 64, TN = BN / 64;
   constexpr int AS = BK + kPad;     // As[BM][AS], Bs[BN][AS]: k contiguous
+  static_assert(BK % 16 == 0 && AS % 8 == 4, "the B transpose mapping below");
   constexpr int KQ = BK / 4;        // float4 per row chunk
   constexpr int A_LD = BM * KQ / kThreads;  // float4 loads per thread per chunk
   constexpr int B_LD = BN * KQ / kThreads;
@@ -81,7 +82,11 @@ __global__ __launch_bounds__(kThreads) void wino_gemm_kernel(WinoArgs g) {
   };
   // A chunk: BM rows of BK contiguous k.  B chunk: BK rows of BN contiguous j
   // (V is [c][t]); stored transposed so that a lane's 8 k values of one
-  // column are contiguous in LDS.
+  // column are contiguous in LDS.  B element q (16 bytes: 4 columns of one
+  // row) is row 16*(q / (4*BN)) + q % 16, column quad (q / 16) % (BN/4): a
+  // half-wave holds 16 rows x 2 column quads, whose transposed 4-byte
+  // stores (row stride AS = 4 mod 8 floats) hit 32 distinct banks; a wave
+  // loads 16 rows x 64 contiguous bytes.
   auto gload = [&](Stage& st, int kt) {
 #pragma unroll
     for (int u = 0; u < A_LD; ++u) {
@@ -92,7 +97,7 @@ __global__ __launch_bounds__(kThreads) void wino_gemm_kernel(WinoArgs g) {
 #pragma unroll
     for (int u = 0; u < B_LD; ++u) {
       const int q = tid + u * kThreads;
-      const int row = q / (BN / 4), jq = (q % (BN / 4)) * 4;
+      const int row = (q / (4 * BN)) * 16 + (q & 15), jq = ((q >> 4) % (BN / 4)) * 4;
       st.b[u] = *reinterpret_cast<const v4f*>(B + (int64_t)(kt * BK + row) * g.t_pad + jq);
     }
   };
@@ -106,7 +111,7 @@ __global__ __launch_bounds__(kThreads) void wino_gemm_kernel(WinoArgs g) {
 #pragma unroll
     for (int u = 0; u < B_LD; ++u) {
       const int q = tid + u * kThreads;
-      const int k = q / (BN / 4), jq = (q % (BN / 4)) * 4;
+      const int k = (q / (4 * BN)) * 16 + (q & 15), jq = ((q >> 4) % (BN / 4)) * 4;
       float* dst = &Bs[buf][jq * AS + k];
       dst[0] = st.b[u].x;
       dst[AS] = st.b[u].y;
