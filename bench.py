@@ -151,7 +151,7 @@ def measured_traffic(kernel):
 
 def fused_stage(c, hw):
     """The library's default Winograd path choice: the fused GEMM from 256
-    tiles up (winograd.hip, fused_selected)."""
+    tiles up (winograd.hip, direct_selected / fused_selected)."""
     t = -(-hw // 4)
     return BATCH * t * t >= 256
 

@@ -27,6 +27,9 @@ namespace nhip {
 int launch_wino_gemm_out(const nhip_conv_plan* p, const float* V, int t_pad, const float* residual, float* out,
                          int n, int oh, int ow, float* parts, hipStream_t s);
 uint64_t wino_gemm_out_parts_bytes(const nhip_conv_plan* p, int n, int oh, int ow);
+int launch_wino_fused_direct(const nhip_conv_plan* p, const float* in, int h, int w, const float* residual,
+                             float* out, int n, int oh, int ow, float* parts, hipStream_t s);
+bool wino_direct_staged_shape(const nhip_conv_plan* p, int n, int h, int w, int oh, int ow);
 
 // Path selection: input transform + GEMM with the output transform fused
 // (winograd_fused.hip), or the three-kernel path (M through HBM).
@@ -37,6 +40,18 @@ uint64_t wino_gemm_out_parts_bytes(const nhip_conv_plan* p, int n, int oh, int o
 static int variant_requested() {
   const char* env = std::getenv("NHIP_WINOGRAD_VARIANT");
   return (env && *env) ? std::atoi(env) : 0;
+}
+
+// The fused GEMM transforming the input itself (no V in HBM), selected by
+// NHIP_WINOGRAD_VARIANT = 4.  Not a default: on gfx950 the transform's VALU
+// work serializes with the MFMAs of the same SIMDs and the staged rows add
+// LDS traffic, so even at 64@56 (two output blocks, the largest V round
+// trip against the GEMM) a conv chain measures no faster than the separate
+// transform kernel.
+static bool direct_selected(const nhip_conv_plan* p, int n, int oh, int ow) {
+  const int64_t h = (int64_t)oh + 2 - p->g.pt - p->g.pb, w = (int64_t)ow + 2 - p->g.pl - p->g.pr;
+  if ((int64_t)n * p->g.c * h * w * (int64_t)sizeof(float) > (int64_t(1) << 30)) return false;
+  return variant_requested() == 4;
 }
 
 static bool fused_selected(const nhip_conv_plan* p, int n, int oh, int ow) {
@@ -273,6 +288,7 @@ int winograd_prepack_weights(nhip_conv_plan* p, const float* weight) {
 uint64_t conv_winograd_f32_workspace(const nhip_conv_plan* p, int n, int oh, int ow) {
   const int th = (int)ceil_div(oh, 4), tw = (int)ceil_div(ow, 4);
   const int64_t t_pad = round_up((int64_t)n * th * tw, 128);
+  if (direct_selected(p, n, oh, ow)) return wino_gemm_out_parts_bytes(p, n, oh, ow);
   if (fused_selected(p, n, oh, ow))  // V, then the GEMM's partial sums
     return (uint64_t)36 * t_pad * p->c_pad * sizeof(float) + wino_gemm_out_parts_bytes(p, n, oh, ow);
   const WinoGemmCfg cfg = wino_gemm_config(p->m_pad, p->c_pad, (int)t_pad);
@@ -285,9 +301,11 @@ int launch_conv_winograd_f32(const nhip_conv_plan* p, const float* in,
                              hipStream_t s) {
   const WinoShape ws_ = wino_shape(p, n, h, w, oh, ow);
   const uint64_t need = conv_winograd_f32_workspace(p, n, oh, ow);
-  if (ws == nullptr || ws_bytes < need)
+  if (need > 0 && (ws == nullptr || ws_bytes < need))
     return fail(NHIP_STATUS_OUTPUT_CAPACITY_INSUFFICIENT,
                 "winograd conv: workspace of " + std::to_string(need) + " bytes required");
+  if (direct_selected(p, n, oh, ow))
+    return launch_wino_fused_direct(p, in, h, w, residual, out, n, oh, ow, static_cast<float*>(ws), s);
   const bool fused = fused_selected(p, n, oh, ow);
   float* V = static_cast<float*>(ws);
   float* M = V + (int64_t)36 * ws_.c_pad * ws_.t_pad;

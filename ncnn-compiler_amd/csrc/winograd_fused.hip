@@ -59,7 +59,8 @@ static_assert(kTB == 32 && kKB == 32 && kCB == 8, "the load mappings below assum
 typedef float v2f __attribute__((ext_vector_type(2)));
 
 struct FusedArgs {
-  const float* V;       // [36][c_pad/2][t_pad][2]
+  const float* x;       // direct variant: the input [N][C][H][W] (<= 1 GiB)
+  const float* V;       // otherwise: [36][c_pad/2][t_pad][2]
   const float* U;       // [c_pad/8][36][4][m_pad][2]
   const float* bias;    // [m_pad]
   const float* residual;
@@ -76,6 +77,8 @@ struct FusedArgs {
   //   2  32-tile pieces of a tile row (tw > 32), bpr per row.
   // G = N * th tile rows.
   int mode, R, bpi, bpr, G;
+  int C, H, W, pt, pl;  // direct variant: input geometry
+  uint32_t x_bytes;     // size of x
   uint32_t v_bytes;     // size of V (< 2^31)
   uint32_t u_bytes;     // size of U (< 2^31)
 };
@@ -372,17 +375,252 @@ __device__ __forceinline__ void write_out(const FusedArgs& a, const Block& bk, c
   }
 }
 
-// 8 waves, 4 load + 4 MFMA, chunks of 8 channels in 2 x 72 KB of LDS (one
-// workgroup per CU).  FINAL: write act(Y + bias (+ residual)) with
-// activation ACT; otherwise the raw part of channel split cs.
-template <int ACT, bool FINAL>
+// Input transform V = B^T d B of one 6x6 patch; each value is handed to
+// `store(xi, value)` as soon as it is computed.
+template <class Store>
+__device__ __forceinline__ void input_transform(float (&d)[36], Store store) {
+#pragma unroll
+  for (int j = 0; j < 6; ++j) {  // columns: d <- B^T d, in place
+    const float d0 = d[0 * 6 + j], d1 = d[1 * 6 + j], d2 = d[2 * 6 + j];
+    const float d3 = d[3 * 6 + j], d4 = d[4 * 6 + j], d5 = d[5 * 6 + j];
+    d[0 * 6 + j] = 4.f * d0 - 5.f * d2 + d4;
+    d[1 * 6 + j] = -4.f * (d1 + d2) + d3 + d4;
+    d[2 * 6 + j] = 4.f * (d1 - d2) - d3 + d4;
+    d[3 * 6 + j] = -2.f * (d1 - d3) - d2 + d4;
+    d[4 * 6 + j] = 2.f * (d1 - d3) - d2 + d4;
+    d[5 * 6 + j] = 4.f * d1 - 5.f * d3 + d5;
+  }
+#pragma unroll
+  for (int i = 0; i < 6; ++i) {  // rows: (B^T d) B
+    const float d0 = d[i * 6 + 0], d1 = d[i * 6 + 1], d2 = d[i * 6 + 2];
+    const float d3 = d[i * 6 + 3], d4 = d[i * 6 + 4], d5 = d[i * 6 + 5];
+    store(i * 6 + 0, 4.f * d0 - 5.f * d2 + d4);
+    store(i * 6 + 1, -4.f * (d1 + d2) + d3 + d4);
+    store(i * 6 + 2, 4.f * (d1 - d2) - d3 + d4);
+    store(i * 6 + 3, -2.f * (d1 - d3) - d2 + d4);
+    store(i * 6 + 4, 2.f * (d1 - d3) - d2 + d4);
+    store(i * 6 + 5, 4.f * d1 - 5.f * d3 + d5);
+  }
+}
+
+// The transform waves of the direct variant (no V in HBM): for chunks
+// ch_begin .. ch_begin + n - 1 they load the 6x6 input patches of the
+// block's tiles (thread p = tile p % 32, channel p / 32 of the chunk),
+// transform them into the chunk's V slot ([xi][channel pair][tile][2]) and
+// copy the U slice as load_role does; same slots, same n + 1 barriers.
+// Patch offsets are plane + row + column (bytes), each term exact or kOOB1
+// (a channel or tile past the end, a row or column outside the image): one
+// invalid term puts the sum at or past 2^30 >= the input size, so the raw
+// buffer load returns 0; three stay below 2^32.  Every load has its own
+// offset register, so the compiler does not merge neighbouring loads into
+// vectors (a vector that straddles the end of the input would come back
+// zero as a whole).  VEC (left padding 1, W % 4 == 0): columns 1..4 of a
+// patch row are the 16-byte aligned run x = 4*tx .. +3, wholly inside the row
+// or wholly past its end, loaded as one vector.
+constexpr uint32_t kOOB1 = 0x40000000u;
+
+template <bool VEC>
+__device__ __forceinline__ void transform_role(const FusedArgs& a, float* lds, int p, const Block& bk) {
+  const int t_l = p % kTB, c_l = p / kTB;
+  const bool t_ok = t_l < bk.ntiles;
+  int g, tx;
+  if (a.mode == 2) {
+    g = bk.g0;
+    tx = bk.tx_a + t_l;
+  } else {
+    g = bk.g0 + t_l / a.tw;
+    tx = t_l - (t_l / a.tw) * a.tw;
+  }
+  const int im = t_ok ? g / a.th : 0, ty = t_ok ? g - im * a.th : 0;
+  const int y0 = ty * 4 - a.pt, x0 = tx * 4 - a.pl;
+  uint32_t rowoff[6], coloff[6];
+#pragma unroll
+  for (int i = 0; i < 6; ++i) {
+    const int y = y0 + i, x = x0 + i;
+    rowoff[i] = (unsigned)y < (unsigned)a.H ? (uint32_t)(y * a.W) * 4u : kOOB1;
+    coloff[i] = (unsigned)x < (unsigned)a.W ? (uint32_t)x * 4u : kOOB1;
+  }
+  const uint32_t plane_bytes = (uint32_t)(a.H * a.W) * 4u;
+  const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, a.x_bytes);
+  const __amdgpu_buffer_rsrc_t ur = make_rsrc(a.U, a.u_bytes);
+  // U slice addressing as in load_role
+  const int xi0 = p >> 6, cp = (p & 63) >> 4, r2 = 2 * (p & 15);
+  const uint32_t u_lane = (uint32_t)((((xi0 * 4 + cp) * a.m_pad + bk.k0 + r2) * 2) * 4);
+  const uint32_t u_it = (uint32_t)(4 * 4 * a.m_pad * 2 * 4);
+  const uint32_t u_ch = (uint32_t)(36 * 4 * a.m_pad * 2 * 4);
+
+  // Two chunks in flight, loads issued unconditionally (see load_role).
+  float dA[36], dB[36];
+  v4f uA[kULoads], uB[kULoads];
+  auto load = [&](int ch, bool live, float (&d)[36], v4f (&u)[kULoads]) {
+    const int c = ch * kCB + c_l;
+    const uint32_t pb = (live && t_ok && c < a.C) ? (uint32_t)(im * a.C + c) * plane_bytes : kOOB1;
+#pragma unroll
+    for (int i = 0; i < 6; ++i) {
+      const uint32_t rb = pb + rowoff[i];
+      if constexpr (VEC) {
+        d[i * 6 + 0] = buf_load_f32(xr, rb + coloff[0]);
+        const v4f m = __builtin_bit_cast(v4f, buf_load_b128(xr, rb + coloff[1]));
+        d[i * 6 + 1] = m[0];
+        d[i * 6 + 2] = m[1];
+        d[i * 6 + 3] = m[2];
+        d[i * 6 + 4] = m[3];
+        d[i * 6 + 5] = buf_load_f32(xr, rb + coloff[5]);
+      } else {
+#pragma unroll
+        for (int j = 0; j < 6; ++j) d[i * 6 + j] = buf_load_f32(xr, rb + coloff[j]);
+      }
+    }
+    const uint32_t uo = live ? u_lane + (uint32_t)ch * u_ch : 0x80000000u;
+#pragma unroll
+    for (int it = 0; it < kULoads; ++it)
+      u[it] = __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(ur, uo, it * u_it, 0));
+  };
+  const int v_off = ((c_l >> 1) * kTB + t_l) * 2 + (c_l & 1);
+  auto fill = [&](int slot_idx, float (&d)[36], v4f (&u)[kULoads]) {
+    float* slot = lds + slot_idx * kSlotElems;
+    float* vw = slot + v_off;
+    input_transform(d, [&](int xi, float v) { vw[xi * kTB * kCB] = v; });
+#pragma unroll
+    for (int it = 0; it < kULoads; ++it)
+      *reinterpret_cast<v4f*>(slot + kVElems + (it * kProducers + p) * 4) = u[it];
+  };
+
+  const int n = bk.n, ch_begin = bk.ch_begin;
+  load(ch_begin, n > 0, dA, uA);
+  load(ch_begin + 1, n > 1, dB, uB);
+  for (int i = 0; i <= n; i += 2) {
+    if (i < n) fill(0, dA, uA);
+    load(ch_begin + i + 2, i + 2 < n, dA, uA);
+    __syncthreads();  // slot 0 full; slot 1 consumed
+    if (i + 1 < n) fill(1, dB, uB);
+    load(ch_begin + i + 3, i + 3 < n, dB, uB);
+    if (i + 1 <= n) __syncthreads();  // slot 1 full; slot 0 consumed
+  }
+}
+
+// The transform waves, staged form (tile blocks of up to R tile rows of one
+// image (mode 1), left padding 1, W % 4 == 0): wave w stages the input rows
+// its two channels of the chunk need, (4 * nrows + 2) rows x W columns each,
+// from row 4 * ty0 - pt, through
+// LDS with 16-byte loads, then reads each thread's 6x6 patch from there.
+// The rows live in the wave's own quarter of the chunk slot's U region
+// ([channel][row][x + 4], row stride W + 8, halo columns zero), which the
+// wave overwrites with its share of the U slice only after its patch reads:
+// a wave's LDS operations complete in order, so no barrier is needed.
+// Its U share is the contiguous quarter e4 = w*576 + it*64 + lane.
+__device__ __forceinline__ void transform_role_staged(const FusedArgs& a, float* lds, int p, const Block& bk) {
+  const int lane = p & 63, w = p >> 6;
+  const int t_l = p % kTB, c_l = p / kTB;  // c_l = 2w + lane / 32
+  const bool t_ok = t_l < bk.ntiles;
+  const int im = bk.g0 / a.th, ty0 = bk.g0 - im * a.th;
+  const int rows = 4 * bk.nrows + 2;
+  const int RS = a.W + 8;
+  const int quads = a.W >> 2;
+  const int per_ch = rows * quads;           // 16-byte row pieces per channel
+  const int n_rows_ld = 2 * per_ch;          // per wave and chunk (<= 5 * 64, checked on the host)
+  const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, a.x_bytes);
+  const __amdgpu_buffer_rsrc_t ur = make_rsrc(a.U, a.u_bytes);
+  // row piece e (lane + 64u) of the wave: channel e / per_ch, row, quad
+  uint32_t roff[5];
+  int rlds[5], rch[5];
+#pragma unroll
+  for (int u = 0; u < 5; ++u) {
+    const int e = lane + 64 * u;
+    const int ch = e / per_ch, rem = e - ch * per_ch;
+    const int r = rem / quads, xq = rem - r * quads;
+    const int y = 4 * ty0 - a.pt + r;
+    const bool ok = e < n_rows_ld && (unsigned)y < (unsigned)a.H;
+    roff[u] = ok ? (uint32_t)(((im * a.C + 2 * w + ch) * a.H + y) * a.W + 4 * xq) * 4u : 0x80000000u;
+    rlds[u] = e < n_rows_ld ? (ch * rows + r) * RS + 4 + 4 * xq : -1;
+    rch[u] = 2 * w + ch;  // channel within the chunk
+  }
+  const uint32_t plane_bytes = (uint32_t)(a.H * a.W) * 4u;
+  // U share: e4 = w*576 + it*64 + lane -> xi = 9w + it, pair lane/16, rows 2*(lane%16)
+  const uint32_t u_lane = (uint32_t)((((9 * w * 4) + (lane >> 4)) * a.m_pad + bk.k0 + 2 * (lane & 15)) * 2 * 4);
+  const uint32_t u_it = (uint32_t)(4 * a.m_pad * 2 * 4);
+  const uint32_t u_ch = (uint32_t)(36 * 4 * a.m_pad * 2 * 4);
+  // patch of this thread: tile (ty, tx) of the block, rows 4*(ty - ty0) .. +5 of its channel's rows
+  const int tyl = t_l / a.tw, tx = t_l - tyl * a.tw;
+  const int pbase = ((lane >> 5) * rows + 4 * tyl) * RS + 3 + 4 * tx;  // x = 4tx - 1 at offset 4tx + 3
+
+  v4f rA[5], rB[5], uA[kULoads], uB[kULoads];
+  auto load = [&](int ch, bool live, v4f (&r)[5], v4f (&u)[kULoads]) {
+    const uint32_t cb = (uint32_t)(ch * kCB) * plane_bytes;  // chunk's channel offset
+#pragma unroll
+    for (int q = 0; q < 5; ++q)
+      r[q] = __builtin_bit_cast(v4f, buf_load_b128(xr, (live && ch * kCB + rch[q] < a.C) ? roff[q] + cb : 0x80000000u));
+    const uint32_t uo = live ? u_lane + (uint32_t)ch * u_ch : 0x80000000u;
+#pragma unroll
+    for (int it = 0; it < kULoads; ++it)
+      u[it] = __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(ur, uo, it * u_it, 0));
+  };
+  const int v_off = ((c_l >> 1) * kTB + t_l) * 2 + (c_l & 1);
+  auto fill = [&](int slot_idx, v4f (&r)[5], v4f (&u)[kULoads]) {
+    float* slot = lds + slot_idx * kSlotElems;
+    float* raw = slot + kVElems + w * (kUElems / 4);
+#pragma unroll
+    for (int q = 0; q < 5; ++q)
+      if (rlds[q] >= 0) *reinterpret_cast<v4f*>(raw + rlds[q]) = r[q];
+    // halo columns x = -1 and x = W of the wave's rows
+    for (int e = lane; e < 2 * rows; e += 64) {
+      raw[e * RS + 3] = 0.f;
+      raw[e * RS + a.W + 4] = 0.f;
+    }
+    float d[36];
+    const float* pr = raw + pbase;
+#pragma unroll
+    for (int i = 0; i < 6; ++i) {
+      d[i * 6 + 0] = pr[i * RS];
+      const v4f m = *reinterpret_cast<const v4f*>(pr + i * RS + 1);
+      d[i * 6 + 1] = m[0];
+      d[i * 6 + 2] = m[1];
+      d[i * 6 + 3] = m[2];
+      d[i * 6 + 4] = m[3];
+      d[i * 6 + 5] = pr[i * RS + 5];
+    }
+    if (!t_ok) {
+#pragma unroll
+      for (int e = 0; e < 36; ++e) d[e] = 0.f;
+    }
+    float* vw = slot + v_off;
+    input_transform(d, [&](int xi, float v) { vw[xi * kTB * kCB] = v; });
+    float* us = slot + kVElems + w * (kUElems / 4) + lane * 4;
+#pragma unroll
+    for (int it = 0; it < kULoads; ++it) *reinterpret_cast<v4f*>(us + it * 256) = u[it];
+  };
+
+  const int n = bk.n, ch_begin = bk.ch_begin;
+  load(ch_begin, n > 0, rA, uA);
+  load(ch_begin + 1, n > 1, rB, uB);
+  for (int i = 0; i <= n; i += 2) {
+    if (i < n) fill(0, rA, uA);
+    load(ch_begin + i + 2, i + 2 < n, rA, uA);
+    __syncthreads();  // slot 0 full; slot 1 consumed
+    if (i + 1 < n) fill(1, rB, uB);
+    load(ch_begin + i + 3, i + 3 < n, rB, uB);
+    if (i + 1 <= n) __syncthreads();  // slot 1 full; slot 0 consumed
+  }
+}
+
+// 8 waves, 4 load (XFORM: transform) + 4 MFMA, chunks of 8 channels in
+// 2 x 72 KB of LDS (one workgroup per CU).  FINAL: write act(Y + bias
+// (+ residual)) with activation ACT; otherwise the raw part of channel split
+// cs.  XFORM: the direct variant, V computed from the input in the kernel
+// (VEC: the staged form, transform_role_staged).
+template <int ACT, bool FINAL, bool XFORM, bool VEC>
 __global__ __launch_bounds__(kThreads, 1) void wino_fused_kernel(FusedArgs a) {
   extern __shared__ __attribute__((aligned(16))) float lds[];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const Block bk = block_of(a, kCB);
 
   if (wave >= 4) {
-    load_role(a, lds, tid - 4 * 64, bk.t0, bk.k0, bk.ch_begin, bk.n);
+    if constexpr (XFORM && VEC)
+      transform_role_staged(a, lds, tid - 4 * 64, bk);
+    else if constexpr (XFORM)
+      transform_role<false>(a, lds, tid - 4 * 64, bk);
+    else
+      load_role(a, lds, tid - 4 * 64, bk.t0, bk.k0, bk.ch_begin, bk.n);
   } else {
     // ---- MFMA waves ----------------------------------------------------------
     const int li = lane & 15, q = lane >> 4;
@@ -477,18 +715,25 @@ __global__ void wino_fused_reduce(const float* __restrict__ part, int splits, in
   }
 }
 
-template <int ACT, bool FINAL>
+template <int ACT, bool FINAL, bool XFORM, bool VEC>
 int launch_kernel(const FusedArgs& a, int64_t blocks, hipStream_t s) {
   static bool attr_set = false;  // dynamic LDS above 64 KB needs the attribute
   if (!attr_set) {
-    NHIP_TRY(check_hip(hipFuncSetAttribute(reinterpret_cast<const void*>(&wino_fused_kernel<ACT, FINAL>),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes),
-                       "hipFuncSetAttribute(wino_fused)"));
+    NHIP_TRY(check_hip(
+        hipFuncSetAttribute(reinterpret_cast<const void*>(&wino_fused_kernel<ACT, FINAL, XFORM, VEC>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes),
+        "hipFuncSetAttribute(wino_fused)"));
     attr_set = true;
   }
-  NHIP_LAUNCH("wino_fused", (wino_fused_kernel<ACT, FINAL>), dim3((unsigned)blocks), dim3(kThreads), kLdsBytes, s,
-              a);
+  NHIP_LAUNCH("wino_fused", (wino_fused_kernel<ACT, FINAL, XFORM, VEC>), dim3((unsigned)blocks), dim3(kThreads),
+              kLdsBytes, s, a);
   return check_launch("wino_fused");
+}
+
+template <int ACT, bool FINAL>
+int launch_kernel(const FusedArgs& a, int64_t blocks, bool xform, bool vec, hipStream_t s) {
+  if (!xform) return launch_kernel<ACT, FINAL, false, false>(a, blocks, s);
+  return vec ? launch_kernel<ACT, FINAL, true, true>(a, blocks, s) : launch_kernel<ACT, FINAL, true, false>(a, blocks, s);
 }
 
 template <int VEC, int ACT>
@@ -551,23 +796,21 @@ uint64_t wino_gemm_out_parts_bytes(const nhip_conv_plan* p, int n, int oh, int o
   return f.splits > 1 ? (uint64_t)f.splits * n * p->g.k * oh * ow * sizeof(float) : 0;
 }
 
-int launch_wino_gemm_out(const nhip_conv_plan* p, const float* V, int t_pad, const float* residual, float* out,
-                         int n, int oh, int ow, float* parts, hipStream_t s) {
-  const size_t v_bytes = (size_t)36 * p->c_pad * t_pad * sizeof(float);
-  const size_t u_bytes = (size_t)36 * p->m_pad * p->c_pad * sizeof(float);
-  if (v_bytes >= (size_t(1) << 31) || u_bytes >= (size_t(1) << 31))
-    return fail(NHIP_STATUS_CONSTRAINT_VIOLATION, "winograd GEMM: transformed input or weights above 2 GiB");
-  if (p->c_pad % kCB != 0 || p->m_pad % kKB != 0 || t_pad % kTB != 0)
-    return fail(NHIP_STATUS_CONSTRAINT_VIOLATION, "winograd GEMM: padding mismatch");
+namespace {
+
+// Shared by both entries: a = the operand sources already set (V or x).
+int launch_fused(const nhip_conv_plan* p, FusedArgs& a, const FusedShape& f, bool xform, bool vec,
+                 const float* residual, float* out, int n, int oh, int ow, float* parts, hipStream_t s) {
   if ((reinterpret_cast<uintptr_t>(out) & 15) || (residual && (reinterpret_cast<uintptr_t>(residual) & 15)) ||
-      (reinterpret_cast<uintptr_t>(parts) & 15) || (reinterpret_cast<uintptr_t>(V) & 15))
+      (reinterpret_cast<uintptr_t>(parts) & 15))
     return fail(NHIP_STATUS_CONSTRAINT_VIOLATION, "winograd: buffers must be 16-byte aligned");
-  const FusedShape f = fused_shape(p, n, oh, ow);
   if (f.splits > 1 && parts == nullptr)
     return fail(NHIP_STATUS_NULL_POINTER, "winograd GEMM: partial-sum workspace missing");
-  FusedArgs a{};
-  a.V = V;
-  a.v_bytes = (uint32_t)v_bytes;
+  const size_t u_bytes = (size_t)36 * p->m_pad * p->c_pad * sizeof(float);
+  if (u_bytes >= (size_t(1) << 31))
+    return fail(NHIP_STATUS_CONSTRAINT_VIOLATION, "winograd GEMM: transformed weights above 2 GiB");
+  if (p->c_pad % kCB != 0 || p->m_pad % kKB != 0)
+    return fail(NHIP_STATUS_CONSTRAINT_VIOLATION, "winograd GEMM: padding mismatch");
   a.U = p->weight_fused;
   a.u_bytes = (uint32_t)u_bytes;
   a.bias = p->bias;
@@ -584,7 +827,6 @@ int launch_wino_gemm_out(const nhip_conv_plan* p, const float* V, int t_pad, con
   a.bpi = f.bpi;
   a.bpr = f.bpr;
   a.G = f.G;
-  a.t_pad = t_pad;
   a.m_pad = p->m_pad;
   a.c_pad = p->c_pad;
   a.nt = f.nt;
@@ -594,13 +836,13 @@ int launch_wino_gemm_out(const nhip_conv_plan* p, const float* V, int t_pad, con
   const int64_t blocks = (int64_t)f.nt * f.nk * f.splits;
   if (f.splits == 1) {
     switch (p->g.act) {
-      case NHIP_ACT_NONE: return launch_kernel<NHIP_ACT_NONE, true>(a, blocks, s);
-      case NHIP_ACT_RELU: return launch_kernel<NHIP_ACT_RELU, true>(a, blocks, s);
-      case NHIP_ACT_SIGMOID: return launch_kernel<NHIP_ACT_SIGMOID, true>(a, blocks, s);
+      case NHIP_ACT_NONE: return launch_kernel<NHIP_ACT_NONE, true>(a, blocks, xform, vec, s);
+      case NHIP_ACT_RELU: return launch_kernel<NHIP_ACT_RELU, true>(a, blocks, xform, vec, s);
+      case NHIP_ACT_SIGMOID: return launch_kernel<NHIP_ACT_SIGMOID, true>(a, blocks, xform, vec, s);
       default: return fail(NHIP_STATUS_UNSUPPORTED, "winograd GEMM: unsupported activation");
     }
   }
-  NHIP_TRY((launch_kernel<NHIP_ACT_NONE, false>(a, blocks, s)));
+  NHIP_TRY((launch_kernel<NHIP_ACT_NONE, false>(a, blocks, xform, vec, s)));
   const int64_t total = (int64_t)n * p->g.k * oh * ow;
   const int ohw = oh * ow;
 #define NHIP_REDUCE(V_)                                                                                       \
@@ -617,6 +859,51 @@ int launch_wino_gemm_out(const nhip_conv_plan* p, const float* V, int t_pad, con
     NHIP_REDUCE(1)
   }
 #undef NHIP_REDUCE
+}
+
+}  // namespace
+
+int launch_wino_gemm_out(const nhip_conv_plan* p, const float* V, int t_pad, const float* residual, float* out,
+                         int n, int oh, int ow, float* parts, hipStream_t s) {
+  const size_t v_bytes = (size_t)36 * p->c_pad * t_pad * sizeof(float);
+  if (v_bytes >= (size_t(1) << 31))
+    return fail(NHIP_STATUS_CONSTRAINT_VIOLATION, "winograd GEMM: transformed input above 2 GiB");
+  if (t_pad % kTB != 0 || (reinterpret_cast<uintptr_t>(V) & 15))
+    return fail(NHIP_STATUS_CONSTRAINT_VIOLATION, "winograd GEMM: V padding or alignment");
+  FusedArgs a{};
+  a.V = V;
+  a.v_bytes = (uint32_t)v_bytes;
+  a.t_pad = t_pad;
+  return launch_fused(p, a, fused_shape(p, n, oh, ow), false, false, residual, out, n, oh, ow, parts, s);
+}
+
+// The direct variant's staged input rows apply (by shape; the input must also
+// be 16-byte aligned at launch, else the direct kernel gathers patches).
+bool wino_direct_staged_shape(const nhip_conv_plan* p, int n, int h, int w, int oh, int ow) {
+  const FusedShape f = fused_shape(p, n, oh, ow);
+  const int rows = 4 * f.R + 2;
+  return f.mode == 1 && p->g.pl == 1 && w % 4 == 0 && 2 * rows * (w / 4) <= 5 * 64 &&
+         2 * rows * (w + 8) <= kUElems / 4 && (int64_t)n * p->g.c * h * w * 4 < (int64_t(1) << 30);
+}
+
+int launch_wino_fused_direct(const nhip_conv_plan* p, const float* in, int h, int w, const float* residual,
+                             float* out, int n, int oh, int ow, float* parts, hipStream_t s) {
+  const size_t x_bytes = (size_t)n * p->g.c * h * w * sizeof(float);
+  if (x_bytes > (size_t(1) << 30))
+    return fail(NHIP_STATUS_CONSTRAINT_VIOLATION, "winograd direct: input above 1 GiB");
+  FusedArgs a{};
+  a.x = in;
+  a.x_bytes = (uint32_t)x_bytes;
+  a.C = p->g.c;
+  a.H = h;
+  a.W = w;
+  a.pt = p->g.pt;
+  a.pl = p->g.pl;
+  // staged rows: tile rows of one image (mode 1), left padding 1, 16-byte
+  // rows, and a wave's two channels of rows (<= 5 x 64 pieces, and within
+  // its quarter of the U region) per chunk
+  const bool staged = wino_direct_staged_shape(p, n, h, w, oh, ow) && (reinterpret_cast<uintptr_t>(in) & 15) == 0;
+  return launch_fused(p, a, fused_shape(p, n, oh, ow), true, staged, residual, out, n, oh, ow, parts, s);
 }
 
 }  // namespace nhip

@@ -114,10 +114,11 @@ WINO_CASES = [
 ]
 
 
-@pytest.fixture(params=["auto", "1", "2"])
+@pytest.fixture(params=["auto", "1", "2", "4"])
 def wino_variant(request, monkeypatch):
     """Winograd implementations: the default per-shape choice (auto), the
-    three-kernel path (1) and the GEMM with the output transform fused (2)."""
+    three-kernel path (1), the GEMM with the output transform fused (2) and
+    the same GEMM transforming the input itself (4)."""
     if request.param == "auto":
         monkeypatch.delenv("NHIP_WINOGRAD_VARIANT", raising=False)
     else:
@@ -193,8 +194,8 @@ def test_resnet_stage_full_batch(stage):
         assert_close(igemm[i:i + 1], exp, IGEMM_RTOL, f"igemm image {i}")
 
 
-@pytest.mark.parametrize("variant", ["2", "1"])
-def test_batch_is_independent_images(variant, monkeypatch):  # 1 = three-kernel path, 2 = fused
+@pytest.mark.parametrize("variant", ["4", "2", "1"])
+def test_batch_is_independent_images(variant, monkeypatch):  # 1 = three-kernel path, 2/4 = fused
     """The [N,C,H,W] batch equals N single-image calls (the reference ABI),
     bit for bit for a fixed kernel variant."""
     monkeypatch.setenv("NHIP_WINOGRAD_VARIANT", variant)
