@@ -445,6 +445,7 @@ IgemmCfg igemm_config(const nhip_conv_plan* p, int64_t npix) {
 }  // namespace
 
 uint64_t conv_igemm_f32_workspace(const nhip_conv_plan* p, int n, int oh, int ow) {
+  if (pointwise_selected(p, n, oh, ow)) return 0;
   const int64_t npix = (int64_t)n * oh * ow;
   const IgemmCfg c = igemm_config(p, npix);
   return c.splits > 1 ? (uint64_t)c.splits * p->g.k * npix * sizeof(float) : 0;
@@ -454,6 +455,7 @@ int launch_conv_igemm_f32(const nhip_conv_plan* p, const float* in,
                           const float* residual, float* out, int n, int h,
                           int w, int oh, int ow, void* ws, uint64_t ws_bytes,
                           hipStream_t s) {
+  if (pointwise_selected(p, n, h, w)) return launch_conv_pointwise_f32(p, in, residual, out, n, h, w, s);
   GemmArgs g{};
   g.a = p->weight;
   g.lda = p->kred_pad;

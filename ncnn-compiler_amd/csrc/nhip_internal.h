@@ -141,6 +141,11 @@ int launch_conv_igemm_f32(const nhip_conv_plan* p, const float* in,
                           hipStream_t s);
 uint64_t conv_igemm_f32_workspace(const nhip_conv_plan* p, int n, int oh,
                                   int ow);
+// 1x1 stride-1 unpadded convolutions (pointwise.hip): true when the
+// streaming pointwise kernel takes the layer (no workspace).
+bool pointwise_selected(const nhip_conv_plan* p, int n, int h, int w);
+int launch_conv_pointwise_f32(const nhip_conv_plan* p, const float* in, const float* residual, float* out, int n,
+                              int h, int w, hipStream_t s);
 int launch_conv_winograd_f32(const nhip_conv_plan* p, const float* in,
                              const float* residual, float* out, int n, int h,
                              int w, int oh, int ow, void* ws,
