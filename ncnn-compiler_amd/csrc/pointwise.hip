@@ -5,22 +5,27 @@
 // tosa.conv2d -> linalg.conv_2d_nhwc_hwcf: NCNNToTosa.cpp:1107-1530).
 //
 // These layers move far more bytes than they compute (16 -> 96 channels at
-// 112x112 is 1.2 GFLOP against 180 MB), so the kernel is built to stream x
-// once per output-channel slice and write out once at HBM speed:
+// 112x112 is 1.2 GFLOP against 180 MB), so the kernel streams x once per
+// output-channel slice and writes out once:
 //   * a workgroup (4 waves) holds the weights of its slice of 16*KT output
-//     channels in LDS for its whole life and walks 256-pixel tiles
-//     (persistent grid);
-//   * a wave owns 64 consecutive pixels x the slice, so every element of x
-//     is loaded by exactly one wave per slice, straight into MFMA B
-//     fragments (no LDS staging);
+//     channels in LDS for its whole life and walks pixel tiles (persistent
+//     grid when the tiles outnumber what fits on the GPU);
 //   * input channels stream in chunks of 16 (four v_mfma_f32_16x16x4_f32
-//     k-steps) through a ring of NB register buffers, NB - 1 chunks in
-//     flight ahead of the one being multiplied, across tile boundaries;
-//   * lane l loads pixels 4*(l%16) .. +3 and feeds pixel 4*(l%16) + v to
-//     MFMA v of a k-step, so register r of the four accumulators of a
-//     channel block holds four consecutive pixels of one output channel: the
-//     result leaves as 16-byte stores, 16 lanes covering 256 contiguous bytes
-//     of an output row.
+//     k-steps) straight from HBM into MFMA B fragments (no LDS staging),
+//     through a ring of NB register buffers, NB - 1 chunks in flight ahead
+//     of the one being multiplied, across tile boundaries;
+//   * lane l holds pixels 4*(l%16) .. +3 and feeds pixel 4*(l%16) + v to MFMA
+//     v of a k-step, so register r of the four accumulators of a channel
+//     block holds four consecutive pixels of one output channel: the result
+//     leaves as 16-byte stores, 16 lanes covering 256 contiguous bytes.
+// Two work splits inside a workgroup (WC):
+//   WC = 1  each wave owns 64 pixels of a 256-pixel tile and all channels
+//           (long pixel rows: the 112/56/28 layers);
+//   WC = 4  the four waves share one 64-pixel tile and take every fourth
+//           chunk of the channels, their partial sums added through LDS in
+//           a fixed order (few pixels, long reductions: 14x14 and 7x7).
+// SCALAR (H*W % 4 != 0, e.g. 7x7): a lane's four pixels may lie in two
+// images, so they are loaded and stored one float at a time.
 #include <cstdio>
 #include <cstdlib>
 
@@ -31,9 +36,9 @@ namespace {
 
 constexpr int kThreads = 256;   // 4 waves
 constexpr int kChunk = 16;      // input channels per chunk (4 MFMA k-steps)
-constexpr int kTilePix = 256;   // pixels per workgroup tile (4 waves x 64)
 constexpr int kXcds = 8;
-constexpr int kMaxLds = 64 * 1024;
+constexpr int kMaxLds = 144 * 1024;
+constexpr int kRedFloats = 4 * 4 * 4 * 64;  // WC = 4 reduction area: [src wave][v][r][lane]
 
 struct PwArgs {
   const float* x;        // [N][C][P]
@@ -43,7 +48,7 @@ struct PwArgs {
   float* out;            // [N][K][P]
   int C, K, P, ldw, c4;  // c4 = C rounded up to 4
   int np;                // N * P pixels (< 2^29: x is < 2^31 bytes)
-  int ntiles, nch;       // pixel tiles, channel chunks
+  int ntiles, nch;       // pixel tiles, channel chunks (nch >= WC)
   uint32_t x_bytes, out_bytes;
 };
 
@@ -58,31 +63,68 @@ __device__ __forceinline__ v4f load4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   return __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
 }
 
-// LDS: Ws[c][j][t] = W[k0 + 16t + j][c] (c < c4, j < 16, t < KT), so the A
-// fragments of one k-step (KT floats per lane, lane l = (c%4)*16 + j) are
-// one contiguous 64*KT-float run; then bias[k0 .. k0 + 16*KT).
+// Per-lane pixel geometry of a tile: byte offsets of (n, channel 0, p) in x
+// and in out / the residual for the lane's four pixels (one offset when they
+// are consecutive in one image); out of range past the last pixel.
+template <bool SCALAR>
+struct Geo {
+  uint32_t xo[SCALAR ? 4 : 1], oo[SCALAR ? 4 : 1];
+};
+
+// LDS: W[k0 + 16t + j][c] at (c*16 + j)*KT + t + c/4 (c < c4, j < 16,
+// t < KT): the A fragments of one k-step (KT floats per lane, lane
+// l = (c%4)*16 + j) are one contiguous 64*KT-float run, and the float of
+// padding per four channels spreads the staging writes (consecutive threads
+// take consecutive groups of four channels) over the banks; then
+// bias[k0 .. k0 + 16*KT); then, for WC = 4, the reduction area.
 // RES: add the residual.  Its loads for a tile go out right after the X
-// loads of the tile's last chunk when the tile has at least NB chunks (one
-// tile's residual pending at a time), otherwise just before the prefetch
-// issued beside that chunk's MFMAs; either way waiting for them never waits
-// for later prefetches (vmcnt retires in issue order).
-// Stores and loads are raw buffer operations on 32-bit offsets: positions
+// loads of the wave's last chunk of the tile when the wave has at least NB
+// chunks per tile (one tile's residual pending at a time), otherwise just
+// before the prefetch issued beside that chunk's MFMAs; either way waiting
+// for them never waits for later prefetches (vmcnt retires in issue order).
+// Loads and stores are raw buffer operations on 32-bit offsets: positions
 // past the last pixel or channel carry an offset past the buffer's size, so
 // they neither branch nor touch memory.
-template <int KT, int NB, int ACT, bool RES>
+template <int KT, int ACT, bool RES, int WC, bool SCALAR>
 __global__ __launch_bounds__(kThreads, 2) void pw_conv_kernel(PwArgs a) {
+  static_assert(WC == 1 || WC == 4, "channel split over 1 or 4 waves");
+  static_assert(!SCALAR || WC == 4, "unaligned pixel rows use the 64-pixel tiles");
+  constexpr int NB = WC == 1 ? 2 : 4;   // chunk buffers
+  constexpr int TP = 256 / WC;          // pixels per tile
+  constexpr int KS = 16 * KT;           // output channels per slice
+  constexpr int RR = WC == 1 ? 4 : 1;   // accumulator rows a wave finalizes
   extern __shared__ __attribute__((aligned(16))) float ws[];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  constexpr int KS = 16 * KT;  // output channels per slice
   const int k0 = blockIdx.y * KS;
-  float* bs = ws + a.c4 * KS;
+  float* bs = ws + a.c4 * KS + a.c4 / 4;
+  float* red = bs + KS;
 
-  // ---- weights and bias of the slice into LDS (coalesced over c) ----------
-  for (int e = tid; e < KS * a.c4; e += kThreads) {
-    const int kl = e / a.c4, c = e - kl * a.c4;
-    const int k = k0 + kl;
-    const float v = (c < a.C && k < a.K) ? a.w[(int64_t)k * a.ldw + c] : 0.f;
-    ws[(c * 16 + (kl & 15)) * KT + (kl >> 4)] = v;
+  // ---- weights and bias of the slice into LDS -----------------------------
+  // 16-byte loads along c (weight rows are 16-float aligned and zero past C),
+  // eight in flight per thread before their LDS stores: a 960-channel slice
+  // is then two round trips to memory, not sixty.
+  {
+    const int q4 = a.c4 / 4, total = KS * q4;
+    for (int e0 = 0; e0 < total; e0 += 8 * kThreads) {
+      v4f v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int e = e0 + u * kThreads + tid;
+        const int kl = e / q4, k = k0 + kl;
+        v[u] = (e < total && k < a.K)
+                   ? *reinterpret_cast<const v4f*>(a.w + (int64_t)k * a.ldw + 4 * (e - kl * q4))
+                   : v4f{0.f, 0.f, 0.f, 0.f};
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int e = e0 + u * kThreads + tid;
+        if (e < total) {
+          const int kl = e / q4, c = 4 * (e - kl * q4);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) ws[((c + i) * 16 + (kl & 15)) * KT + (kl >> 4) + (c >> 2)] = v[u][i];
+        }
+      }
+    }
   }
   for (int e = tid; e < KS; e += kThreads) bs[e] = (k0 + e < a.K) ? a.bias[k0 + e] : 0.f;
   __syncthreads();
@@ -96,44 +138,54 @@ __global__ __launch_bounds__(kThreads, 2) void pw_conv_kernel(PwArgs a) {
     const int x = blockIdx.x % kXcds, q = blockIdx.x / kXcds;
     first = x * (nb / kXcds) + min(x, nb % kXcds) + q;
   }
-  if (first >= a.ntiles) return;
+  if (first >= a.ntiles) return;  // uniform over the workgroup
   const int my_tiles = (a.ntiles - 1 - first) / gridDim.x + 1;
 
   const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, a.x_bytes);
   const __amdgpu_buffer_rsrc_t orr = make_rsrc(a.out, a.out_bytes);
-  const __amdgpu_buffer_rsrc_t rr = make_rsrc(a.res, RES ? a.out_bytes : 0u);
+  const __amdgpu_buffer_rsrc_t resr = make_rsrc(a.res, RES ? a.out_bytes : 0u);
   const int jl = lane & 15, cl = lane >> 4;
-  const uint32_t cstride = (uint32_t)a.P * 4u;  // bytes between channel planes
+  const int wave_c = WC == 1 ? 0 : wave;            // first chunk of this wave
+  const int nchw = (a.nch - wave_c + WC - 1) / WC;  // chunks per tile (>= 1)
+  const uint32_t cstride = (uint32_t)a.P * 4u;      // bytes between channel planes
   const float inv_p = 1.0f / (float)a.P;
 
-  // Lane geometry of a tile: pixel q = tile*256 + wave*64 + 4*jl of image n
-  // at position p; xo = byte offset of (n, c = 0, p) in x, oo = byte offset
-  // of (n, k = 0, p) in out (and the residual); q past the end: both out of
-  // range.  P % 4 == 0, so the lane's four pixels lie in one image.
-  struct Geo {
-    uint32_t xo, oo;
-  };
   auto geo = [&](int tile) {
-    const int q0 = tile * kTilePix;  // uniform
+    const int q0 = tile * TP;  // uniform
     const int n0 = q0 / a.P, p0 = q0 - n0 * a.P;
-    const int u = p0 + wave * 64 + 4 * jl;
-    int dn = (int)((float)u * inv_p);
-    int p = u - dn * a.P;
-    if (p < 0) { --dn; p += a.P; }
-    if (p >= a.P) { ++dn; p -= a.P; }
-    const int n = n0 + dn;
-    const bool ok = q0 + (u - p0) < a.np;
-    Geo g;
-    g.xo = ok ? (uint32_t)(n * a.C * a.P + p) * 4u : kBufOOB;
-    g.oo = ok ? (uint32_t)(n * a.K * a.P + p) * 4u : kBufOOB;
+    const int u0 = p0 + (WC == 1 ? wave * 64 : 0) + 4 * jl;
+    Geo<SCALAR> g;
+#pragma unroll
+    for (int v = 0; v < (SCALAR ? 4 : 1); ++v) {
+      const int u = u0 + v;  // pixel of image n0 + dn at position p
+      int dn = (int)((float)u * inv_p);
+      int p = u - dn * a.P;
+      if (p < 0) { --dn; p += a.P; }
+      if (p >= a.P) { ++dn; p -= a.P; }
+      const int n = n0 + dn;
+      const bool ok = q0 + (u - p0) < a.np;
+      g.xo[v] = ok ? (uint32_t)(n * a.C * a.P + p) * 4u : kBufOOB;
+      g.oo[v] = ok ? (uint32_t)(n * a.K * a.P + p) * 4u : kBufOOB;
+    }
     return g;
   };
+  auto load_px = [&](__amdgpu_buffer_rsrc_t r, const uint32_t* base, uint32_t add, bool on) {
+    if constexpr (SCALAR) {
+      v4f v;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = buf_load_f32(r, (on && base[e] != kBufOOB) ? base[e] + add : kBufOOB);
+      return v;
+    } else {
+      return load4(r, (on && base[0] != kBufOOB) ? base[0] + add : kBufOOB);
+    }
+  };
 
-  auto issue = [&](v4f (&xb)[4], const Geo& g, int cc, bool live) {
+  // chunk j of this wave's share of a tile: channels (wave_c + WC*j)*16 ..
+  auto issue = [&](v4f (&xb)[4], const Geo<SCALAR>& g, int j, bool live) {
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
-      const int c = cc * kChunk + 4 * s + cl;
-      xb[s] = load4(xr, (live && c < a.C && g.xo != kBufOOB) ? g.xo + (uint32_t)c * cstride : kBufOOB);
+      const int c = (wave_c + WC * j) * kChunk + 4 * s + cl;
+      xb[s] = load_px(xr, g.xo, (uint32_t)c * cstride, live && c < a.C);
     }
   };
 
@@ -143,13 +195,13 @@ __global__ __launch_bounds__(kThreads, 2) void pw_conv_kernel(PwArgs a) {
 #pragma unroll
     for (int v = 0; v < 4; ++v) acc[t][v] = v4f{0.f, 0.f, 0.f, 0.f};
 
-  auto compute = [&](const v4f (&xb)[4], int cc) {
+  auto compute = [&](const v4f (&xb)[4], int j) {
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
-      const int cs = cc * kChunk + 4 * s;  // first channel of the k-step
+      const int cs = (wave_c + WC * j) * kChunk + 4 * s;  // first channel of the k-step
       if (cs >= a.c4) break;
       float av[KT];
-      const float* wp = ws + ((cs >> 2) * 64 + lane) * KT;
+      const float* wp = ws + ((cs >> 2) * 64 + lane) * KT + (cs >> 2);
 #pragma unroll
       for (int t = 0; t < KT; ++t) av[t] = wp[t];
 #pragma unroll
@@ -159,59 +211,94 @@ __global__ __launch_bounds__(kThreads, 2) void pw_conv_kernel(PwArgs a) {
     }
   };
 
-  // offset of output channel k0 + 16t + 4cl + r at the lane's pixels
-  auto out_off = [&](const Geo& g, int t, int r) {
-    const int k = k0 + 16 * t + 4 * cl + r;
-    return (k < a.K && g.oo != kBufOOB) ? g.oo + (uint32_t)k * cstride : kBufOOB;
-  };
+  // Row q of the rows this wave finalizes in a channel block: all four
+  // (WC = 1) or row `wave` (WC = 4); output channel k0 + 16t + 4cl + row.
+  auto row_of = [&](int q) { return WC == 1 ? q : wave; };
+  auto krow = [&](int t, int q) { return k0 + 16 * t + 4 * cl + row_of(q); };
 
-  v4f rv[RES ? KT : 1][4];
-  auto issue_res = [&](const Geo& g) {
+  v4f rv[RES ? KT : 1][RES ? RR : 1];
+  auto issue_res = [&](const Geo<SCALAR>& g) {
 #pragma unroll
     for (int t = 0; t < KT; ++t)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) rv[RES ? t : 0][r] = load4(rr, out_off(g, t, r));
+      for (int q = 0; q < RR; ++q) {
+        const int k = krow(t, q);
+        rv[RES ? t : 0][RES ? q : 0] = load_px(resr, g.oo, (uint32_t)k * cstride, k < a.K);
+      }
   };
 
-  auto epilogue = [&](const Geo& g) {
+  auto finish = [&](v4f y, int t, int q, const Geo<SCALAR>& g) {
+    const int k = krow(t, q);
+    const float b = bs[k - k0];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      float o = y[v] + b;
+      if constexpr (RES) o += rv[t][q][v];
+      y[v] = activate<ACT>(o);
+    }
+    const bool on = k < a.K;
+    if constexpr (SCALAR) {
+      // one element at a time through a scalar: a bit cast of a vector
+      // element subscript reads element 0 whatever the index
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_int(static_cast<float>(y[e])), orr,
+                                              (on && g.oo[e] != kBufOOB) ? g.oo[e] + (uint32_t)k * cstride : kBufOOB,
+                                              0, 0);
+    } else {
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4i, y), orr,
+                                             (on && g.oo[0] != kBufOOB) ? g.oo[0] + (uint32_t)k * cstride : kBufOOB,
+                                             0, 0);
+    }
+  };
+
+  auto epilogue = [&](const Geo<SCALAR>& g) {
 #pragma unroll
     for (int t = 0; t < KT; ++t) {
-      const v4f b4 = *reinterpret_cast<const v4f*>(bs + 16 * t + 4 * cl);
+      if constexpr (WC == 1) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        v4f y;
+        for (int r = 0; r < 4; ++r) finish(v4f{acc[t][0][r], acc[t][1][r], acc[t][2][r], acc[t][3][r]}, t, r, g);
+      } else {
+        // partial sums of the four waves through red[src][v][r][lane],
+        // added in source order
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          float o = acc[t][v][r] + b4[r];
-          if constexpr (RES) o += rv[t][r][v];
-          y[v] = activate<ACT>(o);
-        }
-        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4i, y), orr, out_off(g, t, r), 0, 0);
+        for (int v = 0; v < 4; ++v)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) red[((wave * 4 + v) * 4 + r) * 64 + lane] = acc[t][v][r];
+        __syncthreads();
+        v4f y = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int src = 0; src < 4; ++src)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) y[v] += red[((src * 4 + v) * 4 + wave) * 64 + lane];
+        __syncthreads();  // the area is free for the next block
+        finish(y, t, 0, g);
       }
 #pragma unroll
       for (int v = 0; v < 4; ++v) acc[t][v] = v4f{0.f, 0.f, 0.f, 0.f};
     }
   };
 
-  // Chunk stream: chunk (i, cc) = channel chunk cc of this workgroup's tile
-  // i.  The issue side (ii, icc, gi) runs NB - 1 chunks ahead of the compute
-  // side (i, cc, gc); issues past the last tile load nothing.
-  const bool res_early = RES && a.nch >= NB;
-  int ii = 0, icc = 0;
-  Geo gi = geo(first);
+  // Chunk stream: chunk (i, j) = this wave's chunk j of its workgroup's tile
+  // i.  The issue side (ii, ij, gi) runs NB - 1 chunks ahead of the compute
+  // side (i, j, gc); issues past the last tile load nothing.  Every wave
+  // walks the same tiles, so the WC = 4 reduction barriers line up.
+  const bool res_early = RES && nchw >= NB;
+  int ii = 0, ij = 0;
+  Geo<SCALAR> gi = geo(first);
   auto issue_next = [&](v4f (&buf)[4]) {
     const bool live = ii < my_tiles;
-    issue(buf, gi, icc, live);
+    issue(buf, gi, ij, live);
     if constexpr (RES)
-      if (res_early && live && icc == a.nch - 1) issue_res(gi);
-    if (++icc == a.nch) {
-      icc = 0;
+      if (res_early && live && ij == nchw - 1) issue_res(gi);
+    if (++ij == nchw) {
+      ij = 0;
       ++ii;
       gi = geo(first + ii * (int)gridDim.x);
     }
   };
-  int i = 0, cc = 0;
-  Geo gc = gi;
+  int i = 0, j = 0;
+  Geo<SCALAR> gc = gi;
 
   v4f xb[NB][4];
 #pragma unroll
@@ -220,48 +307,53 @@ __global__ __launch_bounds__(kThreads, 2) void pw_conv_kernel(PwArgs a) {
   while (!done) {
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
-      const bool last = cc == a.nch - 1;
+      const bool last = j == nchw - 1;
       if constexpr (RES)
         if (!res_early && last) issue_res(gc);
       issue_next(xb[(b + NB - 1) % NB]);
-      compute(xb[b], cc);
+      compute(xb[b], j);
       if (last) {
         epilogue(gc);
         ++i;
-        cc = 0;
+        j = 0;
         if (i >= my_tiles) {
           done = true;
           break;
         }
         gc = geo(first + i * (int)gridDim.x);
       } else {
-        ++cc;
+        ++j;
       }
     }
   }
 }
 
-// Workgroups of `kernel` resident per CU with `lds` bytes of LDS each (the
-// runtime's occupancy calculation, cached for the last LDS size asked).
-template <class Kernel>
-int resident_per_cu(Kernel kernel, size_t lds) {
-  static size_t last_lds = ~size_t(0);
-  static int last = 1;
-  if (lds != last_lds) {
-    int occ = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kernel, kThreads, lds) != hipSuccess || occ < 1) occ = 1;
-    last = occ;
-    last_lds = lds;
-  }
-  return last;
+struct PwCfg {
+  int kt, wc;
+  bool scalar;
+  int slices;
+};
+
+size_t pw_lds(int c, const PwCfg& k) {
+  const size_t c4 = (size_t)round_up(c, 4);
+  return ((c4 + 1) * 16 * k.kt + c4 / 4 + (k.wc == 4 ? kRedFloats : 0)) * sizeof(float);
 }
 
 // Grid: one workgroup per (tile, slice) when they all fit on the GPU at
 // once, otherwise as many as fit, each walking an equal share of the tiles;
-// gridDim.y = slices.
+// gridDim.y = slices.  The runtime's occupancy figure is cached per kernel
+// for the last LDS size asked.
 template <class Kernel>
 dim3 pw_grid(Kernel kernel, const PwArgs& a, int slices, size_t lds) {
-  const int64_t fit = (int64_t)resident_per_cu(kernel, lds) * cu_count();
+  static size_t last_lds = ~size_t(0);
+  static int resident = 1;
+  if (lds != last_lds) {
+    int occ = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kernel, kThreads, lds) != hipSuccess || occ < 1) occ = 1;
+    resident = occ;
+    last_lds = lds;
+  }
+  const int64_t fit = (int64_t)resident * cu_count();
   int64_t gx = a.ntiles;
   if (gx * slices > fit) {
     const int64_t per = std::max<int64_t>(1, fit / slices);
@@ -276,59 +368,81 @@ dim3 pw_grid(Kernel kernel, const PwArgs& a, int slices, size_t lds) {
   return dim3((unsigned)round_up(gx, kXcds), (unsigned)slices);
 }
 
-template <int KT, int NB, int ACT, bool RES>
+template <int KT, int ACT, bool RES, int WC, bool SCALAR>
 int launch_one(const PwArgs& a, int slices, size_t lds, hipStream_t s) {
-  const auto kernel = pw_conv_kernel<KT, NB, ACT, RES>;
+  const auto kernel = pw_conv_kernel<KT, ACT, RES, WC, SCALAR>;
+  static bool attr_set = false;  // dynamic LDS above 64 KB needs the attribute
+  if (!attr_set) {
+    NHIP_TRY(check_hip(hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds),
+                       "hipFuncSetAttribute(pw_conv)"));
+    attr_set = true;
+  }
   NHIP_LAUNCH("pw_conv_f32", kernel, pw_grid(kernel, a, slices, lds), dim3(kThreads), lds, s, a);
   return check_launch("pw_conv_f32");
 }
 
-template <int KT, int NB, bool RES>
-int launch_act(const PwArgs& a, int act, int slices, size_t lds, hipStream_t s) {
-  if (act == NHIP_ACT_RELU) return launch_one<KT, NB, NHIP_ACT_RELU, RES>(a, slices, lds, s);
-  if (act == NHIP_ACT_SIGMOID) return launch_one<KT, NB, NHIP_ACT_SIGMOID, RES>(a, slices, lds, s);
-  return launch_one<KT, NB, NHIP_ACT_NONE, RES>(a, slices, lds, s);
+template <int KT, int WC, bool SCALAR>
+int launch_act(const PwArgs& a, int act, bool res, int slices, size_t lds, hipStream_t s) {
+  if (res) {
+    if (act == NHIP_ACT_RELU) return launch_one<KT, NHIP_ACT_RELU, true, WC, SCALAR>(a, slices, lds, s);
+    if (act == NHIP_ACT_SIGMOID) return launch_one<KT, NHIP_ACT_SIGMOID, true, WC, SCALAR>(a, slices, lds, s);
+    return launch_one<KT, NHIP_ACT_NONE, true, WC, SCALAR>(a, slices, lds, s);
+  }
+  if (act == NHIP_ACT_RELU) return launch_one<KT, NHIP_ACT_RELU, false, WC, SCALAR>(a, slices, lds, s);
+  if (act == NHIP_ACT_SIGMOID) return launch_one<KT, NHIP_ACT_SIGMOID, false, WC, SCALAR>(a, slices, lds, s);
+  return launch_one<KT, NHIP_ACT_NONE, false, WC, SCALAR>(a, slices, lds, s);
 }
 
-struct PwCfg {
-  int kt, nb, slices;
-};
+template <int WC, bool SCALAR>
+int launch_kt(const PwArgs& a, const PwCfg& c, int act, bool res, size_t lds, hipStream_t s) {
+  switch (c.kt) {
+    case 1: return launch_act<1, WC, SCALAR>(a, act, res, c.slices, lds, s);
+    case 2: return launch_act<2, WC, SCALAR>(a, act, res, c.slices, lds, s);
+    case 3: return launch_act<3, WC, SCALAR>(a, act, res, c.slices, lds, s);
+  }
+  return fail(NHIP_STATUS_CONSTRAINT_VIOLATION, "pointwise conv: no kernel for the configuration");
+}
 
-// Instantiated (KT, NB) pairs, with and without a residual (whose registers
-// are live beside the accumulators).
-constexpr PwCfg kPlain[] = {{1, 2, 1}, {1, 4, 1}, {2, 2, 1}, {2, 4, 1}, {3, 2, 1}, {3, 4, 1}, {4, 2, 1}, {6, 2, 1}};
-constexpr PwCfg kResid[] = {{1, 2, 1}, {1, 4, 1}, {2, 2, 1}, {2, 4, 1}, {3, 2, 1}, {4, 2, 1}};
-
-bool lds_ok(int c, int kt) { return (int64_t)(round_up(c, 4) + 1) * 16 * kt * (int64_t)sizeof(float) <= kMaxLds; }
-
-// Output channels per slice: KT = 1..3 (the fastest measured on the
-// MobileNetV2 layers: the kernel's code stays small and each slice's
-// re-read of x comes from L2), the largest that still gives two (tile,
-// slice) work items per CU and leaves no slice mostly padding; NB = 2.
-bool pw_config(const nhip_conv_plan* p, int64_t np, bool res, PwCfg* out) {
+// Work split and slicing for n images of P pixels:
+//   * WC = 4 when the image rows are not float4-aligned (P % 4 != 0), or
+//     when 256-pixel tiles give fewer work items than two per CU for a long
+//     reduction (8+ chunks): the channel chain of one wave is then the
+//     critical path, and four waves splitting it shorten it fourfold;
+//   * output channels per slice 16*KT with KT = 1..3 (larger KT measured
+//     slower on every MobileNetV2 layer: each slice's re-read of x comes
+//     from L2, and the kernel's code stays small), the largest that still
+//     gives two (tile, slice) work items per CU, fits the LDS and leaves no
+//     slice mostly padding.
+// NHIP_PW_CFG="kt,wc" forces a configuration (tuning and tests).
+bool pw_config(const nhip_conv_plan* p, int64_t np, int P, PwCfg* out) {
   const int kb = (int)ceil_div(p->g.k, 16);
-  const int64_t tiles = ceil_div(np, kTilePix);
-  int kt = 1;
+  const int nch = (int)ceil_div(round_up(p->g.c, 4), kChunk);
+  const int64_t target = 2LL * cu_count();
+  PwCfg c{1, 1, P % 4 != 0, 1};
+  if (c.scalar) c.wc = 4;
+  else if (nch >= 8 && ceil_div(np, 256) * kb < target) c.wc = 4;
+  const int64_t tiles = ceil_div(np, 256 / c.wc);
   for (int t = std::min(3, kb); t >= 1; --t) {
     const int slices = (int)ceil_div(kb, t);
-    if (slices * t - kb >= (t + 1) / 2 && t > 1) continue;  // a slice mostly padding
-    if (tiles * slices >= 2LL * cu_count()) {
-      kt = t;
+    if (t > 1 && slices * t - kb >= (t + 1) / 2) continue;  // a slice mostly padding
+    if (pw_lds(p->g.c, PwCfg{t, c.wc, c.scalar, slices}) > (size_t)kMaxLds) continue;
+    if (tiles * slices >= target || t == 1) {
+      c.kt = t;
       break;
     }
   }
-  int nb = 2;
-  if (const char* env = std::getenv("NHIP_PW_CFG")) {  // tuning override "kt,nb"
-    int ekt = 0, enb = 0;
-    if (std::sscanf(env, "%d,%d", &ekt, &enb) == 2) {
-      const PwCfg* tab = res ? kResid : kPlain;
-      const int nt = res ? (int)(sizeof(kResid) / sizeof(PwCfg)) : (int)(sizeof(kPlain) / sizeof(PwCfg));
-      for (int j = 0; j < nt; ++j)
-        if (tab[j].kt == ekt && tab[j].nb == enb) kt = ekt, nb = enb;
+  if (const char* env = std::getenv("NHIP_PW_CFG")) {
+    int kt = 0, wc = 0;
+    if (std::sscanf(env, "%d,%d", &kt, &wc) == 2 && kt >= 1 && kt <= 3 && (wc == 4 || (wc == 1 && !c.scalar))) {
+      c.kt = kt;
+      c.wc = wc;
     }
   }
-  if (!lds_ok(p->g.c, kt)) return false;
-  *out = {kt, nb, (int)ceil_div(kb, kt)};
+  c.slices = (int)ceil_div(kb, c.kt);
+  if (c.wc == 4 && nch < 4) return false;  // every wave needs a chunk
+  if (pw_lds(p->g.c, c) > (size_t)kMaxLds) return false;
+  *out = c;
   return true;
 }
 
@@ -337,27 +451,27 @@ bool pw_config(const nhip_conv_plan* p, int64_t np, bool res, PwCfg* out) {
 bool pointwise_selected(const nhip_conv_plan* p, int n, int h, int w) {
   const ConvGeom& g = p->g;
   if (g.kh != 1 || g.kw != 1 || g.sh != 1 || g.sw != 1 || g.pt || g.pb || g.pl || g.pr) return false;
-  if ((h * w) % 4 != 0) return false;
-  bool forced = false;
-  if (const char* env = std::getenv("NHIP_POINTWISE")) {
+  if (const char* env = std::getenv("NHIP_POINTWISE"))
     if (env[0] == '0') return false;
-    forced = env[0] == '2';  // every eligible shape (tests)
-  }
-  // Few pixels and long reductions: the chunk chain of one wave is the
-  // critical path, and the implicit GEMM's split-K keeps more CUs busy
-  // (measured on the MobileNetV2 layers: 384 -> 64 and 576 -> 96 at 14x14).
-  if (!forced && (int64_t)n * h * w < 16384 && g.c > 192) return false;
   PwCfg c;
-  if (!pw_config(p, (int64_t)n * h * w, false, &c) || !pw_config(p, (int64_t)n * h * w, true, &c)) return false;
+  const int64_t np = (int64_t)n * h * w;
+  if (!pw_config(p, np, h * w, &c)) return false;
   // x and out are addressed by 32-bit buffer offsets
-  const int64_t xb = (int64_t)n * g.c * h * w * 4, ob = (int64_t)n * g.k * h * w * 4;
-  return xb < (int64_t(1) << 31) && ob < (int64_t(1) << 31);
+  const int64_t xb = np * g.c * 4, ob = np * g.k * 4;
+  if (xb >= (int64_t(1) << 31) || ob >= (int64_t(1) << 31)) return false;
+  // Every tile's workgroups read the whole weight matrix once: when that
+  // exceeds twice the activation traffic (few pixels, many channels: the
+  // 7x7 layers of MobileNetV2), the implicit GEMM, which streams the weights
+  // through its K loop, measured faster.
+  const int64_t w_traffic = ceil_div(np, 256 / c.wc) * (int64_t)g.c * g.k * 4;
+  const bool forced = std::getenv("NHIP_PW_CFG") != nullptr;
+  return forced || w_traffic <= 2 * (xb + ob);
 }
 
 int launch_conv_pointwise_f32(const nhip_conv_plan* p, const float* in, const float* residual, float* out, int n,
                               int h, int w, hipStream_t s) {
   PwCfg c;
-  if ((h * w) % 4 != 0 || !pw_config(p, (int64_t)n * h * w, residual != nullptr, &c))
+  if (!pw_config(p, (int64_t)n * h * w, h * w, &c))
     return fail(NHIP_STATUS_CONSTRAINT_VIOLATION, "pointwise conv: unsupported shape");
   PwArgs a{};
   a.x = in;
@@ -371,34 +485,16 @@ int launch_conv_pointwise_f32(const nhip_conv_plan* p, const float* in, const fl
   a.ldw = p->kred_pad;
   a.c4 = (int)round_up(a.C, 4);
   a.np = n * a.P;
-  a.ntiles = (int)ceil_div(a.np, kTilePix);
+  a.ntiles = (int)ceil_div(a.np, 256 / c.wc);
   a.nch = (int)ceil_div(a.c4, kChunk);
   a.x_bytes = (uint32_t)((int64_t)n * a.C * a.P * 4);
   a.out_bytes = (uint32_t)((int64_t)n * a.K * a.P * 4);
-  const size_t lds = (size_t)(a.c4 + 1) * 16 * c.kt * sizeof(float);
+  const size_t lds = pw_lds(a.C, c);
   const int act = p->g.act;
-  if (residual) {
-    switch (c.kt * 10 + c.nb) {
-      case 12: return launch_act<1, 2, true>(a, act, c.slices, lds, s);
-      case 14: return launch_act<1, 4, true>(a, act, c.slices, lds, s);
-      case 22: return launch_act<2, 2, true>(a, act, c.slices, lds, s);
-      case 24: return launch_act<2, 4, true>(a, act, c.slices, lds, s);
-      case 32: return launch_act<3, 2, true>(a, act, c.slices, lds, s);
-      case 42: return launch_act<4, 2, true>(a, act, c.slices, lds, s);
-    }
-  } else {
-    switch (c.kt * 10 + c.nb) {
-      case 12: return launch_act<1, 2, false>(a, act, c.slices, lds, s);
-      case 14: return launch_act<1, 4, false>(a, act, c.slices, lds, s);
-      case 22: return launch_act<2, 2, false>(a, act, c.slices, lds, s);
-      case 24: return launch_act<2, 4, false>(a, act, c.slices, lds, s);
-      case 32: return launch_act<3, 2, false>(a, act, c.slices, lds, s);
-      case 34: return launch_act<3, 4, false>(a, act, c.slices, lds, s);
-      case 42: return launch_act<4, 2, false>(a, act, c.slices, lds, s);
-      case 62: return launch_act<6, 2, false>(a, act, c.slices, lds, s);
-    }
-  }
-  return fail(NHIP_STATUS_CONSTRAINT_VIOLATION, "pointwise conv: no kernel for the configuration");
+  const bool res = residual != nullptr;
+  if (c.wc == 1) return launch_kt<1, false>(a, c, act, res, lds, s);
+  if (!c.scalar) return launch_kt<4, false>(a, c, act, res, lds, s);
+  return launch_kt<4, true>(a, c, act, res, lds, s);
 }
 
 }  // namespace nhip

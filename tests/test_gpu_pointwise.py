@@ -3,12 +3,13 @@ the CPU oracle restating the reference's Convolution lowering
 (NCNNToTosa.cpp:1316-1529, kernel 1x1 stride 1 pad 0, + the importer's
 separate relu and the BinaryOp add), max relative error <= 1e-4.
 
-The cases cover every weight-slice configuration the host picks (output
-channel blocks KT = 1..12, 2- and 4-pixel lanes, several slices), channel
-counts that are not multiples of 4 or 16, pixel tiles that cross image
-boundaries and end past the last pixel, the persistent loop (a workgroup
-walking many tiles, its prefetch crossing tile boundaries) and all three
-activations with and without a residual.
+The cases cover every kernel configuration (16..48 output channels per
+slice, one or several slices, the channels of a tile split over one or four
+waves, float4-aligned and unaligned pixel rows), channel counts that are not
+multiples of 4 or 16, pixel tiles that cross image boundaries and end past
+the last pixel, the persistent loop (a workgroup walking many tiles, its
+prefetch crossing tile boundaries) and all three activations with and
+without a residual.
 """
 import numpy as np
 import pytest
@@ -30,13 +31,6 @@ RNG = np.random.default_rng(11)
 def _gpu():
     assert torch.cuda.is_available(), "GPU tests need a HIP device"
     nhip.init(0)
-
-
-@pytest.fixture(autouse=True)
-def _every_shape(monkeypatch):
-    """NHIP_POINTWISE=2: the kernel takes every eligible shape, also those
-    below the pixel count from which the library picks it by default."""
-    monkeypatch.setenv("NHIP_POINTWISE", "2")
 
 
 def dev(a):
@@ -95,12 +89,21 @@ CASES = [
     (2, 16, 28, 28, 96, False, nhip.ACT_RELU),      # MobileNetV2 expand shape
     (36, 8, 64, 64, 16, True, nhip.ACT_RELU),       # 576 tiles: more than the default grid
     (32, 16, 28, 28, 64, False, nhip.ACT_RELU),     # 25088 pixels: picked without the override
+    (2, 72, 7, 7, 40, True, nhip.ACT_RELU),         # 7x7: unaligned rows, channels over 4 waves
+    (3, 100, 5, 5, 20, False, nhip.ACT_SIGMOID),    # 5x5
+    (4, 576, 7, 7, 160, False, nhip.ACT_NONE, "1,4"),  # MobileNetV2 576 -> 160 at 7x7 (forced)
+    (2, 384, 14, 14, 64, True, nhip.ACT_NONE),      # MobileNetV2 384 -> 64 (+ residual) at 14x14
+    (1, 960, 7, 7, 320, False, nhip.ACT_NONE, "2,4"),  # a 960-channel weight slice in LDS (forced)
 ]
 
 
 @pytest.mark.parametrize("case", CASES, ids=lambda c: "x".join(map(str, c[:5])) + ("r" if c[5] else "") + f"a{c[6]}")
-def test_pointwise_matches_oracle(case):
-    run(*case)
+def test_pointwise_matches_oracle(case, monkeypatch):
+    """Cases with an eighth entry force that configuration (NHIP_PW_CFG):
+    the library leaves those shapes to the implicit GEMM by default."""
+    if len(case) > 7:
+        monkeypatch.setenv("NHIP_PW_CFG", case[7])
+    run(*case[:7])
 
 
 @pytest.mark.parametrize("wgs", ["1", "3", "8"])
@@ -126,19 +129,21 @@ def test_pointwise_persistent_walk(case, wgs, monkeypatch):
     assert_close(narrow, exp, RTOL, f"walk {case} wgs={wgs}")
 
 
-PLAIN_CFGS = ["1,2", "1,4", "2,2", "2,4", "3,2", "3,4", "4,2", "6,2"]
-RESID_CFGS = ["1,2", "1,4", "2,2", "2,4", "3,2", "4,2"]
+CFGS = ["1,1", "2,1", "3,1", "1,4", "2,4", "3,4"]
 
 
-@pytest.mark.parametrize("cfg", PLAIN_CFGS + ["r" + c for c in RESID_CFGS])
-def test_pointwise_every_instantiation(cfg, monkeypatch):
-    """Each (KT, NB) kernel (16*KT output channels per slice, NB chunk
-    buffers) forced through NHIP_PW_CFG, with K = 70 (several slices, a
-    partial last block) and C = 36 (three chunks, the last partial: fewer
-    chunks than buffers for NB = 4)."""
-    res = cfg.startswith("r")
-    monkeypatch.setenv("NHIP_PW_CFG", cfg.lstrip("r"))
-    run(3, 36, 6, 8, 70, res, nhip.ACT_RELU)
+@pytest.mark.parametrize("res", [False, True], ids=["plain", "res"])
+@pytest.mark.parametrize("cfg", CFGS)
+@pytest.mark.parametrize("hw", [(6, 8), (5, 5)], ids=["aligned", "unaligned"])
+def test_pointwise_every_instantiation(cfg, res, hw, monkeypatch):
+    """Each kernel forced through NHIP_PW_CFG="kt,wc" (16*kt output channels
+    per slice, the channels of a tile over wc waves; unaligned rows always
+    take wc = 4), with K = 70 (several slices, a partial last block) and
+    C = 72 (five chunks: the four waves get 2, 1, 1, 1)."""
+    if hw == (5, 5) and cfg.endswith(",1"):
+        pytest.skip("unaligned pixel rows have no one-wave split")
+    monkeypatch.setenv("NHIP_PW_CFG", cfg)
+    run(3, 72, hw[0], hw[1], 70, res, nhip.ACT_RELU)
 
 
 def test_pointwise_no_bias_and_batch_independence():
@@ -152,28 +157,28 @@ def test_pointwise_no_bias_and_batch_independence():
         np.testing.assert_array_equal(host(conv.forward(dev(x[i:i + 1]))), whole[i:i + 1])
 
 
-def test_pointwise_off_switch_falls_back_to_implicit_gemm(monkeypatch):
+def test_pointwise_off_switch_and_ineligible_shapes(monkeypatch):
     """NHIP_POINTWISE=0 routes 1x1 layers to the implicit GEMM (the tuning
-    comparison); both agree within the budget.  Without a setting, layers
-    with few pixels and more than 192 input channels take the implicit GEMM."""
+    comparison); both agree within the budget.  Shapes the kernel does not
+    take go to the implicit GEMM: stride 2, and unaligned pixel rows with
+    fewer than four channel chunks (one per wave)."""
     n, c, h, w, k = 2, 32, 8, 8, 64
     x = RNG.uniform(-1, 1, (n, c, h, w)).astype(np.float32)
     wt = workloads.he_normal(RNG, (k, c, 1, 1), c)
     d = nhip.conv_desc(c, k, (1, 1), (1, 1), (1, 1), (0, 0, 0, 0), bias=False)
+    nhip.timer_start("pw_conv")
     a = host(nhip.Conv2dF32(d, wt).forward(dev(x)))
+    assert nhip.timer_stop()[0] == 1
     monkeypatch.setenv("NHIP_POINTWISE", "0")
     nhip.timer_start("pw_conv")
     b = host(nhip.Conv2dF32(d, wt).forward(dev(x)))
     assert nhip.timer_stop()[0] == 0
     assert_close(a, b, RTOL, "pointwise vs implicit GEMM")
     monkeypatch.delenv("NHIP_POINTWISE")
-    nhip.timer_start("pw_conv")
-    nhip.Conv2dF32(d, wt).forward(dev(x))  # 32 channels: the pointwise kernel
-    assert nhip.timer_stop()[0] == 1
-    c = 256  # few pixels, long reduction: the implicit GEMM
-    x = RNG.uniform(-1, 1, (n, c, h, w)).astype(np.float32)
-    wt = workloads.he_normal(RNG, (k, c, 1, 1), c)
-    d = nhip.conv_desc(c, k, (1, 1), (1, 1), (1, 1), (0, 0, 0, 0), bias=False)
-    nhip.timer_start("pw_conv")
-    nhip.Conv2dF32(d, wt).forward(dev(x))
-    assert nhip.timer_stop()[0] == 0
+    for c, hw, stride in ((32, 8, 2), (48, 7, 1)):
+        x = dev(RNG.uniform(-1, 1, (n, c, hw, hw)).astype(np.float32))
+        wt = workloads.he_normal(RNG, (k, c, 1, 1), c)
+        d = nhip.conv_desc(c, k, (1, 1), (stride, stride), (1, 1), (0, 0, 0, 0), bias=False)
+        nhip.timer_start("pw_conv")
+        nhip.Conv2dF32(d, wt).forward(x)
+        assert nhip.timer_stop()[0] == 0
