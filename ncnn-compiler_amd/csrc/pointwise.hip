@@ -24,8 +24,9 @@
 //   WC = 4  the four waves share one 64-pixel tile and take every fourth
 //           chunk of the channels, their partial sums added through LDS in
 //           a fixed order (few pixels, long reductions: 14x14 and 7x7).
-// SCALAR (H*W % 4 != 0, e.g. 7x7): a lane's four pixels may lie in two
-// images, so they are loaded and stored one float at a time.
+// SCALAR (H*W % 4 != 0, e.g. 7x7): no 16-byte vectors; lane l holds pixels
+// l%16 + 16*v instead, loaded and stored one float at a time, 16 lanes
+// covering 64 contiguous bytes per instruction.
 #include <cstdio>
 #include <cstdlib>
 
@@ -153,11 +154,14 @@ __global__ __launch_bounds__(kThreads, 2) void pw_conv_kernel(PwArgs a) {
   auto geo = [&](int tile) {
     const int q0 = tile * TP;  // uniform
     const int n0 = q0 / a.P, p0 = q0 - n0 * a.P;
-    const int u0 = p0 + (WC == 1 ? wave * 64 : 0) + 4 * jl;
+    // the lane's pixels: 4*jl + v (one 16-byte vector), or, one float at a
+    // time, jl + 16*v (each load and store instruction then covers 16
+    // consecutive pixels of a channel row)
+    const int u0 = p0 + (WC == 1 ? wave * 64 : 0) + (SCALAR ? jl : 4 * jl);
     Geo<SCALAR> g;
 #pragma unroll
     for (int v = 0; v < (SCALAR ? 4 : 1); ++v) {
-      const int u = u0 + v;  // pixel of image n0 + dn at position p
+      const int u = u0 + 16 * v;  // pixel of image n0 + dn at position p
       int dn = (int)((float)u * inv_p);
       int p = u - dn * a.P;
       if (p < 0) { --dn; p += a.P; }
