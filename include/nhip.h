@@ -167,6 +167,24 @@ int nhip_dwconv2d_f32_forward(nhip_conv_t plan, const float* input,
                               float* output, int32_t n, int32_t h, int32_t w,
                               void* stream);
 
+/* No counterpart in the reference (it lowers every layer on its own): an fp32
+ * 3x3 ConvolutionDepthWise (stride 1 or 2, padding 1, its bias and
+ * activation) whose output only feeds a 1x1 stride-1 fp32 Convolution, run
+ * as one kernel without writing the depthwise output — the depthwise ->
+ * project pair of an inverted-residual block, fused by the graph executor.
+ * Results are those of nhip_dwconv2d_f32_forward followed by
+ * nhip_conv2d_f32_forward (the depthwise values are computed in the same
+ * order).  _supported sets *supported to 1 when the pair and the input
+ * extent qualify (3x3, padding 1, W and the output width multiples of 4);
+ * _forward then takes input [n,C,h,w] of dw, residual/output of pw's shape
+ * (residual may be NULL), device pointers, no workspace. */
+int nhip_dwconv2d_pw_f32_supported(nhip_conv_t dw, nhip_conv_t pw, int32_t n,
+                                   int32_t h, int32_t w, int32_t* supported);
+int nhip_dwconv2d_pw_f32_forward(nhip_conv_t dw, nhip_conv_t pw,
+                                 const float* input, const float* residual,
+                                 float* output, int32_t n, int32_t h, int32_t w,
+                                 void* stream);
+
 /* a3 int8 — ConvolutionDepthWise with int8_scale_term (NCNNToTosa.cpp:
  * 3257-3376).  weight: host [C][1][kh][kw], int8 when weight_is_i8 else fp32
  * quantized per channel with weight_scale; weight_scale has C entries

@@ -467,6 +467,10 @@ struct Op {
   enum class View { Same, Flatten, Reshape, Squeeze } view = View::Same;
   std::vector<int64_t> reshape;  // (w, h, c) targets, -1 infer, 0 absent
   std::vector<int64_t> squeeze_axes;
+  // Depthwise -> 1x1 fusion (nhip_dwconv2d_pw_f32_*): on the depthwise op,
+  // the index of the convolution that is its output's only consumer; on
+  // that convolution, the depthwise op's index.
+  int fuse_into = -1, fuse_from = -1;
 };
 
 struct Blob {
@@ -505,6 +509,31 @@ struct nhip_graph {
 };
 
 namespace {
+
+// Candidates for the depthwise -> 1x1 fusion: an fp32 depthwise op whose
+// output blob is read by exactly one op, an fp32 convolution taking it as its
+// main input (not as a residual), and is no graph output.  Whether the pair's
+// shapes have a fused kernel is asked at run time.
+void mark_dw_pw_pairs(nhip_graph& g) {
+  std::vector<int> uses(g.blobs.size(), 0);
+  for (const Op& op : g.ops) {
+    for (int b : op.in) ++uses[b];
+    if (op.residual >= 0) ++uses[op.residual];
+  }
+  for (int b : g.outputs) ++uses[b];
+  for (size_t i = 0; i < g.ops.size(); ++i) {
+    Op& d = g.ops[i];
+    if (d.kind != OpKind::DwF32 || uses[d.out] != 1) continue;
+    for (size_t j = i + 1; j < g.ops.size(); ++j) {
+      Op& c = g.ops[j];
+      if (c.kind == OpKind::ConvF32 && !c.in.empty() && c.in[0] == d.out && c.residual != d.out) {
+        d.fuse_into = (int)j;
+        c.fuse_from = (int)i;
+        break;
+      }
+    }
+  }
+}
 
 int64_t out_extent(int64_t in, int64_t k, int64_t s, int64_t d, int64_t pa, int64_t pb) {
   if (in < 0) return -1;
@@ -922,6 +951,7 @@ int build(nhip_graph& g, std::vector<Layer>& layers, const int64_t* input_shapes
   for (const Op& op : g.ops)
     if (op.kind != OpKind::Input && !consumed.count(op.out)) g.outputs.push_back(op.out);
   if (g.inputs.empty() || g.outputs.empty()) return fail(NHIP_STATUS_CONSTRAINT_VIOLATION, "graph needs inputs and outputs");
+  mark_dw_pw_pairs(g);
   return ok();
 }
 
@@ -956,8 +986,28 @@ int run_ops(nhip_graph& g, int n, const std::vector<Shape>& sh, const void* cons
   }
   TRY(ensure(&g.ws, &g.ws_cap, std::max<uint64_t>(ws_need, 256)));
   for (size_t i = 0; i < g.inputs.size(); ++i) ptr[g.inputs[i]] = (char*)inputs[i];
-  for (const Op& op : g.ops) {
+  std::vector<char> fused(g.ops.size(), 0);  // depthwise ops folded into their 1x1 consumer
+  for (size_t oi = 0; oi < g.ops.size(); ++oi) {
+    const Op& op = g.ops[oi];
     if (op.kind == OpKind::Input) continue;
+    if (op.kind == OpKind::DwF32 && op.fuse_into >= 0) {
+      const Shape& a = sh[op.in[0]];
+      int32_t sup = 0;
+      TRY(nhip_dwconv2d_pw_f32_supported(op.conv, g.ops[op.fuse_into].conv, n, (int32_t)a.d[1], (int32_t)a.d[2], &sup));
+      if (sup) {
+        fused[oi] = 1;
+        continue;
+      }
+    }
+    if (op.kind == OpKind::ConvF32 && op.fuse_from >= 0 && fused[op.fuse_from]) {
+      const Op& d = g.ops[op.fuse_from];
+      const Shape& a = sh[d.in[0]];
+      ptr[op.out] = (char*)g.blobs[op.out].buf;
+      TRY(nhip_dwconv2d_pw_f32_forward(d.conv, op.conv, (const float*)ptr[d.in[0]],
+                                       op.residual >= 0 ? (const float*)ptr[op.residual] : nullptr,
+                                       (float*)ptr[op.out], n, (int32_t)a.d[1], (int32_t)a.d[2], stream));
+      continue;
+    }
     if (op.kind == OpKind::Alias) {
       ptr[op.out] = ptr[op.in[0]];
       continue;

@@ -146,6 +146,11 @@ uint64_t conv_igemm_f32_workspace(const nhip_conv_plan* p, int n, int oh,
 bool pointwise_selected(const nhip_conv_plan* p, int n, int h, int w);
 int launch_conv_pointwise_f32(const nhip_conv_plan* p, const float* in, const float* residual, float* out, int n,
                               int h, int w, hipStream_t s);
+// A 3x3 depthwise convolution feeding a 1x1 convolution, in one pass
+// (pointwise.hip): dwpw_supported says whether the pair and shape qualify.
+bool dwpw_supported(const nhip_conv_plan* dw, const nhip_conv_plan* pw, int n, int h, int w);
+int launch_dwpw_f32(const nhip_conv_plan* dw, const nhip_conv_plan* pw, const float* in, const float* residual,
+                    float* out, int n, int h, int w, hipStream_t s);
 int launch_conv_winograd_f32(const nhip_conv_plan* p, const float* in,
                              const float* residual, float* out, int n, int h,
                              int w, int oh, int ow, void* ws,

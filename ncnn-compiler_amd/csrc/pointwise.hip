@@ -27,6 +27,15 @@
 // SCALAR (H*W % 4 != 0, e.g. 7x7): no 16-byte vectors; lane l holds pixels
 // l%16 + 16*v instead, loaded and stored one float at a time, 16 lanes
 // covering 64 contiguous bytes per instruction.
+// DW = 1 or 2: the 1x1 convolution's input is computed on the fly as a 3x3
+// depthwise convolution (stride DW, padding 1, ncnn ConvolutionDepthWise,
+// NCNNToTosa.cpp:3376-3503) of x, the inverted-residual block's
+// depthwise -> project pair in one pass: channels stream 4 per chunk, each
+// lane loads its channel's 3 x (4*DW + 2) input window (16-byte loads for
+// the centre, the zero padding through out-of-range offsets) and forms its
+// four depthwise outputs in the reference's order (zero, += x*w over
+// (kh, kw), + bias, activation; no fused multiply-add), which are then the
+// MFMA B operand.  The depthwise output never goes to memory.
 #include <cstdio>
 #include <cstdlib>
 
@@ -49,8 +58,12 @@ struct PwArgs {
   float* out;            // [N][K][P]
   int C, K, P, ldw, c4;  // c4 = C rounded up to 4
   int np;                // N * P pixels (< 2^29: x is < 2^31 bytes)
-  int ntiles, nch;       // pixel tiles, channel chunks (nch >= WC)
+  int ntiles, nch;       // pixel tiles, 16-channel groups (nch >= WC)
   uint32_t x_bytes, out_bytes;
+  // DW: x is the depthwise input [N][C][H][W]; P = OH*OW of the output
+  const float* dw_w;     // [C][9]
+  const float* dw_b;     // [C]
+  int H, W, OW, dw_act;
 };
 
 template <int ACT>
@@ -66,10 +79,31 @@ __device__ __forceinline__ v4f load4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
 
 // Per-lane pixel geometry of a tile: byte offsets of (n, channel 0, p) in x
 // and in out / the residual for the lane's four pixels (one offset when they
-// are consecutive in one image); out of range past the last pixel.
-template <bool SCALAR>
+// are consecutive in one image); out of range past the last pixel.  DW: xo
+// are the three input rows of the depthwise window (byte offset of (n, 0,
+// row, DW*ox), out of range for rows outside the image) and lok / rok say
+// whether the window's left / right halo column lies inside the image.
+template <bool SCALAR, int DW>
 struct Geo {
-  uint32_t xo[SCALAR ? 4 : 1], oo[SCALAR ? 4 : 1];
+  uint32_t xo[DW ? 3 : (SCALAR ? 4 : 1)], oo[SCALAR ? 4 : 1];
+  bool lok, rok;
+};
+
+// One chunk of input in registers: four 16-byte pixel vectors (one per
+// k-step of 4 channels), or the lane's depthwise window rows for one k-step.
+template <int DW>
+struct XChunk {
+  v4f x[4];
+};
+template <>
+struct XChunk<1> {
+  float l[3], r[3];
+  v4f m[3];
+};
+template <>
+struct XChunk<2> {
+  float l[3];
+  v4f m[3], m2[3];
 };
 
 // LDS: W[k0 + 16t + j][c] at (c*16 + j)*KT + t + c/4 (c < c4, j < 16,
@@ -86,11 +120,14 @@ struct Geo {
 // Loads and stores are raw buffer operations on 32-bit offsets: positions
 // past the last pixel or channel carry an offset past the buffer's size, so
 // they neither branch nor touch memory.
-template <int KT, int ACT, bool RES, int WC, bool SCALAR>
+template <int KT, int ACT, bool RES, int WC, bool SCALAR, int DW>
 __global__ __launch_bounds__(kThreads, 2) void pw_conv_kernel(PwArgs a) {
   static_assert(WC == 1 || WC == 4, "channel split over 1 or 4 waves");
   static_assert(!SCALAR || WC == 4, "unaligned pixel rows use the 64-pixel tiles");
-  constexpr int NB = WC == 1 ? 2 : 4;   // chunk buffers
+  static_assert(!(SCALAR && DW), "the depthwise input needs float4-aligned rows");
+  constexpr int CCH = DW ? 4 : kChunk;  // channels per chunk
+  constexpr int SPC = CCH / 4;          // MFMA k-steps per chunk
+  constexpr int NB = (WC == 1 && !DW) ? 2 : 4;  // chunk buffers
   constexpr int TP = 256 / WC;          // pixels per tile
   constexpr int KS = 16 * KT;           // output channels per slice
   constexpr int RR = WC == 1 ? 4 : 1;   // accumulator rows a wave finalizes
@@ -98,7 +135,8 @@ __global__ __launch_bounds__(kThreads, 2) void pw_conv_kernel(PwArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int k0 = blockIdx.y * KS;
   float* bs = ws + a.c4 * KS + a.c4 / 4;
-  float* red = bs + KS;
+  float* dws = bs + KS;                          // DW: [c][12] weights, bias
+  float* red = dws + (DW ? a.c4 * 12 : 0);
 
   // ---- weights and bias of the slice into LDS -----------------------------
   // 16-byte loads along c (weight rows are 16-float aligned and zero past C),
@@ -128,6 +166,11 @@ __global__ __launch_bounds__(kThreads, 2) void pw_conv_kernel(PwArgs a) {
     }
   }
   for (int e = tid; e < KS; e += kThreads) bs[e] = (k0 + e < a.K) ? a.bias[k0 + e] : 0.f;
+  if constexpr (DW != 0)
+    for (int e = tid; e < a.c4 * 12; e += kThreads) {
+      const int c = e / 12, t = e - c * 12;
+      dws[e] = c >= a.C ? 0.f : t < 9 ? a.dw_w[c * 9 + t] : t == 9 ? a.dw_b[c] : 0.f;
+    }
   __syncthreads();
 
   // XCD-contiguous renumbering of the pixel tiles: consecutive tiles stay on
@@ -146,9 +189,17 @@ __global__ __launch_bounds__(kThreads, 2) void pw_conv_kernel(PwArgs a) {
   const __amdgpu_buffer_rsrc_t orr = make_rsrc(a.out, a.out_bytes);
   const __amdgpu_buffer_rsrc_t resr = make_rsrc(a.res, RES ? a.out_bytes : 0u);
   const int jl = lane & 15, cl = lane >> 4;
-  const int wave_c = WC == 1 ? 0 : wave;            // first chunk of this wave
-  const int nchw = (a.nch - wave_c + WC - 1) / WC;  // chunks per tile (>= 1)
+  // The channels of a tile come in 16-channel groups; with WC = 4 wave w
+  // takes groups w, w+4, ... (the same split, and so the same summation
+  // order, with or without the depthwise input).  A chunk is one group, or
+  // with DW a quarter of one.
+  const int wave_c = WC == 1 ? 0 : wave;                       // first group of this wave
+  const int nchw = (a.nch - wave_c + WC - 1) / WC * (16 / CCH);  // chunks per tile (>= 1)
+  auto chunk_c0 = [&](int j) {  // first channel of chunk j of this wave
+    return DW ? (wave_c + WC * (j >> 2)) * kChunk + (j & 3) * CCH : (wave_c + WC * j) * kChunk;
+  };
   const uint32_t cstride = (uint32_t)a.P * 4u;      // bytes between channel planes
+  const uint32_t xcstride = DW ? (uint32_t)(a.H * a.W) * 4u : cstride;  // ... of x
   const float inv_p = 1.0f / (float)a.P;
 
   auto geo = [&](int tile) {
@@ -158,7 +209,7 @@ __global__ __launch_bounds__(kThreads, 2) void pw_conv_kernel(PwArgs a) {
     // time, jl + 16*v (each load and store instruction then covers 16
     // consecutive pixels of a channel row)
     const int u0 = p0 + (WC == 1 ? wave * 64 : 0) + (SCALAR ? jl : 4 * jl);
-    Geo<SCALAR> g;
+    Geo<SCALAR, DW> g;
 #pragma unroll
     for (int v = 0; v < (SCALAR ? 4 : 1); ++v) {
       const int u = u0 + 16 * v;  // pixel of image n0 + dn at position p
@@ -168,7 +219,21 @@ __global__ __launch_bounds__(kThreads, 2) void pw_conv_kernel(PwArgs a) {
       if (p >= a.P) { ++dn; p -= a.P; }
       const int n = n0 + dn;
       const bool ok = q0 + (u - p0) < a.np;
-      g.xo[v] = ok ? (uint32_t)(n * a.C * a.P + p) * 4u : kBufOOB;
+      if constexpr (DW != 0) {
+        // output (oy, ox .. ox+3), OW % 4 == 0; window rows DW*oy - 1 .. +1,
+        // columns DW*ox - 1 .. DW*(ox+3) + 1
+        const int oy = p / a.OW, ox = p - oy * a.OW;
+#pragma unroll
+        for (int i = 0; i < 3; ++i) {
+          const int iy = DW * oy - 1 + i;
+          g.xo[i] = (ok && (unsigned)iy < (unsigned)a.H) ? (uint32_t)((n * a.C * a.H + iy) * a.W + DW * ox) * 4u
+                                                         : kBufOOB;
+        }
+        g.lok = ox > 0;
+        g.rok = DW * ox + 4 < a.W;
+      } else {
+        g.xo[v] = ok ? (uint32_t)(n * a.C * a.P + p) * 4u : kBufOOB;
+      }
       g.oo[v] = ok ? (uint32_t)(n * a.K * a.P + p) * 4u : kBufOOB;
     }
     return g;
@@ -184,12 +249,29 @@ __global__ __launch_bounds__(kThreads, 2) void pw_conv_kernel(PwArgs a) {
     }
   };
 
-  // chunk j of this wave's share of a tile: channels (wave_c + WC*j)*16 ..
-  auto issue = [&](v4f (&xb)[4], const Geo<SCALAR>& g, int j, bool live) {
+  // chunk j of this wave's share of a tile: channels (wave_c + WC*j)*CCH ..
+  auto issue = [&](XChunk<DW>& xb, const Geo<SCALAR, DW>& g, int j, bool live) {
+    if constexpr (DW == 0) {
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const int c = (wave_c + WC * j) * kChunk + 4 * s + cl;
-      xb[s] = load_px(xr, g.xo, (uint32_t)c * cstride, live && c < a.C);
+      for (int s = 0; s < 4; ++s) {
+        const int c = chunk_c0(j) + 4 * s + cl;
+        xb.x[s] = load_px(xr, g.xo, (uint32_t)c * cstride, live && c < a.C);
+      }
+    } else {
+      const int c = chunk_c0(j) + cl;
+      const bool on = live && c < a.C;
+      const uint32_t add = (uint32_t)c * xcstride;
+#pragma unroll
+      for (int i = 0; i < 3; ++i) {
+        const bool row = on && g.xo[i] != kBufOOB;
+        const uint32_t b = g.xo[i] + add;
+        xb.l[i] = buf_load_f32(xr, (row && g.lok) ? b - 4u : kBufOOB);
+        xb.m[i] = load4(xr, row ? b : kBufOOB);
+        if constexpr (DW == 1)
+          xb.r[i] = buf_load_f32(xr, (row && g.rok) ? b + 16u : kBufOOB);
+        else
+          xb.m2[i] = load4(xr, row ? b + 16u : kBufOOB);
+      }
     }
   };
 
@@ -199,11 +281,48 @@ __global__ __launch_bounds__(kThreads, 2) void pw_conv_kernel(PwArgs a) {
 #pragma unroll
     for (int v = 0; v < 4; ++v) acc[t][v] = v4f{0.f, 0.f, 0.f, 0.f};
 
-  auto compute = [&](const v4f (&xb)[4], int j) {
+  // depthwise outputs of the lane's channel at its four pixels
+  auto depthwise = [&](const XChunk<DW>& xb, int c) {
+    v4f d = {0.f, 0.f, 0.f, 0.f};
+    if constexpr (DW != 0) {
+#pragma clang fp contract(off)
+      const float* wq = dws + c * 12;
+      float w[10];
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const int cs = (wave_c + WC * j) * kChunk + 4 * s;  // first channel of the k-step
+      for (int t = 0; t < 10; ++t) w[t] = wq[t];
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        float acc = 0.f;
+#pragma unroll
+        for (int i = 0; i < 3; ++i) {
+          // window row i: columns DW*ox - 1 + (0 .. 4*DW + 1)
+          float row[4 * DW + 2];
+          row[0] = xb.l[i];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) row[1 + e] = xb.m[i][e];
+          if constexpr (DW == 1) row[5] = xb.r[i];
+          else
+#pragma unroll
+            for (int e = 0; e < 4; ++e) row[5 + e] = xb.m2[i][e];
+#pragma unroll
+          for (int jj = 0; jj < 3; ++jj) acc = acc + row[DW * v + jj] * w[i * 3 + jj];
+        }
+        acc = acc + w[9];
+        if (a.dw_act == NHIP_ACT_RELU) acc = acc < 0.f ? 0.f : acc;
+        d[v] = acc;
+      }
+    }
+    return d;
+  };
+
+  auto compute = [&](const XChunk<DW>& xb, int j) {
+#pragma unroll
+    for (int s = 0; s < SPC; ++s) {
+      const int cs = chunk_c0(j) + 4 * s;  // first channel of the k-step
       if (cs >= a.c4) break;
+      v4f bx;
+      if constexpr (DW == 0) bx = xb.x[s];
+      else bx = depthwise(xb, cs + cl);
       float av[KT];
       const float* wp = ws + ((cs >> 2) * 64 + lane) * KT + (cs >> 2);
 #pragma unroll
@@ -211,7 +330,7 @@ __global__ __launch_bounds__(kThreads, 2) void pw_conv_kernel(PwArgs a) {
 #pragma unroll
       for (int t = 0; t < KT; ++t)
 #pragma unroll
-        for (int v = 0; v < 4; ++v) acc[t][v] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[t], xb[s][v], acc[t][v], 0, 0, 0);
+        for (int v = 0; v < 4; ++v) acc[t][v] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[t], bx[v], acc[t][v], 0, 0, 0);
     }
   };
 
@@ -221,7 +340,7 @@ __global__ __launch_bounds__(kThreads, 2) void pw_conv_kernel(PwArgs a) {
   auto krow = [&](int t, int q) { return k0 + 16 * t + 4 * cl + row_of(q); };
 
   v4f rv[RES ? KT : 1][RES ? RR : 1];
-  auto issue_res = [&](const Geo<SCALAR>& g) {
+  auto issue_res = [&](const Geo<SCALAR, DW>& g) {
 #pragma unroll
     for (int t = 0; t < KT; ++t)
 #pragma unroll
@@ -231,7 +350,7 @@ __global__ __launch_bounds__(kThreads, 2) void pw_conv_kernel(PwArgs a) {
       }
   };
 
-  auto finish = [&](v4f y, int t, int q, const Geo<SCALAR>& g) {
+  auto finish = [&](v4f y, int t, int q, const Geo<SCALAR, DW>& g) {
     const int k = krow(t, q);
     const float b = bs[k - k0];
 #pragma unroll
@@ -256,7 +375,7 @@ __global__ __launch_bounds__(kThreads, 2) void pw_conv_kernel(PwArgs a) {
     }
   };
 
-  auto epilogue = [&](const Geo<SCALAR>& g) {
+  auto epilogue = [&](const Geo<SCALAR, DW>& g) {
 #pragma unroll
     for (int t = 0; t < KT; ++t) {
       if constexpr (WC == 1) {
@@ -289,8 +408,8 @@ __global__ __launch_bounds__(kThreads, 2) void pw_conv_kernel(PwArgs a) {
   // walks the same tiles, so the WC = 4 reduction barriers line up.
   const bool res_early = RES && nchw >= NB;
   int ii = 0, ij = 0;
-  Geo<SCALAR> gi = geo(first);
-  auto issue_next = [&](v4f (&buf)[4]) {
+  Geo<SCALAR, DW> gi = geo(first);
+  auto issue_next = [&](XChunk<DW>& buf) {
     const bool live = ii < my_tiles;
     issue(buf, gi, ij, live);
     if constexpr (RES)
@@ -302,9 +421,9 @@ __global__ __launch_bounds__(kThreads, 2) void pw_conv_kernel(PwArgs a) {
     }
   };
   int i = 0, j = 0;
-  Geo<SCALAR> gc = gi;
+  Geo<SCALAR, DW> gc = gi;
 
-  v4f xb[NB][4];
+  XChunk<DW> xb[NB];
 #pragma unroll
   for (int b = 0; b + 1 < NB; ++b) issue_next(xb[b]);
   bool done = false;
@@ -336,11 +455,12 @@ struct PwCfg {
   int kt, wc;
   bool scalar;
   int slices;
+  int dw;  // depthwise input stride (0: plain 1x1)
 };
 
 size_t pw_lds(int c, const PwCfg& k) {
   const size_t c4 = (size_t)round_up(c, 4);
-  return ((c4 + 1) * 16 * k.kt + c4 / 4 + (k.wc == 4 ? kRedFloats : 0)) * sizeof(float);
+  return ((c4 + 1) * 16 * k.kt + c4 / 4 + (k.dw ? c4 * 12 : 0) + (k.wc == 4 ? kRedFloats : 0)) * sizeof(float);
 }
 
 // Grid: one workgroup per (tile, slice) when they all fit on the GPU at
@@ -372,9 +492,9 @@ dim3 pw_grid(Kernel kernel, const PwArgs& a, int slices, size_t lds) {
   return dim3((unsigned)round_up(gx, kXcds), (unsigned)slices);
 }
 
-template <int KT, int ACT, bool RES, int WC, bool SCALAR>
+template <int KT, int ACT, bool RES, int WC, bool SCALAR, int DW>
 int launch_one(const PwArgs& a, int slices, size_t lds, hipStream_t s) {
-  const auto kernel = pw_conv_kernel<KT, ACT, RES, WC, SCALAR>;
+  const auto kernel = pw_conv_kernel<KT, ACT, RES, WC, SCALAR, DW>;
   static bool attr_set = false;  // dynamic LDS above 64 KB needs the attribute
   if (!attr_set) {
     NHIP_TRY(check_hip(hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
@@ -382,28 +502,31 @@ int launch_one(const PwArgs& a, int slices, size_t lds, hipStream_t s) {
                        "hipFuncSetAttribute(pw_conv)"));
     attr_set = true;
   }
-  NHIP_LAUNCH("pw_conv_f32", kernel, pw_grid(kernel, a, slices, lds), dim3(kThreads), lds, s, a);
+  NHIP_LAUNCH(DW ? "dwpw_conv_f32" : "pw_conv_f32", kernel, pw_grid(kernel, a, slices, lds), dim3(kThreads), lds,
+              s, a);
   return check_launch("pw_conv_f32");
 }
 
-template <int KT, int WC, bool SCALAR>
+template <int KT, int WC, bool SCALAR, int DW>
 int launch_act(const PwArgs& a, int act, bool res, int slices, size_t lds, hipStream_t s) {
   if (res) {
-    if (act == NHIP_ACT_RELU) return launch_one<KT, NHIP_ACT_RELU, true, WC, SCALAR>(a, slices, lds, s);
-    if (act == NHIP_ACT_SIGMOID) return launch_one<KT, NHIP_ACT_SIGMOID, true, WC, SCALAR>(a, slices, lds, s);
-    return launch_one<KT, NHIP_ACT_NONE, true, WC, SCALAR>(a, slices, lds, s);
+    if (act == NHIP_ACT_RELU) return launch_one<KT, NHIP_ACT_RELU, true, WC, SCALAR, DW>(a, slices, lds, s);
+    if (act == NHIP_ACT_SIGMOID) return launch_one<KT, NHIP_ACT_SIGMOID, true, WC, SCALAR, DW>(a, slices, lds, s);
+    return launch_one<KT, NHIP_ACT_NONE, true, WC, SCALAR, DW>(a, slices, lds, s);
   }
-  if (act == NHIP_ACT_RELU) return launch_one<KT, NHIP_ACT_RELU, false, WC, SCALAR>(a, slices, lds, s);
-  if (act == NHIP_ACT_SIGMOID) return launch_one<KT, NHIP_ACT_SIGMOID, false, WC, SCALAR>(a, slices, lds, s);
-  return launch_one<KT, NHIP_ACT_NONE, false, WC, SCALAR>(a, slices, lds, s);
+  if (act == NHIP_ACT_RELU) return launch_one<KT, NHIP_ACT_RELU, false, WC, SCALAR, DW>(a, slices, lds, s);
+  if (act == NHIP_ACT_SIGMOID) return launch_one<KT, NHIP_ACT_SIGMOID, false, WC, SCALAR, DW>(a, slices, lds, s);
+  return launch_one<KT, NHIP_ACT_NONE, false, WC, SCALAR, DW>(a, slices, lds, s);
 }
 
-template <int WC, bool SCALAR>
+template <int WC, bool SCALAR, int DW>
 int launch_kt(const PwArgs& a, const PwCfg& c, int act, bool res, size_t lds, hipStream_t s) {
   switch (c.kt) {
-    case 1: return launch_act<1, WC, SCALAR>(a, act, res, c.slices, lds, s);
-    case 2: return launch_act<2, WC, SCALAR>(a, act, res, c.slices, lds, s);
-    case 3: return launch_act<3, WC, SCALAR>(a, act, res, c.slices, lds, s);
+    case 1: return launch_act<1, WC, SCALAR, DW>(a, act, res, c.slices, lds, s);
+    case 2: return launch_act<2, WC, SCALAR, DW>(a, act, res, c.slices, lds, s);
+    case 3:
+      if constexpr (DW != 2) return launch_act<3, WC, SCALAR, DW>(a, act, res, c.slices, lds, s);
+      break;
   }
   return fail(NHIP_STATUS_CONSTRAINT_VIOLATION, "pointwise conv: no kernel for the configuration");
 }
@@ -419,18 +542,27 @@ int launch_kt(const PwArgs& a, const PwCfg& c, int act, bool res, size_t lds, hi
 //     gives two (tile, slice) work items per CU, fits the LDS and leaves no
 //     slice mostly padding.
 // NHIP_PW_CFG="kt,wc" forces a configuration (tuning and tests).
-bool pw_config(const nhip_conv_plan* p, int64_t np, int P, PwCfg* out) {
+bool pw_config(const nhip_conv_plan* p, int64_t np, int P, int dw, PwCfg* out) {
   const int kb = (int)ceil_div(p->g.k, 16);
-  const int nch = (int)ceil_div(round_up(p->g.c, 4), kChunk);
+  const int nch = (int)ceil_div(round_up(p->g.c, 4), kChunk);  // 16-channel groups
   const int64_t target = 2LL * cu_count();
-  PwCfg c{1, 1, P % 4 != 0, 1};
+  PwCfg c{1, 1, P % 4 != 0, 1, dw};
+  if (dw && c.scalar) return false;
   if (c.scalar) c.wc = 4;
   else if (nch >= 8 && ceil_div(np, 256) * kb < target) c.wc = 4;
   const int64_t tiles = ceil_div(np, 256 / c.wc);
-  for (int t = std::min(3, kb); t >= 1; --t) {
+  // With a depthwise input every slice recomputes the depthwise values: take
+  // the widest slice there (KT <= 2 at stride 2, whose window with 48 output
+  // channels and a residual would not fit the registers).
+  const int kt_max = std::min(dw == 2 ? 2 : 3, kb);
+  for (int t = kt_max; t >= 1; --t) {
+    if (dw) {
+      c.kt = t;
+      break;
+    }
     const int slices = (int)ceil_div(kb, t);
     if (t > 1 && slices * t - kb >= (t + 1) / 2) continue;  // a slice mostly padding
-    if (pw_lds(p->g.c, PwCfg{t, c.wc, c.scalar, slices}) > (size_t)kMaxLds) continue;
+    if (pw_lds(p->g.c, PwCfg{t, c.wc, c.scalar, slices, dw}) > (size_t)kMaxLds) continue;
     if (tiles * slices >= target || t == 1) {
       c.kt = t;
       break;
@@ -439,7 +571,7 @@ bool pw_config(const nhip_conv_plan* p, int64_t np, int P, PwCfg* out) {
   if (const char* env = std::getenv("NHIP_PW_CFG")) {
     int kt = 0, wc = 0;
     if (std::sscanf(env, "%d,%d", &kt, &wc) == 2 && kt >= 1 && kt <= 3 && (wc == 4 || (wc == 1 && !c.scalar))) {
-      c.kt = kt;
+      c.kt = std::min(kt, dw == 2 ? 2 : 3);
       c.wc = wc;
     }
   }
@@ -459,7 +591,7 @@ bool pointwise_selected(const nhip_conv_plan* p, int n, int h, int w) {
     if (env[0] == '0') return false;
   PwCfg c;
   const int64_t np = (int64_t)n * h * w;
-  if (!pw_config(p, np, h * w, &c)) return false;
+  if (!pw_config(p, np, h * w, 0, &c)) return false;
   // x and out are addressed by 32-bit buffer offsets
   const int64_t xb = np * g.c * 4, ob = np * g.k * 4;
   if (xb >= (int64_t(1) << 31) || ob >= (int64_t(1) << 31)) return false;
@@ -472,33 +604,105 @@ bool pointwise_selected(const nhip_conv_plan* p, int n, int h, int w) {
   return forced || w_traffic <= 2 * (xb + ob);
 }
 
-int launch_conv_pointwise_f32(const nhip_conv_plan* p, const float* in, const float* residual, float* out, int n,
-                              int h, int w, hipStream_t s) {
-  PwCfg c;
-  if (!pw_config(p, (int64_t)n * h * w, h * w, &c))
-    return fail(NHIP_STATUS_CONSTRAINT_VIOLATION, "pointwise conv: unsupported shape");
-  PwArgs a{};
-  a.x = in;
+namespace {
+
+int launch_pw(const nhip_conv_plan* p, const PwCfg& c, PwArgs& a, int n, const float* residual, hipStream_t s) {
   a.w = p->weight;
   a.bias = p->bias;
   a.res = residual;
-  a.out = out;
   a.C = p->g.c;
   a.K = p->g.k;
-  a.P = h * w;
   a.ldw = p->kred_pad;
   a.c4 = (int)round_up(a.C, 4);
   a.np = n * a.P;
   a.ntiles = (int)ceil_div(a.np, 256 / c.wc);
   a.nch = (int)ceil_div(a.c4, kChunk);
-  a.x_bytes = (uint32_t)((int64_t)n * a.C * a.P * 4);
   a.out_bytes = (uint32_t)((int64_t)n * a.K * a.P * 4);
   const size_t lds = pw_lds(a.C, c);
   const int act = p->g.act;
   const bool res = residual != nullptr;
-  if (c.wc == 1) return launch_kt<1, false>(a, c, act, res, lds, s);
-  if (!c.scalar) return launch_kt<4, false>(a, c, act, res, lds, s);
-  return launch_kt<4, true>(a, c, act, res, lds, s);
+  if (c.dw == 1) return c.wc == 1 ? launch_kt<1, false, 1>(a, c, act, res, lds, s) : launch_kt<4, false, 1>(a, c, act, res, lds, s);
+  if (c.dw == 2) return c.wc == 1 ? launch_kt<1, false, 2>(a, c, act, res, lds, s) : launch_kt<4, false, 2>(a, c, act, res, lds, s);
+  if (c.wc == 1) return launch_kt<1, false, 0>(a, c, act, res, lds, s);
+  if (!c.scalar) return launch_kt<4, false, 0>(a, c, act, res, lds, s);
+  return launch_kt<4, true, 0>(a, c, act, res, lds, s);
+}
+
+// The depthwise plan's shape rules for the fused kernel: 3x3, stride 1 or 2
+// (both axes), padding 1 on every side, dilation 1, and float4-aligned input
+// and output rows (W and OW multiples of 4, so a lane's four outputs and
+// their window centres are 16-byte vectors of one row).
+bool dw_shape_ok(const nhip_conv_plan* dw, int h, int w, int* oh, int* ow) {
+  const ConvGeom& g = dw->g;
+  if (dw->kind != PlanKind::DwConvF32 || g.kh != 3 || g.kw != 3 || g.dh != 1 || g.dw != 1 || g.sh != g.sw ||
+      (g.sh != 1 && g.sh != 2) || g.pt != 1 || g.pb != 1 || g.pl != 1 || g.pr != 1)
+    return false;
+  *oh = (h + 2 - 3) / g.sh + 1;
+  *ow = (w + 2 - 3) / g.sw + 1;
+  return w % 4 == 0 && *ow % 4 == 0 && *oh > 0;
+}
+
+}  // namespace
+
+int launch_conv_pointwise_f32(const nhip_conv_plan* p, const float* in, const float* residual, float* out, int n,
+                              int h, int w, hipStream_t s) {
+  PwCfg c;
+  if (!pw_config(p, (int64_t)n * h * w, h * w, 0, &c))
+    return fail(NHIP_STATUS_CONSTRAINT_VIOLATION, "pointwise conv: unsupported shape");
+  PwArgs a{};
+  a.x = in;
+  a.out = out;
+  a.P = h * w;
+  a.x_bytes = (uint32_t)((int64_t)n * p->g.c * a.P * 4);
+  return launch_pw(p, c, a, n, residual, s);
+}
+
+bool dwpw_supported(const nhip_conv_plan* dw, const nhip_conv_plan* pw, int n, int h, int w) {
+  bool every = false;  // NHIP_DWPW=2: every pair the kernel can run (tests)
+  if (const char* env = std::getenv("NHIP_DWPW")) {
+    if (env[0] == '0') return false;
+    every = env[0] == '2';
+  }
+  int oh = 0, ow = 0;
+  if (!dw_shape_ok(dw, h, w, &oh, &ow)) return false;
+  // Measured on the MobileNetV2 pairs (batch 32): a lane forms one row of
+  // four depthwise outputs per channel from 9 loads, twice the standalone
+  // depthwise kernel's loads per output, and every output-channel slice
+  // recomputes the depthwise values.  That pays only when the depthwise
+  // output is a quarter of its input (stride 2) and the 1x1 conv's channels
+  // fit one slice: 96@112 -> 24 in 33.2 us against 43.8 us for the two
+  // layers, 144@56 -> 32 in 21.0 against 23.3; stride 1 measured slower
+  // (32@112 -> 16: 36.1 against 34.6).
+  if (!every && (dw->g.sh != 2 || pw->g.k > 32)) return false;
+  const ConvGeom& g = pw->g;
+  if (pw->kind != PlanKind::ConvF32 || g.c != dw->g.c || g.kh != 1 || g.kw != 1 || g.sh != 1 || g.sw != 1 || g.pt ||
+      g.pb || g.pl || g.pr || pw->algorithm != NHIP_CONV_ALGO_IMPLICIT_GEMM)
+    return false;
+  PwCfg c;
+  const int64_t np = (int64_t)n * oh * ow;
+  if (!pw_config(pw, np, oh * ow, dw->g.sh, &c)) return false;
+  const int64_t xb = (int64_t)n * g.c * h * w * 4, ob = np * g.k * 4;
+  return xb < (int64_t(1) << 31) && ob < (int64_t(1) << 31);
+}
+
+int launch_dwpw_f32(const nhip_conv_plan* dw, const nhip_conv_plan* pw, const float* in, const float* residual,
+                    float* out, int n, int h, int w, hipStream_t s) {
+  int oh = 0, ow = 0;
+  PwCfg c;
+  if (!dw_shape_ok(dw, h, w, &oh, &ow) || !pw_config(pw, (int64_t)n * oh * ow, oh * ow, dw->g.sh, &c))
+    return fail(NHIP_STATUS_CONSTRAINT_VIOLATION, "depthwise + pointwise: unsupported shape");
+  PwArgs a{};
+  a.x = in;
+  a.out = out;
+  a.P = oh * ow;
+  a.x_bytes = (uint32_t)((int64_t)n * pw->g.c * h * w * 4);
+  a.dw_w = dw->weight;
+  a.dw_b = dw->bias;
+  a.H = h;
+  a.W = w;
+  a.OW = ow;
+  a.dw_act = dw->g.act;
+  return launch_pw(pw, c, a, n, residual, s);
 }
 
 }  // namespace nhip

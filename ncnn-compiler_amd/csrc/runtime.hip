@@ -536,6 +536,38 @@ int nhip_dwconv2d_f32_forward(nhip_conv_t p, const float* input, float* output, 
   return launch_dwconv_f32(p, input, output, n, h, w, oh, ow, as_stream(stream));
 }
 
+int nhip_dwconv2d_pw_f32_supported(nhip_conv_t dw, nhip_conv_t pw, int32_t n, int32_t h, int32_t w,
+                                   int32_t* supported) {
+  if (!dw || !pw || !supported) return fail(NHIP_STATUS_NULL_POINTER, "dwconv2d_pw_supported: null pointer");
+  if (n < 0 || h <= 0 || w <= 0) return fail(NHIP_STATUS_INVALID_SHAPE, "dwconv2d_pw_supported: invalid extent");
+  *supported = 0;
+  int oh = 0, ow = 0;
+  if (conv_out(dw->g, h, w, &oh, &ow) != NHIP_STATUS_SUCCESS) return ok();
+  // the forward call runs sub-batches of at most this many images
+  const int64_t img = 4 * std::max((int64_t)dw->g.c * h * w, (int64_t)pw->g.k * oh * ow);
+  const int per = (int)std::max<int64_t>(1, ((int64_t(1) << 31) - 1) / std::max<int64_t>(img, 1));
+  *supported = dwpw_supported(dw, pw, std::max(1, std::min<int>(n, per)), h, w) ? 1 : 0;
+  return ok();
+}
+
+int nhip_dwconv2d_pw_f32_forward(nhip_conv_t dw, nhip_conv_t pw, const float* input, const float* residual,
+                                 float* output, int32_t n, int32_t h, int32_t w, void* stream) {
+  int oh = 0, ow = 0;
+  if (!pw) return fail(NHIP_STATUS_NULL_POINTER, "dwconv2d_pw_forward: null plan");
+  NHIP_TRY(check_forward(dw, input, output, n, h, w, &oh, &ow));
+  if (dw->kind != PlanKind::DwConvF32 || pw->kind != PlanKind::ConvF32 || pw->g.c != dw->g.c)
+    return fail(NHIP_STATUS_CONSTRAINT_VIOLATION,
+                "dwconv2d_pw_forward: needs an fp32 depthwise plan and an fp32 convolution over its channels");
+  if (n == 0) return ok();
+  const int64_t in_img = (int64_t)dw->g.c * h * w, out_img = (int64_t)pw->g.k * oh * ow;
+  return for_each_subbatch(n, 4 * std::max(in_img, out_img), [&](int i0, int nb) {
+    if (!dwpw_supported(dw, pw, nb, h, w))
+      return fail(NHIP_STATUS_UNSUPPORTED, "dwconv2d_pw_forward: this pair or shape has no fused kernel");
+    return launch_dwpw_f32(dw, pw, input + i0 * in_img, residual ? residual + i0 * out_img : nullptr,
+                           output + i0 * out_img, nb, h, w, as_stream(stream));
+  });
+}
+
 int nhip_dwconv2d_int8_create(const nhip_conv_desc* d, const void* weight, int32_t weight_is_i8, const float* bias,
                               const float* weight_scale, int32_t weight_scale_count, float input_scale,
                               float output_scale, nhip_conv_t* plan) {
