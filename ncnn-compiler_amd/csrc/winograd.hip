@@ -18,6 +18,7 @@
 //      activation fused (HBM bound).
 // The weight transform U = G g G^T is done once on the host at plan creation.
 #include <cstdlib>
+#include <type_traits>
 #include <vector>
 
 #include "nhip_internal.h"
@@ -27,9 +28,6 @@ namespace nhip {
 int launch_wino_gemm_out(const nhip_conv_plan* p, const float* V, int t_pad, const float* residual, float* out,
                          int n, int oh, int ow, float* parts, hipStream_t s);
 uint64_t wino_gemm_out_parts_bytes(const nhip_conv_plan* p, int n, int oh, int ow);
-int launch_wino_fused_direct(const nhip_conv_plan* p, const float* in, int h, int w, const float* residual,
-                             float* out, int n, int oh, int ow, float* parts, hipStream_t s);
-bool wino_direct_staged_shape(const nhip_conv_plan* p, int n, int h, int w, int oh, int ow);
 
 // Path selection: input transform + GEMM with the output transform fused
 // (winograd_fused.hip), or the three-kernel path (M through HBM).
@@ -40,18 +38,6 @@ bool wino_direct_staged_shape(const nhip_conv_plan* p, int n, int h, int w, int 
 static int variant_requested() {
   const char* env = std::getenv("NHIP_WINOGRAD_VARIANT");
   return (env && *env) ? std::atoi(env) : 0;
-}
-
-// The fused GEMM transforming the input itself (no V in HBM), selected by
-// NHIP_WINOGRAD_VARIANT = 4.  Not a default: on gfx950 the transform's VALU
-// work serializes with the MFMAs of the same SIMDs and the staged rows add
-// LDS traffic, so even at 64@56 (two output blocks, the largest V round
-// trip against the GEMM) a conv chain measures no faster than the separate
-// transform kernel.
-static bool direct_selected(const nhip_conv_plan* p, int n, int oh, int ow) {
-  const int64_t h = (int64_t)oh + 2 - p->g.pt - p->g.pb, w = (int64_t)ow + 2 - p->g.pl - p->g.pr;
-  if ((int64_t)n * p->g.c * h * w * (int64_t)sizeof(float) > (int64_t(1) << 30)) return false;
-  return variant_requested() == 4;
 }
 
 static bool fused_selected(const nhip_conv_plan* p, int n, int oh, int ow) {
@@ -87,23 +73,101 @@ WinoShape wino_shape(const nhip_conv_plan* p, int n, int h, int w, int oh, int o
   return s;
 }
 
-// Thread (c, t): 6x6 zero-padded patch -> 36 transformed values, V[xi][c][t].
-// PAIRS: thread (channel pair cp, t) transforms channels 2cp and 2cp + 1 and
-// writes V[xi][cp][t][2] (the layout the fused GEMM reads), one 8-byte store
-// per transform point.  VEC (left padding 1, W % 4 == 0, 16-byte aligned
-// input): columns 1..4 of a patch row are the aligned run x = 4*tx .. +3,
-// wholly inside the row or wholly past its end, loaded as one 16-byte vector.
+// Row i of B^T d for one column (d0..d5 = column j of the patch), the
+// interpolation-point rows of B^T for F(4x4, 3x3).
+template <int I>
+__device__ __forceinline__ float bt_row(float d0, float d1, float d2, float d3, float d4, float d5) {
+  if constexpr (I == 0) return 4.f * d0 - 5.f * d2 + d4;
+  if constexpr (I == 1) return -4.f * (d1 + d2) + d3 + d4;
+  if constexpr (I == 2) return 4.f * (d1 - d2) - d3 + d4;
+  if constexpr (I == 3) return -2.f * (d1 - d3) - d2 + d4;
+  if constexpr (I == 4) return 2.f * (d1 - d3) - d2 + d4;
+  return 4.f * d1 - 5.f * d3 + d5;
+}
+
+// V = B^T d B for one (channel, tile), stored V[6i + j] at vout + (6i + j) *
+// plane_stride.  Loads of rows outside the image (or of a padding tile or
+// channel, ok = false) return 0.
+template <bool VEC>
+__device__ __forceinline__ void wino_in_patch(__amdgpu_buffer_rsrc_t rs, bool ok, int plane, int H, int W, int y0,
+                                              int x0, float* __restrict__ vout, int64_t plane_stride) {
+  float d[6][6];
+#pragma unroll
+  for (int i = 0; i < 6; ++i) {
+    const int y = y0 + i;
+    const bool yok = ok && (unsigned)y < (unsigned)H;
+    if constexpr (VEC) {
+      const uint32_t rb = (uint32_t)((plane + y) * W * (int)sizeof(float));
+      d[i][0] = buf_load_f32(rs, (yok && x0 >= 0) ? rb + (uint32_t)(x0 * 4) : kBufOOB);
+      const int4 m = buf_load_b128(rs, (yok && x0 + 1 < W) ? rb + (uint32_t)((x0 + 1) * 4) : kBufOOB);
+      d[i][1] = __builtin_bit_cast(float, m.x);
+      d[i][2] = __builtin_bit_cast(float, m.y);
+      d[i][3] = __builtin_bit_cast(float, m.z);
+      d[i][4] = __builtin_bit_cast(float, m.w);
+      d[i][5] = buf_load_f32(rs, (yok && x0 + 5 < W) ? rb + (uint32_t)((x0 + 5) * 4) : kBufOOB);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 6; ++j) {
+        const int xx = x0 + j;
+        const uint32_t off =
+            (yok && (unsigned)xx < (unsigned)W) ? (uint32_t)(((plane + y) * W + xx) * (int)sizeof(float)) : kBufOOB;
+        d[i][j] = buf_load_f32(rs, off);
+      }
+    }
+  }
+  auto row = [&](auto ic) {
+    constexpr int i = decltype(ic)::value;
+    float tr[6];  // row i of B^T d
+#pragma unroll
+    for (int j = 0; j < 6; ++j) tr[j] = bt_row<i>(d[0][j], d[1][j], d[2][j], d[3][j], d[4][j], d[5][j]);
+    // (B^T d)[i] B: the same six combinations along the row
+    vout[(6 * i + 0) * plane_stride] = bt_row<0>(tr[0], tr[1], tr[2], tr[3], tr[4], tr[5]);
+    vout[(6 * i + 1) * plane_stride] = bt_row<1>(tr[0], tr[1], tr[2], tr[3], tr[4], tr[5]);
+    vout[(6 * i + 2) * plane_stride] = bt_row<2>(tr[0], tr[1], tr[2], tr[3], tr[4], tr[5]);
+    vout[(6 * i + 3) * plane_stride] = bt_row<3>(tr[0], tr[1], tr[2], tr[3], tr[4], tr[5]);
+    vout[(6 * i + 4) * plane_stride] = bt_row<4>(tr[0], tr[1], tr[2], tr[3], tr[4], tr[5]);
+    vout[(6 * i + 5) * plane_stride] = bt_row<5>(tr[0], tr[1], tr[2], tr[3], tr[4], tr[5]);
+  };
+  row(std::integral_constant<int, 0>{});
+  row(std::integral_constant<int, 1>{});
+  row(std::integral_constant<int, 2>{});
+  row(std::integral_constant<int, 3>{});
+  row(std::integral_constant<int, 4>{});
+  row(std::integral_constant<int, 5>{});
+}
+
+// Thread (c, t): the 6x6 transform of the zero-padded patch of channel c,
+// tile t.  Layouts:
+//   PAIRS  V[xi][c_pad/2][t_pad][2] (the fused GEMM's channel pairs); the two
+//          channels of a pair are neighbouring lanes, so a wave's stores for
+//          one point cover 256 contiguous bytes;
+//   else   V[xi][c_pad][t_pad].
+// VEC (left padding 1, W % 4 == 0, 16-byte aligned input): columns 1..4 of a
+// patch row are the aligned run x = 4*tx .. +3, wholly inside the row or
+// wholly past its end, loaded as one 16-byte vector.
 template <bool PAIRS, bool VEC>
 __global__ __launch_bounds__(256) void wino_input_transform(
     const float* __restrict__ x, uint32_t x_bytes, float* __restrict__ V, int C, int H, int W,
     int th, int tw, int T, int t_pad, int c_pad, int pt, int pl) {
-  constexpr int CPT = PAIRS ? 2 : 1;  // channels per thread
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= (int64_t)(c_pad / CPT) * t_pad) return;
-  const int cg = (int)(idx / t_pad);
-  const int t = (int)(idx - (int64_t)cg * t_pad);
-  const int64_t plane_stride = (int64_t)c_pad * t_pad;
-  float* vout = V + ((int64_t)cg * t_pad + t) * CPT;
+  const int64_t per_block = (int64_t)c_pad * t_pad;
+  if (idx >= per_block) return;
+  const int64_t rem = idx;
+  int c, t;
+  float* vout;
+  if constexpr (PAIRS) {
+    const int e = (int)(rem & 1);
+    const int64_t q = rem >> 1;
+    const int cp = (int)(q / t_pad);
+    t = (int)(q - (int64_t)cp * t_pad);
+    c = 2 * cp + e;
+    vout = V + ((int64_t)cp * t_pad + t) * 2 + e;
+  } else {
+    c = (int)(rem / t_pad);
+    t = (int)(rem - (int64_t)c * t_pad);
+    vout = V + (int64_t)c * t_pad + t;
+  }
+  const int64_t plane_stride = per_block;
   const int per_img = th * tw;
   const bool t_ok = t < T;
   const int tt = t_ok ? t : 0;
@@ -111,71 +175,10 @@ __global__ __launch_bounds__(256) void wino_input_transform(
   const int r = tt - img * per_img;
   const int ty = r / tw, tx = r - (r / tw) * tw;
   const int y0 = ty * 4 - pt, x0 = tx * 4 - pl;
+  const bool ok = t_ok && c < C;  // padding tiles / channels transform a zero patch
+  const int plane = (img * C + (ok ? c : 0)) * H;
   const __amdgpu_buffer_rsrc_t rs = make_rsrc(x, x_bytes);  // whole input, < 2^31 bytes
-
-  float v[CPT][36];
-#pragma unroll
-  for (int e = 0; e < CPT; ++e) {
-    const int c = cg * CPT + e;
-    const bool ok = t_ok && c < C;  // padding tiles / channels transform a zero patch
-    const int plane = (img * C + c) * H;
-    float d[6][6];
-#pragma unroll
-    for (int i = 0; i < 6; ++i) {
-      const int y = y0 + i;
-      const bool yok = ok && (unsigned)y < (unsigned)H;
-      if constexpr (VEC) {
-        const uint32_t rb = (uint32_t)((plane + y) * W * (int)sizeof(float));
-        d[i][0] = buf_load_f32(rs, (yok && x0 >= 0) ? rb + (uint32_t)(x0 * 4) : kBufOOB);
-        const int4 m = buf_load_b128(rs, (yok && x0 + 1 < W) ? rb + (uint32_t)((x0 + 1) * 4) : kBufOOB);
-        d[i][1] = __builtin_bit_cast(float, m.x);
-        d[i][2] = __builtin_bit_cast(float, m.y);
-        d[i][3] = __builtin_bit_cast(float, m.z);
-        d[i][4] = __builtin_bit_cast(float, m.w);
-        d[i][5] = buf_load_f32(rs, (yok && x0 + 5 < W) ? rb + (uint32_t)((x0 + 5) * 4) : kBufOOB);
-      } else {
-#pragma unroll
-        for (int j = 0; j < 6; ++j) {
-          const int xx = x0 + j;
-          const uint32_t off =
-              (yok && (unsigned)xx < (unsigned)W) ? (uint32_t)(((plane + y) * W + xx) * (int)sizeof(float)) : kBufOOB;
-          d[i][j] = buf_load_f32(rs, off);
-        }
-      }
-    }
-    // tmp = B^T d  (column-wise)
-    float tmp[6][6];
-#pragma unroll
-    for (int j = 0; j < 6; ++j) {
-      const float d0 = d[0][j], d1 = d[1][j], d2 = d[2][j], d3 = d[3][j], d4 = d[4][j], d5 = d[5][j];
-      tmp[0][j] = 4.f * d0 - 5.f * d2 + d4;
-      tmp[1][j] = -4.f * (d1 + d2) + d3 + d4;
-      tmp[2][j] = 4.f * (d1 - d2) - d3 + d4;
-      tmp[3][j] = -2.f * (d1 - d3) - d2 + d4;
-      tmp[4][j] = 2.f * (d1 - d3) - d2 + d4;
-      tmp[5][j] = 4.f * d1 - 5.f * d3 + d5;
-    }
-    // V = tmp B  (row-wise)
-#pragma unroll
-    for (int i = 0; i < 6; ++i) {
-      const float d0 = tmp[i][0], d1 = tmp[i][1], d2 = tmp[i][2], d3 = tmp[i][3], d4 = tmp[i][4], d5 = tmp[i][5];
-      v[e][i * 6 + 0] = 4.f * d0 - 5.f * d2 + d4;
-      v[e][i * 6 + 1] = -4.f * (d1 + d2) + d3 + d4;
-      v[e][i * 6 + 2] = 4.f * (d1 - d2) - d3 + d4;
-      v[e][i * 6 + 3] = -2.f * (d1 - d3) - d2 + d4;
-      v[e][i * 6 + 4] = 2.f * (d1 - d3) - d2 + d4;
-      v[e][i * 6 + 5] = 4.f * d1 - 5.f * d3 + d5;
-    }
-  }
-#pragma unroll
-  for (int xi = 0; xi < 36; ++xi) {
-    if constexpr (PAIRS) {
-      typedef float v2f_t __attribute__((ext_vector_type(2)));
-      *reinterpret_cast<v2f_t*>(vout + xi * plane_stride) = v2f_t{v[0][xi], v[1][xi]};
-    } else {
-      vout[xi * plane_stride] = v[0][xi];
-    }
-  }
+  wino_in_patch<VEC>(rs, ok, plane, H, W, y0, x0, vout, plane_stride);
 }
 
 // Thread (k, t): 36 GEMM outputs (the sum of S K-partial buffers) -> 4x4
@@ -288,7 +291,6 @@ int winograd_prepack_weights(nhip_conv_plan* p, const float* weight) {
 uint64_t conv_winograd_f32_workspace(const nhip_conv_plan* p, int n, int oh, int ow) {
   const int th = (int)ceil_div(oh, 4), tw = (int)ceil_div(ow, 4);
   const int64_t t_pad = round_up((int64_t)n * th * tw, 128);
-  if (direct_selected(p, n, oh, ow)) return wino_gemm_out_parts_bytes(p, n, oh, ow);
   if (fused_selected(p, n, oh, ow))  // V, then the GEMM's partial sums
     return (uint64_t)36 * t_pad * p->c_pad * sizeof(float) + wino_gemm_out_parts_bytes(p, n, oh, ow);
   const WinoGemmCfg cfg = wino_gemm_config(p->m_pad, p->c_pad, (int)t_pad);
@@ -304,15 +306,13 @@ int launch_conv_winograd_f32(const nhip_conv_plan* p, const float* in,
   if (need > 0 && (ws == nullptr || ws_bytes < need))
     return fail(NHIP_STATUS_OUTPUT_CAPACITY_INSUFFICIENT,
                 "winograd conv: workspace of " + std::to_string(need) + " bytes required");
-  if (direct_selected(p, n, oh, ow))
-    return launch_wino_fused_direct(p, in, h, w, residual, out, n, oh, ow, static_cast<float*>(ws), s);
   const bool fused = fused_selected(p, n, oh, ow);
   float* V = static_cast<float*>(ws);
   float* M = V + (int64_t)36 * ws_.c_pad * ws_.t_pad;
   {
     const uint32_t x_bytes = (uint32_t)((size_t)n * ws_.c * h * w * sizeof(float));
-    const int64_t total = (int64_t)(fused ? ws_.c_pad / 2 : ws_.c_pad) * ws_.t_pad;
-    const dim3 grid((unsigned)ceil_div(total, 256));
+    const int64_t units = (int64_t)ws_.c_pad * ws_.t_pad;
+    const dim3 grid((unsigned)ceil_div(units, 256));
     const bool vec = p->g.pl == 1 && w % 4 == 0 && (reinterpret_cast<uintptr_t>(in) & 15) == 0;
 #define NHIP_WINO_IN(P_, V_)                                                                                  \
   NHIP_LAUNCH("wino_input_transform", (wino_input_transform<P_, V_>), grid, dim3(256), 0, s, in, x_bytes, V, \

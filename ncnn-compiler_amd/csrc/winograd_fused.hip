@@ -59,28 +59,16 @@ static_assert(kTB == 32 && kKB == 32 && kCB == 8, "the load mappings below assum
 typedef float v2f __attribute__((ext_vector_type(2)));
 
 struct FusedArgs {
-  const float* x;       // direct variant: the input [N][C][H][W] (<= 1 GiB)
-  const float* V;       // otherwise: [36][c_pad/2][t_pad][2]
+  const float* V;       // [36][c_pad/2][t_pad][2]
   const float* U;       // [c_pad/8][36][4][m_pad][2]
   const float* bias;    // [m_pad]
   const float* residual;
   float* out;           // [N][K][OH][OW]; with splits > 1 the parts [splits][N][K][OH][OW]
   int K, OH, OW, th, tw, T, t_pad, m_pad, c_pad;
   int nt, nk, splits, per;  // tile blocks, channel blocks, channel splits, chunks per split
-  // Tile blocks (mode = 0, 1, 2):
-  //   0  whole images, R = (32 / tw) / th * th tile rows (th <= 32 / tw): a
-  //      block's outputs for one image are one contiguous run over its 32
-  //      channels;
-  //   1  up to R = 32 / tw tile rows of one image (th > 32 / tw), blocks
-  //      restarting at each image (bpi per image): one contiguous run per
-  //      channel;
-  //   2  32-tile pieces of a tile row (tw > 32), bpr per row.
-  // G = N * th tile rows.
-  int mode, R, bpi, bpr, G;
-  int C, H, W, pt, pl;  // direct variant: input geometry
-  uint32_t x_bytes;     // size of x
-  uint32_t v_bytes;     // size of V (< 2^31)
-  uint32_t u_bytes;     // size of U (< 2^31)
+  int64_t part_stride;      // N*K*OH*OW (< 2^31): elements per channel-split part
+  uint32_t v_bytes;         // size of V (< 2^31)
+  uint32_t u_bytes;         // size of U (< 2^31)
 };
 
 template <int ACT>
@@ -152,15 +140,18 @@ __device__ __forceinline__ void load_role(const FusedArgs& a, float* lds, int p,
   }
 }
 
-// A workgroup's share of the work: tile block tb (mode 0/1/2 above), output
-// channels k0 .. k0 + 31, and chunks ch_begin .. ch_begin + n - 1 of channel
-// split cs (chunks of `cb` input channels).
+// A workgroup's share of the work: tiles t0 .. t0 + ntiles - 1 (32
+// consecutive tiles in (image, tile row, tile column) order, so every tile
+// slot of the MFMA block carries a real tile except in the last block),
+// output channels k0 .. k0 + 31, and chunks ch_begin .. ch_begin + n - 1 of
+// channel split cs (chunks of `cb` input channels).
 struct Block {
-  int tb, kb, cs, k0, g0, nrows, tx_a, t0, ntiles, ch_begin, n;
+  int kb, cs, k0, t0, ntiles, ch_begin, n;
 };
 
 __device__ __forceinline__ Block block_of(const FusedArgs& a, int cb) {
   Block b;
+  int tb;
   // XCD-contiguous renumbering: each XCD gets a contiguous range of logical
   // blocks, ordered (tile block, split, channel block) with the channel
   // block fastest, so the workgroups that read the same V slices share an L2.
@@ -172,25 +163,11 @@ __device__ __forceinline__ Block block_of(const FusedArgs& a, int cb) {
     b.kb = logical % a.nk;
     const int rest = logical / a.nk;
     b.cs = rest % a.splits;
-    b.tb = rest / a.splits;
+    tb = rest / a.splits;
   }
   b.k0 = b.kb * kKB;
-  if (a.mode == 0) {
-    b.g0 = b.tb * a.R;
-    b.nrows = min(a.R, a.G - b.g0);
-    b.tx_a = 0;
-  } else if (a.mode == 1) {
-    const int im = b.tb / a.bpi, ty0 = (b.tb - im * a.bpi) * a.R;
-    b.g0 = im * a.th + ty0;
-    b.nrows = min(a.R, a.th - ty0);
-    b.tx_a = 0;
-  } else {
-    b.g0 = b.tb / a.bpr;
-    b.nrows = 1;
-    b.tx_a = (b.tb - b.g0 * a.bpr) * kTB;
-  }
-  b.t0 = b.g0 * a.tw + b.tx_a;
-  b.ntiles = a.mode == 2 ? min(kTB, a.tw - b.tx_a) : b.nrows * a.tw;
+  b.t0 = tb * kTB;
+  b.ntiles = min(kTB, a.T - b.t0);
   const int nch = a.c_pad / cb;
   b.ch_begin = b.cs * a.per;
   b.n = max(0, min(nch, b.ch_begin + a.per) - b.ch_begin);
@@ -232,395 +209,131 @@ __device__ __forceinline__ void y_to_lds(const v4f (&acc)[36], float* lds, int w
   }
 }
 
-// Write-out of the staged tiles by NW waves, wave w taking channels w + NW*j.
-// Outputs are written in memory order.  All residual loads of a group of
-// four channels are issued before its first store: vmcnt counts loads and
-// stores in issue order, so a load issued after a store would make its wait
-// include the store.  FINAL: act(Y + bias (+ residual)); otherwise the raw
-// part of channel split b.cs for wino_fused_reduce.
+// The block's output, in memory order, as units of VW consecutive pixels
+// (VW = 4 when OW % 4 == 0: a tile row of a full-width tile; else single
+// pixels).  The block's tiles form segments of one tile row each (the first
+// and last may be partial rows); a segment covers rows 4ty .. 4ty + rows - 1
+// (rows <= 4, clipped at OH) and, per row, one run of L pixels (clipped at
+// OW where the segment reaches the row's end).  Runs of consecutive
+// segments of one image are adjacent in memory, so consecutive units are
+// consecutive addresses within a channel plane.  For unit e of the lane the
+// table gives the output offset without the channel term (image plane + row
+// + column, -1 past the block's units) and its place in the staged tiles Ys
+// without the channel term.
+template <int VW, int NU>
+__device__ __forceinline__ void unit_table(const FusedArgs& a, const Block& bk, int lane, int (&go)[NU],
+                                           int (&yo)[NU]) {
+  const int OHW = a.OH * a.OW;
+  const int per_img = a.th * a.tw;
+#pragma unroll
+  for (int m = 0; m < NU; ++m) go[m] = -1, yo[m] = 0;
+  if (VW == 1 && bk.t0 % per_img == 0 && bk.ntiles % per_img == 0) {
+    // whole images: unit e is pixel e % OHW of image t0 / per_img + e / OHW
+    const int img0 = bk.t0 / per_img, cnt = bk.ntiles / per_img * OHW;
+#pragma unroll
+    for (int m = 0; m < NU; ++m) {
+      const int e = lane + 64 * m;
+      if (e < cnt) {
+        const int ir = e / OHW, px = e - ir * OHW;
+        const int oy = px / a.OW, ox = px - oy * a.OW;
+        const int tl = ir * per_img + (oy >> 2) * a.tw + (ox >> 2), i = oy & 3;
+        go[m] = (img0 + ir) * a.K * OHW + px;
+        yo[m] = tl * 16 + ((i ^ tl) & 3) * 4 + (ox & 3);
+      }
+    }
+    return;
+  }
+  int seg_t = bk.t0, first = 0;  // first unit of the segment
+  while (seg_t < bk.t0 + bk.ntiles) {
+    const int img = seg_t / per_img, rr = seg_t - img * per_img;
+    const int ty = rr / a.tw, tx0 = rr - ty * a.tw;
+    const int len = min(a.tw - tx0, bk.t0 + bk.ntiles - seg_t);
+    const int rows = min(4, a.OH - 4 * ty);
+    const int L = VW == 4 ? len : (tx0 + len == a.tw ? a.OW - 4 * tx0 : 4 * len);  // units per row
+    const int cnt = rows * L;
+    const int tl0 = seg_t - bk.t0;
+    const int base = img * a.K * OHW + 4 * ty * a.OW + 4 * tx0;
+#pragma unroll
+    for (int m = 0; m < NU; ++m) {
+      const int u = lane + 64 * m - first;
+      if (u >= 0 && u < cnt) {
+        const int i = (u >= L) + (u >= 2 * L) + (u >= 3 * L), x = u - i * L;  // row, unit within the row
+        const int tt = VW == 4 ? x : x >> 2, j = VW == 4 ? 0 : x & 3;
+        const int tl = tl0 + tt;
+        go[m] = base + i * a.OW + (VW == 4 ? 4 * x : x);
+        yo[m] = tl * 16 + ((i ^ tl) & 3) * 4 + j;
+      }
+    }
+    first += cnt;
+    seg_t += len;
+  }
+}
+
+// Write-out of the staged tiles by NW waves, wave w taking channels w + NW*j,
+// each unit of the block's output (unit_table) once per channel.  All
+// residual loads of a channel are issued before its first store: vmcnt
+// counts loads and stores in issue order, so a load issued after a store
+// would make its wait include the store.  FINAL: act(Y + bias (+ residual));
+// otherwise the raw part of channel split b.cs for wino_fused_reduce.
 template <int NW, int ACT, bool FINAL>
 __device__ __forceinline__ void write_out(const FusedArgs& a, const Block& bk, const float* lds, int lane,
                                           int wave) {
   constexpr int JW = kKB / NW;  // channels per wave
-  float* dst = a.out + (FINAL ? 0 : (int64_t)bk.cs * (a.G / a.th) * a.K * a.OH * a.OW);
+  float* dst = a.out + (FINAL ? 0 : (int64_t)bk.cs * a.part_stride);
   const int OHW = a.OH * a.OW;
-  const int k0 = bk.k0;
-  if (a.mode == 0) {
-    // Whole images: per (image, channel) plane P = OH*OW <= 16 * 32 floats; a
-    // lane's pixels p = lane + 64m (m < 8) and their (tile, row, column)
-    // within the image are computed once, packed as tile*16 + row*4 + column.
-    int tij[8];
+  if (a.OW % 4 == 0) {
+    constexpr int NU = kTB * 4 / 64;  // <= 32 tiles x 4 rows float4 units per channel
+    int go[NU], yo[NU];
+    unit_table<4, NU>(a, bk, lane, go, yo);
+    for (int j = 0; j < JW; ++j) {
+      const int kk = wave + NW * j, k = bk.k0 + kk;
+      if (k >= a.K) break;
+      const float b = FINAL ? a.bias[k] : 0.f;
+      v4f res[NU];
 #pragma unroll
-    for (int m = 0; m < 8; ++m) {
-      const int pix = lane + 64 * m;
-      const int oy = pix / a.OW, ox = pix - (pix / a.OW) * a.OW;
-      tij[m] = pix < OHW ? ((oy >> 2) * a.tw + (ox >> 2)) * 16 + (oy & 3) * 4 + (ox & 3) : -1;
-    }
-    const int nimg = bk.nrows / a.th;
-    const int im0 = bk.g0 / a.th;
-    const int img_tiles = a.th * a.tw;
-    for (int il = 0; il < nimg; ++il) {
-      for (int j = 0; j < JW; ++j) {
-        const int kk = wave + NW * j, k = k0 + kk;
-        if (k >= a.K) break;
-        const float b = FINAL ? a.bias[k] : 0.f;
-        const int64_t base = ((int64_t)(im0 + il) * a.K + k) * OHW;
-        float res[8];
+      for (int m = 0; m < NU; ++m)
+        res[m] = (FINAL && a.residual && go[m] >= 0) ? *reinterpret_cast<const v4f*>(a.residual + go[m] + k * OHW)
+                                                      : v4f{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int m = 0; m < 8; ++m)
-          res[m] = (FINAL && a.residual && tij[m] >= 0) ? a.residual[base + lane + 64 * m] : 0.f;
-#pragma unroll
-        for (int m = 0; m < 8; ++m)
-          if (tij[m] >= 0) {
-            const int tl = il * img_tiles + (tij[m] >> 4);
-            const float y = lds[ys_off(kk, tl, (tij[m] >> 2) & 3) + (tij[m] & 3)];
-            dst[base + lane + 64 * m] = activate<ACT>(y + b + res[m]);
-          }
-      }
-    }
-    return;
-  }
-  if (a.mode == 1) {
-    // One contiguous run of count = orows x OW floats per channel; a group
-    // of 4 channels holds <= 4 x 512 floats, i.e. <= 8 float4 (32 float)
-    // slots per lane, E = lane*VW + 64*VW*u over the group's runs.
-    const int im = bk.g0 / a.th, ty0 = bk.g0 - im * a.th;
-    const int orows = min(4 * bk.nrows, a.OH - 4 * ty0);
-    const int count = orows * a.OW;
-    const int64_t row0 = (int64_t)4 * ty0 * a.OW;
-#pragma unroll
-    for (int jg = 0; jg < JW; jg += 4) {
-      // channels kk = wave + NW*(jg + j), j < 4
-      int nk_g = 0;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) nk_g += (k0 + wave + NW * (jg + j) < a.K) ? 1 : 0;
-      float bias4[4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int k = k0 + wave + NW * (jg + j);
-        bias4[j] = (FINAL && k < a.K) ? a.bias[k] : 0.f;
-      }
-      auto slot = [&](int E, int& j, int64_t& o, int& yo) {
-        j = E / count;
-        const int e = E - j * count;
-        const int i = e / a.OW, x = e - i * a.OW;
-        const int kk = wave + NW * (jg + j);
-        o = ((int64_t)im * a.K + k0 + kk) * OHW + row0 + e;
-        yo = ys_off(kk, (i >> 2) * a.tw + (x >> 2), i & 3) + (x & 3);
-      };
-      if (a.OW % 4 == 0) {
-        v4f res[8];
-        int64_t o[8];
-        int yo[8], jj[8];
-#pragma unroll
-        for (int u = 0; u < 8; ++u) {
-          const int E = lane * 4 + 256 * u;
-          res[u] = v4f{0.f, 0.f, 0.f, 0.f};
-          jj[u] = -1;
-          if (E < nk_g * count) {
-            slot(E, jj[u], o[u], yo[u]);
-            if (FINAL && a.residual) res[u] = *reinterpret_cast<const v4f*>(a.residual + o[u]);
-          }
-        }
-#pragma unroll
-        for (int u = 0; u < 8; ++u) {
-          if (jj[u] < 0) continue;
-          const v4f y = *reinterpret_cast<const v4f*>(lds + yo[u]);
-          const float b = jj[u] == 0 ? bias4[0] : jj[u] == 1 ? bias4[1] : jj[u] == 2 ? bias4[2] : bias4[3];
+      for (int m = 0; m < NU; ++m)
+        if (go[m] >= 0) {
+          const v4f y = *reinterpret_cast<const v4f*>(lds + kk * (kTB * 16) + yo[m]);
           v4f v;
 #pragma unroll
-          for (int q4 = 0; q4 < 4; ++q4) v[q4] = activate<ACT>(y[q4] + b + res[u][q4]);
-          *reinterpret_cast<v4f*>(dst + o[u]) = v;
+          for (int q4 = 0; q4 < 4; ++q4) v[q4] = activate<ACT>(y[q4] + b + res[m][q4]);
+          *reinterpret_cast<v4f*>(dst + go[m] + k * OHW) = v;
         }
-      } else {
-        float res[32];
-        int64_t o[32];
-        int yo[32], jj[32];
-#pragma unroll
-        for (int u = 0; u < 32; ++u) {
-          const int E = lane + 64 * u;
-          res[u] = 0.f;
-          jj[u] = -1;
-          if (E < nk_g * count) {
-            slot(E, jj[u], o[u], yo[u]);
-            if (FINAL && a.residual) res[u] = a.residual[o[u]];
-          }
-        }
-#pragma unroll
-        for (int u = 0; u < 32; ++u) {
-          if (jj[u] < 0) continue;
-          const float b = jj[u] == 0 ? bias4[0] : jj[u] == 1 ? bias4[1] : jj[u] == 2 ? bias4[2] : bias4[3];
-          dst[o[u]] = activate<ACT>(lds[yo[u]] + b + res[u]);
-        }
-      }
     }
-    return;
-  }
-  // mode 2: a cut tile row, written one pixel row at a time per channel.
-  const int im = bk.g0 / a.th, ty = bk.g0 - im * a.th;
-  const int rows = min(4, a.OH - 4 * ty);
-  const int x_base = 4 * bk.tx_a;
-  const int cols = min(4 * bk.ntiles, a.OW - x_base);
-  for (int j = 0; j < JW; ++j) {
-    const int kk = wave + NW * j, k = k0 + kk;
-    if (k >= a.K) break;
-    const float b = FINAL ? a.bias[k] : 0.f;
-    for (int i = 0; i < rows; ++i) {
-      const int64_t base = (((int64_t)im * a.K + k) * a.OH + 4 * ty + i) * a.OW + x_base;
-      for (int x = lane; x < cols; x += 64) {
-        const float r = (FINAL && a.residual) ? a.residual[base + x] : 0.f;
-        dst[base + x] = activate<ACT>(lds[ys_off(kk, x >> 2, i) + (x & 3)] + b + r);
-      }
-    }
-  }
-}
-
-// Input transform V = B^T d B of one 6x6 patch; each value is handed to
-// `store(xi, value)` as soon as it is computed.
-template <class Store>
-__device__ __forceinline__ void input_transform(float (&d)[36], Store store) {
-#pragma unroll
-  for (int j = 0; j < 6; ++j) {  // columns: d <- B^T d, in place
-    const float d0 = d[0 * 6 + j], d1 = d[1 * 6 + j], d2 = d[2 * 6 + j];
-    const float d3 = d[3 * 6 + j], d4 = d[4 * 6 + j], d5 = d[5 * 6 + j];
-    d[0 * 6 + j] = 4.f * d0 - 5.f * d2 + d4;
-    d[1 * 6 + j] = -4.f * (d1 + d2) + d3 + d4;
-    d[2 * 6 + j] = 4.f * (d1 - d2) - d3 + d4;
-    d[3 * 6 + j] = -2.f * (d1 - d3) - d2 + d4;
-    d[4 * 6 + j] = 2.f * (d1 - d3) - d2 + d4;
-    d[5 * 6 + j] = 4.f * d1 - 5.f * d3 + d5;
-  }
-#pragma unroll
-  for (int i = 0; i < 6; ++i) {  // rows: (B^T d) B
-    const float d0 = d[i * 6 + 0], d1 = d[i * 6 + 1], d2 = d[i * 6 + 2];
-    const float d3 = d[i * 6 + 3], d4 = d[i * 6 + 4], d5 = d[i * 6 + 5];
-    store(i * 6 + 0, 4.f * d0 - 5.f * d2 + d4);
-    store(i * 6 + 1, -4.f * (d1 + d2) + d3 + d4);
-    store(i * 6 + 2, 4.f * (d1 - d2) - d3 + d4);
-    store(i * 6 + 3, -2.f * (d1 - d3) - d2 + d4);
-    store(i * 6 + 4, 2.f * (d1 - d3) - d2 + d4);
-    store(i * 6 + 5, 4.f * d1 - 5.f * d3 + d5);
-  }
-}
-
-// The transform waves of the direct variant (no V in HBM): for chunks
-// ch_begin .. ch_begin + n - 1 they load the 6x6 input patches of the
-// block's tiles (thread p = tile p % 32, channel p / 32 of the chunk),
-// transform them into the chunk's V slot ([xi][channel pair][tile][2]) and
-// copy the U slice as load_role does; same slots, same n + 1 barriers.
-// Patch offsets are plane + row + column (bytes), each term exact or kOOB1
-// (a channel or tile past the end, a row or column outside the image): one
-// invalid term puts the sum at or past 2^30 >= the input size, so the raw
-// buffer load returns 0; three stay below 2^32.  Every load has its own
-// offset register, so the compiler does not merge neighbouring loads into
-// vectors (a vector that straddles the end of the input would come back
-// zero as a whole).  VEC (left padding 1, W % 4 == 0): columns 1..4 of a
-// patch row are the 16-byte aligned run x = 4*tx .. +3, wholly inside the row
-// or wholly past its end, loaded as one vector.
-constexpr uint32_t kOOB1 = 0x40000000u;
-
-template <bool VEC>
-__device__ __forceinline__ void transform_role(const FusedArgs& a, float* lds, int p, const Block& bk) {
-  const int t_l = p % kTB, c_l = p / kTB;
-  const bool t_ok = t_l < bk.ntiles;
-  int g, tx;
-  if (a.mode == 2) {
-    g = bk.g0;
-    tx = bk.tx_a + t_l;
   } else {
-    g = bk.g0 + t_l / a.tw;
-    tx = t_l - (t_l / a.tw) * a.tw;
-  }
-  const int im = t_ok ? g / a.th : 0, ty = t_ok ? g - im * a.th : 0;
-  const int y0 = ty * 4 - a.pt, x0 = tx * 4 - a.pl;
-  uint32_t rowoff[6], coloff[6];
+    constexpr int NU = kTB * 16 / 64;  // <= 32 tiles x 16 pixels per channel
+    int go[NU], yo[NU];
+    unit_table<1, NU>(a, bk, lane, go, yo);
+    for (int j = 0; j < JW; ++j) {
+      const int kk = wave + NW * j, k = bk.k0 + kk;
+      if (k >= a.K) break;
+      const float b = FINAL ? a.bias[k] : 0.f;
+      float res[NU];
 #pragma unroll
-  for (int i = 0; i < 6; ++i) {
-    const int y = y0 + i, x = x0 + i;
-    rowoff[i] = (unsigned)y < (unsigned)a.H ? (uint32_t)(y * a.W) * 4u : kOOB1;
-    coloff[i] = (unsigned)x < (unsigned)a.W ? (uint32_t)x * 4u : kOOB1;
-  }
-  const uint32_t plane_bytes = (uint32_t)(a.H * a.W) * 4u;
-  const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, a.x_bytes);
-  const __amdgpu_buffer_rsrc_t ur = make_rsrc(a.U, a.u_bytes);
-  // U slice addressing as in load_role
-  const int xi0 = p >> 6, cp = (p & 63) >> 4, r2 = 2 * (p & 15);
-  const uint32_t u_lane = (uint32_t)((((xi0 * 4 + cp) * a.m_pad + bk.k0 + r2) * 2) * 4);
-  const uint32_t u_it = (uint32_t)(4 * 4 * a.m_pad * 2 * 4);
-  const uint32_t u_ch = (uint32_t)(36 * 4 * a.m_pad * 2 * 4);
-
-  // Two chunks in flight, loads issued unconditionally (see load_role).
-  float dA[36], dB[36];
-  v4f uA[kULoads], uB[kULoads];
-  auto load = [&](int ch, bool live, float (&d)[36], v4f (&u)[kULoads]) {
-    const int c = ch * kCB + c_l;
-    const uint32_t pb = (live && t_ok && c < a.C) ? (uint32_t)(im * a.C + c) * plane_bytes : kOOB1;
+      for (int m = 0; m < NU; ++m)
+        res[m] = (FINAL && a.residual && go[m] >= 0) ? a.residual[go[m] + k * OHW] : 0.f;
 #pragma unroll
-    for (int i = 0; i < 6; ++i) {
-      const uint32_t rb = pb + rowoff[i];
-      if constexpr (VEC) {
-        d[i * 6 + 0] = buf_load_f32(xr, rb + coloff[0]);
-        const v4f m = __builtin_bit_cast(v4f, buf_load_b128(xr, rb + coloff[1]));
-        d[i * 6 + 1] = m[0];
-        d[i * 6 + 2] = m[1];
-        d[i * 6 + 3] = m[2];
-        d[i * 6 + 4] = m[3];
-        d[i * 6 + 5] = buf_load_f32(xr, rb + coloff[5]);
-      } else {
-#pragma unroll
-        for (int j = 0; j < 6; ++j) d[i * 6 + j] = buf_load_f32(xr, rb + coloff[j]);
-      }
+      for (int m = 0; m < NU; ++m)
+        if (go[m] >= 0) dst[go[m] + k * OHW] = activate<ACT>(lds[kk * (kTB * 16) + yo[m]] + b + res[m]);
     }
-    const uint32_t uo = live ? u_lane + (uint32_t)ch * u_ch : 0x80000000u;
-#pragma unroll
-    for (int it = 0; it < kULoads; ++it)
-      u[it] = __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(ur, uo, it * u_it, 0));
-  };
-  const int v_off = ((c_l >> 1) * kTB + t_l) * 2 + (c_l & 1);
-  auto fill = [&](int slot_idx, float (&d)[36], v4f (&u)[kULoads]) {
-    float* slot = lds + slot_idx * kSlotElems;
-    float* vw = slot + v_off;
-    input_transform(d, [&](int xi, float v) { vw[xi * kTB * kCB] = v; });
-#pragma unroll
-    for (int it = 0; it < kULoads; ++it)
-      *reinterpret_cast<v4f*>(slot + kVElems + (it * kProducers + p) * 4) = u[it];
-  };
-
-  const int n = bk.n, ch_begin = bk.ch_begin;
-  load(ch_begin, n > 0, dA, uA);
-  load(ch_begin + 1, n > 1, dB, uB);
-  for (int i = 0; i <= n; i += 2) {
-    if (i < n) fill(0, dA, uA);
-    load(ch_begin + i + 2, i + 2 < n, dA, uA);
-    __syncthreads();  // slot 0 full; slot 1 consumed
-    if (i + 1 < n) fill(1, dB, uB);
-    load(ch_begin + i + 3, i + 3 < n, dB, uB);
-    if (i + 1 <= n) __syncthreads();  // slot 1 full; slot 0 consumed
   }
 }
 
-// The transform waves, staged form (tile blocks of up to R tile rows of one
-// image (mode 1), left padding 1, W % 4 == 0): wave w stages the input rows
-// its two channels of the chunk need, (4 * nrows + 2) rows x W columns each,
-// from row 4 * ty0 - pt, through
-// LDS with 16-byte loads, then reads each thread's 6x6 patch from there.
-// The rows live in the wave's own quarter of the chunk slot's U region
-// ([channel][row][x + 4], row stride W + 8, halo columns zero), which the
-// wave overwrites with its share of the U slice only after its patch reads:
-// a wave's LDS operations complete in order, so no barrier is needed.
-// Its U share is the contiguous quarter e4 = w*576 + it*64 + lane.
-__device__ __forceinline__ void transform_role_staged(const FusedArgs& a, float* lds, int p, const Block& bk) {
-  const int lane = p & 63, w = p >> 6;
-  const int t_l = p % kTB, c_l = p / kTB;  // c_l = 2w + lane / 32
-  const bool t_ok = t_l < bk.ntiles;
-  const int im = bk.g0 / a.th, ty0 = bk.g0 - im * a.th;
-  const int rows = 4 * bk.nrows + 2;
-  const int RS = a.W + 8;
-  const int quads = a.W >> 2;
-  const int per_ch = rows * quads;           // 16-byte row pieces per channel
-  const int n_rows_ld = 2 * per_ch;          // per wave and chunk (<= 5 * 64, checked on the host)
-  const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, a.x_bytes);
-  const __amdgpu_buffer_rsrc_t ur = make_rsrc(a.U, a.u_bytes);
-  // row piece e (lane + 64u) of the wave: channel e / per_ch, row, quad
-  uint32_t roff[5];
-  int rlds[5], rch[5];
-#pragma unroll
-  for (int u = 0; u < 5; ++u) {
-    const int e = lane + 64 * u;
-    const int ch = e / per_ch, rem = e - ch * per_ch;
-    const int r = rem / quads, xq = rem - r * quads;
-    const int y = 4 * ty0 - a.pt + r;
-    const bool ok = e < n_rows_ld && (unsigned)y < (unsigned)a.H;
-    roff[u] = ok ? (uint32_t)(((im * a.C + 2 * w + ch) * a.H + y) * a.W + 4 * xq) * 4u : 0x80000000u;
-    rlds[u] = e < n_rows_ld ? (ch * rows + r) * RS + 4 + 4 * xq : -1;
-    rch[u] = 2 * w + ch;  // channel within the chunk
-  }
-  const uint32_t plane_bytes = (uint32_t)(a.H * a.W) * 4u;
-  // U share: e4 = w*576 + it*64 + lane -> xi = 9w + it, pair lane/16, rows 2*(lane%16)
-  const uint32_t u_lane = (uint32_t)((((9 * w * 4) + (lane >> 4)) * a.m_pad + bk.k0 + 2 * (lane & 15)) * 2 * 4);
-  const uint32_t u_it = (uint32_t)(4 * a.m_pad * 2 * 4);
-  const uint32_t u_ch = (uint32_t)(36 * 4 * a.m_pad * 2 * 4);
-  // patch of this thread: tile (ty, tx) of the block, rows 4*(ty - ty0) .. +5 of its channel's rows
-  const int tyl = t_l / a.tw, tx = t_l - tyl * a.tw;
-  const int pbase = ((lane >> 5) * rows + 4 * tyl) * RS + 3 + 4 * tx;  // x = 4tx - 1 at offset 4tx + 3
-
-  v4f rA[5], rB[5], uA[kULoads], uB[kULoads];
-  auto load = [&](int ch, bool live, v4f (&r)[5], v4f (&u)[kULoads]) {
-    const uint32_t cb = (uint32_t)(ch * kCB) * plane_bytes;  // chunk's channel offset
-#pragma unroll
-    for (int q = 0; q < 5; ++q)
-      r[q] = __builtin_bit_cast(v4f, buf_load_b128(xr, (live && ch * kCB + rch[q] < a.C) ? roff[q] + cb : 0x80000000u));
-    const uint32_t uo = live ? u_lane + (uint32_t)ch * u_ch : 0x80000000u;
-#pragma unroll
-    for (int it = 0; it < kULoads; ++it)
-      u[it] = __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(ur, uo, it * u_it, 0));
-  };
-  const int v_off = ((c_l >> 1) * kTB + t_l) * 2 + (c_l & 1);
-  auto fill = [&](int slot_idx, v4f (&r)[5], v4f (&u)[kULoads]) {
-    float* slot = lds + slot_idx * kSlotElems;
-    float* raw = slot + kVElems + w * (kUElems / 4);
-#pragma unroll
-    for (int q = 0; q < 5; ++q)
-      if (rlds[q] >= 0) *reinterpret_cast<v4f*>(raw + rlds[q]) = r[q];
-    // halo columns x = -1 and x = W of the wave's rows
-    for (int e = lane; e < 2 * rows; e += 64) {
-      raw[e * RS + 3] = 0.f;
-      raw[e * RS + a.W + 4] = 0.f;
-    }
-    float d[36];
-    const float* pr = raw + pbase;
-#pragma unroll
-    for (int i = 0; i < 6; ++i) {
-      d[i * 6 + 0] = pr[i * RS];
-      const v4f m = *reinterpret_cast<const v4f*>(pr + i * RS + 1);
-      d[i * 6 + 1] = m[0];
-      d[i * 6 + 2] = m[1];
-      d[i * 6 + 3] = m[2];
-      d[i * 6 + 4] = m[3];
-      d[i * 6 + 5] = pr[i * RS + 5];
-    }
-    if (!t_ok) {
-#pragma unroll
-      for (int e = 0; e < 36; ++e) d[e] = 0.f;
-    }
-    float* vw = slot + v_off;
-    input_transform(d, [&](int xi, float v) { vw[xi * kTB * kCB] = v; });
-    float* us = slot + kVElems + w * (kUElems / 4) + lane * 4;
-#pragma unroll
-    for (int it = 0; it < kULoads; ++it) *reinterpret_cast<v4f*>(us + it * 256) = u[it];
-  };
-
-  const int n = bk.n, ch_begin = bk.ch_begin;
-  load(ch_begin, n > 0, rA, uA);
-  load(ch_begin + 1, n > 1, rB, uB);
-  for (int i = 0; i <= n; i += 2) {
-    if (i < n) fill(0, rA, uA);
-    load(ch_begin + i + 2, i + 2 < n, rA, uA);
-    __syncthreads();  // slot 0 full; slot 1 consumed
-    if (i + 1 < n) fill(1, rB, uB);
-    load(ch_begin + i + 3, i + 3 < n, rB, uB);
-    if (i + 1 <= n) __syncthreads();  // slot 1 full; slot 0 consumed
-  }
-}
-
-// 8 waves, 4 load (XFORM: transform) + 4 MFMA, chunks of 8 channels in
-// 2 x 72 KB of LDS (one workgroup per CU).  FINAL: write act(Y + bias
-// (+ residual)) with activation ACT; otherwise the raw part of channel split
-// cs.  XFORM: the direct variant, V computed from the input in the kernel
-// (VEC: the staged form, transform_role_staged).
-template <int ACT, bool FINAL, bool XFORM, bool VEC>
+// 8 waves, 4 load + 4 MFMA, chunks of 8 channels in 2 x 72 KB of LDS (one
+// workgroup per CU).  FINAL: write act(Y + bias (+ residual)) with
+// activation ACT; otherwise the raw part of channel split cs.
+template <int ACT, bool FINAL>
 __global__ __launch_bounds__(kThreads, 1) void wino_fused_kernel(FusedArgs a) {
   extern __shared__ __attribute__((aligned(16))) float lds[];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const Block bk = block_of(a, kCB);
 
   if (wave >= 4) {
-    if constexpr (XFORM && VEC)
-      transform_role_staged(a, lds, tid - 4 * 64, bk);
-    else if constexpr (XFORM)
-      transform_role<false>(a, lds, tid - 4 * 64, bk);
-    else
-      load_role(a, lds, tid - 4 * 64, bk.t0, bk.k0, bk.ch_begin, bk.n);
+    load_role(a, lds, tid - 4 * 64, bk.t0, bk.k0, bk.ch_begin, bk.n);
   } else {
     // ---- MFMA waves ----------------------------------------------------------
     const int li = lane & 15, q = lane >> 4;
@@ -715,25 +428,19 @@ __global__ void wino_fused_reduce(const float* __restrict__ part, int splits, in
   }
 }
 
-template <int ACT, bool FINAL, bool XFORM, bool VEC>
+template <int ACT, bool FINAL>
 int launch_kernel(const FusedArgs& a, int64_t blocks, hipStream_t s) {
   static bool attr_set = false;  // dynamic LDS above 64 KB needs the attribute
   if (!attr_set) {
     NHIP_TRY(check_hip(
-        hipFuncSetAttribute(reinterpret_cast<const void*>(&wino_fused_kernel<ACT, FINAL, XFORM, VEC>),
+        hipFuncSetAttribute(reinterpret_cast<const void*>(&wino_fused_kernel<ACT, FINAL>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes),
         "hipFuncSetAttribute(wino_fused)"));
     attr_set = true;
   }
-  NHIP_LAUNCH("wino_fused", (wino_fused_kernel<ACT, FINAL, XFORM, VEC>), dim3((unsigned)blocks), dim3(kThreads),
+  NHIP_LAUNCH("wino_fused", (wino_fused_kernel<ACT, FINAL>), dim3((unsigned)blocks), dim3(kThreads),
               kLdsBytes, s, a);
   return check_launch("wino_fused");
-}
-
-template <int ACT, bool FINAL>
-int launch_kernel(const FusedArgs& a, int64_t blocks, bool xform, bool vec, hipStream_t s) {
-  if (!xform) return launch_kernel<ACT, FINAL, false, false>(a, blocks, s);
-  return vec ? launch_kernel<ACT, FINAL, true, true>(a, blocks, s) : launch_kernel<ACT, FINAL, true, false>(a, blocks, s);
 }
 
 template <int VEC, int ACT>
@@ -745,33 +452,17 @@ int launch_reduce(const float* parts, int splits, int64_t total, int ohw, int K,
 }
 
 struct FusedShape {
-  int th, tw, G, mode, R, bpi, bpr, nt, nk, nch, splits, per;
+  int th, tw, nt, nk, nch, splits, per;
 };
 
-// Tile blocks (whole tile rows, or 32-tile pieces of wider rows); channel
-// splits: the fewest that minimise (rounds of one workgroup per CU) x
-// (chunks per workgroup), each split keeping at least 4 chunks.
+// Tile blocks of 32 consecutive tiles; channel splits: the fewest that
+// minimise (rounds of one workgroup per CU) x (chunks per workgroup), each
+// split keeping at least 4 chunks.
 FusedShape fused_shape(const nhip_conv_plan* p, int n, int oh, int ow) {
   FusedShape f;
   f.th = (int)ceil_div(oh, 4);
   f.tw = (int)ceil_div(ow, 4);
-  f.G = n * f.th;
-  f.bpi = f.bpr = 0;
-  if (f.tw <= kTB && f.th <= kTB / f.tw) {
-    f.mode = 0;
-    f.R = kTB / f.tw / f.th * f.th;
-    f.nt = (int)ceil_div(f.G, f.R);
-  } else if (f.tw <= kTB) {
-    f.mode = 1;
-    f.R = kTB / f.tw;
-    f.bpi = (int)ceil_div(f.th, f.R);
-    f.nt = n * f.bpi;
-  } else {
-    f.mode = 2;
-    f.R = 1;
-    f.bpr = (int)ceil_div(f.tw, kTB);
-    f.nt = f.G * f.bpr;
-  }
+  f.nt = (int)ceil_div((int64_t)n * f.th * f.tw, kTB);
   f.nk = (int)ceil_div(p->g.k, kKB);
   f.nch = p->c_pad / kCB;
   const int64_t cus = cu_count();
@@ -798,9 +489,9 @@ uint64_t wino_gemm_out_parts_bytes(const nhip_conv_plan* p, int n, int oh, int o
 
 namespace {
 
-// Shared by both entries: a = the operand sources already set (V or x).
-int launch_fused(const nhip_conv_plan* p, FusedArgs& a, const FusedShape& f, bool xform, bool vec,
-                 const float* residual, float* out, int n, int oh, int ow, float* parts, hipStream_t s) {
+// a = the operand source (V) already set.
+int launch_fused(const nhip_conv_plan* p, FusedArgs& a, const FusedShape& f, const float* residual, float* out,
+                 int n, int oh, int ow, float* parts, hipStream_t s) {
   if ((reinterpret_cast<uintptr_t>(out) & 15) || (residual && (reinterpret_cast<uintptr_t>(residual) & 15)) ||
       (reinterpret_cast<uintptr_t>(parts) & 15))
     return fail(NHIP_STATUS_CONSTRAINT_VIOLATION, "winograd: buffers must be 16-byte aligned");
@@ -811,6 +502,8 @@ int launch_fused(const nhip_conv_plan* p, FusedArgs& a, const FusedShape& f, boo
     return fail(NHIP_STATUS_CONSTRAINT_VIOLATION, "winograd GEMM: transformed weights above 2 GiB");
   if (p->c_pad % kCB != 0 || p->m_pad % kKB != 0)
     return fail(NHIP_STATUS_CONSTRAINT_VIOLATION, "winograd GEMM: padding mismatch");
+  if ((int64_t)n * p->g.k * oh * ow >= (int64_t(1) << 31))  // 32-bit output offsets in the write-out
+    return fail(NHIP_STATUS_CONSTRAINT_VIOLATION, "winograd GEMM: output above 2^31 elements");
   a.U = p->weight_fused;
   a.u_bytes = (uint32_t)u_bytes;
   a.bias = p->bias;
@@ -822,11 +515,7 @@ int launch_fused(const nhip_conv_plan* p, FusedArgs& a, const FusedShape& f, boo
   a.th = f.th;
   a.tw = f.tw;
   a.T = n * f.th * f.tw;
-  a.mode = f.mode;
-  a.R = f.R;
-  a.bpi = f.bpi;
-  a.bpr = f.bpr;
-  a.G = f.G;
+  a.part_stride = (int64_t)n * p->g.k * oh * ow;
   a.m_pad = p->m_pad;
   a.c_pad = p->c_pad;
   a.nt = f.nt;
@@ -836,13 +525,13 @@ int launch_fused(const nhip_conv_plan* p, FusedArgs& a, const FusedShape& f, boo
   const int64_t blocks = (int64_t)f.nt * f.nk * f.splits;
   if (f.splits == 1) {
     switch (p->g.act) {
-      case NHIP_ACT_NONE: return launch_kernel<NHIP_ACT_NONE, true>(a, blocks, xform, vec, s);
-      case NHIP_ACT_RELU: return launch_kernel<NHIP_ACT_RELU, true>(a, blocks, xform, vec, s);
-      case NHIP_ACT_SIGMOID: return launch_kernel<NHIP_ACT_SIGMOID, true>(a, blocks, xform, vec, s);
+      case NHIP_ACT_NONE: return launch_kernel<NHIP_ACT_NONE, true>(a, blocks, s);
+      case NHIP_ACT_RELU: return launch_kernel<NHIP_ACT_RELU, true>(a, blocks, s);
+      case NHIP_ACT_SIGMOID: return launch_kernel<NHIP_ACT_SIGMOID, true>(a, blocks, s);
       default: return fail(NHIP_STATUS_UNSUPPORTED, "winograd GEMM: unsupported activation");
     }
   }
-  NHIP_TRY((launch_kernel<NHIP_ACT_NONE, false>(a, blocks, xform, vec, s)));
+  NHIP_TRY((launch_kernel<NHIP_ACT_NONE, false>(a, blocks, s)));
   const int64_t total = (int64_t)n * p->g.k * oh * ow;
   const int ohw = oh * ow;
 #define NHIP_REDUCE(V_)                                                                                       \
@@ -874,36 +563,7 @@ int launch_wino_gemm_out(const nhip_conv_plan* p, const float* V, int t_pad, con
   a.V = V;
   a.v_bytes = (uint32_t)v_bytes;
   a.t_pad = t_pad;
-  return launch_fused(p, a, fused_shape(p, n, oh, ow), false, false, residual, out, n, oh, ow, parts, s);
-}
-
-// The direct variant's staged input rows apply (by shape; the input must also
-// be 16-byte aligned at launch, else the direct kernel gathers patches).
-bool wino_direct_staged_shape(const nhip_conv_plan* p, int n, int h, int w, int oh, int ow) {
-  const FusedShape f = fused_shape(p, n, oh, ow);
-  const int rows = 4 * f.R + 2;
-  return f.mode == 1 && p->g.pl == 1 && w % 4 == 0 && 2 * rows * (w / 4) <= 5 * 64 &&
-         2 * rows * (w + 8) <= kUElems / 4 && (int64_t)n * p->g.c * h * w * 4 < (int64_t(1) << 30);
-}
-
-int launch_wino_fused_direct(const nhip_conv_plan* p, const float* in, int h, int w, const float* residual,
-                             float* out, int n, int oh, int ow, float* parts, hipStream_t s) {
-  const size_t x_bytes = (size_t)n * p->g.c * h * w * sizeof(float);
-  if (x_bytes > (size_t(1) << 30))
-    return fail(NHIP_STATUS_CONSTRAINT_VIOLATION, "winograd direct: input above 1 GiB");
-  FusedArgs a{};
-  a.x = in;
-  a.x_bytes = (uint32_t)x_bytes;
-  a.C = p->g.c;
-  a.H = h;
-  a.W = w;
-  a.pt = p->g.pt;
-  a.pl = p->g.pl;
-  // staged rows: tile rows of one image (mode 1), left padding 1, 16-byte
-  // rows, and a wave's two channels of rows (<= 5 x 64 pieces, and within
-  // its quarter of the U region) per chunk
-  const bool staged = wino_direct_staged_shape(p, n, h, w, oh, ow) && (reinterpret_cast<uintptr_t>(in) & 15) == 0;
-  return launch_fused(p, a, fused_shape(p, n, oh, ow), true, staged, residual, out, n, oh, ow, parts, s);
+  return launch_fused(p, a, fused_shape(p, n, oh, ow), residual, out, n, oh, ow, parts, s);
 }
 
 }  // namespace nhip
