@@ -102,6 +102,10 @@ CASES = [
     (2, 16, 15, 13, 20, (3, 3), (2, 2), (1, 1), (1, 1, 1, 1), 1, 1, True, True),
     (1, 24, 12, 12, 130, (3, 3), (1, 1), (2, 2), (2, 2, 2, 2), 2, 0, False, True),
     (3, 33, 8, 10, 48, (2, 3), (1, 2), (1, 1), (0, 1, 2, 0), 102, 1, True, False),
+    # footprint windows: unused last column, two right halo columns, 6 + 1 output rows
+    (2, 32, 16, 16, 40, (3, 3), (2, 2), (1, 1), (0, 0, 0, 0), 101, 1, False, False),
+    (1, 64, 8, 12, 64, (3, 3), (1, 1), (1, 1), (1, 2, 1, 2), 1, 0, True, True),
+    (2, 96, 7, 20, 32, (3, 3), (1, 1), (1, 1), (1, 1, 1, 1), 102, 1, False, True),
 ]
 
 
