@@ -18,6 +18,18 @@
 
 #include "../../include/nhip_graph.h"
 
+extern char** environ;
+
+// Internal helpers of libnhip (csrc/runtime.hip): stream capture into a
+// hipGraph and its replay, and whether the kernel timer is recording.
+namespace nhip {
+bool kernel_timer_active();
+int graph_capture_begin(void* stream);
+int graph_capture_end(void* stream, void** exec);
+int graph_exec_launch(void* exec, void* stream);
+void graph_exec_destroy(void* exec);
+}  // namespace nhip
+
 namespace nhip {
 int fail(int status, const std::string& message);  // runtime.hip
 int ok();
@@ -494,7 +506,14 @@ struct nhip_graph {
   std::vector<uint64_t> host_in_cap;
   std::mutex mu;
   bool host_only = false;  // from nhip_graph_describe: no device plans
+  // The last call plan recorded as a hipGraph (nhip_graph_run on a stream),
+  // valid for calls with the same key: batch, input shapes, input and output
+  // pointers and NHIP_* settings (the buffers it uses stay allocated).
+  void* exec = nullptr;
+  std::string exec_key;
+  std::string seen_key;  // the previous call's key: a plan is recorded on its second call
   ~nhip_graph() {
+    nhip::graph_exec_destroy(exec);
     for (auto& op : ops) {
       if (op.conv) nhip_conv_destroy(op.conv);
       if (op.ip) nhip_innerproduct_destroy(op.ip);
@@ -1148,7 +1167,50 @@ int nhip_graph_run(nhip_graph_t g, int32_t n, const int64_t* input_shapes, const
     if (!outputs[j]) return fail(NHIP_STATUS_NULL_POINTER, "graph_run: null output");
   std::vector<Shape> sh;
   TRY(propagate(*g, input_shapes, sh, true));
-  return run_ops(*g, n, sh, inputs, outputs, stream);
+  std::lock_guard<std::mutex> lock(g->mu);
+  // Replay: when two calls in a row on a stream have the same key, the
+  // second runs eagerly (every buffer is already sized) and is also recorded
+  // into a hipGraph, and later calls with that key launch the recorded graph:
+  // one launch instead of one per kernel (each eager launch costs a few
+  // microseconds of dispatch that the short late layers of a network cannot
+  // hide).  Calls whose pointers change every time stay eager and record
+  // nothing.  The legacy default stream cannot be captured and runs eagerly,
+  // as do runs while the kernel timer records per-launch events;
+  // NHIP_GRAPH_REPLAY=0 turns replay off.
+  const char* rep = std::getenv("NHIP_GRAPH_REPLAY");
+  if (stream == nullptr || (rep && std::atoi(rep) == 0) || nhip::kernel_timer_active())
+    return run_ops(*g, n, sh, inputs, outputs, stream);
+  std::ostringstream key;
+  key << n;
+  for (int b : g->inputs) {
+    key << "|";
+    for (int d = 0; d < sh[b].rank; ++d) key << sh[b].d[d] << ",";
+  }
+  for (size_t i = 0; i < g->inputs.size(); ++i) key << "|" << inputs[i];
+  for (size_t j = 0; j < g->outputs.size(); ++j) key << "|" << outputs[j];
+  for (char** e = environ; e && *e; ++e)
+    if (std::strncmp(*e, "NHIP_", 5) == 0) key << "|" << *e;
+  if (g->exec && key.str() == g->exec_key) return nhip::graph_exec_launch(g->exec, stream);
+  TRY(run_ops(*g, n, sh, inputs, outputs, stream));
+  if (key.str() != g->seen_key) {
+    g->seen_key = key.str();
+    return ok();
+  }
+  nhip::graph_exec_destroy(g->exec);
+  g->exec = nullptr;
+  g->exec_key.clear();
+  if (nhip::graph_capture_begin(stream) == NHIP_STATUS_SUCCESS) {
+    const int st = run_ops(*g, n, sh, inputs, outputs, stream);
+    void* exec = nullptr;
+    const int st2 = nhip::graph_capture_end(stream, &exec);
+    if (st == NHIP_STATUS_SUCCESS && st2 == NHIP_STATUS_SUCCESS && exec) {
+      g->exec = exec;
+      g->exec_key = key.str();
+    } else {
+      nhip::graph_exec_destroy(exec);
+    }
+  }
+  return ok();
 }
 
 int nhip_graph_run_host(nhip_graph_t g, const int64_t* input_shapes, const void* const* inputs, void* const* outputs,

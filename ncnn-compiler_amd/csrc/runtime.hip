@@ -61,6 +61,40 @@ TimerState& timer() {
 }
 }  // namespace
 
+bool kernel_timer_active() {
+  TimerState& t = timer();
+  std::lock_guard<std::mutex> lock(t.mu);
+  return t.on;
+}
+
+// Stream capture for the graph executor's replay (csrc/graph.cpp): the
+// executor records one run of its call plan into a hipGraph and replays the
+// instantiated graph on later calls with the same buffers.
+int graph_capture_begin(void* stream) {
+  return check_hip(hipStreamBeginCapture(as_stream(stream), hipStreamCaptureModeThreadLocal),
+                   "hipStreamBeginCapture");
+}
+
+int graph_capture_end(void* stream, void** exec) {
+  hipGraph_t graph = nullptr;
+  *exec = nullptr;
+  NHIP_TRY(check_hip(hipStreamEndCapture(as_stream(stream), &graph), "hipStreamEndCapture"));
+  hipGraphExec_t e = nullptr;
+  const int st = check_hip(hipGraphInstantiate(&e, graph, nullptr, nullptr, 0), "hipGraphInstantiate");
+  (void)hipGraphDestroy(graph);
+  if (st == NHIP_STATUS_SUCCESS) *exec = e;
+  return st;
+}
+
+int graph_exec_launch(void* exec, void* stream) {
+  NHIP_TRY(check_hip(hipGraphLaunch(reinterpret_cast<hipGraphExec_t>(exec), as_stream(stream)), "hipGraphLaunch"));
+  return check_launch("graph replay");
+}
+
+void graph_exec_destroy(void* exec) {
+  if (exec) (void)hipGraphExecDestroy(reinterpret_cast<hipGraphExec_t>(exec));
+}
+
 LaunchTimer::LaunchTimer(const char* kernel) {
   TimerState& t = timer();
   std::lock_guard<std::mutex> lock(t.mu);

@@ -620,9 +620,13 @@ class Graph:
         check(load().nhip_graph_run_host(self.handle, arg, ins, ops, cap))
         return outs
 
-    def run(self, *tensors, stream=None):
+    def run(self, *tensors, stream=None, out=None):
         """Batch execution: each input a [N, ...] device tensor of N blobs;
-        returns device tensors [N, ...] per output."""
+        returns device tensors [N, ...] per output (written into `out`, a
+        list of preallocated tensors, when given).  On a non-default stream,
+        repeated calls with the same inputs and outputs replay a recorded
+        hipGraph of the call plan (nhip_graph_run), so steady loops should
+        pass `out`."""
         torch = _torch()
         if len(tensors) != len(self.inputs):
             raise ValueError(f"expected {len(self.inputs)} inputs")
@@ -633,8 +637,15 @@ class Graph:
                   for t in xs]
         dyn = any(d < 0 for io in self.inputs for d in io["shape"])
         oshapes = self.infer_shapes(shapes if dyn else None)
-        outs = [torch.empty((n,) + s, dtype=torch.int8 if io["dtype"] == np.int8 else torch.float32,
-                            device=xs[0].device) for s, io in zip(oshapes, self.outputs)]
+        if out is None:
+            outs = [torch.empty((n,) + s, dtype=torch.int8 if io["dtype"] == np.int8 else torch.float32,
+                                device=xs[0].device) for s, io in zip(oshapes, self.outputs)]
+        else:
+            outs = list(out)
+            for o, s, io in zip(outs, oshapes, self.outputs):
+                want = torch.int8 if io["dtype"] == np.int8 else torch.float32
+                if tuple(o.shape) != (n,) + tuple(s) or o.dtype != want or not o.is_contiguous() or not o.is_cuda:
+                    raise ValueError(f"out tensor must be a contiguous {want} device tensor of shape {(n,) + tuple(s)}")
         ins = (_P * len(xs))(*[t.data_ptr() for t in xs])
         ops = (_P * len(outs))(*[o.data_ptr() for o in outs])
         check(load().nhip_graph_run(self.handle, n, self._shape_arg(shapes) if dyn else None, ins, ops,

@@ -1,0 +1,99 @@
+"""GPU: the graph executor's hipGraph replay (nhip_graph_run records the
+call plan on the second call with the same buffers and replays it after)
+gives the eager executor's results bit for bit: on every replay, with the
+program's own device work and synchronizations between replays, after the
+input changes in place, on a side stream, and when a tuning setting changes
+(which must re-record, not replay a stale plan)."""
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+
+import graphs  # noqa: E402
+import ncnn_format  # noqa: E402
+import nhip  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    assert torch.cuda.is_available(), "GPU tests need a HIP device"
+    nhip.init(0)
+
+
+def mobilenet_graph():
+    m = ncnn_format.from_layer_list(graphs.mobilenetv2_layers(seed=0))
+    return nhip.Graph(m.param_text(), bytes(m.payload))
+
+
+def eager(g, x, monkeypatch):
+    monkeypatch.setenv("NHIP_GRAPH_REPLAY", "0")
+    out = g.run(x)[0].clone()
+    torch.cuda.synchronize()
+    monkeypatch.delenv("NHIP_GRAPH_REPLAY")
+    return out
+
+
+def test_replay_matches_eager_on_every_call(monkeypatch):
+    monkeypatch.delenv("NHIP_GRAPH_REPLAY", raising=False)
+    g = mobilenet_graph()
+    rng = np.random.default_rng(1)
+    x = torch.from_numpy(rng.uniform(-1, 1, (2, 3, 224, 224)).astype(np.float32)).cuda()
+    ref = eager(g, x, monkeypatch)
+    out = [torch.empty_like(ref)]
+    for call in range(6):  # call 0: eager, 1: eager + recorded, 2..5: replays
+        out[0].fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.run(x, out=out)
+        torch.cuda.synchronize()
+        assert torch.equal(out[0], ref), f"call {call} differs from the eager run"
+        scratch = torch.randn(1 << 20, device="cuda") * 2  # unrelated eager work between replays
+        torch.cuda.synchronize()
+        del scratch
+    # new input values in the same buffer: the replay reads them
+    x.copy_(torch.from_numpy(rng.uniform(-1, 1, (2, 3, 224, 224)).astype(np.float32)))
+    ref2 = eager(g, x, monkeypatch)
+    assert not torch.equal(ref2, ref)
+    for _ in range(3):
+        g.run(x, out=out)
+        torch.cuda.synchronize()
+        assert torch.equal(out[0], ref2)
+    # on a side stream
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(3):
+            out[0].zero_()
+            g.run(x, out=out)
+    torch.cuda.synchronize()
+    assert torch.equal(out[0], ref2)
+
+
+def test_setting_change_rerecords(monkeypatch):
+    """NHIP_DWPW picks fused or separate depthwise -> 1x1 kernels: after a
+    recorded plan exists, changing it must give that setting's eager result."""
+    monkeypatch.delenv("NHIP_GRAPH_REPLAY", raising=False)
+    g = mobilenet_graph()
+    x = torch.from_numpy(np.random.default_rng(2).uniform(-1, 1, (2, 3, 224, 224)).astype(np.float32)).cuda()
+    out = [torch.empty((2, 1000), device="cuda")]
+    for setting in ("1", "0", "2", "1"):
+        monkeypatch.setenv("NHIP_DWPW", setting)
+        ref = eager(g, x, monkeypatch)
+        for _ in range(3):
+            g.run(x, out=out)
+            torch.cuda.synchronize()
+            assert torch.equal(out[0], ref), f"NHIP_DWPW={setting}"
+
+
+def test_changing_outputs_stay_eager_and_correct(monkeypatch):
+    """Fresh output tensors on every call (no out=) never reuse a recorded
+    plan with stale pointers."""
+    monkeypatch.delenv("NHIP_GRAPH_REPLAY", raising=False)
+    g = mobilenet_graph()
+    x = torch.from_numpy(np.random.default_rng(3).uniform(-1, 1, (2, 3, 224, 224)).astype(np.float32)).cuda()
+    ref = eager(g, x, monkeypatch)
+    keep = [g.run(x)[0] for _ in range(4)]  # kept alive: every call has new output pointers
+    torch.cuda.synchronize()
+    for o in keep:
+        assert torch.equal(o, ref)
