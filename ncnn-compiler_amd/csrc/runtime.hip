@@ -474,7 +474,7 @@ int nhip_conv2d_int8_create(const nhip_conv_desc* d, const void* weight, int32_t
   p->m_pad = (int)round_up(K, 64);
   p->c_pad = (int)round_up(C, 16);
   p->kred = KH * KW * p->c_pad;
-  p->kred_pad = (int)round_up(p->kred, 256);  // whole GEMM K stages (128 or 256 bytes)
+  p->kred_pad = (int)round_up(p->kred, 128);  // whole 128-byte GEMM K stages (256-byte tiles where it divides)
   // Weights to int8 [m_pad][kh][kw][c_pad] (OHWI with channel padding).
   std::vector<int8_t> wq((size_t)p->m_pad * p->kred_pad, 0);
   for (int k = 0; k < K; ++k) {
