@@ -315,9 +315,9 @@ __global__ __launch_bounds__(kThreads) void conv_int8_kernel(Int8Args g) {
 // is then read straight from that window, so only the weights stream through
 // the two-stage K pipeline (they are shared by all workgroups and stay in
 // L2).  Same MFMA mapping, accumulation and epilogue as conv_int8_kernel.
-template <int BM>
+template <int BM, int BK>
 __global__ __launch_bounds__(kThreads) void conv_int8_fp_kernel(Int8Args g) {
-  constexpr int BN = 128, BK = 128;
+  constexpr int BN = 128;
   constexpr int TM = BM / 64, TN = BN / 64;
   constexpr int ROW = BK + 16;
   constexpr int CH = BK / 16;
@@ -557,17 +557,40 @@ int launch_conv_int8(const nhip_conv_plan* p, const void* in, int in_is_i8,
       g.FS = p->c_pad + 16;
       g.fp_bytes = (int)round_up((int64_t)g.FH * g.FW * g.FS, 16);
       const int bm = p->m_pad % 128 == 0 && p->m_pad >= 256 ? 128 : 64;
-      const int64_t lds_oper = (int64_t)g.fp_bytes + 2LL * bm * (128 + 16);
-      const int64_t lds_epi = (int64_t)bm * (128 + 16) * 4;
-      const int64_t lds = std::max(lds_oper, lds_epi);
+      // K stage: the widest of 384 / 192 / 128 bytes that divides the
+      // reduction and keeps the workgroup's LDS within 64 KB (fewer stages,
+      // fewer global-load round trips and barriers per workgroup);
+      // NHIP_INT8_FP_BK overrides (tuning switch, ignored when invalid).
+      auto lds_for = [&](int bk) {
+        const int64_t oper = (int64_t)g.fp_bytes + 2LL * bm * (bk + 16);
+        const int64_t epi = (int64_t)bm * (128 + 16) * 4;
+        return std::max(oper, epi);
+      };
+      int bk = 128;
+      for (int c : {384, 192})
+        if (p->kred_pad % c == 0 && lds_for(c) <= 64 * 1024) {
+          bk = c;
+          break;
+        }
+      if (const char* e = std::getenv("NHIP_INT8_FP_BK")) {
+        const int c = std::atoi(e);
+        if ((c == 128 || c == 192 || c == 384) && p->kred_pad % c == 0 && lds_for(c) <= 64 * 1024) bk = c;
+      }
+      const int64_t lds = lds_for(bk);
       if (lds <= 64 * 1024) {
         const dim3 grid((unsigned)(n * ceil_div(oh, g.R)), (unsigned)(p->m_pad / bm));
-        if (bm == 128) {
-          NHIP_LAUNCH("conv_int8_fp<128>", conv_int8_fp_kernel<128>, grid, dim3(kThreads), (unsigned)lds, s, g);
-        } else {
-          NHIP_LAUNCH("conv_int8_fp<64>", conv_int8_fp_kernel<64>, grid, dim3(kThreads), (unsigned)lds, s, g);
-        }
-        return check_launch("conv_int8_fp");
+#define NHIP_FP_CASE(BM_, BK_)                                                                             \
+  if (bm == BM_ && bk == BK_) {                                                                           \
+    NHIP_LAUNCH("conv_int8_fp", (conv_int8_fp_kernel<BM_, BK_>), grid, dim3(kThreads), (unsigned)lds, s, g); \
+    return check_launch("conv_int8_fp");                                                                  \
+  }
+        NHIP_FP_CASE(64, 128)
+        NHIP_FP_CASE(64, 192)
+        NHIP_FP_CASE(64, 384)
+        NHIP_FP_CASE(128, 128)
+        NHIP_FP_CASE(128, 192)
+        NHIP_FP_CASE(128, 384)
+#undef NHIP_FP_CASE
       }
     }
   }
