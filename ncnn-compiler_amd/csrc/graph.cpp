@@ -511,7 +511,9 @@ struct nhip_graph {
   // pointers and NHIP_* settings (the buffers it uses stay allocated).
   void* exec = nullptr;
   std::string exec_key;
-  std::string seen_key;  // the previous call's key: a plan is recorded on its second call
+  std::vector<const void*> exec_bufs;  // the internal buffers the recorded plan uses
+  std::string seen_key;   // the previous call's key: a plan is recorded on its second call
+  std::string nocap_key;  // a key whose capture failed: runs eagerly
   ~nhip_graph() {
     nhip::graph_exec_destroy(exec);
     for (auto& op : ops) {
@@ -1190,15 +1192,31 @@ int nhip_graph_run(nhip_graph_t g, int32_t n, const int64_t* input_shapes, const
   for (size_t j = 0; j < g->outputs.size(); ++j) key << "|" << outputs[j];
   for (char** e = environ; e && *e; ++e)
     if (std::strncmp(*e, "NHIP_", 5) == 0) key << "|" << *e;
-  if (g->exec && key.str() == g->exec_key) return nhip::graph_exec_launch(g->exec, stream);
+  // The blob buffers and workspace grow (free + malloc) when a call needs
+  // more: a recorded plan is only replayed while they are the ones it was
+  // recorded with.
+  auto internal_bufs = [&]() {
+    std::vector<const void*> v;
+    v.reserve(g->blobs.size() + 1);
+    for (const Blob& b : g->blobs) v.push_back(b.buf);
+    v.push_back(g->ws);
+    return v;
+  };
+  if (g->exec && key.str() == g->exec_key) {
+    if (internal_bufs() == g->exec_bufs) return nhip::graph_exec_launch(g->exec, stream);
+    nhip::graph_exec_destroy(g->exec);
+    g->exec = nullptr;
+    g->exec_key.clear();
+  }
   TRY(run_ops(*g, n, sh, inputs, outputs, stream));
-  if (key.str() != g->seen_key) {
+  if (key.str() != g->seen_key || key.str() == g->nocap_key) {
     g->seen_key = key.str();
     return ok();
   }
   nhip::graph_exec_destroy(g->exec);
   g->exec = nullptr;
   g->exec_key.clear();
+  bool recorded = false;
   if (nhip::graph_capture_begin(stream) == NHIP_STATUS_SUCCESS) {
     const int st = run_ops(*g, n, sh, inputs, outputs, stream);
     void* exec = nullptr;
@@ -1206,10 +1224,13 @@ int nhip_graph_run(nhip_graph_t g, int32_t n, const int64_t* input_shapes, const
     if (st == NHIP_STATUS_SUCCESS && st2 == NHIP_STATUS_SUCCESS && exec) {
       g->exec = exec;
       g->exec_key = key.str();
+      g->exec_bufs = internal_bufs();
+      recorded = true;
     } else {
       nhip::graph_exec_destroy(exec);
     }
   }
+  if (!recorded) g->nocap_key = key.str();
   return ok();
 }
 

@@ -1,9 +1,11 @@
 """GPU: the graph executor's hipGraph replay (nhip_graph_run records the
-call plan on the second call with the same buffers and replays it after)
-gives the eager executor's results bit for bit: on every replay, with the
-program's own device work and synchronizations between replays, after the
-input changes in place, on a side stream, and when a tuning setting changes
-(which must re-record, not replay a stale plan)."""
+call plan on the second call with the same buffers and replays it after;
+replay needs a non-default stream, which every test here runs on) gives the
+eager executor's results bit for bit: on every replay, with the program's
+own device work and synchronizations between replays, after the input
+changes in place, on another stream, when a tuning setting changes (which
+must re-record, not replay a stale plan), with fresh output tensors, and
+after a larger batch has reallocated the executor's buffers."""
 import numpy as np
 import pytest
 
@@ -20,6 +22,18 @@ pytestmark = pytest.mark.gpu
 def _gpu():
     assert torch.cuda.is_available(), "GPU tests need a HIP device"
     nhip.init(0)
+
+
+@pytest.fixture(autouse=True)
+def _side_stream():
+    """Replay needs a capturable stream: torch's default stream is the legacy
+    null stream (handle 0), on which the executor always runs eagerly."""
+    s = torch.cuda.Stream()
+    assert s.cuda_stream != 0
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        yield
+    torch.cuda.synchronize()
 
 
 def mobilenet_graph():
@@ -59,7 +73,7 @@ def test_replay_matches_eager_on_every_call(monkeypatch):
         g.run(x, out=out)
         torch.cuda.synchronize()
         assert torch.equal(out[0], ref2)
-    # on a side stream
+    # on another stream: the recorded plan is launched there
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
@@ -68,6 +82,20 @@ def test_replay_matches_eager_on_every_call(monkeypatch):
             g.run(x, out=out)
     torch.cuda.synchronize()
     assert torch.equal(out[0], ref2)
+
+
+def test_default_stream_runs_eagerly_and_correct(monkeypatch):
+    monkeypatch.delenv("NHIP_GRAPH_REPLAY", raising=False)
+    g = mobilenet_graph()
+    x = torch.from_numpy(np.random.default_rng(5).uniform(-1, 1, (2, 3, 224, 224)).astype(np.float32)).cuda()
+    ref = eager(g, x, monkeypatch)
+    out = [torch.empty_like(ref)]
+    torch.cuda.synchronize()
+    with torch.cuda.stream(torch.cuda.default_stream()):
+        for _ in range(3):
+            g.run(x, out=out)
+    torch.cuda.synchronize()
+    assert torch.equal(out[0], ref)
 
 
 def test_setting_change_rerecords(monkeypatch):
@@ -97,3 +125,31 @@ def test_changing_outputs_stay_eager_and_correct(monkeypatch):
     torch.cuda.synchronize()
     for o in keep:
         assert torch.equal(o, ref)
+
+
+def test_buffers_grown_by_a_larger_batch_invalidate_the_recorded_plan(monkeypatch):
+    """A recorded plan uses the executor's blob buffers; a call with a larger
+    batch reallocates them, and the next call with the recorded key must not
+    replay the plan over the freed buffers."""
+    monkeypatch.delenv("NHIP_GRAPH_REPLAY", raising=False)
+    g = mobilenet_graph()
+    rng = np.random.default_rng(4)
+    xa = torch.from_numpy(rng.uniform(-1, 1, (2, 3, 224, 224)).astype(np.float32)).cuda()
+    xb = torch.from_numpy(rng.uniform(-1, 1, (4, 3, 224, 224)).astype(np.float32)).cuda()
+    ref_a = eager(g, xa, monkeypatch)
+    ref_b = eager(g, xb, monkeypatch)  # the executor's buffers now hold batch 4
+    g2 = mobilenet_graph()
+    out_a, out_b = [torch.empty_like(ref_a)], [torch.empty_like(ref_b)]
+    for _ in range(3):  # records and replays batch 2
+        g2.run(xa, out=out_a)
+    torch.cuda.synchronize()
+    assert torch.equal(out_a[0], ref_a)
+    for _ in range(2):  # grows every buffer
+        g2.run(xb, out=out_b)
+    torch.cuda.synchronize()
+    assert torch.equal(out_b[0], ref_b)
+    for _ in range(3):  # the batch-2 key again: buffers changed since it was recorded
+        out_a[0].zero_()
+        g2.run(xa, out=out_a)
+        torch.cuda.synchronize()
+        assert torch.equal(out_a[0], ref_a)
