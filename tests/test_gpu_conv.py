@@ -140,6 +140,40 @@ def test_winograd_matches_oracle(case, wino_variant):
     assert max_rel_err(got, exp) <= WINO_RTOL
 
 
+def _random_wino_cases(count, seed):
+    """Seeded random shapes for the fused GEMM's write-out: tile blocks that
+    start mid-row and span images, rows and columns clipped by OH, OW % 4,
+    float4 and single-pixel units, channel splits (few blocks), residual."""
+    r = np.random.default_rng(seed)
+    cases = []
+    for _ in range(count):
+        n = int(r.integers(1, 5))
+        h, w = int(r.integers(3, 42)), int(r.integers(3, 42))
+        c = int(r.choice([3, 8, 16, 24, 40, 64]))
+        k = int(r.choice([8, 16, 32, 40, 72]))
+        pad = tuple(int(v) for v in r.integers(0, 3, 4))
+        if h + pad[0] + pad[1] < 3 or w + pad[2] + pad[3] < 3:
+            pad = (1, 1, 1, 1)
+        cases.append((n, c, h, w, k, pad, bool(r.integers(0, 2))))
+    return cases
+
+
+@pytest.mark.parametrize("case", _random_wino_cases(16, 7), ids=lambda c: "x".join(map(str, c[:5])))
+def test_winograd_fused_random_shapes(case, monkeypatch):
+    monkeypatch.setenv("NHIP_WINOGRAD_VARIANT", "2")  # the fused GEMM whatever the tile count
+    n, c, h, w, k, pad, with_res = case
+    rng = np.random.default_rng(hash(case) % (2 ** 32))
+    x = rng.uniform(-1, 1, (n, c, h, w)).astype(np.float32)
+    wt = workloads.he_normal(rng, (k, c, 3, 3), c * 9)
+    b = rng.normal(0, 0.05, k).astype(np.float32)
+    oh, ow = h + pad[0] + pad[1] - 2, w + pad[2] + pad[3] - 2
+    res = rng.uniform(-1, 1, (n, k, oh, ow)).astype(np.float32) if with_res else None
+    d = nhip.conv_desc(c, k, pad=pad, act=nhip.ACT_RELU, algorithm=nhip.ALGO_WINOGRAD)
+    got = host(nhip.Conv2dF32(d, wt, b).forward(dev(x), residual=dev(res) if with_res else None))
+    exp = oracle_conv(x, wt, b, (1, 1), (1, 1), pad, nhip.ACT_RELU, residual=res)
+    assert_close(got, exp, WINO_RTOL, f"winograd fused {case}")
+
+
 @pytest.mark.parametrize("algo", [nhip.ALGO_IMPLICIT_GEMM, nhip.ALGO_WINOGRAD])
 def test_config1_single_conv(algo):
     x, wt, b = workloads.conv_single(seed=0)
