@@ -668,12 +668,14 @@ bool dwpw_supported(const nhip_conv_plan* dw, const nhip_conv_plan* pw, int n, i
   // Measured on the MobileNetV2 pairs (batch 32): a lane forms one row of
   // four depthwise outputs per channel from 9 loads, twice the standalone
   // depthwise kernel's loads per output, and every output-channel slice
-  // recomputes the depthwise values.  That pays only when the depthwise
-  // output is a quarter of its input (stride 2) and the 1x1 conv's channels
-  // fit one slice: 96@112 -> 24 in 33.2 us against 43.8 us for the two
-  // layers, 144@56 -> 32 in 21.0 against 23.3; stride 1 measured slower
-  // (32@112 -> 16: 36.1 against 34.6).
-  if (!every && (dw->g.sh != 2 || pw->g.k > 32)) return false;
+  // recomputes the depthwise values.  That pays when the 1x1 conv's channels
+  // fit one slice (K <= 32) and the depthwise output is a quarter of its
+  // input (stride 2: 96@112 -> 24 in 55.2 us against ~57 us for the two
+  // layers, 144@56 -> 32 in 24.4 against ~25) or the planes are wide
+  // (stride 1, 56 columns and up: 32@112 -> 16 in 35.8 against 37.7 us,
+  // 144@56 -> 24 with residual 42.9 against 44.9); at 28 columns stride 1
+  // measured slower (192@28 -> 32: 25.2 against 22.4).
+  if (!every && (pw->g.k > 32 || (dw->g.sh != 2 && !(dw->g.sh == 1 && ow >= 56)))) return false;
   const ConvGeom& g = pw->g;
   if (pw->kind != PlanKind::ConvF32 || g.c != dw->g.c || g.kh != 1 || g.kw != 1 || g.sh != 1 || g.sw != 1 || g.pt ||
       g.pb || g.pl || g.pr || pw->algorithm != NHIP_CONV_ALGO_IMPLICIT_GEMM)
