@@ -153,8 +153,9 @@ __device__ __forceinline__ Block block_of(const FusedArgs& a, int cb) {
   Block b;
   int tb;
   // XCD-contiguous renumbering: each XCD gets a contiguous range of logical
-  // blocks, ordered (tile block, split, channel block) with the channel
-  // block fastest, so the workgroups that read the same V slices share an L2.
+  // blocks, ordered (split, tile block, channel block) with the channel
+  // block fastest, so the workgroups that read the same V slices share an L2
+  // and, with channel splits, an XCD fetches only its split's half of U.
   {
     const int total = a.nt * a.nk * a.splits;
     const int L = blockIdx.x;
@@ -162,8 +163,8 @@ __device__ __forceinline__ Block block_of(const FusedArgs& a, int cb) {
     const int logical = x * (total / kXcds) + min(x, total % kXcds) + q;
     b.kb = logical % a.nk;
     const int rest = logical / a.nk;
-    b.cs = rest % a.splits;
-    tb = rest / a.splits;
+    tb = rest % a.nt;
+    b.cs = rest / a.nt;
   }
   b.k0 = b.kb * kKB;
   b.t0 = tb * kTB;
