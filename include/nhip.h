@@ -76,6 +76,13 @@ int nhip_memcpy_d2h(void* dst, const void* src, uint64_t bytes, void* stream);
 int nhip_memcpy_d2d(void* dst, const void* src, uint64_t bytes, void* stream);
 int nhip_stream_sync(void* stream);
 
+/* NHIP_* environment switches (kernel-choice tuning and test overrides; no
+ * counterpart in the reference).  The library reads them once, at first use,
+ * into an immutable snapshot; this call re-reads the environment and
+ * publishes a new snapshot (launches already in progress keep the old one).
+ * The graph executor records a new hipGraph after a reload. */
+int nhip_reload_settings(void);
+
 /* Kernel timer (observability; the reference has no timing code at all).
  * While started, every kernel launch of this library whose name contains
  * `kernel_filter` (NULL or "" = all) is bracketed by a pair of HIP events

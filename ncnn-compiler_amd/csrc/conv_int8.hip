@@ -545,8 +545,7 @@ int launch_conv_int8(const nhip_conv_plan* p, const void* in, int in_is_i8,
   // of at most 128 output pixels); NHIP_INT8_FOOTPRINT=0 turns it off (a
   // tuning and comparison switch).
   {
-    const char* env = std::getenv("NHIP_INT8_FOOTPRINT");
-    const bool allowed = !(env && std::atoi(env) == 0);
+    const bool allowed = setting_int("NHIP_INT8_FOOTPRINT", 1) != 0;
     const int R = ow > 0 ? 128 / ow : 0;
     const int max_dy = (p->g.kh - 1) * p->g.dh, max_dx = (p->g.kw - 1) * p->g.dw;
     if (allowed && R >= 1 && p->kred_pad % 128 == 0) {
@@ -576,8 +575,8 @@ int launch_conv_int8(const nhip_conv_plan* p, const void* in, int in_is_i8,
           bk = c;
           break;
         }
-      if (const char* e = std::getenv("NHIP_INT8_FP_BK")) {
-        const int c = std::atoi(e);
+      if (setting("NHIP_INT8_FP_BK")) {
+        const int c = setting_int("NHIP_INT8_FP_BK", 0);
         if ((c == 128 || c == 192 || c == 384) && p->kred_pad % c == 0 && lds_for(c) <= kMaxLds) bk = c;
       }
       const int64_t lds = lds_for(bk);
@@ -585,13 +584,7 @@ int launch_conv_int8(const nhip_conv_plan* p, const void* in, int in_is_i8,
         const dim3 grid((unsigned)(n * ceil_div(oh, g.R)), (unsigned)(p->m_pad / bm));
 #define NHIP_FP_CASE(BM_, BK_)                                                                             \
   if (bm == BM_ && bk == BK_) {                                                                           \
-    static bool attr_set = false; /* dynamic LDS above 64 KB needs the attribute */                       \
-    if (!attr_set) {                                                                                      \
-      NHIP_TRY(check_hip(hipFuncSetAttribute(reinterpret_cast<const void*>(&conv_int8_fp_kernel<BM_, BK_>), \
-                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMaxLds),    \
-                         "hipFuncSetAttribute(conv_int8_fp)"));                                            \
-      attr_set = true;                                                                                    \
-    }                                                                                                     \
+    NHIP_TRY(ensure_dynamic_lds(reinterpret_cast<const void*>(&conv_int8_fp_kernel<BM_, BK_>), (int)kMaxLds)); \
     NHIP_LAUNCH("conv_int8_fp", (conv_int8_fp_kernel<BM_, BK_>), grid, dim3(kThreads), (unsigned)lds, s, g); \
     return check_launch("conv_int8_fp");                                                                  \
   }
@@ -608,7 +601,7 @@ int launch_conv_int8(const nhip_conv_plan* p, const void* in, int in_is_i8,
   // Tile shape: NHIP_INT8_TILE="bm,bn,bk" overrides (tuning switch, ignored
   // when not valid for the plan).
   int bm = p->m_pad % 128 == 0 ? 128 : 64, bn = 64, bk = 128;
-  if (const char* env = std::getenv("NHIP_INT8_TILE")) {
+  if (const char* env = setting("NHIP_INT8_TILE")) {
     int a = 0, b = 0, c = 0;
     if (std::sscanf(env, "%d,%d,%d", &a, &b, &c) == 3 && (a == 64 || a == 128) && (b == 64 || b == 128) &&
         (c == 128 || c == 256) && p->m_pad % a == 0 && p->kred_pad % c == 0) {

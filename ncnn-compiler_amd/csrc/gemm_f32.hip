@@ -431,7 +431,7 @@ IgemmCfg igemm_config(const nhip_conv_plan* p, int64_t npix) {
     else if (mt64 * nt128 >= target) c = {64, 128, 1};
   }
   // Tuning override NHIP_IGEMM_TILE="bm,bn" (64x64, 64x128, 128x128).
-  if (const char* env = std::getenv("NHIP_IGEMM_TILE")) {
+  if (const char* env = setting("NHIP_IGEMM_TILE")) {
     int bm = 0, bn = 0;
     if (std::sscanf(env, "%d,%d", &bm, &bn) == 2 && (bm == 64 || (bm == 128 && p->m_pad % 128 == 0)) &&
         (bn == 64 || bn == 128) && !(bm == 128 && bn == 64))

@@ -18,12 +18,14 @@
 
 #include "../../include/nhip_graph.h"
 
-extern char** environ;
-
 // Internal helpers of libnhip (csrc/runtime.hip): stream capture into a
-// hipGraph and its replay, and whether the kernel timer is recording.
+// hipGraph and its replay, whether the kernel timer is recording, and the
+// NHIP_* settings snapshot.
 namespace nhip {
 bool kernel_timer_active();
+bool stream_capturing(void* stream);
+int setting_int(const char* name, int fallback);
+uint64_t settings_generation();
 int graph_capture_begin(void* stream);
 int graph_capture_end(void* stream, void** exec);
 int graph_exec_launch(void* exec, void* stream);
@@ -1177,10 +1179,11 @@ int nhip_graph_run(nhip_graph_t g, int32_t n, const int64_t* input_shapes, const
   // microseconds of dispatch that the short late layers of a network cannot
   // hide).  Calls whose pointers change every time stay eager and record
   // nothing.  The legacy default stream cannot be captured and runs eagerly,
-  // as do runs while the kernel timer records per-launch events;
-  // NHIP_GRAPH_REPLAY=0 turns replay off.
-  const char* rep = std::getenv("NHIP_GRAPH_REPLAY");
-  if (stream == nullptr || (rep && std::atoi(rep) == 0) || nhip::kernel_timer_active())
+  // as do runs while the kernel timer records per-launch events and runs on
+  // a stream the caller is capturing itself (the launches then become part
+  // of the caller's graph); NHIP_GRAPH_REPLAY=0 turns replay off.
+  if (stream == nullptr || nhip::setting_int("NHIP_GRAPH_REPLAY", 1) == 0 || nhip::kernel_timer_active() ||
+      nhip::stream_capturing(stream))
     return run_ops(*g, n, sh, inputs, outputs, stream);
   std::ostringstream key;
   key << n;
@@ -1190,8 +1193,7 @@ int nhip_graph_run(nhip_graph_t g, int32_t n, const int64_t* input_shapes, const
   }
   for (size_t i = 0; i < g->inputs.size(); ++i) key << "|" << inputs[i];
   for (size_t j = 0; j < g->outputs.size(); ++j) key << "|" << outputs[j];
-  for (char** e = environ; e && *e; ++e)
-    if (std::strncmp(*e, "NHIP_", 5) == 0) key << "|" << *e;
+  key << "|settings " << nhip::settings_generation();
   // The blob buffers and workspace grow (free + malloc) when a call needs
   // more: a recorded plan is only replayed while they are the ones it was
   // recorded with.

@@ -58,6 +58,17 @@ class LaunchTimer {
 
 int cu_count();  // compute units of the current device (cached)
 
+// NHIP_* tuning / test switches from the settings snapshot (environment at
+// first use or at the last nhip_reload_settings); nullptr when unset.
+const char* setting(const char* name);
+int setting_int(const char* name, int fallback);
+uint64_t settings_generation();
+// Dynamic LDS above 64 KB needs a per-kernel attribute, set once per device.
+int ensure_dynamic_lds(const void* kernel, int bytes);
+// Workgroups of `kernel` resident per CU at this block size and dynamic
+// LDS (cached per device).
+int resident_blocks(const void* kernel, int threads, size_t lds);
+
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 inline int64_t round_up(int64_t a, int64_t b) { return ceil_div(a, b) * b; }
 

@@ -465,18 +465,11 @@ size_t pw_lds(int c, const PwCfg& k) {
 
 // Grid: one workgroup per (tile, slice) when they all fit on the GPU at
 // once, otherwise as many as fit, each walking an equal share of the tiles;
-// gridDim.y = slices.  The runtime's occupancy figure is cached per kernel
-// for the last LDS size asked.
+// gridDim.y = slices.  The occupancy figure is cached per device, kernel and
+// LDS size by the runtime.
 template <class Kernel>
 dim3 pw_grid(Kernel kernel, const PwArgs& a, int slices, size_t lds) {
-  static size_t last_lds = ~size_t(0);
-  static int resident = 1;
-  if (lds != last_lds) {
-    int occ = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kernel, kThreads, lds) != hipSuccess || occ < 1) occ = 1;
-    resident = occ;
-    last_lds = lds;
-  }
+  const int resident = resident_blocks(reinterpret_cast<const void*>(kernel), kThreads, lds);
   const int64_t fit = (int64_t)resident * cu_count();
   int64_t gx = a.ntiles;
   if (gx * slices > fit) {
@@ -485,8 +478,7 @@ dim3 pw_grid(Kernel kernel, const PwArgs& a, int slices, size_t lds) {
   }
   // Tuning / test override NHIP_PW_WGS=n: at most n workgroups per slice
   // (each then walks more tiles).
-  if (const char* env = std::getenv("NHIP_PW_WGS"))
-    if (const int v = std::atoi(env); v > 0) gx = std::min<int64_t>(gx, v);
+  if (const int v = setting_int("NHIP_PW_WGS", 0); v > 0) gx = std::min<int64_t>(gx, v);
   // a multiple of 8, so that blockIdx.x % 8 is the XCD (workgroups past the
   // last tile exit at once)
   return dim3((unsigned)round_up(gx, kXcds), (unsigned)slices);
@@ -495,13 +487,7 @@ dim3 pw_grid(Kernel kernel, const PwArgs& a, int slices, size_t lds) {
 template <int KT, int ACT, bool RES, int WC, bool SCALAR, int DW>
 int launch_one(const PwArgs& a, int slices, size_t lds, hipStream_t s) {
   const auto kernel = pw_conv_kernel<KT, ACT, RES, WC, SCALAR, DW>;
-  static bool attr_set = false;  // dynamic LDS above 64 KB needs the attribute
-  if (!attr_set) {
-    NHIP_TRY(check_hip(hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds),
-                       "hipFuncSetAttribute(pw_conv)"));
-    attr_set = true;
-  }
+  NHIP_TRY(ensure_dynamic_lds(reinterpret_cast<const void*>(kernel), kMaxLds));
   NHIP_LAUNCH(DW ? "dwpw_conv_f32" : "pw_conv_f32", kernel, pw_grid(kernel, a, slices, lds), dim3(kThreads), lds,
               s, a);
   return check_launch("pw_conv_f32");
@@ -568,7 +554,7 @@ bool pw_config(const nhip_conv_plan* p, int64_t np, int P, int dw, PwCfg* out) {
       break;
     }
   }
-  if (const char* env = std::getenv("NHIP_PW_CFG")) {
+  if (const char* env = setting("NHIP_PW_CFG")) {
     int kt = 0, wc = 0;
     if (std::sscanf(env, "%d,%d", &kt, &wc) == 2 && kt >= 1 && kt <= 3 && (wc == 4 || (wc == 1 && !c.scalar))) {
       c.kt = std::min(kt, dw == 2 ? 2 : 3);
@@ -587,7 +573,7 @@ bool pw_config(const nhip_conv_plan* p, int64_t np, int P, int dw, PwCfg* out) {
 bool pointwise_selected(const nhip_conv_plan* p, int n, int h, int w) {
   const ConvGeom& g = p->g;
   if (g.kh != 1 || g.kw != 1 || g.sh != 1 || g.sw != 1 || g.pt || g.pb || g.pl || g.pr) return false;
-  if (const char* env = std::getenv("NHIP_POINTWISE"))
+  if (const char* env = setting("NHIP_POINTWISE"))
     if (env[0] == '0') return false;
   PwCfg c;
   const int64_t np = (int64_t)n * h * w;
@@ -600,7 +586,7 @@ bool pointwise_selected(const nhip_conv_plan* p, int n, int h, int w) {
   // 7x7 layers of MobileNetV2), the implicit GEMM, which streams the weights
   // through its K loop, measured faster.
   const int64_t w_traffic = ceil_div(np, 256 / c.wc) * (int64_t)g.c * g.k * 4;
-  const bool forced = std::getenv("NHIP_PW_CFG") != nullptr;
+  const bool forced = setting("NHIP_PW_CFG") != nullptr;
   return forced || w_traffic <= 2 * (xb + ob);
 }
 
@@ -659,7 +645,7 @@ int launch_conv_pointwise_f32(const nhip_conv_plan* p, const float* in, const fl
 
 bool dwpw_supported(const nhip_conv_plan* dw, const nhip_conv_plan* pw, int n, int h, int w) {
   bool every = false;  // NHIP_DWPW=2: every pair the kernel can run (tests)
-  if (const char* env = std::getenv("NHIP_DWPW")) {
+  if (const char* env = setting("NHIP_DWPW")) {
     if (env[0] == '0') return false;
     every = env[0] == '2';
   }

@@ -6,11 +6,15 @@
 // quantization and the dequantize reciprocals must be the same separately
 // rounded fp32 operations as the reference's compile-time folding.
 #include <algorithm>
+#include <atomic>
 #include <cmath>
 #include <cstring>
 #include <limits>
 #include <mutex>
+#include <tuple>
 #include <vector>
+
+#include <unistd.h>
 
 #include "nhip_internal.h"
 
@@ -70,19 +74,36 @@ bool kernel_timer_active() {
 // Stream capture for the graph executor's replay (csrc/graph.cpp): the
 // executor records one run of its call plan into a hipGraph and replays the
 // instantiated graph on later calls with the same buffers.
+// A failed capture call leaves HIP's thread-local last error set; it is
+// cleared here so that the next launch check does not report it as its own
+// failure.
+bool stream_capturing(void* stream) {
+  hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(as_stream(stream), &st) != hipSuccess) {
+    (void)hipGetLastError();
+    return true;  // unknown: treat as not capturable
+  }
+  return st != hipStreamCaptureStatusNone;
+}
+
 int graph_capture_begin(void* stream) {
-  return check_hip(hipStreamBeginCapture(as_stream(stream), hipStreamCaptureModeThreadLocal),
-                   "hipStreamBeginCapture");
+  const int st = check_hip(hipStreamBeginCapture(as_stream(stream), hipStreamCaptureModeThreadLocal),
+                           "hipStreamBeginCapture");
+  if (st != NHIP_STATUS_SUCCESS) (void)hipGetLastError();
+  return st;
 }
 
 int graph_capture_end(void* stream, void** exec) {
   hipGraph_t graph = nullptr;
   *exec = nullptr;
-  NHIP_TRY(check_hip(hipStreamEndCapture(as_stream(stream), &graph), "hipStreamEndCapture"));
-  hipGraphExec_t e = nullptr;
-  const int st = check_hip(hipGraphInstantiate(&e, graph, nullptr, nullptr, 0), "hipGraphInstantiate");
-  (void)hipGraphDestroy(graph);
-  if (st == NHIP_STATUS_SUCCESS) *exec = e;
+  int st = check_hip(hipStreamEndCapture(as_stream(stream), &graph), "hipStreamEndCapture");
+  if (st == NHIP_STATUS_SUCCESS) {
+    hipGraphExec_t e = nullptr;
+    st = check_hip(hipGraphInstantiate(&e, graph, nullptr, nullptr, 0), "hipGraphInstantiate");
+    if (st == NHIP_STATUS_SUCCESS) *exec = e;
+  }
+  if (graph) (void)hipGraphDestroy(graph);
+  if (st != NHIP_STATUS_SUCCESS) (void)hipGetLastError();
   return st;
 }
 
@@ -109,6 +130,93 @@ LaunchTimer::LaunchTimer(const char* kernel) {
     return;
   }
   t.events.emplace_back(start_, stop_);
+}
+
+// ---- NHIP_* switches ----------------------------------------------------------
+// Tuning and test switches are read from the environment into an immutable
+// snapshot at the first use; nhip_reload_settings() publishes a new one.
+// Readers take the current snapshot with one atomic load, so launches never
+// call getenv and a reload never invalidates a value a reader still holds
+// (snapshots are kept until the process ends; a reload is a rare tuning or
+// test action).
+namespace {
+struct Settings {
+  std::vector<std::pair<std::string, std::string>> kv;
+  uint64_t generation = 0;
+};
+std::atomic<const Settings*> g_settings{nullptr};
+std::mutex g_settings_mu;
+
+const Settings* load_settings_locked(uint64_t generation) {
+  auto* s = new Settings;
+  s->generation = generation;
+  for (char** e = environ; e && *e; ++e) {
+    if (std::strncmp(*e, "NHIP_", 5) != 0) continue;
+    const char* eq = std::strchr(*e, '=');
+    if (eq) s->kv.emplace_back(std::string(*e, (size_t)(eq - *e)), std::string(eq + 1));
+  }
+  return s;
+}
+
+const Settings* settings_snapshot() {
+  const Settings* s = g_settings.load(std::memory_order_acquire);
+  if (s) return s;
+  std::lock_guard<std::mutex> lock(g_settings_mu);
+  s = g_settings.load(std::memory_order_acquire);
+  if (!s) {
+    s = load_settings_locked(1);
+    g_settings.store(s, std::memory_order_release);
+  }
+  return s;
+}
+}  // namespace
+
+const char* setting(const char* name) {
+  for (const auto& kv : settings_snapshot()->kv)
+    if (kv.first == name) return kv.second.c_str();
+  return nullptr;
+}
+
+int setting_int(const char* name, int fallback) {
+  const char* v = setting(name);
+  return v && *v ? std::atoi(v) : fallback;
+}
+
+uint64_t settings_generation() { return settings_snapshot()->generation; }
+
+// ---- per-device kernel attributes and occupancy -----------------------------
+namespace {
+std::mutex g_attr_mu;
+std::vector<std::tuple<int, const void*>> g_attr_done;
+std::vector<std::tuple<int, const void*, int, size_t, int>> g_occupancy;
+}  // namespace
+
+int ensure_dynamic_lds(const void* kernel, int bytes) {
+  int dev = 0;
+  NHIP_TRY(check_hip(hipGetDevice(&dev), "hipGetDevice"));
+  std::lock_guard<std::mutex> lock(g_attr_mu);
+  for (const auto& d : g_attr_done)
+    if (std::get<0>(d) == dev && std::get<1>(d) == kernel) return ok();
+  NHIP_TRY(check_hip(hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, bytes),
+                     "hipFuncSetAttribute(max dynamic LDS)"));
+  g_attr_done.emplace_back(dev, kernel);
+  return ok();
+}
+
+int resident_blocks(const void* kernel, int threads, size_t lds) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 1;
+  std::lock_guard<std::mutex> lock(g_attr_mu);
+  for (const auto& o : g_occupancy)
+    if (std::get<0>(o) == dev && std::get<1>(o) == kernel && std::get<2>(o) == threads && std::get<3>(o) == lds)
+      return std::get<4>(o);
+  int occ = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kernel, threads, lds) != hipSuccess || occ < 1) {
+    (void)hipGetLastError();
+    occ = 1;
+  }
+  g_occupancy.emplace_back(dev, kernel, threads, lds, occ);
+  return occ;
 }
 
 int cu_count() {
@@ -258,6 +366,13 @@ int nhip_init(int32_t device) {
   NHIP_TRY(check_hip(hipSetDevice(device), "hipSetDevice"));
   NHIP_TRY(check_hip(hipFree(nullptr), "device initialisation"));
   cu_count();
+  return ok();
+}
+
+int nhip_reload_settings(void) {
+  std::lock_guard<std::mutex> lock(nhip::g_settings_mu);
+  const nhip::Settings* cur = nhip::g_settings.load(std::memory_order_acquire);
+  nhip::g_settings.store(nhip::load_settings_locked(cur ? cur->generation + 1 : 1), std::memory_order_release);
   return ok();
 }
 

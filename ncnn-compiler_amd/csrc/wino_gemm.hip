@@ -223,7 +223,7 @@ bool cfg_valid(const WinoGemmCfg& c, int m_pad, int c_pad, int t_pad) {
 WinoGemmCfg wino_gemm_config(int m_pad, int c_pad, int t_pad) {
   // Tuning override: NHIP_WINO_GEMM="bm,bn,bk,splits" (ignored when not
   // valid for the shape).
-  if (const char* env = std::getenv("NHIP_WINO_GEMM")) {
+  if (const char* env = setting("NHIP_WINO_GEMM")) {
     WinoGemmCfg c{};
     if (std::sscanf(env, "%d,%d,%d,%d", &c.bm, &c.bn, &c.bk, &c.splits) == 4 && cfg_valid(c, m_pad, c_pad, t_pad))
       return c;

@@ -36,8 +36,7 @@ uint64_t wino_gemm_out_parts_bytes(const nhip_conv_plan* p, int n, int oh, int o
 // 256 tiles up (on MI355X it measures faster there; with fewer tiles its
 // channel-split partial sums cost more than the M round trip saves).
 static int variant_requested() {
-  const char* env = std::getenv("NHIP_WINOGRAD_VARIANT");
-  return (env && *env) ? std::atoi(env) : 0;
+  return setting_int("NHIP_WINOGRAD_VARIANT", 0);
 }
 
 static bool fused_selected(const nhip_conv_plan* p, int n, int oh, int ow) {

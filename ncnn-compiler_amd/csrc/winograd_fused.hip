@@ -431,14 +431,7 @@ __global__ void wino_fused_reduce(const float* __restrict__ part, int splits, in
 
 template <int ACT, bool FINAL>
 int launch_kernel(const FusedArgs& a, int64_t blocks, hipStream_t s) {
-  static bool attr_set = false;  // dynamic LDS above 64 KB needs the attribute
-  if (!attr_set) {
-    NHIP_TRY(check_hip(
-        hipFuncSetAttribute(reinterpret_cast<const void*>(&wino_fused_kernel<ACT, FINAL>),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes),
-        "hipFuncSetAttribute(wino_fused)"));
-    attr_set = true;
-  }
+  NHIP_TRY(ensure_dynamic_lds(reinterpret_cast<const void*>(&wino_fused_kernel<ACT, FINAL>), kLdsBytes));
   NHIP_LAUNCH("wino_fused", (wino_fused_kernel<ACT, FINAL>), dim3((unsigned)blocks), dim3(kThreads),
               kLdsBytes, s, a);
   return check_launch("wino_fused");

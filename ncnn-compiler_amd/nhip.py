@@ -34,7 +34,7 @@ ACT_NONE, ACT_RELU, ACT_SIGMOID = 0, 1, 4
 EXPORTS = (
     "nhip_init", "nhip_device_count", "nhip_last_error", "nhip_malloc",
     "nhip_free", "nhip_memcpy_h2d", "nhip_memcpy_d2h", "nhip_memcpy_d2d",
-    "nhip_stream_sync", "nhip_timer_start", "nhip_timer_stop",
+    "nhip_stream_sync", "nhip_reload_settings", "nhip_timer_start", "nhip_timer_stop",
     "nhip_conv_output_shape", "nhip_conv2d_f32_create",
     "nhip_conv2d_workspace_size", "nhip_conv2d_f32_forward",
     "nhip_conv2d_int8_create", "nhip_conv2d_int8_forward",
@@ -101,6 +101,7 @@ def load():
         "nhip_memcpy_d2h": [_P, _P, u64, _P],
         "nhip_memcpy_d2d": [_P, _P, u64, _P],
         "nhip_stream_sync": [_P],
+        "nhip_reload_settings": [],
         "nhip_timer_start": [ctypes.c_char_p],
         "nhip_timer_stop": [ctypes.POINTER(u64), ctypes.POINTER(ctypes.c_double)],
         "nhip_conv_output_shape": [D, i32, i32, ctypes.POINTER(i32), ctypes.POINTER(i32)],
@@ -164,6 +165,12 @@ def _torch():
 
 def init(device: int = 0) -> None:
     check(load().nhip_init(device))
+
+
+def reload_settings() -> None:
+    """Re-read the NHIP_* tuning / test switches from the environment (the
+    library reads them once, at first use)."""
+    check(load().nhip_reload_settings())
 
 
 def timer_start(kernel_filter: str = "") -> None:

@@ -117,13 +117,13 @@ WINO_CASES = [
 
 
 @pytest.fixture(params=["auto", "1", "2"])
-def wino_variant(request, monkeypatch):
+def wino_variant(request, nhip_env):
     """Winograd implementations: the default per-shape choice (auto), the
     three-kernel path (1) and the GEMM with the output transform fused (2)."""
     if request.param == "auto":
-        monkeypatch.delenv("NHIP_WINOGRAD_VARIANT", raising=False)
+        nhip_env.delenv("NHIP_WINOGRAD_VARIANT", raising=False)
     else:
-        monkeypatch.setenv("NHIP_WINOGRAD_VARIANT", request.param)
+        nhip_env.setenv("NHIP_WINOGRAD_VARIANT", request.param)
     return request.param
 
 
@@ -159,8 +159,8 @@ def _random_wino_cases(count, seed):
 
 
 @pytest.mark.parametrize("case", _random_wino_cases(16, 7), ids=lambda c: "x".join(map(str, c[:5])))
-def test_winograd_fused_random_shapes(case, monkeypatch):
-    monkeypatch.setenv("NHIP_WINOGRAD_VARIANT", "2")  # the fused GEMM whatever the tile count
+def test_winograd_fused_random_shapes(case, nhip_env):
+    nhip_env.setenv("NHIP_WINOGRAD_VARIANT", "2")  # the fused GEMM whatever the tile count
     n, c, h, w, k, pad, with_res = case
     rng = np.random.default_rng(hash(case) % (2 ** 32))
     x = rng.uniform(-1, 1, (n, c, h, w)).astype(np.float32)
@@ -214,26 +214,38 @@ def test_resnet_stage_n2_matches_oracle(stage, algo, wino_variant):
 
 
 @pytest.mark.parametrize("stage", workloads.RESNET18_STAGES, ids=lambda s: f"{s[0]}x{s[1]}")
-def test_resnet_stage_full_batch(stage):
-    """Batch 32 (the bench shape): images are independent ncnn blobs, so the
-    oracle is run on sampled images; Winograd and implicit GEMM must also
-    agree on every image."""
+def test_resnet_stage_full_batch(stage, nhip_env):
+    """Batch 32, the bench's exact plans (default per-shape Winograd choice,
+    workspace passed the way bench.py passes it): every one of the 32 images
+    is checked against the oracle, for Winograd and the implicit GEMM."""
+    nhip_env.delenv("NHIP_WINOGRAD_VARIANT", raising=False)
     c, hw = stage
     x, w1, b1, w2, b2 = workloads.resnet_stage(c, hw, n=32, seed=0)
-    wino = run_stage(c, hw, 32, nhip.ALGO_WINOGRAD, x, w1, b1, w2, b2)
+    exp = oracle_stage(x, w1, b1, w2, b2)
+    d = nhip.conv_desc(c, c, act=nhip.ACT_RELU, algorithm=nhip.ALGO_WINOGRAD)
+    c1, c2 = nhip.Conv2dF32(d, w1, b1), nhip.Conv2dF32(d, w2, b2)
+    ws = torch.empty(max(c1.workspace_size(32, hw, hw), c2.workspace_size(32, hw, hw)),
+                     dtype=torch.uint8, device="cuda")
+    xd = dev(x)
+    y = torch.empty_like(xd)
+    out = torch.empty_like(xd)
+    for rep in range(2):  # the second pass reuses the workspace and outputs, as bench steps do
+        c1.forward(xd, out=y, workspace=ws)
+        c2.forward(y, residual=xd, out=out, workspace=ws)
+        wino = host(out)
+        for i in range(32):
+            assert_close(wino[i:i + 1], exp[i:i + 1], WINO_RTOL, f"wino image {i} pass {rep}")
+        assert max_rel_err(wino, exp) <= WINO_RTOL
     igemm = run_stage(c, hw, 32, nhip.ALGO_IMPLICIT_GEMM, x, w1, b1, w2, b2)
-    assert_close(wino, igemm, WINO_RTOL, f"wino vs igemm {stage}")
-    for i in (0, 31):
-        exp = oracle_stage(x[i:i + 1], w1, b1, w2, b2)
-        assert_close(wino[i:i + 1], exp, WINO_RTOL, f"wino image {i}")
-        assert_close(igemm[i:i + 1], exp, IGEMM_RTOL, f"igemm image {i}")
+    for i in range(32):
+        assert_close(igemm[i:i + 1], exp[i:i + 1], IGEMM_RTOL, f"igemm image {i}")
 
 
 @pytest.mark.parametrize("variant", ["2", "1"])
-def test_batch_is_independent_images(variant, monkeypatch):  # 1 = three-kernel path, 2 = fused
+def test_batch_is_independent_images(variant, nhip_env):  # 1 = three-kernel path, 2 = fused
     """The [N,C,H,W] batch equals N single-image calls (the reference ABI),
     bit for bit for a fixed kernel variant."""
-    monkeypatch.setenv("NHIP_WINOGRAD_VARIANT", variant)
+    nhip_env.setenv("NHIP_WINOGRAD_VARIANT", variant)
     c, k = 32, 32
     x = RNG.uniform(-1, 1, (4, c, 10, 10)).astype(np.float32)
     wt = workloads.he_normal(RNG, (k, c, 3, 3), c * 9)
@@ -245,8 +257,8 @@ def test_batch_is_independent_images(variant, monkeypatch):  # 1 = three-kernel 
             np.testing.assert_array_equal(one, whole[i:i + 1])
 
 
-def test_empty_batch_and_workspace_errors(monkeypatch):
-    monkeypatch.delenv("NHIP_WINOGRAD_VARIANT", raising=False)  # default path needs a workspace
+def test_empty_batch_and_workspace_errors(nhip_env):
+    nhip_env.delenv("NHIP_WINOGRAD_VARIANT", raising=False)  # default path needs a workspace
     c, k = 16, 16
     wt = workloads.he_normal(RNG, (k, c, 3, 3), c * 9)
     conv = nhip.Conv2dF32(nhip.conv_desc(c, k, bias=False, algorithm=nhip.ALGO_WINOGRAD), wt)

@@ -33,11 +33,11 @@ def _gpu():
 
 
 @pytest.fixture(autouse=True)
-def _every_pair(monkeypatch):
+def _every_pair(nhip_env):
     """NHIP_DWPW=2: fuse every pair the kernel can run; by default the library
     fuses only the stride-2 pairs with up to 32 output channels, where it
     measured faster than the two layers."""
-    monkeypatch.setenv("NHIP_DWPW", "2")
+    nhip_env.setenv("NHIP_DWPW", "2")
 
 
 def dev(a):
@@ -115,11 +115,11 @@ def test_dw_pw_fused_matches_separate_and_oracle(case):
 
 @pytest.mark.parametrize("stride", [1, 2])
 @pytest.mark.parametrize("cfg", ["1,1", "2,1", "3,1", "1,4", "2,4", "3,4"])
-def test_dw_pw_every_configuration(cfg, stride, monkeypatch):
+def test_dw_pw_every_configuration(cfg, stride, nhip_env):
     """Each (KT, WC) forced through NHIP_PW_CFG (stride 2 caps KT at 2), with
     C = 72: five 16-channel groups, split 2, 1, 1, 1 over four waves, the
     last group partial."""
-    monkeypatch.setenv("NHIP_PW_CFG", cfg)
+    nhip_env.setenv("NHIP_PW_CFG", cfg)
     check_pair(2, 72, 12, 16, 70, stride, R, N0, True)
 
 
@@ -139,7 +139,7 @@ def test_dw_pw_unsupported_shapes():
     assert not nhip.dwconv_pw_supported(dw, pw2, 1, 8, 8)
 
 
-def test_graph_executor_fuses_depthwise_into_project(monkeypatch):
+def test_graph_executor_fuses_depthwise_into_project(nhip_env):
     """A graph with two dw -> 1x1 pairs (the first feeding a residual add)
     runs each pair as one launch, bit-identical to NHIP_DWPW=0; by default
     only the stride-2 pair with 24 output channels is fused."""
@@ -160,12 +160,12 @@ def test_graph_executor_fuses_depthwise_into_project(monkeypatch):
     nhip.timer_start("dwpw")
     fused = host(g.run(x)[0])
     assert nhip.timer_stop()[0] == 2
-    monkeypatch.setenv("NHIP_DWPW", "0")
+    nhip_env.setenv("NHIP_DWPW", "0")
     nhip.timer_start("dwpw")
     separate = host(g.run(x)[0])
     assert nhip.timer_stop()[0] == 0
     np.testing.assert_array_equal(fused, separate)
-    monkeypatch.delenv("NHIP_DWPW")
+    nhip_env.delenv("NHIP_DWPW")
     nhip.timer_start("dwpw")
     default = host(g.run(x)[0])
     assert nhip.timer_stop()[0] == 1

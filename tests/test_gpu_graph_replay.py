@@ -41,20 +41,20 @@ def mobilenet_graph():
     return nhip.Graph(m.param_text(), bytes(m.payload))
 
 
-def eager(g, x, monkeypatch):
-    monkeypatch.setenv("NHIP_GRAPH_REPLAY", "0")
+def eager(g, x, nhip_env):
+    nhip_env.setenv("NHIP_GRAPH_REPLAY", "0")
     out = g.run(x)[0].clone()
     torch.cuda.synchronize()
-    monkeypatch.delenv("NHIP_GRAPH_REPLAY")
+    nhip_env.delenv("NHIP_GRAPH_REPLAY")
     return out
 
 
-def test_replay_matches_eager_on_every_call(monkeypatch):
-    monkeypatch.delenv("NHIP_GRAPH_REPLAY", raising=False)
+def test_replay_matches_eager_on_every_call(nhip_env):
+    nhip_env.delenv("NHIP_GRAPH_REPLAY", raising=False)
     g = mobilenet_graph()
     rng = np.random.default_rng(1)
     x = torch.from_numpy(rng.uniform(-1, 1, (2, 3, 224, 224)).astype(np.float32)).cuda()
-    ref = eager(g, x, monkeypatch)
+    ref = eager(g, x, nhip_env)
     out = [torch.empty_like(ref)]
     for call in range(6):  # call 0: eager, 1: eager + recorded, 2..5: replays
         out[0].fill_(float("nan"))
@@ -67,7 +67,7 @@ def test_replay_matches_eager_on_every_call(monkeypatch):
         del scratch
     # new input values in the same buffer: the replay reads them
     x.copy_(torch.from_numpy(rng.uniform(-1, 1, (2, 3, 224, 224)).astype(np.float32)))
-    ref2 = eager(g, x, monkeypatch)
+    ref2 = eager(g, x, nhip_env)
     assert not torch.equal(ref2, ref)
     for _ in range(3):
         g.run(x, out=out)
@@ -84,11 +84,11 @@ def test_replay_matches_eager_on_every_call(monkeypatch):
     assert torch.equal(out[0], ref2)
 
 
-def test_default_stream_runs_eagerly_and_correct(monkeypatch):
-    monkeypatch.delenv("NHIP_GRAPH_REPLAY", raising=False)
+def test_default_stream_runs_eagerly_and_correct(nhip_env):
+    nhip_env.delenv("NHIP_GRAPH_REPLAY", raising=False)
     g = mobilenet_graph()
     x = torch.from_numpy(np.random.default_rng(5).uniform(-1, 1, (2, 3, 224, 224)).astype(np.float32)).cuda()
-    ref = eager(g, x, monkeypatch)
+    ref = eager(g, x, nhip_env)
     out = [torch.empty_like(ref)]
     torch.cuda.synchronize()
     with torch.cuda.stream(torch.cuda.default_stream()):
@@ -98,46 +98,46 @@ def test_default_stream_runs_eagerly_and_correct(monkeypatch):
     assert torch.equal(out[0], ref)
 
 
-def test_setting_change_rerecords(monkeypatch):
+def test_setting_change_rerecords(nhip_env):
     """NHIP_DWPW picks fused or separate depthwise -> 1x1 kernels: after a
     recorded plan exists, changing it must give that setting's eager result."""
-    monkeypatch.delenv("NHIP_GRAPH_REPLAY", raising=False)
+    nhip_env.delenv("NHIP_GRAPH_REPLAY", raising=False)
     g = mobilenet_graph()
     x = torch.from_numpy(np.random.default_rng(2).uniform(-1, 1, (2, 3, 224, 224)).astype(np.float32)).cuda()
     out = [torch.empty((2, 1000), device="cuda")]
     for setting in ("1", "0", "2", "1"):
-        monkeypatch.setenv("NHIP_DWPW", setting)
-        ref = eager(g, x, monkeypatch)
+        nhip_env.setenv("NHIP_DWPW", setting)
+        ref = eager(g, x, nhip_env)
         for _ in range(3):
             g.run(x, out=out)
             torch.cuda.synchronize()
             assert torch.equal(out[0], ref), f"NHIP_DWPW={setting}"
 
 
-def test_changing_outputs_stay_eager_and_correct(monkeypatch):
+def test_changing_outputs_stay_eager_and_correct(nhip_env):
     """Fresh output tensors on every call (no out=) never reuse a recorded
     plan with stale pointers."""
-    monkeypatch.delenv("NHIP_GRAPH_REPLAY", raising=False)
+    nhip_env.delenv("NHIP_GRAPH_REPLAY", raising=False)
     g = mobilenet_graph()
     x = torch.from_numpy(np.random.default_rng(3).uniform(-1, 1, (2, 3, 224, 224)).astype(np.float32)).cuda()
-    ref = eager(g, x, monkeypatch)
+    ref = eager(g, x, nhip_env)
     keep = [g.run(x)[0] for _ in range(4)]  # kept alive: every call has new output pointers
     torch.cuda.synchronize()
     for o in keep:
         assert torch.equal(o, ref)
 
 
-def test_buffers_grown_by_a_larger_batch_invalidate_the_recorded_plan(monkeypatch):
+def test_buffers_grown_by_a_larger_batch_invalidate_the_recorded_plan(nhip_env):
     """A recorded plan uses the executor's blob buffers; a call with a larger
     batch reallocates them, and the next call with the recorded key must not
     replay the plan over the freed buffers."""
-    monkeypatch.delenv("NHIP_GRAPH_REPLAY", raising=False)
+    nhip_env.delenv("NHIP_GRAPH_REPLAY", raising=False)
     g = mobilenet_graph()
     rng = np.random.default_rng(4)
     xa = torch.from_numpy(rng.uniform(-1, 1, (2, 3, 224, 224)).astype(np.float32)).cuda()
     xb = torch.from_numpy(rng.uniform(-1, 1, (4, 3, 224, 224)).astype(np.float32)).cuda()
-    ref_a = eager(g, xa, monkeypatch)
-    ref_b = eager(g, xb, monkeypatch)  # the executor's buffers now hold batch 4
+    ref_a = eager(g, xa, nhip_env)
+    ref_b = eager(g, xb, nhip_env)  # the executor's buffers now hold batch 4
     g2 = mobilenet_graph()
     out_a, out_b = [torch.empty_like(ref_a)], [torch.empty_like(ref_b)]
     for _ in range(3):  # records and replays batch 2

@@ -8,6 +8,7 @@ import pytest
 torch = pytest.importorskip("torch")
 
 import graphs  # noqa: E402
+import ncnn_format  # noqa: E402
 import nhip  # noqa: E402
 from numerics import assert_close, max_rel_err  # noqa: E402
 from oracle_graphs import oracle_forward  # noqa: E402
@@ -38,3 +39,36 @@ def test_mobilenetv2_matches_oracle(n):
     assert max_rel_err(got, exp["fc"]) <= 1e-4
     # same top-1 class per image as the oracle
     np.testing.assert_array_equal(got.argmax(1), exp["fc"].argmax(1))
+
+
+@pytest.mark.parametrize("n", [2, 32])
+def test_native_executor_mobilenetv2_matches_oracle(n):
+    """The path bench.py times: the graph from its .param/.bin form through
+    the native executor (nhip_graph_run) with its default lowering
+    (depthwise->1x1 fusion, pointwise kernel choice by batch size).  On a
+    non-default stream the second identical call is recorded into a hipGraph
+    and the third replays it; each result is checked against the oracle."""
+    layers = graphs.mobilenetv2_layers(seed=0)
+    m = ncnn_format.from_layer_list(layers)
+    g = nhip.Graph(m.param_text(), bytes(m.payload))
+    x = np.random.default_rng(0).uniform(-1, 1, (n, 3, 224, 224)).astype(np.float32)
+    exp = oracle_forward(layers, x)["fc"]
+    xd = torch.from_numpy(x).cuda()
+
+    def check(got, what):
+        torch.cuda.synchronize()
+        got = got.cpu().numpy().reshape(n, -1)
+        assert_close(got, exp, 1e-4, f"native mobilenetv2 n={n} {what}")
+        assert max_rel_err(got, exp) <= 1e-4, what
+        np.testing.assert_array_equal(got.argmax(1), exp.argmax(1))
+
+    check(g.run(xd)[0], "default stream")
+    out = [torch.empty((n, 1000), device="cuda").fill_(float("nan"))]
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        for what in ("eager", "record", "replay", "replay 2"):
+            out[0].fill_(float("nan"))
+            g.run(xd, out=out, stream=s)
+            s.synchronize()
+            check(out[0], what)
+    g.close()

@@ -98,11 +98,11 @@ CASES = [
 
 
 @pytest.mark.parametrize("case", CASES, ids=lambda c: "x".join(map(str, c[:5])) + ("r" if c[5] else "") + f"a{c[6]}")
-def test_pointwise_matches_oracle(case, monkeypatch):
+def test_pointwise_matches_oracle(case, nhip_env):
     """Cases with an eighth entry force that configuration (NHIP_PW_CFG):
     the library leaves those shapes to the implicit GEMM by default."""
     if len(case) > 7:
-        monkeypatch.setenv("NHIP_PW_CFG", case[7])
+        nhip_env.setenv("NHIP_PW_CFG", case[7])
     run(*case[:7])
 
 
@@ -111,7 +111,7 @@ def test_pointwise_matches_oracle(case, monkeypatch):
                                   (2, 48, 10, 10, 96, False, nhip.ACT_NONE),
                                   (2, 16, 8, 8, 200, False, nhip.ACT_RELU)],
                          ids=["res", "kt6", "slices"])
-def test_pointwise_persistent_walk(case, wgs, monkeypatch):
+def test_pointwise_persistent_walk(case, wgs, nhip_env):
     """A few workgroups walking every tile: the chunk prefetch crosses tile
     boundaries, and the results equal the one-tile-per-workgroup launch bit
     for bit (the per-pixel arithmetic does not depend on the walk)."""
@@ -122,7 +122,7 @@ def test_pointwise_persistent_walk(case, wgs, monkeypatch):
     r = dev(RNG.uniform(-1, 1, (n, k, h, w)).astype(np.float32)) if res else None
     conv = nhip.Conv2dF32(nhip.conv_desc(c, k, (1, 1), (1, 1), (1, 1), (0, 0, 0, 0), act=act), wt, b)
     wide = host(conv.forward(x, residual=r))
-    monkeypatch.setenv("NHIP_PW_WGS", wgs)
+    nhip_env.setenv("NHIP_PW_WGS", wgs)
     narrow = host(conv.forward(x, residual=r))
     np.testing.assert_array_equal(narrow, wide)
     exp = oracle(host(x), wt, b, act, host(r) if res else None)
@@ -135,14 +135,14 @@ CFGS = ["1,1", "2,1", "3,1", "1,4", "2,4", "3,4"]
 @pytest.mark.parametrize("res", [False, True], ids=["plain", "res"])
 @pytest.mark.parametrize("cfg", CFGS)
 @pytest.mark.parametrize("hw", [(6, 8), (5, 5)], ids=["aligned", "unaligned"])
-def test_pointwise_every_instantiation(cfg, res, hw, monkeypatch):
+def test_pointwise_every_instantiation(cfg, res, hw, nhip_env):
     """Each kernel forced through NHIP_PW_CFG="kt,wc" (16*kt output channels
     per slice, the channels of a tile over wc waves; unaligned rows always
     take wc = 4), with K = 70 (several slices, a partial last block) and
     C = 72 (five chunks: the four waves get 2, 1, 1, 1)."""
     if hw == (5, 5) and cfg.endswith(",1"):
         pytest.skip("unaligned pixel rows have no one-wave split")
-    monkeypatch.setenv("NHIP_PW_CFG", cfg)
+    nhip_env.setenv("NHIP_PW_CFG", cfg)
     run(3, 72, hw[0], hw[1], 70, res, nhip.ACT_RELU)
 
 
@@ -157,7 +157,7 @@ def test_pointwise_no_bias_and_batch_independence():
         np.testing.assert_array_equal(host(conv.forward(dev(x[i:i + 1]))), whole[i:i + 1])
 
 
-def test_pointwise_off_switch_and_ineligible_shapes(monkeypatch):
+def test_pointwise_off_switch_and_ineligible_shapes(nhip_env):
     """NHIP_POINTWISE=0 routes 1x1 layers to the implicit GEMM (the tuning
     comparison); both agree within the budget.  Shapes the kernel does not
     take go to the implicit GEMM: stride 2, and unaligned pixel rows with
@@ -169,12 +169,12 @@ def test_pointwise_off_switch_and_ineligible_shapes(monkeypatch):
     nhip.timer_start("pw_conv")
     a = host(nhip.Conv2dF32(d, wt).forward(dev(x)))
     assert nhip.timer_stop()[0] == 1
-    monkeypatch.setenv("NHIP_POINTWISE", "0")
+    nhip_env.setenv("NHIP_POINTWISE", "0")
     nhip.timer_start("pw_conv")
     b = host(nhip.Conv2dF32(d, wt).forward(dev(x)))
     assert nhip.timer_stop()[0] == 0
     assert_close(a, b, RTOL, "pointwise vs implicit GEMM")
-    monkeypatch.delenv("NHIP_POINTWISE")
+    nhip_env.delenv("NHIP_POINTWISE")
     for c, hw, stride in ((32, 8, 2), (48, 7, 1)):
         x = dev(RNG.uniform(-1, 1, (n, c, hw, hw)).astype(np.float32))
         wt = workloads.he_normal(RNG, (k, c, 1, 1), c)
