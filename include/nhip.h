@@ -144,6 +144,19 @@ int nhip_conv2d_f32_forward(nhip_conv_t plan, const float* input,
                             const float* residual, float* output, int32_t n,
                             int32_t h, int32_t w, void* workspace,
                             uint64_t workspace_bytes, void* stream);
+/* No counterpart in the reference: nhip_conv2d_f32_forward for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc).  Same kernels and results; the
+ * scratch is a static 64 MiB device array per GPU (held until the process
+ * ends) instead of a workspace argument, and the call allocates nothing.  A
+ * batch needing more scratch than that (nhip_conv2d_workspace_size) returns
+ * NHIP_STATUS_OUTPUT_CAPACITY_INSUFFICIENT.  Every call on a GPU shares that
+ * GPU's array: calls that overlap on one GPU (other threads, other streams)
+ * race. */
+int nhip_conv2d_f32_forward_noalloc(nhip_conv_t plan, const float* input,
+                                    const float* residual, float* output,
+                                    int32_t n, int32_t h, int32_t w,
+                                    void* stream);
 
 /* a2 — int8 Convolution (NCNNToTosa.cpp:1136-1315).  weight: host
  * [num_output][C][kh][kw], int8 when weight_is_i8 (used as stored), else fp32

@@ -219,6 +219,34 @@ int resident_blocks(const void* kernel, int threads, size_t lds) {
   return occ;
 }
 
+// ---- static scratch of nhip_conv2d_f32_forward_noalloc ----------------------
+// Device memory for callers that cannot allocate: one array per GPU, set up
+// once per device.  In host code `scratch` names a host-side stand-in, so the
+// device address is taken with hipGetSymbolAddress (per device, with that
+// device current) and only that address is handed to kernels.
+constexpr uint64_t kScratchBytes = uint64_t(64) << 20;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+namespace {
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[64];
+}  // namespace
+
+int scratch_address(void** out) {
+  *out = nullptr;
+  int dev = 0;
+  NHIP_TRY(check_hip(hipGetDevice(&dev), "hipGetDevice"));
+  if (dev < 0 || dev >= 64) return fail(NHIP_STATUS_UNSUPPORTED, "static scratch: device index above 63");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    NHIP_TRY(check_hip(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)"));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return ok();
+}
+
 int cu_count() {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
@@ -366,6 +394,8 @@ int nhip_init(int32_t device) {
   NHIP_TRY(check_hip(hipSetDevice(device), "hipSetDevice"));
   NHIP_TRY(check_hip(hipFree(nullptr), "device initialisation"));
   cu_count();
+  void* scratch_dev = nullptr;  // the static scratch's address on this device
+  NHIP_TRY(scratch_address(&scratch_dev));
   return ok();
 }
 
@@ -560,6 +590,25 @@ int nhip_conv2d_f32_forward(nhip_conv_t p, const float* input, const float* resi
     return launch_conv_igemm_f32(p, in, res, out, nb, h, w, oh, ow, workspace, workspace_bytes,
                                  as_stream(stream));
   });
+}
+
+int nhip_conv2d_f32_forward_noalloc(nhip_conv_t p, const float* input, const float* residual, float* output,
+                                    int32_t n, int32_t h, int32_t w, void* stream) {
+  int oh = 0, ow = 0;
+  NHIP_TRY(check_forward(p, input, output, n, h, w, &oh, &ow));
+  if (p->kind != PlanKind::ConvF32)
+    return fail(NHIP_STATUS_CONSTRAINT_VIOLATION, "conv2d_f32_forward_noalloc: not an fp32 conv plan");
+  if (n == 0) return ok();
+  uint64_t need = 0;
+  NHIP_TRY(nhip_conv2d_workspace_size(p, n, h, w, &need));
+  if (need > kScratchBytes)
+    return fail(NHIP_STATUS_OUTPUT_CAPACITY_INSUFFICIENT,
+                "conv2d_f32_forward_noalloc: this batch needs " + std::to_string(need) +
+                    " bytes of scratch; the static scratch holds " + std::to_string(kScratchBytes) +
+                    " (use nhip_conv2d_f32_forward with a workspace, or a smaller batch)");
+  void* ws = nullptr;
+  NHIP_TRY(scratch_address(&ws));
+  return nhip_conv2d_f32_forward(p, input, residual, output, n, h, w, ws, kScratchBytes, stream);
 }
 
 int nhip_conv2d_int8_create(const nhip_conv_desc* d, const void* weight, int32_t weight_is_i8, const float* bias,

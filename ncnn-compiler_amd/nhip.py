@@ -36,7 +36,7 @@ EXPORTS = (
     "nhip_free", "nhip_memcpy_h2d", "nhip_memcpy_d2h", "nhip_memcpy_d2d",
     "nhip_stream_sync", "nhip_reload_settings", "nhip_timer_start", "nhip_timer_stop",
     "nhip_conv_output_shape", "nhip_conv2d_f32_create",
-    "nhip_conv2d_workspace_size", "nhip_conv2d_f32_forward",
+    "nhip_conv2d_workspace_size", "nhip_conv2d_f32_forward", "nhip_conv2d_f32_forward_noalloc",
     "nhip_conv2d_int8_create", "nhip_conv2d_int8_forward",
     "nhip_dwconv2d_f32_create", "nhip_dwconv2d_f32_forward",
     "nhip_dwconv2d_pw_f32_supported", "nhip_dwconv2d_pw_f32_forward",
@@ -108,6 +108,7 @@ def load():
         "nhip_conv2d_f32_create": [D, _P, _P, ctypes.POINTER(_P)],
         "nhip_conv2d_workspace_size": [_P, i32, i32, i32, ctypes.POINTER(u64)],
         "nhip_conv2d_f32_forward": [_P, _P, _P, _P, i32, i32, i32, _P, u64, _P],
+        "nhip_conv2d_f32_forward_noalloc": [_P, _P, _P, _P, i32, i32, i32, _P],
         "nhip_conv2d_int8_create": [D, _P, i32, _P, _P, i32, f32, f32, ctypes.POINTER(_P)],
         "nhip_conv2d_int8_forward": [_P, _P, i32, _P, i32, i32, i32, _P, u64, _P],
         "nhip_dwconv2d_f32_create": [D, _P, _P, ctypes.POINTER(_P)],

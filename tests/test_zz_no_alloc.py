@@ -1,0 +1,86 @@
+"""The entry point that allocates nothing: nhip_conv2d_f32_forward_noalloc
+(static per-GPU scratch) against nhip_conv2d_f32_forward with a caller
+workspace, through the C ABI.  Both run the same kernels, so the results are
+identical bit for bit; two calls in a row, the second smaller, must both
+match (the scratch keeps the first call's contents)."""
+import ctypes
+
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+
+import nhip  # noqa: E402
+import workloads  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+
+SCRATCH_BYTES = 64 << 20
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    assert torch.cuda.is_available(), "GPU tests need a HIP device"
+    nhip.init(0)
+
+
+def _plan(c, k, algo, stride=1):
+    rng = np.random.default_rng([c, k, algo, stride])
+    w = workloads.he_normal(rng, (k, c, 3, 3), c * 9)
+    b = (rng.standard_normal(k) * 0.05).astype(np.float32)
+    d = nhip.conv_desc(c, k, stride=(stride, stride), act=nhip.ACT_RELU, algorithm=algo)
+    return nhip.Conv2dF32(d, w, b)
+
+
+def _with_workspace(conv, x, res):
+    n, _, h, w = x.shape
+    oh, ow = nhip.output_shape(conv.desc, h, w)
+    out = torch.empty((n, conv.desc.num_output, oh, ow), device="cuda")
+    conv.forward(x, residual=res, out=out)
+    torch.cuda.synchronize()
+    return out.cpu()
+
+
+def _noalloc(conv, x, res):
+    n, _, h, w = x.shape
+    oh, ow = nhip.output_shape(conv.desc, h, w)
+    out = torch.full((n, conv.desc.num_output, oh, ow), float("nan"), device="cuda")
+    st = nhip.load().nhip_conv2d_f32_forward_noalloc(conv.handle, nhip._ptr(x), nhip._ptr(res), nhip._ptr(out),
+                                                     n, h, w, nhip._stream())
+    torch.cuda.synchronize()
+    return st, out.cpu()
+
+
+@pytest.mark.parametrize("algo,stride,shapes", [
+    # Winograd: the fused GEMM (>= 256 tiles) then the three-kernel path
+    (nhip.ALGO_WINOGRAD, 1, [(8, 64, 56, 56), (2, 64, 20, 20)]),
+    # implicit GEMM (3x3 stride 2), split-K partial sums in the scratch
+    (nhip.ALGO_IMPLICIT_GEMM, 2, [(4, 256, 28, 28), (1, 256, 14, 14)]),
+])
+def test_noalloc_matches_workspace_entry(algo, stride, shapes):
+    conv = _plan(shapes[0][1], shapes[0][1], algo, stride)
+    rng = np.random.default_rng(1)
+    for n, c, h, w in shapes:  # second call smaller than the first
+        need = conv.workspace_size(n, h, w)
+        assert 0 < need <= SCRATCH_BYTES, need
+        x = torch.from_numpy(rng.uniform(-1, 1, (n, c, h, w)).astype(np.float32)).cuda()
+        oh, ow = nhip.output_shape(conv.desc, h, w)
+        res = torch.from_numpy(rng.uniform(-1, 1, (n, c, oh, ow)).astype(np.float32)).cuda()
+        st, got = _noalloc(conv, x, res)
+        assert st == 0, nhip.load().nhip_last_error()
+        exp = _with_workspace(conv, x, res)
+        assert torch.equal(got, exp), f"{(n, c, h, w)}: no-alloc result differs from the workspace entry"
+
+
+def test_noalloc_rejects_batches_beyond_the_scratch():
+    conv = _plan(64, 64, nhip.ALGO_WINOGRAD)
+    n, h, w = 64, 56, 56
+    assert conv.workspace_size(n, h, w) > SCRATCH_BYTES
+    x = torch.zeros((n, 64, h, w), device="cuda")
+    st, out = _noalloc(conv, x, None)
+    assert st == 5  # NHIP_STATUS_OUTPUT_CAPACITY_INSUFFICIENT
+    assert "static scratch" in nhip.load().nhip_last_error().decode()
+    assert torch.isnan(out).all()  # nothing was launched
+    # and a batch that fits still runs after the rejection
+    st, _ = _noalloc(conv, x[:8], None)
+    assert st == 0
