@@ -17,8 +17,9 @@
  * Layer types: Input, Convolution and ConvolutionDepthWise (fp32, int8 terms
  * 1/2/101/102), InnerProduct (fp32, int8 terms 1/2), ReLU (slope 0),
  * BatchNorm (folded into the producing fp32 convolution), BinaryOp add and
- * Eltwise sum of equal shapes, Pooling global average, Quantize, Split,
- * Reshape/Flatten/Squeeze, Dropout/Noop.  Anything else is rejected with
+ * Eltwise sum of equal shapes, Pooling global average, Quantize, Dequantize
+ * and Requantize (on i32 Input blobs, the reference's integer storage),
+ * Split, Reshape/Flatten/Squeeze, Dropout/Noop.  Anything else is rejected with
  * NHIP_STATUS_UNSUPPORTED and a message naming the layer.
  *
  * Shapes: an ncnn blob is [C,H,W] (rank 3) or a rank 1/2 view of it.  An
@@ -38,6 +39,7 @@ extern "C" {
 
 #define NHIP_DTYPE_F32 0
 #define NHIP_DTYPE_I8 1
+#define NHIP_DTYPE_I32 2 /* Input blobs read by Dequantize / Requantize / Embed */
 
 typedef struct nhip_graph* nhip_graph_t;
 
@@ -45,7 +47,8 @@ typedef struct nhip_graph* nhip_graph_t;
  * input_shape_count rank-3 CHW shapes (3 int64 each, -1 = dynamic), one per
  * Input layer in source order, overriding the .param dims (the reference's
  * --input-shape, docs/ncnn-compile-command-line.md section 2.5).  Weights are
- * uploaded to the current device.  On error *graph is NULL and
+ * uploaded to the calling thread's current device, which the graph keeps.
+ * On error *graph is NULL and
  * nhip_last_error() names the layer. */
 int nhip_graph_load(const char* param_text, uint64_t param_len, const void* bin,
                     uint64_t bin_len, const int64_t* input_shapes,
@@ -77,16 +80,23 @@ int nhip_graph_infer_shapes(nhip_graph_t graph, const int64_t* input_shapes,
 
 /* Batch execution on device memory: n images per input, inputs[i] and
  * outputs[j] are device pointers of n back-to-back blobs.  input_shapes as in
- * nhip_graph_infer_shapes.  Calls on one graph must not overlap: it owns the
- * intermediate buffers. */
+ * nhip_graph_infer_shapes.  Calls on one graph are serialised (it owns the
+ * intermediate buffers).  Kernels run on the device the graph was loaded
+ * on; the calling thread's current device is restored afterwards.  On a
+ * non-default stream, a call repeating the previous call's batch, shapes,
+ * buffers and stream is recorded into a hipGraph, and later such calls
+ * replay it. */
 int nhip_graph_run(nhip_graph_t graph, int32_t n, const int64_t* input_shapes,
                    const void* const* inputs, void* const* outputs,
                    void* stream);
 
-/* The reference entry semantics: one image, host buffers, synchronous on
- * the default stream.  output_capacity (elements per output, NULL = not
- * checked) returns NHIP_STATUS_OUTPUT_CAPACITY_INSUFFICIENT when too small.
- * Serialised per graph, so concurrent callers are safe. */
+/* The reference entry semantics: one image, host buffers, synchronous.
+ * output_capacity (elements per output, NULL = not checked) returns
+ * NHIP_STATUS_OUTPUT_CAPACITY_INSUFFICIENT when too small.  Runs on the
+ * graph's own stream on the device the graph was loaded on (the calling
+ * thread's current device is left as it was), staging the copies through
+ * pinned host buffers; repeated calls replay one recorded hipGraph of the
+ * plan.  Serialised per graph, so concurrent callers are safe. */
 int nhip_graph_run_host(nhip_graph_t graph, const int64_t* input_shapes,
                         const void* const* inputs, void* const* outputs,
                         const uint64_t* output_capacity);

@@ -30,6 +30,13 @@ int graph_capture_begin(void* stream);
 int graph_capture_end(void* stream, void** exec);
 int graph_exec_launch(void* exec, void* stream);
 void graph_exec_destroy(void* exec);
+int device_current(int* dev);
+int device_set(int dev);
+void device_restore(int dev);
+int stream_create(void** s);
+void stream_destroy(void* s);
+int host_pinned_alloc(void** p, uint64_t bytes);
+void host_pinned_free(void* p);
 }  // namespace nhip
 
 namespace nhip {
@@ -254,6 +261,11 @@ int load_weight(BinCursor& c, int64_t count, bool tagged, Tensor& t, const std::
   if (count <= 0 || count > (int64_t)1 << 31) return fail(NHIP_STATUS_INVALID_SHAPE, what + ": bad element count");
   uint32_t flag = 0;
   if (tagged) TRY(c.read(&flag, 4, what + " flag"));
+  // The payload must be present before anything is allocated for it (a
+  // count taken from a hostile .param cannot force a large allocation).
+  const uint64_t esz = (!tagged || flag == 0 || flag == kFlagF32) ? 4 : flag == kFlagF16 ? 2 : 1;
+  if ((uint64_t)count * esz > (uint64_t)(c.size - c.pos))
+    return fail(NHIP_STATUS_CONSTRAINT_VIOLATION, ".bin: truncated " + what);
   if (!tagged || flag == 0 || flag == kFlagF32) {
     t.dtype = NHIP_DTYPE_F32;
     t.f.resize((size_t)count);
@@ -309,8 +321,26 @@ int load_layer_weights(Layer& L, BinCursor& c) {
   } else if (ty == "BatchNorm") {
     for (const char* w : {"slope", "mean", "variance", "bias"}) TRY(add(L.geti(0, 0), false, w));
   } else if (ty == "Quantize") {
+    // decode_quantize_params / load_quantize_weights (graph.cpp:748-756,1960-1973)
+    if (L.geti(0, 1) <= 0) return fail(NHIP_STATUS_CONSTRAINT_VIOLATION, where(L) + "Quantize scale count must be positive");
     TRY(add(L.geti(0, 1), false, "scale"));
-  } else if (ty == "Dequantize" || ty == "Requantize" || ty == "PReLU" || ty == "Gemm" || ty == "MemoryData" ||
+  } else if (ty == "Dequantize") {
+    // decode_dequantize_params / load_dequantize_weights (graph.cpp:758-770,1975-1996)
+    const int64_t scales = L.geti(0, 1), bias = L.geti(1, 0);
+    if (scales <= 0 || bias < 0)
+      return fail(NHIP_STATUS_CONSTRAINT_VIOLATION,
+                  where(L) + "Dequantize scale count must be positive and bias count non-negative");
+    TRY(add(scales, false, "Dequantize scale"));
+    if (bias != 0) TRY(add(bias, false, "Dequantize bias"));
+  } else if (ty == "Requantize") {
+    // decode_requantize_params / load_requantize_weights (graph.cpp:772-790,1998-2022)
+    const int64_t in = L.geti(0, 1), out = L.geti(1, 1), bias = L.geti(2, 0), act = L.geti(3, 0);
+    if (in <= 0 || out <= 0 || bias < 0 || act < 0 || act > 6)
+      return fail(NHIP_STATUS_CONSTRAINT_VIOLATION, where(L) + "invalid Requantize scale, bias, or activation");
+    TRY(add(in, false, "Requantize input scale"));
+    TRY(add(out, false, "Requantize output scale"));
+    if (bias != 0) TRY(add(bias, false, "Requantize bias"));
+  } else if (ty == "PReLU" || ty == "Gemm" || ty == "MemoryData" ||
              ty == "Deconvolution" || ty == "LayerNorm" || ty == "Embed" || ty == "MultiHeadAttention") {
     return fail(NHIP_STATUS_UNSUPPORTED, where(L) + "layer type is not on this runtime's path");
   }
@@ -452,7 +482,9 @@ void fuse_relu(std::vector<Layer>& layers) {
 }
 
 // ------------------------------------------------------------- call plan
-enum class OpKind { Input, ConvF32, ConvInt8, DwF32, DwInt8, IP, IPInt8, Relu, Add, Gap, Quantize, Alias };
+enum class OpKind {
+  Input, ConvF32, ConvInt8, DwF32, DwInt8, IP, IPInt8, Relu, Add, Gap, Quantize, Dequantize, Requantize, Alias
+};
 
 struct Shape {
   int rank = 0;
@@ -474,8 +506,15 @@ struct Op {
   nhip_conv_t conv = nullptr;
   nhip_ip_t ip = nullptr;
   int64_t ip_k = 0, ip_n = 0;
+  // Quantize: scale; Dequantize: scale (+ bias); Requantize: input scale,
+  // output scale (+ bias).  Device copies, counts 1 or the channel extent.
   float* scale_dev = nullptr;
   int32_t scale_count = 0;
+  float* scale2_dev = nullptr;
+  int32_t scale2_count = 0;
+  float* bias_dev = nullptr;
+  int32_t bias_count = 0;
+  int32_t quant_act = 0;
   int out_dtype = NHIP_DTYPE_F32;
   // Alias view rules
   enum class View { Same, Flatten, Reshape, Squeeze } view = View::Same;
@@ -504,8 +543,14 @@ struct nhip_graph {
   std::vector<int> inputs, outputs;
   void* ws = nullptr;
   uint64_t ws_cap = 0;
-  std::vector<void*> host_in;  // staging for run_host
+  // nhip_graph_run_host: device copies of one image's inputs and outputs,
+  // pinned host staging for them, and the graph's own stream
+  std::vector<void*> host_in;
   std::vector<uint64_t> host_in_cap;
+  std::vector<void*> pinned;
+  std::vector<uint64_t> pinned_cap;
+  void* host_stream = nullptr;
+  int device = 0;  // the device the plans were uploaded to (current at load)
   std::mutex mu;
   bool host_only = false;  // from nhip_graph_describe: no device plans
   // The last call plan recorded as a hipGraph (nhip_graph_run on a stream),
@@ -522,12 +567,16 @@ struct nhip_graph {
       if (op.conv) nhip_conv_destroy(op.conv);
       if (op.ip) nhip_innerproduct_destroy(op.ip);
       if (op.scale_dev) nhip_free(op.scale_dev);
+      if (op.scale2_dev) nhip_free(op.scale2_dev);
+      if (op.bias_dev) nhip_free(op.bias_dev);
     }
     for (auto& b : blobs)
       if (b.buf) nhip_free(b.buf);
     if (ws) nhip_free(ws);
     for (void* p : host_in)
       if (p) nhip_free(p);
+    for (void* p : pinned) nhip::host_pinned_free(p);
+    nhip::stream_destroy(host_stream);
   }
 };
 
@@ -612,9 +661,21 @@ int infer_op(const nhip_graph& g, const Op& op, const std::vector<Shape>& sh, Sh
       return ok();
     }
     case OpKind::Relu:
-    case OpKind::Quantize:
       out = a;
       return ok();
+    case OpKind::Quantize:
+    case OpKind::Dequantize:
+    case OpKind::Requantize: {
+      // validateScale / validateOptionalBias (NCNNOps.cpp:1378-1416): a
+      // count is one or the extent of dimension zero (the channel of a
+      // [C,H,W] blob).
+      for (int32_t cnt : {op.scale_count, op.scale2_count, op.bias_count})
+        if (cnt > 1 && (a.rank == 0 || a.d[0] != cnt))
+          return fail(NHIP_STATUS_INVALID_SHAPE,
+                      op.name + ": scale and bias counts must be one or match dimension zero");
+      out = a;
+      return ok();
+    }
     case OpKind::Add: {
       const Shape& b = sh[op.in[1]];
       if (a.rank != b.rank) return fail(NHIP_STATUS_INVALID_SHAPE, op.name + ": add operands differ in rank");
@@ -782,6 +843,16 @@ int build(nhip_graph& g, std::vector<Layer>& layers, const int64_t* input_shapes
     g.blobs.push_back(b);
     return blob_id[name] = (int)g.blobs.size() - 1;
   };
+  // Integer input storage (NCNNImporter.cpp:370-376, ImportInput.cpp:78-80):
+  // the reference gives an Input blob i32 elements when an Embed layer reads
+  // it; Dequantize and Requantize need i32 operands
+  // (NCNNOps.cpp:1434-1470), so an Input blob they read is i32 here as well
+  // (the reference rejects such a graph at import, so no graph it accepts
+  // changes meaning).
+  std::set<std::string> integer_inputs;
+  for (const Layer& L : layers)
+    if (!L.removed && (L.type == "Embed" || L.type == "Dequantize" || L.type == "Requantize"))
+      integer_inputs.insert(L.bottoms.begin(), L.bottoms.end());
   std::vector<Shape> sh;
   int next_input = 0;
   for (Layer& L : layers) {
@@ -814,6 +885,7 @@ int build(nhip_graph& g, std::vector<Layer>& layers, const int64_t* input_shapes
         if (s.d[k] == 0 || s.d[k] < -1)
           return fail(NHIP_STATUS_INVALID_SHAPE, where(L) + "Input requires positive or dynamic (-1) extents");
       ++next_input;
+      if (integer_inputs.count(L.tops[0])) g.blobs[id].dtype = NHIP_DTYPE_I32;
       g.blobs[id].declared = s;
       g.inputs.push_back(id);
       if (sh.size() < g.blobs.size()) sh.resize(g.blobs.size());
@@ -917,11 +989,43 @@ int build(nhip_graph& g, std::vector<Layer>& layers, const int64_t* input_shapes
         return fail(NHIP_STATUS_UNSUPPORTED, where(L) + "only global average pooling is on this path");
       op.kind = OpKind::Gap;
     } else if (ty == "Quantize") {
-      if (L.weights.empty()) return fail(NHIP_STATUS_INVALID_SHAPE, where(L) + "missing scale");
+      // import_quantize (ImportQuantization.cpp:37-62); computeQuantizeResult
+      // (NCNNOps.cpp:1420-1432): an f32 input
+      if (L.weights.size() != 1 || L.bottoms.size() != 1) return fail(NHIP_STATUS_INVALID_SHAPE, where(L) + "unexpected weight count");
+      if (g.blobs[op.in[0]].dtype != NHIP_DTYPE_F32)
+        return fail(NHIP_STATUS_CONSTRAINT_VIOLATION, where(L) + "Quantize input must be ranked f32");
       if (!dry) TRY(upload_floats(L.weights[0].f, &op.scale_dev));
       op.scale_count = (int32_t)L.weights[0].f.size();
       op.kind = OpKind::Quantize;
       op.out_dtype = NHIP_DTYPE_I8;
+    } else if (ty == "Dequantize" || ty == "Requantize") {
+      // import_dequantize / import_requantize (ImportQuantization.cpp:65-161),
+      // ConvertDequantize / ConvertRequantize (NCNNToTosa.cpp:4823-4888):
+      // an i32 input; Dequantize scale [+ bias] -> f32; Requantize input
+      // scale, output scale [+ bias], activation none or ReLU -> i8.
+      const bool deq = ty == "Dequantize";
+      if (L.bottoms.size() != 1) return fail(NHIP_STATUS_UNSUPPORTED, where(L) + "one input");
+      if (g.blobs[op.in[0]].dtype != NHIP_DTYPE_I32)
+        return fail(NHIP_STATUS_CONSTRAINT_VIOLATION, where(L) + ty + " input must be ranked i32");
+      if (!deq) {
+        const int64_t act = L.geti(3, 0);
+        if (act != 0 && act != 1)
+          return fail(NHIP_STATUS_UNSUPPORTED, where(L) + "Requantize supports no activation or ReLU only");
+        op.quant_act = (int32_t)act;
+      }
+      const size_t nscale = deq ? 1 : 2;
+      op.scale_count = (int32_t)L.weights[0].f.size();
+      if (!dry) TRY(upload_floats(L.weights[0].f, &op.scale_dev));
+      if (!deq) {
+        op.scale2_count = (int32_t)L.weights[1].f.size();
+        if (!dry) TRY(upload_floats(L.weights[1].f, &op.scale2_dev));
+      }
+      if (L.weights.size() > nscale) {
+        op.bias_count = (int32_t)L.weights[nscale].f.size();
+        if (!dry) TRY(upload_floats(L.weights[nscale].f, &op.bias_dev));
+      }
+      op.kind = deq ? OpKind::Dequantize : OpKind::Requantize;
+      op.out_dtype = deq ? NHIP_DTYPE_F32 : NHIP_DTYPE_I8;
     } else if (ty == "Split" || ty == "Dropout" || ty == "Noop") {
       op.kind = OpKind::Alias;
       op.view = Op::View::Same;
@@ -949,6 +1053,12 @@ int build(nhip_graph& g, std::vector<Layer>& layers, const int64_t* input_shapes
     if (op.kind != OpKind::Alias || op.view != Op::View::Same) {
       if (L.tops.size() != 1) return fail(NHIP_STATUS_UNSUPPORTED, where(L) + "one output expected");
     }
+    // i32 blobs (integer-storage inputs) are read only by the layers that
+    // take accumulators, or viewed
+    if (op.kind != OpKind::Dequantize && op.kind != OpKind::Requantize && op.kind != OpKind::Alias)
+      for (int b : op.in)
+        if (g.blobs[b].dtype == NHIP_DTYPE_I32)
+          return fail(NHIP_STATUS_UNSUPPORTED, where(L) + "int32 operand (only Dequantize / Requantize read i32 blobs)");
     // outputs (Split fans its input out to several aliases of it, so that
     // each top can also be a graph output)
     for (size_t t = 0; t < L.tops.size(); ++t) {
@@ -978,7 +1088,7 @@ int build(nhip_graph& g, std::vector<Layer>& layers, const int64_t* input_shapes
   return ok();
 }
 
-int esize(int dtype) { return dtype == NHIP_DTYPE_I8 ? 1 : 4; }
+int esize(int dtype) { return dtype == NHIP_DTYPE_I8 ? 1 : 4; }  // f32 and i32: 4 bytes
 
 int ensure(void** buf, uint64_t* cap, uint64_t bytes) {
   if (*cap >= bytes) return ok();
@@ -1076,12 +1186,27 @@ int run_ops(nhip_graph& g, int n, const std::vector<Shape>& sh, const void* cons
         TRY(nhip_global_avgpool_f32((const float*)in, (float*)out, n, (int32_t)a.d[0], (int32_t)a.d[1], (int32_t)a.d[2],
                                     stream));
         break;
+      // per-channel parameters index dimension zero of the blob
+      // (quantizeSignedI8 / dequantizeNcnn scale dimension, NCNNToTosa.cpp:
+      // 322-389,411-460): the channel of [C,H,W], the first extent of a
+      // rank-1/2 view
       case OpKind::Quantize: {
-        const int64_t c = a.rank == 3 ? a.d[0] : 1;
-        if (op.scale_count != 1 && op.scale_count != c)
-          return fail(NHIP_STATUS_INVALID_SHAPE, op.name + ": scale count must be 1 or the channel count");
+        const int64_t c = a.rank >= 1 ? a.d[0] : 1;
         TRY(nhip_quantize_f32_i8((const float*)in, (int8_t*)out, n, (int32_t)c, a.elems() / c, op.scale_dev,
                                  op.scale_count, stream));
+        break;
+      }
+      case OpKind::Dequantize: {
+        const int64_t c = a.rank >= 1 ? a.d[0] : 1;
+        TRY(nhip_dequantize_i32_f32((const int32_t*)in, (float*)out, n, (int32_t)c, a.elems() / c, op.scale_dev,
+                                    op.scale_count, op.bias_dev, op.bias_count, stream));
+        break;
+      }
+      case OpKind::Requantize: {
+        const int64_t c = a.rank >= 1 ? a.d[0] : 1;
+        TRY(nhip_requantize_i32_i8((const int32_t*)in, (int8_t*)out, n, (int32_t)c, a.elems() / c, op.scale_dev,
+                                   op.scale_count, op.scale2_dev, op.scale2_count, op.bias_dev, op.bias_count,
+                                   op.quant_act, stream));
         break;
       }
       default:
@@ -1106,15 +1231,22 @@ static int load_impl(const char* param_text, uint64_t param_len, const void* bin
   if (!param_text || (!bin && bin_len)) return fail(NHIP_STATUS_NULL_POINTER, "graph_load: null model data");
   if (input_shape_count < 0 || (input_shape_count > 0 && !input_shapes))
     return fail(NHIP_STATUS_NULL_POINTER, "graph_load: null input shapes");
-  std::vector<Layer> layers;
-  TRY(parse_param_text(std::string(param_text, param_len), layers));
-  BinCursor cur{static_cast<const uint8_t*>(bin), (size_t)bin_len};
-  for (Layer& L : layers) TRY(load_layer_weights(L, cur));
-  auto g = std::make_unique<nhip_graph>();
-  g->host_only = dry;
-  TRY(build(*g, layers, input_shape_count ? input_shapes : nullptr, input_shape_count, dry));
-  *graph = g.release();
-  return ok();
+  try {
+    std::vector<Layer> layers;
+    TRY(parse_param_text(std::string(param_text, param_len), layers));
+    BinCursor cur{static_cast<const uint8_t*>(bin), (size_t)bin_len};
+    for (Layer& L : layers) TRY(load_layer_weights(L, cur));
+    auto g = std::make_unique<nhip_graph>();
+    g->host_only = dry;
+    if (!dry) TRY(nhip::device_current(&g->device));  // plans are uploaded to the caller's current device
+    TRY(build(*g, layers, input_shape_count ? input_shapes : nullptr, input_shape_count, dry));
+    *graph = g.release();
+    return ok();
+  } catch (const std::bad_alloc&) {
+    return fail(NHIP_STATUS_SHAPE_ARITHMETIC_OVERFLOW, "graph_load: out of host memory");
+  } catch (const std::exception& e) {
+    return fail(NHIP_STATUS_CONSTRAINT_VIOLATION, std::string("graph_load: ") + e.what());
+  }
 }
 
 int nhip_graph_load(const char* param_text, uint64_t param_len, const void* bin, uint64_t bin_len,
@@ -1159,6 +1291,119 @@ int nhip_graph_infer_shapes(nhip_graph_t g, const int64_t* input_shapes, int64_t
   return ok();
 }
 
+}  // extern "C"
+
+namespace {
+
+// Makes the graph's device current for one call and restores the caller's
+// afterwards (a call never changes the calling thread's current device).
+class DeviceGuard {
+ public:
+  explicit DeviceGuard(int dev) {
+    if (nhip::device_current(&prev_) != NHIP_STATUS_SUCCESS) {
+      status_ = NHIP_STATUS_DEVICE_ERROR;
+      return;
+    }
+    if (prev_ != dev) {
+      status_ = nhip::device_set(dev);
+      switched_ = status_ == NHIP_STATUS_SUCCESS;
+    }
+  }
+  ~DeviceGuard() {
+    if (switched_) nhip::device_restore(prev_);
+  }
+  int status() const { return status_; }
+
+ private:
+  int prev_ = 0, status_ = NHIP_STATUS_SUCCESS;
+  bool switched_ = false;
+};
+
+// One run of the call plan on `stream`, with replay.  When two calls in a
+// row on a stream have the same key, the second runs eagerly (every buffer
+// is already sized) and is also recorded into a hipGraph, and later calls
+// with that key launch the recorded graph: one launch instead of one per
+// kernel (each eager launch costs a few microseconds of dispatch that the
+// short late layers of a network cannot hide).  Calls whose pointers change
+// every time stay eager and record nothing.  The legacy default stream
+// cannot be captured and runs eagerly, as do runs while the kernel timer
+// records per-launch events and runs on a stream the caller is capturing
+// itself (the launches then become part of the caller's graph);
+// NHIP_GRAPH_REPLAY=0 turns replay off.  The graph's mutex is held.
+int run_with_replay(nhip_graph& g, int32_t n, const std::vector<Shape>& sh, const void* const* inputs,
+                    void* const* outputs, void* stream) {
+  if (stream == nullptr || nhip::setting_int("NHIP_GRAPH_REPLAY", 1) == 0 || nhip::kernel_timer_active() ||
+      nhip::stream_capturing(stream))
+    return run_ops(g, n, sh, inputs, outputs, stream);
+  std::ostringstream key;
+  key << n;
+  for (int b : g.inputs) {
+    key << "|";
+    for (int d = 0; d < sh[b].rank; ++d) key << sh[b].d[d] << ",";
+  }
+  for (size_t i = 0; i < g.inputs.size(); ++i) key << "|" << inputs[i];
+  for (size_t j = 0; j < g.outputs.size(); ++j) key << "|" << outputs[j];
+  key << "|stream " << stream << "|settings " << nhip::settings_generation();
+  // The blob buffers and workspace grow (free + malloc) when a call needs
+  // more: a recorded plan is only replayed while they are the ones it was
+  // recorded with.
+  auto internal_bufs = [&]() {
+    std::vector<const void*> v;
+    v.reserve(g.blobs.size() + 1);
+    for (const Blob& b : g.blobs) v.push_back(b.buf);
+    v.push_back(g.ws);
+    return v;
+  };
+  if (g.exec && key.str() == g.exec_key) {
+    if (internal_bufs() == g.exec_bufs) return nhip::graph_exec_launch(g.exec, stream);
+    nhip::graph_exec_destroy(g.exec);
+    g.exec = nullptr;
+    g.exec_key.clear();
+  }
+  TRY(run_ops(g, n, sh, inputs, outputs, stream));
+  if (key.str() != g.seen_key || key.str() == g.nocap_key) {
+    g.seen_key = key.str();
+    return ok();
+  }
+  nhip::graph_exec_destroy(g.exec);
+  g.exec = nullptr;
+  g.exec_key.clear();
+  bool recorded = false;
+  if (nhip::graph_capture_begin(stream) == NHIP_STATUS_SUCCESS) {
+    const int st = run_ops(g, n, sh, inputs, outputs, stream);
+    void* exec = nullptr;
+    const int st2 = nhip::graph_capture_end(stream, &exec);
+    if (st == NHIP_STATUS_SUCCESS && st2 == NHIP_STATUS_SUCCESS && exec) {
+      g.exec = exec;
+      g.exec_key = key.str();
+      g.exec_bufs = internal_bufs();
+      recorded = true;
+    } else {
+      nhip::graph_exec_destroy(exec);
+    }
+  }
+  if (!recorded) g.nocap_key = key.str();
+  return ok();
+}
+
+int ensure_pinned(nhip_graph& g, size_t slot, uint64_t bytes) {
+  if (g.pinned.size() <= slot) {
+    g.pinned.resize(slot + 1, nullptr);
+    g.pinned_cap.resize(slot + 1, 0);
+  }
+  if (g.pinned_cap[slot] >= bytes) return ok();
+  nhip::host_pinned_free(g.pinned[slot]);
+  g.pinned[slot] = nullptr;
+  g.pinned_cap[slot] = 0;
+  TRY(nhip::host_pinned_alloc(&g.pinned[slot], bytes));
+  g.pinned_cap[slot] = bytes;
+  return ok();
+}
+
+}  // namespace
+
+extern "C" {
+
 int nhip_graph_run(nhip_graph_t g, int32_t n, const int64_t* input_shapes, const void* const* inputs,
                    void* const* outputs, void* stream) {
   if (!g || !inputs || !outputs) return fail(NHIP_STATUS_NULL_POINTER, "graph_run: null pointer");
@@ -1172,68 +1417,9 @@ int nhip_graph_run(nhip_graph_t g, int32_t n, const int64_t* input_shapes, const
   std::vector<Shape> sh;
   TRY(propagate(*g, input_shapes, sh, true));
   std::lock_guard<std::mutex> lock(g->mu);
-  // Replay: when two calls in a row on a stream have the same key, the
-  // second runs eagerly (every buffer is already sized) and is also recorded
-  // into a hipGraph, and later calls with that key launch the recorded graph:
-  // one launch instead of one per kernel (each eager launch costs a few
-  // microseconds of dispatch that the short late layers of a network cannot
-  // hide).  Calls whose pointers change every time stay eager and record
-  // nothing.  The legacy default stream cannot be captured and runs eagerly,
-  // as do runs while the kernel timer records per-launch events and runs on
-  // a stream the caller is capturing itself (the launches then become part
-  // of the caller's graph); NHIP_GRAPH_REPLAY=0 turns replay off.
-  if (stream == nullptr || nhip::setting_int("NHIP_GRAPH_REPLAY", 1) == 0 || nhip::kernel_timer_active() ||
-      nhip::stream_capturing(stream))
-    return run_ops(*g, n, sh, inputs, outputs, stream);
-  std::ostringstream key;
-  key << n;
-  for (int b : g->inputs) {
-    key << "|";
-    for (int d = 0; d < sh[b].rank; ++d) key << sh[b].d[d] << ",";
-  }
-  for (size_t i = 0; i < g->inputs.size(); ++i) key << "|" << inputs[i];
-  for (size_t j = 0; j < g->outputs.size(); ++j) key << "|" << outputs[j];
-  key << "|settings " << nhip::settings_generation();
-  // The blob buffers and workspace grow (free + malloc) when a call needs
-  // more: a recorded plan is only replayed while they are the ones it was
-  // recorded with.
-  auto internal_bufs = [&]() {
-    std::vector<const void*> v;
-    v.reserve(g->blobs.size() + 1);
-    for (const Blob& b : g->blobs) v.push_back(b.buf);
-    v.push_back(g->ws);
-    return v;
-  };
-  if (g->exec && key.str() == g->exec_key) {
-    if (internal_bufs() == g->exec_bufs) return nhip::graph_exec_launch(g->exec, stream);
-    nhip::graph_exec_destroy(g->exec);
-    g->exec = nullptr;
-    g->exec_key.clear();
-  }
-  TRY(run_ops(*g, n, sh, inputs, outputs, stream));
-  if (key.str() != g->seen_key || key.str() == g->nocap_key) {
-    g->seen_key = key.str();
-    return ok();
-  }
-  nhip::graph_exec_destroy(g->exec);
-  g->exec = nullptr;
-  g->exec_key.clear();
-  bool recorded = false;
-  if (nhip::graph_capture_begin(stream) == NHIP_STATUS_SUCCESS) {
-    const int st = run_ops(*g, n, sh, inputs, outputs, stream);
-    void* exec = nullptr;
-    const int st2 = nhip::graph_capture_end(stream, &exec);
-    if (st == NHIP_STATUS_SUCCESS && st2 == NHIP_STATUS_SUCCESS && exec) {
-      g->exec = exec;
-      g->exec_key = key.str();
-      g->exec_bufs = internal_bufs();
-      recorded = true;
-    } else {
-      nhip::graph_exec_destroy(exec);
-    }
-  }
-  if (!recorded) g->nocap_key = key.str();
-  return ok();
+  DeviceGuard dev(g->device);
+  TRY(dev.status());
+  return run_with_replay(*g, n, sh, inputs, outputs, stream);
 }
 
 int nhip_graph_run_host(nhip_graph_t g, const int64_t* input_shapes, const void* const* inputs, void* const* outputs,
@@ -1252,29 +1438,40 @@ int nhip_graph_run_host(nhip_graph_t g, const int64_t* input_shapes, const void*
       if ((uint64_t)sh[g->outputs[j]].elems() > output_capacity[j])
         return fail(NHIP_STATUS_OUTPUT_CAPACITY_INSUFFICIENT,
                     "output " + std::to_string(j + 1) + " needs " + std::to_string(sh[g->outputs[j]].elems()) + " elements");
-  g->host_in.resize(g->inputs.size() + g->outputs.size(), nullptr);
-  g->host_in_cap.resize(g->host_in.size(), 0);
-  std::vector<const void*> din(g->inputs.size());
-  std::vector<void*> dout(g->outputs.size());
-  for (size_t i = 0; i < g->inputs.size(); ++i) {
+  DeviceGuard dev(g->device);
+  TRY(dev.status());
+  if (!g->host_stream) TRY(nhip::stream_create(&g->host_stream));
+  void* const s = g->host_stream;
+  const size_t nin = g->inputs.size(), nout = g->outputs.size();
+  g->host_in.resize(nin + nout, nullptr);
+  g->host_in_cap.resize(nin + nout, 0);
+  std::vector<const void*> din(nin);
+  std::vector<void*> dout(nout);
+  std::vector<uint64_t> out_bytes(nout);
+  // inputs: caller buffer -> pinned staging -> device (DMA on the graph's stream)
+  for (size_t i = 0; i < nin; ++i) {
     const int b = g->inputs[i];
     const uint64_t bytes = (uint64_t)sh[b].elems() * esize(g->blobs[b].dtype);
     TRY(ensure(&g->host_in[i], &g->host_in_cap[i], bytes));
-    TRY(nhip_memcpy_h2d(g->host_in[i], inputs[i], bytes, nullptr));
+    TRY(ensure_pinned(*g, i, bytes));
+    std::memcpy(g->pinned[i], inputs[i], bytes);
+    TRY(nhip_memcpy_h2d(g->host_in[i], g->pinned[i], bytes, s));
     din[i] = g->host_in[i];
   }
-  for (size_t j = 0; j < g->outputs.size(); ++j) {
+  for (size_t j = 0; j < nout; ++j) {
     const int b = g->outputs[j];
-    const size_t slot = g->inputs.size() + j;
-    TRY(ensure(&g->host_in[slot], &g->host_in_cap[slot], (uint64_t)sh[b].elems() * esize(g->blobs[b].dtype)));
-    dout[j] = g->host_in[slot];
+    out_bytes[j] = (uint64_t)sh[b].elems() * esize(g->blobs[b].dtype);
+    TRY(ensure(&g->host_in[nin + j], &g->host_in_cap[nin + j], out_bytes[j]));
+    TRY(ensure_pinned(*g, nin + j, out_bytes[j]));
+    dout[j] = g->host_in[nin + j];
   }
-  TRY(run_ops(*g, 1, sh, din.data(), dout.data(), nullptr));
-  for (size_t j = 0; j < g->outputs.size(); ++j) {
-    const int b = g->outputs[j];
-    TRY(nhip_memcpy_d2h(outputs[j], dout[j], (uint64_t)sh[b].elems() * esize(g->blobs[b].dtype), nullptr));
-  }
-  return nhip_stream_sync(nullptr);
+  // the device buffers stay the same from call to call, so repeated calls
+  // replay one recorded hipGraph of the plan
+  TRY(run_with_replay(*g, 1, sh, din.data(), dout.data(), s));
+  for (size_t j = 0; j < nout; ++j) TRY(nhip_memcpy_d2h(g->pinned[nin + j], dout[j], out_bytes[j], s));
+  TRY(nhip_stream_sync(s));
+  for (size_t j = 0; j < nout; ++j) std::memcpy(outputs[j], g->pinned[nin + j], out_bytes[j]);
+  return ok();
 }
 
 int nhip_graph_destroy(nhip_graph_t g) {

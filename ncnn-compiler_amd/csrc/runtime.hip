@@ -107,6 +107,30 @@ int graph_capture_end(void* stream, void** exec) {
   return st;
 }
 
+// Device, stream and pinned host memory for the graph executor's host-buffer
+// entry (csrc/graph.cpp is host-only C++ without HIP headers).
+int device_current(int* dev) { return check_hip(hipGetDevice(dev), "hipGetDevice"); }
+int device_set(int dev) { return check_hip(hipSetDevice(dev), "hipSetDevice"); }
+void device_restore(int dev) {  // leaves the thread's last error message alone
+  if (hipSetDevice(dev) != hipSuccess) (void)hipGetLastError();
+}
+int stream_create(void** s) {
+  hipStream_t st = nullptr;  // default priority, never blocks on the legacy stream
+  NHIP_TRY(check_hip(hipStreamCreateWithFlags(&st, hipStreamNonBlocking), "hipStreamCreateWithFlags"));
+  *s = st;
+  return ok();
+}
+void stream_destroy(void* s) {
+  if (s) (void)hipStreamDestroy(as_stream(s));
+}
+int host_pinned_alloc(void** p, uint64_t bytes) {
+  *p = nullptr;
+  return check_hip(hipHostMalloc(p, bytes ? bytes : 1, hipHostMallocDefault), "hipHostMalloc");
+}
+void host_pinned_free(void* p) {
+  if (p) (void)hipHostFree(p);
+}
+
 int graph_exec_launch(void* exec, void* stream) {
   NHIP_TRY(check_hip(hipGraphLaunch(reinterpret_cast<hipGraphExec_t>(exec), as_stream(stream)), "hipGraphLaunch"));
   return check_launch("graph replay");

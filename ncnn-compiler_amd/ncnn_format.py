@@ -134,6 +134,35 @@ class Model:
         self._layer("Quantize", name, [bottom], [top], {0: scale.size})
         self._raw(scale)
 
+    def dequantize(self, name, bottom, top, scale, bias=None):
+        """Dequantize (graph.cpp:1975-1996): scale [, bias], raw fp32."""
+        scale = np.atleast_1d(np.asarray(scale, np.float32))
+        p = {0: scale.size}
+        if bias is not None:
+            bias = np.atleast_1d(np.asarray(bias, np.float32))
+            p[1] = bias.size
+        self._layer("Dequantize", name, [bottom], [top], p)
+        self._raw(scale)
+        if bias is not None:
+            self._raw(bias)
+
+    def requantize(self, name, bottom, top, in_scale, out_scale, bias=None, act=0):
+        """Requantize (graph.cpp:1998-2022): input scale, output scale
+        [, bias], raw fp32; activation_type 0 or 1."""
+        in_scale = np.atleast_1d(np.asarray(in_scale, np.float32))
+        out_scale = np.atleast_1d(np.asarray(out_scale, np.float32))
+        p = {0: in_scale.size, 1: out_scale.size}
+        if bias is not None:
+            bias = np.atleast_1d(np.asarray(bias, np.float32))
+            p[2] = bias.size
+        if act:
+            p[3] = act
+        self._layer("Requantize", name, [bottom], [top], p)
+        self._raw(in_scale)
+        self._raw(out_scale)
+        if bias is not None:
+            self._raw(bias)
+
     def layer(self, typ, name, bottoms, tops, params=None):
         """Any other layer type (no weights)."""
         self._layer(typ, name, bottoms, tops, params)

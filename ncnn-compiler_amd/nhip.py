@@ -55,7 +55,8 @@ GRAPH_EXPORTS = (
     "nhip_graph_io_info", "nhip_graph_infer_shapes", "nhip_graph_run",
     "nhip_graph_run_host", "nhip_graph_destroy",
 )
-DTYPE_F32, DTYPE_I8 = 0, 1
+DTYPE_F32, DTYPE_I8, DTYPE_I32 = 0, 1, 2
+_NP_DTYPE = {DTYPE_F32: np.float32, DTYPE_I8: np.int8, DTYPE_I32: np.int32}
 
 
 class NhipError(RuntimeError):
@@ -188,6 +189,11 @@ def timer_stop():
 
 def _ptr(t):
     return None if t is None else _P(t.data_ptr())
+
+
+def _torch_dtype(np_dtype):
+    torch = _torch()
+    return {np.int8: torch.int8, np.int32: torch.int32}.get(np_dtype, torch.float32)
 
 
 def _stream(stream=None):
@@ -592,7 +598,7 @@ class Graph:
         check(load().nhip_graph_io_info(self.handle, is_output, index, ctypes.byref(rank), dims,
                                         ctypes.byref(dtype), ctypes.byref(name)))
         return dict(name=name.value.decode(), shape=tuple(dims[:rank.value]),
-                    dtype=np.int8 if dtype.value == DTYPE_I8 else np.float32)
+                    dtype=_NP_DTYPE[dtype.value])
 
     @staticmethod
     def _shape_arg(shapes):
@@ -639,19 +645,19 @@ class Graph:
         if len(tensors) != len(self.inputs):
             raise ValueError(f"expected {len(self.inputs)} inputs")
         n = int(tensors[0].shape[0])
-        xs = [_dev(t, torch.int8 if io["dtype"] == np.int8 else torch.float32)
+        xs = [_dev(t, _torch_dtype(io["dtype"]))
               for t, io in zip(tensors, self.inputs)]
         shapes = [tuple(t.shape[1:]) if t.dim() == 4 else (1,) * (4 - t.dim()) + tuple(t.shape[1:])
                   for t in xs]
         dyn = any(d < 0 for io in self.inputs for d in io["shape"])
         oshapes = self.infer_shapes(shapes if dyn else None)
         if out is None:
-            outs = [torch.empty((n,) + s, dtype=torch.int8 if io["dtype"] == np.int8 else torch.float32,
+            outs = [torch.empty((n,) + s, dtype=_torch_dtype(io["dtype"]),
                                 device=xs[0].device) for s, io in zip(oshapes, self.outputs)]
         else:
             outs = list(out)
             for o, s, io in zip(outs, oshapes, self.outputs):
-                want = torch.int8 if io["dtype"] == np.int8 else torch.float32
+                want = _torch_dtype(io["dtype"])
                 if tuple(o.shape) != (n,) + tuple(s) or o.dtype != want or not o.is_contiguous() or not o.is_cuda:
                     raise ValueError(f"out tensor must be a contiguous {want} device tensor of shape {(n,) + tuple(s)}")
         ins = (_P * len(xs))(*[t.data_ptr() for t in xs])

@@ -14,9 +14,12 @@
 #include <unistd.h>
 
 #include <cctype>
+#include <cerrno>
+#include <cmath>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <algorithm>
 #include <fstream>
 #include <iostream>
 #include <set>
@@ -28,10 +31,18 @@
 
 namespace {
 
+// --input-dim-constraint=INPUT:DIM:min=N,multiple=N (the reference's
+// tools/ncnn-mlir-driver.cpp:191-243 grammar): INPUT indexes the Input
+// layers in source order, DIM is a CHW dimension that must be dynamic.
+struct DimConstraint {
+  int64_t input = 0, dim = 0, minimum = 0, multiple_of = 0;
+};
+
 struct Options {
   std::string param, bin, model_name, output_dir, runtime_dir, precision = "auto";
   std::vector<std::vector<int64_t>> input_shapes;
-  bool emit_manifest = false, verbose = false, keep_source = false;
+  std::vector<DimConstraint> constraints;
+  bool emit_manifest = false, verbose = false, keep_source = false, verify_execution = false;
 };
 
 [[noreturn]] void die(const std::string& msg, int code = 1) {
@@ -45,6 +56,9 @@ void usage() {
                "  --model-name=<name>     entry/header/library name (default: from the .param file name)\n"
                "  -o, --output-dir=<dir>  output directory (default: ./<model-name>)\n"
                "  --input-shape=<CxHxW>   Input extents, '?' = given at run time (repeatable)\n"
+               "  --input-dim-constraint=<INPUT:DIM:min=N,multiple=N>\n"
+               "                          run-time minimum and divisor of a '?' extent (repeatable)\n"
+               "  --verify-execution      build and run an ABI harness against the library before publishing\n"
                "  --emit-manifest         also write <model-name>.json\n"
                "  --precision=<p>         auto|f32|int8 (recorded; int8 comes from the model's scale terms)\n"
                "  --runtime-dir=<dir>     directory holding libnhip.so (default: next to this tool)\n"
@@ -75,6 +89,42 @@ std::vector<int64_t> parse_shape(const std::string& s) {
   return dims;
 }
 
+bool parse_int(const std::string& t, int64_t* v) {
+  if (t.empty()) return false;
+  char* end = nullptr;
+  errno = 0;
+  const long long r = std::strtoll(t.c_str(), &end, 10);
+  if (*end || errno) return false;
+  *v = r;
+  return true;
+}
+
+// Both fields are required, once each, with positive values.
+bool parse_constraint(const std::string& text, DimConstraint* c) {
+  const auto a = text.find(':');
+  const auto b = a == std::string::npos ? a : text.find(':', a + 1);
+  if (b == std::string::npos) return false;
+  if (!parse_int(text.substr(0, a), &c->input) || !parse_int(text.substr(a + 1, b - a - 1), &c->dim)) return false;
+  bool saw_min = false, saw_mult = false;
+  std::stringstream fields(text.substr(b + 1));
+  std::string f;
+  while (std::getline(fields, f, ',')) {
+    const auto eq = f.find('=');
+    if (eq == std::string::npos) return false;
+    const std::string name = f.substr(0, eq), value = f.substr(eq + 1);
+    if (name == "min" && !saw_min) {
+      saw_min = parse_int(value, &c->minimum) && c->minimum > 0;
+      if (!saw_min) return false;
+    } else if (name == "multiple" && !saw_mult) {
+      saw_mult = parse_int(value, &c->multiple_of) && c->multiple_of > 0;
+      if (!saw_mult) return false;
+    } else {
+      return false;
+    }
+  }
+  return saw_min && saw_mult && c->input >= 0 && c->dim >= 0;
+}
+
 Options parse_args(int argc, char** argv) {
   Options o;
   auto value = [&](int& i, const std::string& a, const std::string& key) -> std::string {
@@ -101,8 +151,15 @@ Options parse_args(int argc, char** argv) {
       const std::string v = value(i, a, "--input-shape");
       if (v == "*") die("--input-shape=* (dynamic rank) is not supported by the GPU runtime", 2);
       o.input_shapes.push_back(parse_shape(v));
+    } else if (is("--input-dim-constraint")) {
+      DimConstraint c;
+      if (!parse_constraint(value(i, a, "--input-dim-constraint"), &c))
+        die("--input-dim-constraint must be INPUT:DIM:min=N,multiple=N with positive values");
+      o.constraints.push_back(c);
     } else if (a == "--emit-manifest") {
       o.emit_manifest = true;
+    } else if (a == "--verify-execution") {
+      o.verify_execution = true;
     } else if (is("--precision")) {
       o.precision = value(i, a, "--precision");
       if (o.precision != "auto" && o.precision != "f32" && o.precision != "int8")
@@ -194,13 +251,18 @@ std::string abs_path(const std::string& p) {
   return p;
 }
 
-int run(const std::vector<std::string>& cmd, bool verbose) {
+// Runs a subprocess; with `capture`, its stdout goes to that file.
+int run(const std::vector<std::string>& cmd, bool verbose, const std::string& capture = "") {
   std::string line;
   for (auto& c : cmd) line += (line.empty() ? "" : " ") + c;
-  if (verbose) std::cerr << "+ " << line << "\n";
+  if (verbose) std::cerr << "+ " << line << (capture.empty() ? "" : " > " + capture) << "\n";
   const pid_t pid = fork();
   if (pid < 0) die("fork failed");
   if (pid == 0) {
+    if (!capture.empty()) {
+      FILE* f = std::fopen(capture.c_str(), "w");
+      if (!f || dup2(fileno(f), 1) < 0) _exit(126);
+    }
     std::vector<char*> av;
     for (auto& c : cmd) av.push_back(const_cast<char*>(c.c_str()));
     av.push_back(nullptr);
@@ -216,6 +278,7 @@ struct Arg {
   std::string name, ctype, etype;
   std::vector<int64_t> shape;
   uint32_t mask = 0;
+  std::vector<DimConstraint> constraints;  // inputs: on dynamic dimensions, by dimension
 };
 
 std::string upper(std::string s) {
@@ -248,6 +311,10 @@ std::string header_text(const std::string& fn, const std::vector<Arg>& ins, cons
     char mask[32];
     std::snprintf(mask, sizeof mask, "UINT32_C(0x%x)", a.mask);
     h << "#define " << macro(fn, a, "dynamic_dim_mask") << " " << mask << "\n";
+    for (const DimConstraint& c : a.constraints)  // tools/ncnn-compile.cpp:1059-1073
+      h << "#define " << macro(fn, a, "dim" + std::to_string(c.dim) + "_minimum") << " INT64_C(" << c.minimum << ")\n"
+        << "#define " << macro(fn, a, "dim" + std::to_string(c.dim) + "_multiple_of") << " INT64_C(" << c.multiple_of
+        << ")\n";
     if (a.mask == 0) {
       uint64_t e = 1;
       for (int64_t d : a.shape) e *= (uint64_t)d;
@@ -301,7 +368,15 @@ std::string manifest_text(const std::string& fn, const std::vector<Arg>& ins, co
   auto arr = [&](const std::vector<Arg>& v) {
     j << "[";
     for (size_t i = 0; i < v.size(); ++i) {
-      j << (i ? ",\n    " : "\n    ") << "{\n      \"dynamic_dim_mask\": " << v[i].mask << ",\n      \"element_type\": \""
+      j << (i ? ",\n    " : "\n    ") << "{\n";
+      if (!v[i].constraints.empty()) {  // tools/ncnn-compile.cpp:818-830
+        j << "      \"dimension_constraints\": [";
+        for (size_t c = 0; c < v[i].constraints.size(); ++c)
+          j << (c ? ", " : "") << "{\"dimension\": " << v[i].constraints[c].dim << ", \"minimum\": "
+            << v[i].constraints[c].minimum << ", \"multiple_of\": " << v[i].constraints[c].multiple_of << "}";
+        j << "],\n";
+      }
+      j << "      \"dynamic_dim_mask\": " << v[i].mask << ",\n      \"element_type\": \""
         << v[i].etype << "\",\n      \"name\": \"" << v[i].name << "\",\n      \"shape\": [";
       for (size_t k = 0; k < v[i].shape.size(); ++k) j << (k ? ", " : "") << v[i].shape[k];
       j << "]\n    }";
@@ -338,8 +413,11 @@ std::string wrapper_source(const std::string& fn, const std::vector<Arg>& ins, c
   s << "};\nstatic const int32_t kNumShapes = " << flat_shapes.size() / 3 << ";\n"
     << "static nhip_graph_t g_exec, g_desc;\nstatic int g_exec_status, g_desc_status;\n"
     << "static pthread_once_t g_exec_once = PTHREAD_ONCE_INIT, g_desc_once = PTHREAD_ONCE_INIT;\n"
-    << "static void init_exec(void) {\n  g_exec_status = nhip_init(0);\n  if (g_exec_status == 0)\n"
-    << "    g_exec_status = nhip_graph_load(nhip_model_param, (uint64_t)(nhip_model_param_end - nhip_model_param),\n"
+    << "/* The model is loaded onto the device current in the thread of the first call (device 0\n"
+    << "   unless that thread chose another); every call then runs there on the graph's own stream,\n"
+    << "   leaving the calling thread's current device as it was. */\n"
+    << "static void init_exec(void) {\n"
+    << "  g_exec_status = nhip_graph_load(nhip_model_param, (uint64_t)(nhip_model_param_end - nhip_model_param),\n"
     << "                                    nhip_model_bin, (uint64_t)(nhip_model_bin_end - nhip_model_bin),\n"
     << "                                    kNumShapes ? kShapes : 0, kNumShapes, &g_exec);\n}\n"
     << "static void init_desc(void) {\n"
@@ -357,6 +435,15 @@ std::string wrapper_source(const std::string& fn, const std::vector<Arg>& ins, c
         if (ins[i].mask) b << ins[i].name << "_shape[" << k << "];\n";
         else b << ins[i].shape[k] << ";\n";
       }
+    // The reference wrapper's order (GenerateCAPI.cpp:1440-1480): invalid
+    // extents are status 2 before constraint violations are status 3.
+    for (size_t i = 0; i < ins.size(); ++i)
+      for (int k = 0; k < 3; ++k)
+        if (ins[i].mask & (1u << k)) b << "  if (shapes[" << 3 * i + k << "] <= 0) return 2;\n";
+    for (size_t i = 0; i < ins.size(); ++i)
+      for (const DimConstraint& c : ins[i].constraints)
+        b << "  if (shapes[" << 3 * i + c.dim << "] < INT64_C(" << c.minimum << ") || shapes[" << 3 * i + c.dim
+          << "] % INT64_C(" << c.multiple_of << ") != 0) return 3;  /* NCNN_STATUS_CONSTRAINT_VIOLATION */\n";
     return b.str();
   };
   s << "extern \"C\" __attribute__((visibility(\"default\"))) int " << fn << "(";
@@ -444,6 +531,158 @@ std::string wrapper_source(const std::string& fn, const std::vector<Arg>& ins, c
   return s.str();
 }
 
+// Symbol names from `nm -D` output (the last column, version suffix dropped).
+std::set<std::string> nm_symbols(const std::string& text) {
+  std::set<std::string> out;
+  std::istringstream in(text);
+  std::string line;
+  while (std::getline(in, line)) {
+    std::istringstream ls(line);
+    std::string tok, last;
+    while (ls >> tok) last = tok;
+    if (last.empty()) continue;
+    const auto at = last.find('@');
+    out.insert(at == std::string::npos ? last : last.substr(0, at));
+  }
+  return out;
+}
+
+// The reference's artifact audit (tools/ncnn-compile.cpp:2070-2196), with
+// its allowlists extended by exactly what a GPU-backed library needs: the
+// libnhip graph entry points (nhip_*) and pthread_once (the one-time graph
+// load) as undefined symbols, libnhip.so (and the HIP runtime it loads) as a
+// DT_NEEDED entry.  Returns "" or the failure.
+std::string audit_library(const std::string& lib, const std::string& fn, bool dynamic_output,
+                          const std::string& scratch_dir, bool verbose) {
+  const std::string cap = scratch_dir + "/audit.txt";
+  if (run({"nm", "-D", "--undefined-only", lib}, verbose, cap) != 0) return "nm failed on " + lib;
+  static const std::set<std::string> kAllowed = {"ceilf", "erfcf", "erff",   "expf",   "floorf",      "free",
+                                                 "malloc", "memcpy", "memset", "powf", "tanhf", "pthread_once"};
+  std::string unexpected;
+  for (const std::string& s : nm_symbols(read_file(cap)))
+    if (!kAllowed.count(s) && s.rfind("nhip_", 0) != 0) unexpected += (unexpected.empty() ? "" : ", ") + s;
+  if (!unexpected.empty()) return "shared library contains unexpected undefined symbols: " + unexpected;
+  if (run({"nm", "-D", "--defined-only", lib}, verbose, cap) != 0) return "nm failed on " + lib;
+  std::set<std::string> expected = {fn};
+  if (dynamic_output) expected.insert(fn + "_infer_output_shapes");
+  if (nm_symbols(read_file(cap)) != expected) return "shared library exports symbols outside the model ABI entry points";
+  if (run({"readelf", "-d", "-W", lib}, verbose, cap) != 0) return "readelf failed on " + lib;
+  {
+    std::istringstream in(read_file(cap));
+    std::string line;
+    while (std::getline(in, line)) {
+      if (line.find("(NEEDED)") == std::string::npos) continue;
+      const auto a = line.find('['), b = line.find(']');
+      if (a == std::string::npos || b == std::string::npos || b < a) return "unreadable DT_NEEDED entry: " + line;
+      const std::string name = line.substr(a + 1, b - a - 1);
+      auto starts = [&](const char* p) { return name.rfind(p, 0) == 0; };
+      if (!starts("libc.so") && !starts("libm.so") && name != "libnhip.so" && !starts("libamdhip64.so"))
+        return "shared library has an unexpected dependency: " + name;
+    }
+  }
+  if (run({"nm", "-D", lib}, verbose, cap) != 0) return "nm failed on " + lib;
+  const std::string all = read_file(cap);
+  for (const char* forbidden : {"memrefCopy", "runner_utils", "RunnerUtils", "ncnn_runtime"})
+    if (all.find(forbidden) != std::string::npos) return "forbidden runtime symbol found in shared library";
+  std::remove(cap.c_str());
+  return "";
+}
+
+// --verify-execution: the reference's ABI harness (tools/ncnn-compile.cpp:
+// 1383-1636) for fixed-rank models: zero inputs (dynamic extents 2, or the
+// smallest extent a constraint allows), output shapes from
+// <model>_infer_output_shapes, one call that must succeed with finite
+// floating-point outputs, every pointer argument rejected when NULL, and a
+// dynamic output's capacity one short rejected with status 5.
+std::string harness_source(const std::string& fn, const std::vector<Arg>& ins, const std::vector<Arg>& outs) {
+  std::ostringstream c;
+  c << "#include <math.h>\n#include <stddef.h>\n#include <stdio.h>\n#include <stdlib.h>\n#include \"" << fn
+    << ".h\"\n\nstatic size_t element_count(const int64_t *shape, size_t rank) {\n  size_t count = 1;\n"
+    << "  for (size_t i = 0; i < rank; ++i) count *= (size_t)shape[i];\n  return count;\n}\n\nint main(void) {\n";
+  std::vector<std::string> args;
+  for (const Arg& a : ins) {
+    if (a.mask) {
+      c << "  int64_t " << a.name << "_shape[" << a.shape.size() << "] = {";
+      for (size_t k = 0; k < a.shape.size(); ++k) {
+        int64_t e = 2;
+        for (const DimConstraint& d : a.constraints)
+          if (d.dim == (int64_t)k) e = (d.minimum + d.multiple_of - 1) / d.multiple_of * d.multiple_of;
+        c << (k ? ", " : "") << (a.shape[k] < 0 ? e : a.shape[k]);
+      }
+      c << "};\n  size_t " << a.name << "_count = element_count(" << a.name << "_shape, " << a.shape.size() << ");\n";
+    } else {
+      uint64_t e = 1;
+      for (int64_t d : a.shape) e *= (uint64_t)d;
+      c << "  size_t " << a.name << "_count = " << e << ";\n";
+    }
+    c << "  " << a.ctype << " *" << a.name << " = calloc(" << a.name << "_count, sizeof(" << a.ctype << "));\n"
+      << "  if (!" << a.name << ") { fprintf(stderr, \"ABI verification failed: cannot allocate " << a.name
+      << "\\n\"); return 2; }\n";
+  }
+  bool dyn_out = false;
+  std::string shape_call = fn + "_infer_output_shapes(";
+  bool first = true;
+  for (const Arg& a : ins)
+    if (a.mask) {
+      shape_call += (first ? "" : ", ") + a.name + "_shape";
+      first = false;
+    }
+  for (const Arg& a : outs)
+    if (a.mask) {
+      dyn_out = true;
+      c << "  int64_t " << a.name << "_shape[" << a.shape.size() << "] = {0};\n";
+      shape_call += (first ? "" : ", ") + a.name + "_shape";
+      first = false;
+    }
+  shape_call += ")";
+  if (dyn_out) c << "  if (" << shape_call << " != 0) return 6;\n";
+  for (const Arg& a : outs) {
+    if (a.mask) {
+      c << "  size_t " << a.name << "_count = element_count(" << a.name << "_shape, " << a.shape.size() << ");\n"
+        << "  uint64_t " << a.name << "_capacity = " << a.name << "_count;\n";
+    } else {
+      uint64_t e = 1;
+      for (int64_t d : a.shape) e *= (uint64_t)d;
+      c << "  size_t " << a.name << "_count = " << e << ";\n";
+    }
+    c << "  " << a.ctype << " *" << a.name << " = calloc(" << a.name << "_count, sizeof(" << a.ctype << "));\n"
+      << "  if (!" << a.name << ") return 2;\n";
+  }
+  for (const Arg& a : ins) {
+    args.push_back(a.name);
+    if (a.mask) args.push_back(a.name + "_shape");
+  }
+  for (const Arg& a : outs) args.push_back(a.name);
+  for (const Arg& a : outs)
+    if (a.mask) args.push_back(a.name + "_capacity");
+  auto call = [&](long null_index, long short_index) {
+    std::string r = fn + "(";
+    for (size_t i = 0; i < args.size(); ++i)
+      r += (i ? ", " : "") + ((long)i == null_index ? std::string("NULL") : args[i] + ((long)i == short_index ? " - 1" : ""));
+    return r + ")";
+  };
+  c << "  int model_status = " << call(-1, -1) << ";\n"
+    << "  if (model_status != 0) { fprintf(stderr, \"ABI verification failed: model returned %d\\n\", model_status); "
+       "return 4; }\n";
+  for (const Arg& a : outs)
+    if (a.etype == "f32")
+      c << "  for (size_t i = 0; i < " << a.name << "_count; ++i) if (!isfinite(" << a.name
+        << "[i])) { fprintf(stderr, \"ABI verification failed: output " << a.name
+        << "[%zu] is not finite\\n\", i); return 5; }\n";
+  for (size_t i = 0; i < args.size(); ++i) {
+    if (args[i].size() > 9 && args[i].compare(args[i].size() - 9, 9, "_capacity") == 0) continue;
+    c << "  if (" << call((long)i, -1) << " == 0) { fprintf(stderr, \"ABI verification failed: NULL argument "
+      << args[i] << " was accepted\\n\"); return 3; }\n";
+  }
+  for (size_t i = 0; i < args.size(); ++i)
+    if (args[i].size() > 9 && args[i].compare(args[i].size() - 9, 9, "_capacity") == 0)
+      c << "  if (" << call(-1, (long)i) << " != NCNN_STATUS_OUTPUT_CAPACITY_INSUFFICIENT) return 14;\n";
+  for (const Arg& a : ins) c << "  free(" << a.name << ");\n";
+  for (const Arg& a : outs) c << "  free(" << a.name << ");\n";
+  c << "  return 0;\n}\n";
+  return c.str();
+}
+
 }  // namespace
 
 int main(int argc, char** argv) {
@@ -477,14 +716,34 @@ int main(int argc, char** argv) {
       nhip_graph_io_info(g, io, i, &rank, dims, &dtype, nullptr);
       Arg a;
       a.name = (io ? "output" : "input") + std::to_string(i + 1);
-      a.ctype = dtype == NHIP_DTYPE_I8 ? "int8_t" : "float";
-      a.etype = dtype == NHIP_DTYPE_I8 ? "i8" : "f32";
+      // ABI element types of GenerateCAPI.cpp:50-80
+      a.ctype = dtype == NHIP_DTYPE_I8 ? "int8_t" : dtype == NHIP_DTYPE_I32 ? "int32_t" : "float";
+      a.etype = dtype == NHIP_DTYPE_I8 ? "i8" : dtype == NHIP_DTYPE_I32 ? "i32" : "f32";
       for (int k = 0; k < rank; ++k) {
         a.shape.push_back(dims[k]);
         if (dims[k] < 0) a.mask |= 1u << k;
       }
       (io ? outs : ins).push_back(a);
     }
+  // Constraints name dynamic extents of existing inputs, once each.
+  for (size_t a = 0; a < o.constraints.size(); ++a) {
+    const DimConstraint& c = o.constraints[a];
+    if (c.input >= (int64_t)ins.size())
+      die("--input-dim-constraint: input index " + std::to_string(c.input) + " is out of range");
+    Arg& in = ins[(size_t)c.input];
+    if (c.dim >= (int64_t)in.shape.size())
+      die("--input-dim-constraint: dimension " + std::to_string(c.dim) + " is out of range");
+    if (in.shape[(size_t)c.dim] >= 0)
+      die("--input-dim-constraint: input " + std::to_string(c.input) + " dimension " + std::to_string(c.dim) +
+          " is static; constraints apply to '?' extents");
+    for (const DimConstraint& d : in.constraints)
+      if (d.dim == c.dim) die("--input-dim-constraint: duplicate constraint on input " + std::to_string(c.input) +
+                              " dimension " + std::to_string(c.dim));
+    in.constraints.push_back(c);
+  }
+  for (Arg& in : ins)
+    std::sort(in.constraints.begin(), in.constraints.end(),
+              [](const DimConstraint& x, const DimConstraint& y) { return x.dim < y.dim; });
   // Inputs with a dynamic extent need the full [C,H,W] in kShapes.
   if (flat.empty()) {
     for (auto& a : ins) flat.insert(flat.end(), a.shape.begin(), a.shape.end());
@@ -512,13 +771,43 @@ int main(int argc, char** argv) {
   exports += "  local: *;\n};\n";
   write_file(src_dir + "/exports.map", exports);
   const char* cxx = std::getenv("CXX");
+  // Linked like the reference's artifact (tools/ncnn-compile.cpp:2045-2069):
+  // no start files or default libraries, every symbol resolved at link time,
+  // exports from a version script; the wrapper needs no C++ runtime.
+  const std::string lib = stage + "/lib" + fn + ".so";
   std::vector<std::string> cmd = {cxx && *cxx ? cxx : "g++", "-O2", "-fPIC", "-shared", "-std=c++17",
-                                  "-fvisibility=hidden", "-I" + include_dir,
-                                  src_dir + "/" + fn + "_wrapper.cpp", "-o", stage + "/lib" + fn + ".so",
+                                  "-fvisibility=hidden", "-fno-exceptions", "-fno-rtti", "-fno-stack-protector",
+                                  "-nostdlib", "-I" + include_dir, src_dir + "/" + fn + "_wrapper.cpp", "-o", lib,
                                   "-L" + runtime_dir, "-lnhip", "-Wl,-rpath," + runtime_dir,
                                   "-Wl,--version-script=" + src_dir + "/exports.map", "-Wl,-z,defs",
-                                  "-Wl,--build-id=none", "-lpthread"};
-  if (run(cmd, o.verbose) != 0) die("compiling the model library failed");
+                                  "-Wl,--no-undefined", "-Wl,--build-id=none", "-lc"};
+  if (run(cmd, o.verbose) != 0) {
+    run({"rm", "-rf", stage}, o.verbose);
+    die("compiling the model library failed");
+  }
+  bool dynamic_output = false;
+  for (auto& a : outs) dynamic_output |= a.mask != 0;
+  const std::string audit = audit_library(lib, fn, dynamic_output, src_dir, o.verbose);
+  if (!audit.empty()) {
+    run({"rm", "-rf", stage}, o.verbose);
+    die(audit);
+  }
+  if (o.verify_execution) {
+    const char* cc = std::getenv("CC");
+    write_file(src_dir + "/harness.c", harness_source(fn, ins, outs));
+    if (run({cc && *cc ? cc : "gcc", "-std=c11", src_dir + "/harness.c", "-I", stage, "-L", stage, "-l" + fn,
+             "-Wl,-rpath," + stage, "-lm", "-o", src_dir + "/harness"},
+            o.verbose) != 0) {
+      run({"rm", "-rf", stage}, o.verbose);
+      die("ABI verification harness compilation failed");
+    }
+    const int st = run({src_dir + "/harness"}, o.verbose);
+    if (st != 0) {
+      run({"rm", "-rf", stage}, o.verbose);
+      die("ABI execution verification failed with harness exit code " + std::to_string(st), st);
+    }
+    std::cerr << "ncnn-compile: ABI execution verification passed\n";
+  }
   if (o.keep_source) {
     std::rename((src_dir + "/" + fn + "_wrapper.cpp").c_str(), (stage + "/" + fn + "_wrapper.cpp").c_str());
   }

@@ -137,6 +137,95 @@ def test_int8_chain_io_types():
     assert outs == [("q8", [4, 5, 5], 1)]
 
 
+def requantize_model(c=6, hw=5, deq=False, bias=True, act=1):
+    """Input (i32 storage: read by Requantize / Dequantize) -> one layer."""
+    m = ncnn_format.Model()
+    m.input("data", c, hw, hw)
+    b = RNG.standard_normal(c).astype(np.float32) if bias else None
+    if deq:
+        m.dequantize("deq", "data", "out", RNG.uniform(1e-3, 1e-2, c).astype(np.float32), b)
+    else:
+        m.requantize("rq", "data", "out", RNG.uniform(1e-3, 1e-2, c).astype(np.float32), np.float32(4.0), b, act=act)
+    return m
+
+
+def test_quantization_layers_io_types():
+    # Requantize: i32 in, i8 out; Dequantize: i32 in, f32 out
+    st, msg, ins, outs = describe(requantize_model())
+    assert st == 0, msg
+    assert ins == [("data", [6, 5, 5], 2)] and outs == [("out", [6, 5, 5], 1)]
+    st, msg, ins, outs = describe(requantize_model(deq=True))
+    assert st == 0, msg
+    assert ins == [("data", [6, 5, 5], 2)] and outs == [("out", [6, 5, 5], 0)]
+
+
+def test_quantization_layers_consume_raw_fp32_weights_in_order():
+    """test/Unit/malformed_graph_test.cpp:564-597: Quantize (1 scale),
+    Dequantize (scale + bias), Requantize (two scales + bias) read six raw
+    fp32 words in layer order; the reference's importer then rejects the
+    Dequantize, whose operand is the Quantize's i8 output, not i32
+    (NCNNOps.cpp:1440-1442), and a truncated payload names the Requantize
+    bias."""
+    text = ("7767517\n4 4\nInput input 0 1 in\nQuantize quantize 1 1 in quantized 0=1\n"
+            "Dequantize dequantize 1 1 quantized restored 0=1 1=1\n"
+            "Requantize requantize 1 1 restored out 0=1 1=1 2=1 3=0\n")
+
+    class Raw:
+        def __init__(self, payload):
+            self.payload = payload
+
+        def param_text(self):
+            return text
+
+    ones = np.ones(6, "<f4").tobytes()
+    st, msg, _, _ = describe(Raw(ones), shapes=[(1, 1, 1)])
+    assert st == 3 and "Dequantize input must be ranked i32" in msg, msg  # weights loaded, import rejected
+    st, msg, _, _ = describe(Raw(ones[:-1]), shapes=[(1, 1, 1)])
+    assert st == 3 and "truncated" in msg and "Requantize bias" in msg, msg
+
+
+@pytest.mark.parametrize("case,needle", [
+    ("act6", "no activation or ReLU"),
+    ("count", "dimension zero"),
+    ("negative", "invalid Requantize"),
+    ("f32_operand", "int32 operand"),
+])
+def test_quantization_layer_rejections(case, needle):
+    if case == "act6":
+        m = requantize_model(act=6)
+    elif case == "count":  # 4 scales on 6 channels
+        m = ncnn_format.Model()
+        m.input("data", 6, 5, 5)
+        m.dequantize("deq", "data", "out", np.ones(4, np.float32))
+    elif case == "negative":
+        m = requantize_model()
+        m.lines[-1] = m.lines[-1].replace("2=6", "2=-1")
+    else:  # an i32 Input also read by a convolution
+        m = requantize_model()
+        m.conv("c", "data", "c_out", RNG.standard_normal((2, 6, 3, 3)).astype(np.float32))
+    st, msg, _, _ = describe(m)
+    assert st != 0 and needle in msg, msg
+
+
+def test_quantization_model_compiles_with_int32_input(tmp_path):
+    out = compile_model(tmp_path, requantize_model(), "rq", ["--emit-manifest"])
+    h = (out / "rq.h").read_text()
+    assert "int rq(const int32_t *input1, int8_t *output1);" in h
+    man = json.loads((out / "rq.json").read_text())
+    assert man["inputs"][0]["element_type"] == "i32" and man["outputs"][0]["element_type"] == "i8"
+
+
+def test_weight_count_beyond_the_payload_allocates_nothing():
+    # a .param claiming 2^31 weights with an 8-byte .bin fails as truncated
+    m = ncnn_format.Model()
+    m.input("data", 4, 6, 6)
+    m.conv("c", "data", "out", RNG.standard_normal((4, 4, 3, 3)).astype(np.float32))
+    m.lines[-1] = m.lines[-1].replace("6=144", "6=2147483648")
+    m.payload = m.payload[:8]
+    st, msg, _, _ = describe(m)
+    assert st == 3 and "truncated" in msg, msg
+
+
 @pytest.mark.parametrize("case,status,needle", [
     ("softmax", 7, "Softmax 'prob'"),
     ("magic", 3, "magic"),

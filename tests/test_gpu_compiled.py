@@ -205,3 +205,38 @@ def test_mobilenetv2_entry_and_device_batch(tmp_path):
     torch.cuda.synchronize()
     assert_close(yd.cpu().numpy(), exp, 1e-4, "nhip_graph_run batch")
     L.nhip_graph_destroy(g)
+
+
+def test_repeated_host_calls_replay_and_stay_correct(tmp_path):
+    """The generated entry on host buffers, called repeatedly: the second
+    call records the plan on the graph's stream and later calls replay it;
+    every call (new input values each time, the same buffers) matches the
+    oracle, and a call from another thread matches too."""
+    import threading
+    x, w, b = workloads.conv_single(seed=0)
+    m = ncnn_format.Model()
+    m.input("data", 64, 56, 56)
+    m.conv("conv", "data", "output", w, b, act=1)
+    lib = build(tmp_path, m, "conv")
+    lib.conv.argtypes = [P, P]
+    xin = np.empty((64, 56, 56), np.float32)
+    out = np.zeros((64, 56, 56), np.float32)
+    rng = np.random.default_rng(9)
+    for call in range(5):
+        xin[...] = rng.uniform(-1, 1, xin.shape)
+        out[...] = np.nan
+        assert lib.conv(ptr(xin), ptr(out)) == 0
+        exp = refcpu.relu_f32(refcpu.conv2d_f32(refcpu.geom(1, 64, 56, 56, 64), xin[None], w, b))[0]
+        assert_close(out, exp, 1e-3, f"compiled conv call {call}")
+    res = {}
+
+    def worker():
+        o = np.zeros_like(out)
+        res["st"] = lib.conv(ptr(xin), ptr(o))
+        res["out"] = o
+
+    t = threading.Thread(target=worker)
+    t.start()
+    t.join()
+    assert res["st"] == 0
+    np.testing.assert_array_equal(res["out"], out)

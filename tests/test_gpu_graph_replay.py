@@ -153,3 +153,47 @@ def test_buffers_grown_by_a_larger_batch_invalidate_the_recorded_plan(nhip_env):
         g2.run(xa, out=out_a)
         torch.cuda.synchronize()
         assert torch.equal(out_a[0], ref_a)
+
+
+def test_calls_inside_a_callers_capture_run_eagerly_into_it(nhip_env):
+    """A caller capturing its own stream (torch.cuda.graph): the executor
+    sees the capture, records nothing of its own and launches eagerly into
+    the caller's graph; no error is left behind for later calls, and every
+    replay of the caller's graph gives the eager result."""
+    nhip_env.delenv("NHIP_GRAPH_REPLAY", raising=False)
+    g = mobilenet_graph()
+    rng = np.random.default_rng(5)
+    x = torch.from_numpy(rng.uniform(-1, 1, (2, 3, 224, 224)).astype(np.float32)).cuda()
+    ref = eager(g, x, nhip_env)
+    out = [torch.empty_like(ref)]
+    s = torch.cuda.current_stream()
+    g.run(x, out=out, stream=s)  # sizes every buffer before the capture
+    torch.cuda.synchronize()
+    cg = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(cg, stream=s):
+        for _ in range(2):  # twice: the second would record if the capture went unseen
+            g.run(x, out=out, stream=s)
+    torch.cuda.synchronize()
+    for rep in range(4):
+        out[0].fill_(float("nan"))
+        torch.cuda.synchronize()
+        _ = torch.ones(1 << 20, device="cuda").sum()  # the program's own eager work between replays
+        cg.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out[0], ref), f"replay {rep} of the caller's graph"
+    # the next call of the library succeeds and is still correct
+    out[0].fill_(float("nan"))
+    g.run(x, out=out, stream=s)
+    torch.cuda.synchronize()
+    assert torch.equal(out[0], ref)
+    del cg
+    g.close()
+
+
+def test_run_leaves_the_callers_current_device():
+    g = mobilenet_graph()
+    x = torch.zeros((1, 3, 224, 224), device="cuda")
+    before = torch.cuda.current_device()
+    g.run(x)
+    assert torch.cuda.current_device() == before
+    g.close()
