@@ -142,17 +142,34 @@ int parse_param_text(const std::string& text, std::vector<Layer>& layers) {
     }
     return false;
   };
-  int64_t magic = 0;
-  if (!next_line(line) || parse_number(line.substr(0, line.find_last_not_of(" \t\r") + 1), false, &magic, nullptr) ||
-      magic != 7767517)
-    return fail(NHIP_STATUS_CONSTRAINT_VIOLATION, ".param: bad magic (expected 7767517)");
-  if (!next_line(line)) return fail(NHIP_STATUS_CONSTRAINT_VIOLATION, ".param: missing layer/blob counts");
+  // Header (graph.cpp:2139-2170): the magic 7767517 on a line of its own,
+  // or the legacy form with only the "layer_count blob_count" line.
+  if (!next_line(line)) return fail(NHIP_STATUS_CONSTRAINT_VIOLATION, ".param: empty param file");
+  {
+    std::istringstream hs(line);
+    std::vector<std::string> toks;
+    std::string t;
+    while (hs >> t) toks.push_back(t);
+    if (toks.size() == 1) {
+      int64_t magic = 0;
+      if (parse_number(toks[0], false, &magic, nullptr) != NHIP_STATUS_SUCCESS || magic != 7767517)
+        return fail(NHIP_STATUS_CONSTRAINT_VIOLATION, ".param: magic mismatch (expected 7767517)");
+      if (!next_line(line)) return fail(NHIP_STATUS_CONSTRAINT_VIOLATION, ".param: missing layer/blob count header");
+    } else if (toks.size() != 2) {
+      return fail(NHIP_STATUS_CONSTRAINT_VIOLATION, ".param: bad magic / header line");
+    }
+  }
   int64_t layer_count = 0, blob_count = 0;
   {
     std::istringstream hs(line);
-    if (!(hs >> layer_count >> blob_count) || layer_count <= 0 || blob_count <= 0)
-      return fail(NHIP_STATUS_CONSTRAINT_VIOLATION, ".param: bad layer/blob counts");
+    std::string a, b, extra;
+    if (!(hs >> a >> b) || (hs >> extra) || parse_number(a, false, &layer_count, nullptr) != NHIP_STATUS_SUCCESS ||
+        parse_number(b, false, &blob_count, nullptr) != NHIP_STATUS_SUCCESS)
+      return fail(NHIP_STATUS_CONSTRAINT_VIOLATION, ".param: bad layer/blob count header");
+    if (layer_count < 0 || blob_count < 0 || layer_count > (1 << 24) || blob_count > (1 << 24))
+      return fail(NHIP_STATUS_CONSTRAINT_VIOLATION, ".param: layer and blob counts must be non-negative");
   }
+  std::map<std::string, int> producer;  // blob -> producing layer (declared blobs so far)
   while ((int64_t)layers.size() < layer_count && next_line(line)) {
     std::istringstream ls(line);
     Layer L;
@@ -207,10 +224,25 @@ int parse_param_text(const std::string& text, std::vector<Layer>& layers) {
       }
       L.params[(int)id] = P;
     }
+    // Blob bookkeeping (graph.cpp:2257-2282): bottoms are produced by an
+    // earlier layer, every blob has one producer, and no more blobs are
+    // created than the header declares.
+    const int index = (int)layers.size();
+    for (const std::string& b : L.bottoms)
+      if (!producer.count(b))
+        return fail(NHIP_STATUS_CONSTRAINT_VIOLATION,
+                    "layer " + std::to_string(index) + " has unresolved bottom blob: " + b);
+    for (const std::string& t : L.tops) {
+      if (producer.count(t)) return fail(NHIP_STATUS_CONSTRAINT_VIOLATION, "blob has multiple producers: " + t);
+      if ((int64_t)producer.size() >= blob_count)
+        return fail(NHIP_STATUS_CONSTRAINT_VIOLATION, ".param: model creates more blobs than declared");
+      producer[t] = index;
+    }
     layers.push_back(std::move(L));
   }
   if ((int64_t)layers.size() != layer_count)
-    return fail(NHIP_STATUS_CONSTRAINT_VIOLATION, ".param: fewer layers than declared");
+    return fail(NHIP_STATUS_CONSTRAINT_VIOLATION, ".param: truncated before all layers were read");
+  if (next_line(line)) return fail(NHIP_STATUS_CONSTRAINT_VIOLATION, ".param: contains trailing layer lines");
   return ok();
 }
 
@@ -254,13 +286,24 @@ struct BinCursor {
     pos += n;
     return ok();
   }
-  void align4() { pos = std::min(size, (pos + 3) & ~(size_t)3); }
+  // fp16 / int8 payloads are padded to 4 bytes; the padding must be present
+  int align4(const std::string& what) {
+    const size_t to = (pos + 3) & ~(size_t)3;
+    if (to > size) return fail(NHIP_STATUS_CONSTRAINT_VIOLATION, ".bin: weight alignment padding missing after " + what);
+    pos = to;
+    return ok();
+  }
 };
 
 int load_weight(BinCursor& c, int64_t count, bool tagged, Tensor& t, const std::string& what) {
   if (count <= 0 || count > (int64_t)1 << 31) return fail(NHIP_STATUS_INVALID_SHAPE, what + ": bad element count");
   uint32_t flag = 0;
   if (tagged) TRY(c.read(&flag, 4, what + " flag"));
+  if (tagged && flag != 0 && flag != kFlagF32 && flag != kFlagF16 && flag != kFlagI8) {
+    char buf[64];
+    std::snprintf(buf, sizeof buf, " flag 0x%08x is unsupported", flag);
+    return fail(NHIP_STATUS_UNSUPPORTED, what + buf);
+  }
   // The payload must be present before anything is allocated for it (a
   // count taken from a hostile .param cannot force a large allocation).
   const uint64_t esz = (!tagged || flag == 0 || flag == kFlagF32) ? 4 : flag == kFlagF16 ? 2 : 1;
@@ -274,7 +317,7 @@ int load_weight(BinCursor& c, int64_t count, bool tagged, Tensor& t, const std::
   if (flag == kFlagF16) {
     std::vector<uint16_t> h((size_t)count);
     TRY(c.read(h.data(), (size_t)count * 2, what));
-    c.align4();
+    TRY(c.align4(what));
     t.dtype = NHIP_DTYPE_F32;  // fp16 storage is promoted, as the importer does
     t.f.resize((size_t)count);
     for (size_t i = 0; i < h.size(); ++i) t.f[i] = half_to_float(h[i]);
@@ -284,7 +327,7 @@ int load_weight(BinCursor& c, int64_t count, bool tagged, Tensor& t, const std::
     t.dtype = NHIP_DTYPE_I8;
     t.q.resize((size_t)count);
     TRY(c.read(t.q.data(), (size_t)count, what));
-    c.align4();
+    TRY(c.align4(what));
     return ok();
   }
   char buf[64];
@@ -292,7 +335,53 @@ int load_weight(BinCursor& c, int64_t count, bool tagged, Tensor& t, const std::
   return fail(NHIP_STATUS_UNSUPPORTED, what + buf);
 }
 
+// Parameter rules applied before any .bin read: decode_convolution_params
+// and its depthwise twin (graph.cpp:219-397) and decode_inner_product_params
+// (:486-515).  Extents are also bounded so that the shape arithmetic below
+// cannot overflow.
+int check_layer_params(const Layer& L) {
+  const std::string& ty = L.type;
+  constexpr int64_t kMaxExtent = 1 << 16, kMaxCount = (int64_t)1 << 31;
+  auto bad = [&](const std::string& m) { return fail(NHIP_STATUS_CONSTRAINT_VIOLATION, where(L) + m); };
+  if (ty == "Convolution" || ty == "ConvolutionDepthWise") {
+    const int64_t k = L.geti(0, 0), kw = L.geti(1, 0), kh = L.geti(11, kw), dw = L.geti(2, 1), dh = L.geti(12, dw),
+                  sw = L.geti(3, 1), sh = L.geti(13, sw), wsize = L.geti(6, 0), bias = L.geti(5, 0),
+                  term = L.geti(8, 0);
+    if (k <= 0 || k > kMaxCount) return bad("convolution num_output must be positive");
+    if (wsize <= 0 || wsize > kMaxCount) return bad("convolution weight count must be positive");
+    if (kw <= 0 || kh <= 0 || kw > kMaxExtent || kh > kMaxExtent) return bad("convolution kernel dimensions must be positive");
+    if (dw <= 0 || dh <= 0 || dw > kMaxExtent || dh > kMaxExtent) return bad("convolution dilation must be positive");
+    if (sw <= 0 || sh <= 0 || sw > kMaxExtent || sh > kMaxExtent) return bad("convolution stride must be positive");
+    for (int id : {4, 14, 15, 16}) {
+      const int64_t v = L.geti(id, 0);
+      if (v > kMaxExtent || (v < 0 && v != -233 && v != -234)) return bad("convolution padding out of range");
+    }
+    if (bias != 0 && bias != 1) return bad("convolution bias_term must be 0 or 1");
+    if (term != 0 && term != 1 && term != 2 && term != 101 && term != 102)
+      return bad("convolution int8_scale_term must be 0, 1, 2, 101, or 102");
+    if (ty == "Convolution") {
+      if (wsize % (k * kh * kw) != 0) return bad("convolution weight count is not divisible by num_output*kernel_h*kernel_w");
+    } else {
+      const int64_t group = L.geti(7, 1);
+      if (group <= 0 || group > kMaxCount || wsize % group != 0)
+        return bad("convolution depthwise group must be positive and divide the weight count");
+    }
+  } else if (ty == "InnerProduct") {
+    const int64_t n = L.geti(0, 0), wsize = L.geti(2, 0), bias = L.geti(1, 0), term = L.geti(8, 0);
+    if (n <= 0 || n > kMaxCount) return bad("inner product num_output must be positive");
+    if (wsize <= 0 || wsize > kMaxCount || wsize % n != 0)
+      return bad("inner product weight count must be positive and divisible by num_output");
+    if (bias != 0 && bias != 1) return bad("inner product bias_term must be 0 or 1");
+    if (term != 0 && term != 1 && term != 2) return bad("inner product int8_scale_term must be 0, 1, or 2");
+  } else if (ty == "Input") {
+    for (int id : {0, 1, 2})
+      if (L.geti(id, 0) > kMaxCount || L.geti(id, 0) < -1) return bad("Input extent out of range");
+  }
+  return ok();
+}
+
 int load_layer_weights(Layer& L, BinCursor& c) {
+  TRY(check_layer_params(L));
   auto add = [&](int64_t count, bool tagged, const char* what) {
     Tensor t;
     TRY(load_weight(c, count, tagged, t, where(L) + what));
@@ -489,9 +578,14 @@ enum class OpKind {
 struct Shape {
   int rank = 0;
   int64_t d[4] = {0, 0, 0, 0};
+  // -1 when an extent is dynamic; saturates at INT64_MAX instead of
+  // overflowing (the shape checks then reject it)
   int64_t elems() const {
     int64_t e = 1;
-    for (int i = 0; i < rank; ++i) e *= d[i];
+    for (int i = 0; i < rank; ++i) {
+      if (d[i] < 0) return -1;
+      if (__builtin_mul_overflow(e, d[i], &e)) return INT64_MAX;
+    }
     return e;
   }
 };
@@ -719,13 +813,17 @@ int infer_op(const nhip_graph& g, const Op& op, const std::vector<Shape>& sh, Sh
           if (dims[i] == -1) {
             if (infer >= 0) return fail(NHIP_STATUS_UNSUPPORTED, op.name + ": more than one inferred extent");
             infer = (int64_t)i;
-          } else {
-            known *= dims[i];
+          } else if (dims[i] <= 0 || dims[i] > ((int64_t)1 << 31)) {
+            return fail(NHIP_STATUS_INVALID_SHAPE, op.name + ": reshape extents must be positive or -1");
+          } else if (__builtin_mul_overflow(known, dims[i], &known)) {
+            return fail(NHIP_STATUS_SHAPE_ARITHMETIC_OVERFLOW, op.name + ": reshape extents overflow");
           }
         }
         int64_t total = a.elems();
         for (int i = 0; i < a.rank; ++i)
           if (a.d[i] < 0) total = -1;
+        if (infer >= 0 && total >= 0 && total % known != 0)
+          return fail(NHIP_STATUS_INVALID_SHAPE, op.name + ": reshape extents do not divide the element count");
         if (infer >= 0) dims[(size_t)infer] = total < 0 ? -1 : total / known;
         else if (total >= 0 && total != known)
           return fail(NHIP_STATUS_INVALID_SHAPE, op.name + ": reshape changes the element count");
@@ -751,6 +849,7 @@ int propagate(const nhip_graph& g, const int64_t* input_shapes, std::vector<Shap
           return fail(NHIP_STATUS_INVALID_SHAPE, "input " + std::to_string(i + 1) + " extent " + std::to_string(k) +
                                                      " must be " + std::to_string(s.d[k]));
         if (v <= 0) return fail(NHIP_STATUS_INVALID_SHAPE, "input extents must be positive");
+        if (v > ((int64_t)1 << 31)) return fail(NHIP_STATUS_SHAPE_ARITHMETIC_OVERFLOW, "input extent too large");
         s.d[k] = v;
       }
     } else if (concrete) {
@@ -882,7 +981,7 @@ int build(nhip_graph& g, std::vector<Layer>& layers, const int64_t* input_shapes
         return fail(NHIP_STATUS_INVALID_SHAPE, where(L) + "Input dimensions are omitted without an override");
       }
       for (int k = 0; k < 3; ++k)
-        if (s.d[k] == 0 || s.d[k] < -1)
+        if (s.d[k] == 0 || s.d[k] < -1 || s.d[k] > ((int64_t)1 << 31))
           return fail(NHIP_STATUS_INVALID_SHAPE, where(L) + "Input requires positive or dynamic (-1) extents");
       ++next_input;
       if (integer_inputs.count(L.tops[0])) g.blobs[id].dtype = NHIP_DTYPE_I32;
@@ -1236,6 +1335,9 @@ static int load_impl(const char* param_text, uint64_t param_len, const void* bin
     TRY(parse_param_text(std::string(param_text, param_len), layers));
     BinCursor cur{static_cast<const uint8_t*>(bin), (size_t)bin_len};
     for (Layer& L : layers) TRY(load_layer_weights(L, cur));
+    if (bin && cur.pos != cur.size)  // graph.cpp:2299-2306
+      return fail(NHIP_STATUS_CONSTRAINT_VIOLATION, ".bin: size mismatch: consumed " + std::to_string(cur.pos) +
+                                                        " bytes of " + std::to_string(cur.size));
     auto g = std::make_unique<nhip_graph>();
     g->host_only = dry;
     if (!dry) TRY(nhip::device_current(&g->device));  // plans are uploaded to the caller's current device

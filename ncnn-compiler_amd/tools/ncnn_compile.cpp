@@ -472,8 +472,8 @@ std::string wrapper_source(const std::string& fn, const std::vector<Arg>& ins, c
   }
   for (auto& a : outs) s << " || !" << a.name;
   s << ") return 1;  /* NCNN_STATUS_NULL_POINTER */\n"
-    << "  pthread_once(&g_exec_once, init_exec);\n  if (g_exec_status != 0) return g_exec_status;\n"
-    << shape_block() << "  const void* ins[] = {";
+    << shape_block() << "  pthread_once(&g_exec_once, init_exec);\n  if (g_exec_status != 0) return g_exec_status;\n"
+    << "  const void* ins[] = {";
   for (size_t i = 0; i < ins.size(); ++i) s << (i ? ", " : "") << ins[i].name;
   s << "};\n  void* outs[] = {";
   for (size_t j = 0; j < outs.size(); ++j) s << (j ? ", " : "") << outs[j].name;
@@ -519,8 +519,9 @@ std::string wrapper_source(const std::string& fn, const std::vector<Arg>& ins, c
         s << (first ? "" : " || ") << "!" << a.name << "_shape";
         first = false;
       }
-    s << ") return 1;\n  pthread_once(&g_desc_once, init_desc);\n  if (g_desc_status != 0) return g_desc_status;\n"
-      << shape_block() << "  int64_t oshape[" << 4 * outs.size() << "];\n  int32_t orank[" << outs.size() << "];\n"
+    s << ") return 1;\n" << shape_block()
+      << "  pthread_once(&g_desc_once, init_desc);\n  if (g_desc_status != 0) return g_desc_status;\n"
+      << "  int64_t oshape[" << 4 * outs.size() << "];\n  int32_t orank[" << outs.size() << "];\n"
       << "  const int st = nhip_graph_infer_shapes(g_desc, shapes, oshape, orank);\n  if (st != 0) return st;\n";
     for (size_t j = 0; j < outs.size(); ++j)
       if (outs[j].mask)

@@ -216,11 +216,11 @@ def test_quantization_model_compiles_with_int32_input(tmp_path):
 
 
 def test_weight_count_beyond_the_payload_allocates_nothing():
-    # a .param claiming 2^31 weights with an 8-byte .bin fails as truncated
+    # a .param claiming 1.2e9 weights with an 8-byte .bin fails as truncated
     m = ncnn_format.Model()
     m.input("data", 4, 6, 6)
     m.conv("c", "data", "out", RNG.standard_normal((4, 4, 3, 3)).astype(np.float32))
-    m.lines[-1] = m.lines[-1].replace("6=144", "6=2147483648")
+    m.lines[-1] = m.lines[-1].replace("6=144", "6=1207959552")  # 36 * 2^25 weights, passes the parameter rules
     m.payload = m.payload[:8]
     st, msg, _, _ = describe(m)
     assert st == 3 and "truncated" in msg, msg
@@ -327,4 +327,93 @@ def test_compile_failure_publishes_nothing(tmp_path):
     m.save(p, b)
     r = subprocess.run([TOOL, str(p), "-o", str(tmp_path / "out")], capture_output=True, text=True)
     assert r.returncode != 0 and "Softmax 'prob'" in r.stderr
+    assert not (tmp_path / "out").exists()
+
+
+def run_tool(tmp_path, model, name, extra=()):
+    p, b = tmp_path / f"{name}.param", tmp_path / f"{name}.bin"
+    model.save(p, b)
+    return subprocess.run([TOOL, str(p), "-o", str(tmp_path / "out"), *extra], capture_output=True, text=True)
+
+
+@pytest.mark.parametrize("flag,needle", [
+    ("--input-dim-constraint=0:1:min=32", "INPUT:DIM:min=N,multiple=N"),          # multiple missing
+    ("--input-dim-constraint=0:1:min=0,multiple=4", "positive"),                  # non-positive
+    ("--input-dim-constraint=0:1:min=4,multiple=4,min=8", "INPUT:DIM"),           # repeated field
+    ("--input-dim-constraint=1:1:min=4,multiple=4", "input index 1 is out of range"),
+    ("--input-dim-constraint=0:5:min=4,multiple=4", "dimension 5 is out of range"),
+    ("--input-dim-constraint=0:2:min=4,multiple=4", "is static"),
+])
+def test_input_dim_constraint_rejections(tmp_path, flag, needle):
+    r = run_tool(tmp_path, ip_dynamic_model(), "ip", ["--input-shape=1x?x2048", flag])
+    assert r.returncode != 0 and needle in r.stderr, r.stderr
+    assert not (tmp_path / "out").exists()
+
+
+def test_input_dim_constraint_duplicate_rejected(tmp_path):
+    c = "--input-dim-constraint=0:1:min=4,multiple=4"
+    r = run_tool(tmp_path, ip_dynamic_model(), "ip", ["--input-shape=1x?x2048", c, c])
+    assert r.returncode != 0 and "duplicate" in r.stderr
+
+
+def test_input_dim_constraint_header_manifest_and_checks(tmp_path):
+    """docs/ncnn-compile-command-line.md section 2.6: per-dimension minimum
+    and divisor macros (tools/ncnn-compile.cpp:1059-1073), the manifest's
+    dimension_constraints (:818-830), and status 3 from the entry points
+    when an extent breaks them (status 2 first for a non-positive extent)."""
+    out = compile_model(tmp_path, ip_dynamic_model(), "ip",
+                        ["--input-shape=1x?x2048", "--input-dim-constraint=0:1:min=32,multiple=16",
+                         "--emit-manifest"])
+    h = (out / "ip.h").read_text()
+    assert "#define IP_INPUT1_DIM1_MINIMUM INT64_C(32)" in h
+    assert "#define IP_INPUT1_DIM1_MULTIPLE_OF INT64_C(16)" in h
+    man = json.loads((out / "ip.json").read_text())
+    assert man["inputs"][0]["dimension_constraints"] == [{"dimension": 1, "minimum": 32, "multiple_of": 16}]
+    lib = ctypes.CDLL(str(out / "libip.so"))
+    lib.ip_infer_output_shapes.argtypes = [i64p, i64p]
+    oshape = (ctypes.c_int64 * 2)()
+    for m, status in ((48, 0), (32, 0), (16, 3), (40, 3), (0, 2), (-5, 2)):
+        ishape = (ctypes.c_int64 * 3)(1, m, 2048)
+        assert lib.ip_infer_output_shapes(ishape, oshape) == status, m
+    # the model entry checks the same before any device work
+    lib.ip.argtypes = [ctypes.c_void_p, i64p, ctypes.c_void_p, ctypes.c_uint64]
+    buf = np.zeros(64 * 2048, np.float32)
+    ishape = (ctypes.c_int64 * 3)(1, 40, 2048)
+    assert lib.ip(buf.ctypes.data, ishape, buf.ctypes.data, 64 * 1000) == 3
+
+
+def test_artifact_passes_the_extended_audit(tmp_path):
+    """The generated library satisfies the reference's audit rules
+    (tools/ncnn-compile.cpp:2070-2196) as extended for the GPU runtime:
+    exports exactly the entry points, undefined symbols are the reference's
+    libc/libm allowlist plus pthread_once and nhip_*, DT_NEEDED is libc /
+    libm / libnhip, and no forbidden runtime names appear."""
+    for model, extra, name in ((conv_model(c=4, k=4, hw=6), [], "conv"),
+                               (ip_dynamic_model(), ["--input-shape=1x?x2048"], "ip")):
+        (tmp_path / name).mkdir()
+        out = compile_model(tmp_path / name, model, name, extra)
+        lib = str(out / f"lib{name}.so")
+        und = subprocess.run(["nm", "-D", "--undefined-only", lib], capture_output=True, text=True).stdout.split()
+        und = {s.split("@")[0] for s in und if s not in ("U", "w")}
+        assert und <= {"memcpy", "memset", "malloc", "free", "pthread_once"} | {s for s in und if s.startswith("nhip_")}
+        need = subprocess.run(["readelf", "-d", lib], capture_output=True, text=True).stdout
+        needed = {line.split("[")[1].split("]")[0] for line in need.splitlines() if "(NEEDED)" in line}
+        assert needed <= {"libc.so.6", "libm.so.6", "libnhip.so"}, needed
+        allsyms = subprocess.run(["nm", "-D", lib], capture_output=True, text=True).stdout
+        assert not any(f in allsyms for f in ("memrefCopy", "runner_utils", "RunnerUtils", "ncnn_runtime"))
+
+
+def _gpu_present():
+    count = ctypes.c_int32(0)
+    return nhip.load().nhip_device_count(ctypes.byref(count)) == 0 and count.value > 0
+
+
+def test_verify_execution_without_a_gpu_fails_closed(tmp_path):
+    """--verify-execution builds the ABI harness and runs it; on a host with
+    no GPU the model call fails, so the tool fails and publishes nothing
+    (the GPU tests run the passing case)."""
+    if _gpu_present():
+        pytest.skip("a GPU is present: the passing case is covered by the GPU tests")
+    r = run_tool(tmp_path, conv_model(c=4, k=4, hw=6), "conv", ["--verify-execution"])
+    assert r.returncode != 0 and "ABI execution verification failed" in r.stderr, r.stderr
     assert not (tmp_path / "out").exists()

@@ -240,3 +240,62 @@ def test_repeated_host_calls_replay_and_stay_correct(tmp_path):
     t.join()
     assert res["st"] == 0
     np.testing.assert_array_equal(res["out"], out)
+
+
+def _verify(tmp_path, model, name, extra=()):
+    p, b = tmp_path / f"{name}.param", tmp_path / f"{name}.bin"
+    model.save(p, b)
+    r = subprocess.run([TOOL, str(p), "-o", str(tmp_path / name), "--verify-execution", *extra],
+                       capture_output=True, text=True)
+    return r
+
+
+@pytest.mark.parametrize("case", ["static_conv", "dynamic_ip_constrained", "int8_out", "i32_requantize"])
+def test_verify_execution_passes(tmp_path, case):
+    """ncnn-compile --verify-execution (tools/ncnn-compile.cpp:2198-2233):
+    the generated harness calls the library on zero inputs (dynamic extents
+    at a constraint's smallest allowed value), checks finite outputs, NULL
+    rejection for every pointer and the capacity-one-short status 5."""
+    m = ncnn_format.Model()
+    extra = []
+    if case == "static_conv":
+        m.input("data", 8, 12, 12)
+        m.conv("conv", "data", "output", RNG.standard_normal((8, 8, 3, 3)).astype(np.float32),
+               RNG.standard_normal(8).astype(np.float32), act=1)
+    elif case == "dynamic_ip_constrained":
+        x, w, b = workloads.innerproduct(seed=0, m=4, k=64, n=10)
+        m.input("data", 0, 0, 0)
+        m.squeeze("squeeze", "data", "matrix", [0])
+        m.innerproduct("ip", "matrix", "output", w, b)
+        extra = ["--input-shape=1x?x64", "--input-dim-constraint=0:1:min=5,multiple=4"]
+    elif case == "int8_out":
+        m.input("data", 8, 6, 6)
+        m.conv("q", "data", "output", RNG.integers(-127, 128, (4, 8, 3, 3)).astype(np.int8),
+               RNG.standard_normal(4).astype(np.float32),
+               int8=dict(term=101, ws=np.full(4, 50.0, np.float32), **{"is": 20.0, "os": 10.0}))
+    else:
+        m.input("data", 6, 4, 4)
+        m.requantize("rq", "data", "output", np.full(6, 1e-3, np.float32), np.float32(2.0), None, act=1)
+    r = _verify(tmp_path, m, "v", extra)
+    assert r.returncode == 0, r.stderr
+    assert "ABI execution verification passed" in r.stderr
+
+
+def test_dynamic_constraint_checked_per_call(tmp_path):
+    """A dynamic-M InnerProduct compiled with min=32,multiple=32 on M: a
+    call with M=48 is status 3 (nothing runs), M=64 runs and matches the
+    oracle."""
+    x, w, b = workloads.innerproduct(seed=1, m=64, k=256, n=100)
+    m = ncnn_format.Model()
+    m.input("data", 0, 0, 0)
+    m.squeeze("squeeze", "data", "matrix", [0])
+    m.innerproduct("ip", "matrix", "output", w, b)
+    lib = build(tmp_path, m, "ipc", ["--input-shape=1x?x256", "--input-dim-constraint=0:1:min=32,multiple=32"])
+    lib.ipc.argtypes = [P, ctypes.POINTER(ctypes.c_int64), P, ctypes.c_uint64]
+    out = np.full((64, 100), np.nan, np.float32)
+    bad = (ctypes.c_int64 * 3)(1, 48, 256)
+    assert lib.ipc(ptr(x), bad, ptr(out), out.size) == 3
+    assert np.isnan(out).all()
+    good = (ctypes.c_int64 * 3)(1, 64, 256)
+    assert lib.ipc(ptr(x), good, ptr(out), out.size) == 0
+    assert_close(out, refcpu.innerproduct_f32(x, w, b), 1e-4, "constrained dynamic-M InnerProduct")
