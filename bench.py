@@ -1,36 +1,52 @@
-"""Benchmark: ResNet-18-shape 3x3 conv stack, batch 32, fp32,
-through the libnhip C ABI on one MI355X, plus the int8 requantized conv
-(config 4) as a secondary figure.
+"""Benchmark: the ResNet-18-shape 3x3 conv stack, batch 32, fp32 (BASELINE
+config 3) is the headline `value`; configs 1, 2, 4 and 5 are measured in the
+same run and reported under `config`, each with the roofline of its dominant
+kernel and a CPU baseline.
 
-Secondary figures in the same line: the int8 conv (config 4) and the
-MobileNetV2-shape graph at batch 32 (config 5).
+One step (config 3) = the four ResNet-18 basic-block stages (64@56, 128@28,
+256@14, 512@7), each two 3x3 s1 p1 convs with folded-BN bias, ReLU and the
+residual add: 8 Winograd F(4,3) convolutions over 32 images whose inputs are
+already resident in HBM.  value = direct-equivalent conv TFLOP/s
+(2*N*K*OH*OW*C*9 per conv, the same count for Winograd as for direct
+convolution).
 
-One step = the four ResNet-18 basic-block stages (64@56, 128@28, 256@14,
-512@7), each two 3x3 s1 p1 convs with folded-BN bias, ReLU and the residual
-add: 8 Winograd F(4,3) convolutions over 32 images whose inputs are already
-resident in HBM.
+Every timed region runs exactly K steps between synchronizations with no
+per-launch instrumentation; kernel durations come from a second run of the
+same K steps with HIP events that each kernel's own dispatch stamps on its
+launch stream (nhip_timer_*).
 
-value = direct-equivalent conv TFLOP/s (2*N*K*OH*OW*C*9 per conv, the same
-count for Winograd as for direct convolution).  roofline = the dominant
-kernel, the Winograd GEMM with the output transform fused (wino_fused: 36
-fp32 MFMA GEMMs and the output transform per conv; it runs the three stages
-with at least 256 tiles, the 512@7 stage takes the three-kernel path): its
-work 2*36*T*C*K per launch (T = N*ceil(OH/4)*ceil(OW/4) tiles) over its
-duration, from HIP events stamped by each of its dispatches on the launch
-stream over a second run of the same K steps (the events cost ~5% of a
-step, so the timed region that gives value runs without them); traffic = its HBM bytes per launch from the
-committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary
-(profiles/wino_fused_traffic.json).  cpu_baseline = the
-CPU oracle (restatement of the reference's lowered loops, compiled like the
-reference's .so: -O3, no -march, no FP contraction, OpenMP) on a bounded
-sample of the same stages.
+Secondary figures:
+- config 1: one 64->64 3x3 conv on 1x64x56x56 through the layer ABI
+  (device buffers), and the same model through the library ncnn-compile
+  writes, called on host buffers (the reference's entry: H2D, kernels, D2H);
+- config 2: InnerProduct 256x2048 -> 1000 (device buffers);
+- config 4: int8 conv 32x128x28x28 -> 128, requantize (term 101) + ReLU,
+  fp32 input (quantize pass + int8 MFMA GEMM);
+- config 5: the MobileNetV2-shape graph at batch 32 through the native
+  executor from its .param/.bin form, and the compiled library on one image
+  from host buffers.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+roofline: the dominant kernel's algorithmic work per launch over its average
+duration.  For config 3 that is the Winograd GEMM with the output transform
+fused (wino_fused: executed FLOPs 2*36*T*C*K per launch, T tiles); traffic =
+its HBM bytes per launch from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE
+summary (profiles/wino_fused_traffic.json, copy-calibrated).
+
+cpu_baseline: the CPU oracle (a restatement of the reference's lowered loop
+nests, compiled like the reference's .so: -O3, no -march, no FP contraction,
+OpenMP over the outer loops) on bounded samples, one image per call as the
+reference's entry runs, with all threads of this job's CPU share and with one
+thread.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
 """
 import argparse
+import ctypes
 import json
 import os
+import subprocess
 import sys
+import tempfile
 import time
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
@@ -41,9 +57,126 @@ for p in (ROOT, os.path.join(ROOT, "ncnn-compiler_amd")):
 METRIC = "conv TFLOP/s (% MFMA peak) + images/sec, ResNet-18-shape b32 fp32/int8"
 PEAK_FP32_TFLOPS = 157.3
 PEAK_INT8_TOPS = 5000.0
+PEAK_HBM_GBS = 8000.0
 BATCH = 32
+TOOL = os.path.join(ROOT, "ncnn-compiler_amd", "bin", "ncnn-compile")
 
 
+# ----------------------------------------------------------------- helpers
+def timed(torch, fn, steps):
+    """Wall time per call of `fn` over exactly `steps` calls, synchronized on
+    both sides (seconds)."""
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        fn()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) / steps
+
+
+def kernel_time(nhip, torch, fn, steps, name):
+    """(launches per call, seconds per launch) of the kernels whose name
+    contains `name`, from HIP events on their own dispatches."""
+    torch.cuda.synchronize()
+    nhip.timer_start(name)
+    for _ in range(steps):
+        fn()
+    torch.cuda.synchronize()
+    launches, ms = nhip.timer_stop()
+    if launches == 0:
+        return 0, 0.0
+    return launches / steps, ms / 1e3 / launches
+
+
+def dominant(nhip, torch, fn, steps, names):
+    """The kernel of `names` with the largest time per call:
+    (name, launches per call, seconds per launch)."""
+    best = None
+    for nm in names:
+        per, sec = kernel_time(nhip, torch, fn, steps, nm)
+        if per and (best is None or per * sec > best[1] * best[2]):
+            best = (nm, per, sec)
+    return best
+
+
+def roofline(bound, kernel, work_per_launch, sec_per_launch, launches_per_step, traffic=None):
+    peak, unit = {"mfma": (PEAK_FP32_TFLOPS, "TFLOP/s"), "mfma_int8": (PEAK_INT8_TOPS, "TOP/s"),
+                  "hbm": (PEAK_HBM_GBS, "GB/s")}[bound]
+    achieved = work_per_launch / sec_per_launch / (1e9 if bound == "hbm" else 1e12)
+    return {"bound": "mfma" if bound.startswith("mfma") else "hbm", "kernel": kernel, "achieved": round(achieved, 3),
+            "peak": peak, "unit": unit, "frac": round(achieved / peak, 4), "traffic": traffic,
+            "avg_launch_us": round(sec_per_launch * 1e6, 2), "launches_per_step": round(launches_per_step, 2)}
+
+
+def rounded(d):
+    if isinstance(d, dict):
+        return {k: rounded(v) for k, v in d.items()}
+    return round(d, 4) if isinstance(d, float) else d
+
+
+def cpu_info():
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    share = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or (os.cpu_count() or 1)
+    return model, os.cpu_count() or 1, share
+
+
+def cpu_rate(fn, work, target_s):
+    """Repeat fn until about target_s elapsed: (work units per second,
+    calls made, seconds)."""
+    fn()  # warm
+    t0 = time.perf_counter()
+    calls = 0
+    while True:
+        fn()
+        calls += 1
+        dt = time.perf_counter() - t0
+        if dt >= target_s:
+            return work * calls / dt, calls, dt
+
+
+def cpu_pair(fn_threads, work, unit, what, target_s, share):
+    """The same sample with all threads of the job's share and with one."""
+    out = {}
+    for label, threads in (("all", share), ("one", 1)):
+        rate, calls, dt = cpu_rate(lambda: fn_threads(threads), work, target_s)
+        out[label] = {"value": rate, "unit": unit, "threads": threads,
+                      "sample": f"{calls} x {what} in {dt:.1f} s"}
+    return out
+
+
+def compile_model(model, name, workdir, extra=()):
+    """The model through ncnn-compile -> ctypes handle of lib<name>.so, or
+    None when the tool has not been built."""
+    if not os.path.exists(TOOL):
+        return None
+    p, b = os.path.join(workdir, f"{name}.param"), os.path.join(workdir, f"{name}.bin")
+    model.save(p, b)
+    r = subprocess.run([TOOL, p, "-o", os.path.join(workdir, name), *extra], capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(r.stderr)
+    return ctypes.CDLL(os.path.join(workdir, name, f"lib{name}.so"))
+
+
+def host_entry_latency(entry, args, calls):
+    """Seconds per call of a generated entry on host buffers (synchronous:
+    H2D, kernels, D2H), after warm calls."""
+    for _ in range(5):
+        assert entry(*args) == 0
+    t0 = time.perf_counter()
+    for _ in range(calls):
+        entry(*args)
+    return (time.perf_counter() - t0) / calls
+
+
+# ------------------------------------------------------------ config 3
 def stage_stack(nhip, workloads, torch, batch):
     stages = []
     for c, hw in workloads.RESNET18_STAGES:
@@ -66,87 +199,11 @@ def run_step(stages):
         s["conv2"].forward(s["y"], residual=s["x"], out=s["out"], workspace=s["ws"])
 
 
-def cpu_baseline(workloads, target_s=12.0):
-    """Oracle on a bounded sample: one image per stage through both convs,
-    the relu and the residual add, repeated until about target_s elapsed."""
-    from oracle import refcpu
-    threads = min(16, os.cpu_count() or 1)
-    samples = []
-    for c, hw in workloads.RESNET18_STAGES:
-        x, w1, b1, w2, b2 = workloads.resnet_stage(c, hw, n=1, seed=0)
-        samples.append((c, hw, x, w1, b1, w2, b2))
-    flops = 0.0
-    t0 = time.perf_counter()
-    rounds = 0
-    while True:
-        for c, hw, x, w1, b1, w2, b2 in samples:
-            g = refcpu.geom(1, c, hw, hw, c)
-            y = refcpu.relu_f32(refcpu.conv2d_f32(g, x, w1, b1, threads=threads))
-            refcpu.relu_f32(refcpu.add_f32(refcpu.conv2d_f32(g, y, w2, b2, threads=threads), x))
-            flops += 2 * workloads.conv_flops(1, c, c, hw, hw)
-        rounds += 1
-        if time.perf_counter() - t0 >= target_s:
-            break
-    dt = time.perf_counter() - t0
-    return {"value": flops / dt / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
-            "sample": f"{rounds} x (1 image through each of the 4 stages: 8 convs + relu + add), "
-                      f"{dt:.1f} s, OpenMP {threads} threads; {rounds / dt:.3f} images/s through the stack"}
-
-
-def int8_secondary(nhip, workloads, torch, steps, warmup):
-    cfg = workloads.int8_conv(seed=0, n=BATCH)
-    d = nhip.conv_desc(128, 128, act=nhip.ACT_RELU, int8_scale_term=101)
-    conv = nhip.Conv2dInt8(d, cfg["w"], cfg["bias"], cfg["ws"], cfg["input_scale"], cfg["output_scale"])
-    x = torch.from_numpy(cfg["x"]).cuda()
-    out = torch.empty((BATCH, 128, 28, 28), dtype=torch.int8, device="cuda")
-    ws = torch.empty(conv.workspace_size(BATCH, 28, 28), dtype=torch.uint8, device="cuda")
-    for _ in range(warmup):
-        conv.forward(x, out=out, workspace=ws)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(steps):
-        conv.forward(x, out=out, workspace=ws)
-    torch.cuda.synchronize()
-    dt = (time.perf_counter() - t0) / steps
-    nhip.timer_start("conv_int8")  # the GEMM kernel's duration, in a second instrumented pass
-    for _ in range(steps):
-        conv.forward(x, out=out, workspace=ws)
-    torch.cuda.synchronize()
-    launches, kms = nhip.timer_stop()
-    ops = workloads.conv_flops(BATCH, 128, 128, 28, 28)
-    kavg = kms / max(launches, 1) / 1e3
-    return {"workload": "int8 conv 32x128x28x28 3x3 requant(term 101)+relu, fp32 input",
-            "ms_per_step": dt * 1e3, "tops": ops / dt / 1e12,
-            "images_per_sec": BATCH / dt,
-            "gemm_kernel_tops": ops / kavg / 1e12,
-            "gemm_kernel_frac_int8_peak": ops / kavg / 1e12 / PEAK_INT8_TOPS}
-
-
-def mobilenetv2_secondary(nhip, torch, steps, warmup):
-    """The graph runs through the native executor (`nhip_graph_run`) from
-    its .param/.bin form, as a compiled model would (on torch's default
-    stream, so every kernel is launched eagerly: replay of a recorded
-    hipGraph applies to calls on other streams and measured the same GPU
-    time)."""
-    import graphs
-    import ncnn_format
-    layers = graphs.mobilenetv2_layers(seed=0)
-    m = ncnn_format.from_layer_list(layers)
-    g = nhip.Graph(m.param_text(), bytes(m.payload))
-    x = torch.from_numpy(
-        __import__("numpy").random.default_rng(0).uniform(-1, 1, (BATCH, 3, 224, 224)).astype("float32")).cuda()
-    out = g.run(x)  # outputs reused by every step
-    for _ in range(warmup):
-        g.run(x, out=out)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(steps):
-        g.run(x, out=out)
-    torch.cuda.synchronize()
-    dt = (time.perf_counter() - t0) / steps
-    flops = graphs.graph_flops(layers, BATCH, 224, 224)
-    return {"workload": "MobileNetV2-shape graph b32 224x224 fp32 (53 conv/dw layers, GAP, IP 1280->1000), native graph executor",
-            "ms_per_step": dt * 1e3, "images_per_sec": BATCH / dt, "tflops": flops / dt / 1e12}
+def fused_stage(c, hw):
+    """The library's default Winograd path choice: the fused GEMM from 256
+    tiles up (winograd.hip, fused_selected)."""
+    t = -(-hw // 4)
+    return BATCH * t * t >= 256
 
 
 def measured_traffic(kernel):
@@ -161,11 +218,220 @@ def measured_traffic(kernel):
         return None
 
 
-def fused_stage(c, hw):
-    """The library's default Winograd path choice: the fused GEMM from 256
-    tiles up (winograd.hip, direct_selected / fused_selected)."""
-    t = -(-hw // 4)
-    return BATCH * t * t >= 256
+def cpu_config3(workloads, share, target_s):
+    from oracle import refcpu
+    samples = []
+    for c, hw in workloads.RESNET18_STAGES:
+        x, w1, b1, w2, b2 = workloads.resnet_stage(c, hw, n=1, seed=0)
+        samples.append((c, hw, x, w1, b1, w2, b2))
+
+    def one_image(threads):
+        for c, hw, x, w1, b1, w2, b2 in samples:
+            g = refcpu.geom(1, c, hw, hw, c)
+            y = refcpu.relu_f32(refcpu.conv2d_f32(g, x, w1, b1, threads=threads))
+            refcpu.relu_f32(refcpu.add_f32(refcpu.conv2d_f32(g, y, w2, b2, threads=threads), x))
+
+    flops = sum(2 * workloads.conv_flops(1, c, c, hw, hw) for c, hw in workloads.RESNET18_STAGES)
+    return cpu_pair(one_image, flops / 1e12, "TFLOP/s", "(1 image through the 4 stages: 8 convs + relu + add)",
+                    target_s, share)
+
+
+# ------------------------------------------------------------ config 1
+def config1(nhip, workloads, torch, steps, warmup, workdir, share, cpu, target_s):
+    import ncnn_format
+    x, w, b = workloads.conv_single(seed=0)
+    d = nhip.conv_desc(64, 64, act=nhip.ACT_RELU)
+    conv = nhip.Conv2dF32(d, w, b)
+    xd = torch.from_numpy(x).cuda()
+    out = torch.empty((1, 64, 56, 56), device="cuda")
+    ws = torch.empty(max(conv.workspace_size(1, 56, 56), 256), dtype=torch.uint8, device="cuda")
+
+    def fn():
+        conv.forward(xd, out=out, workspace=ws)
+
+    for _ in range(warmup):
+        fn()
+    n = max(steps * 10, 100)
+    dt = timed(torch, fn, n)
+    flops = workloads.conv_flops(1, 64, 64, 56, 56)
+    # one image = 196 Winograd tiles: the three-kernel path (input transform,
+    # batched GEMM, output transform) or the fused GEMM, whichever the
+    # library picks; the roofline is the GEMM's
+    name, per, sec = dominant(nhip, torch, fn, n, ["wino_gemm", "wino_fused"])
+    wflops = workloads.winograd_flops(1, 64, 64, 56, 56)
+    kernels = {}
+    for k in ("wino_input_transform", "wino_gemm", "wino_output_transform", "wino_fused"):
+        kp, ks = kernel_time(nhip, torch, fn, n, k)
+        if kp:
+            kernels[k] = round(kp * ks * 1e6, 2)
+    res = {"workload": "conv fp32 1x64x56x56 -> 64, 3x3 s1 p1, bias + ReLU (Winograd F(4,3), device buffers)",
+           "ms_per_step": dt * 1e3, "tflops_direct_equivalent": flops / dt / 1e12, "images_per_sec": 1 / dt,
+           "kernel_us_per_step": kernels,
+           "roofline": roofline("mfma", f"{name} (executed 2*36*T*C*K, T=196 tiles)", wflops / per, sec, per)}
+    m = ncnn_format.Model()
+    m.input("data", 64, 56, 56)
+    m.conv("conv", "data", "output", w, b, act=1)
+    lib = compile_model(m, "conv", workdir)
+    if lib is not None:
+        lib.conv.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+        xh = x[0].copy()
+        oh = __import__("numpy").empty((64, 56, 56), "float32")
+        lat = host_entry_latency(lib.conv, (xh.ctypes.data, oh.ctypes.data), max(steps * 5, 50))
+        res["dropin_entry"] = {"what": "generated int conv(const float*, float*) on host buffers, one image "
+                                       "(H2D + kernels + D2H, synchronous)",
+                               "ms_per_call": lat * 1e3, "images_per_sec": 1 / lat}
+    if cpu:
+        from oracle import refcpu
+        g = refcpu.geom(1, 64, 56, 56, 64)
+        res["cpu_baseline"] = cpu_pair(
+            lambda t: refcpu.relu_f32(refcpu.conv2d_f32(g, x, w, b, threads=t)), flops / 1e12, "TFLOP/s",
+            "(1 image: conv + bias + relu)", target_s, share)
+    return res
+
+
+# ------------------------------------------------------------ config 2
+def config2(nhip, workloads, torch, steps, warmup, share, cpu, target_s):
+    x, w, b = workloads.innerproduct(seed=0)
+    ip = nhip.InnerProductF32(w, b)
+    xd = torch.from_numpy(x).cuda()
+    out = torch.empty((256, 1000), device="cuda")
+    ws = torch.empty(max(ip.workspace_size(256), 256), dtype=torch.uint8, device="cuda")
+
+    def fn():
+        ip.forward(xd, out=out, workspace=ws)
+
+    for _ in range(warmup):
+        fn()
+    n = max(steps * 10, 100)
+    dt = timed(torch, fn, n)
+    flops = 2.0 * 256 * 1000 * 2048
+    per, sec = kernel_time(nhip, torch, fn, n, "innerproduct_f32")
+    res = {"workload": "InnerProduct fp32 256x2048 -> 1000 + bias (device buffers)",
+           "ms_per_step": dt * 1e3, "tflops": flops / dt / 1e12,
+           "roofline": roofline("mfma", "innerproduct_f32 (MFMA GEMM, split-K partials)", flops / per, sec, per)}
+    if cpu:
+        from oracle import refcpu
+        res["cpu_baseline"] = cpu_pair(lambda t: refcpu.innerproduct_f32(x, w, b, threads=t), flops / 1e12,
+                                       "TFLOP/s", "(256x2048 @ 2048x1000 + bias)", target_s, share)
+    return res
+
+
+# ------------------------------------------------------------ config 4
+def config4(nhip, workloads, torch, steps, warmup, share, cpu, target_s):
+    cfg = workloads.int8_conv(seed=0, n=BATCH)
+    d = nhip.conv_desc(128, 128, act=nhip.ACT_RELU, int8_scale_term=101)
+    conv = nhip.Conv2dInt8(d, cfg["w"], cfg["bias"], cfg["ws"], cfg["input_scale"], cfg["output_scale"])
+    x = torch.from_numpy(cfg["x"]).cuda()
+    out = torch.empty((BATCH, 128, 28, 28), dtype=torch.int8, device="cuda")
+    ws = torch.empty(max(conv.workspace_size(BATCH, 28, 28), 256), dtype=torch.uint8, device="cuda")
+
+    def fn():
+        conv.forward(x, out=out, workspace=ws)
+
+    for _ in range(warmup):
+        fn()
+    n = max(steps * 5, 50)
+    dt = timed(torch, fn, n)
+    ops = workloads.conv_flops(BATCH, 128, 128, 28, 28)
+    per, sec = kernel_time(nhip, torch, fn, n, "conv_int8")
+    qper, qsec = kernel_time(nhip, torch, fn, n, "quantize")
+    res = {"workload": "int8 conv 32x128x28x28 3x3 requant(term 101)+relu, fp32 input",
+           "ms_per_step": dt * 1e3, "tops": ops / dt / 1e12, "images_per_sec": BATCH / dt,
+           "roofline": roofline("mfma_int8", "conv_int8 (int8 MFMA GEMM, exact requantize epilogue)", ops / per,
+                                sec, per)}
+    if qper:
+        # quantize pass: reads the fp32 input once, writes the int8 NHWC image
+        qbytes = BATCH * 128 * 28 * 28 * 5
+        res["quantize_kernel"] = {"avg_launch_us": round(qsec * 1e6, 2),
+                                  "gbs": round(qbytes / qsec / 1e9, 1),
+                                  "frac_hbm": round(qbytes / qsec / 1e9 / PEAK_HBM_GBS, 4)}
+    if cpu:
+        from oracle import refcpu
+        g = refcpu.geom(1, 128, 28, 28, 128)
+        x1 = cfg["x"][:1]
+        res["cpu_baseline"] = cpu_pair(
+            lambda t: refcpu.conv2d_int8(g, x1, cfg["w"], cfg["bias"], cfg["ws"], 1.0, 1.0, 101, 1, threads=t),
+            ops / BATCH / 1e12, "TOP/s", "(1 image: quantize, int8 conv, requantize, relu)", target_s, share)
+    return res
+
+
+# ------------------------------------------------------------ config 5
+def config5(nhip, torch, steps, warmup, workdir, share, cpu, target_s):
+    import numpy as np
+
+    import graphs
+    import ncnn_format
+    layers = graphs.mobilenetv2_layers(seed=0)
+    m = ncnn_format.from_layer_list(layers)
+    g = nhip.Graph(m.param_text(), bytes(m.payload))
+    x = torch.from_numpy(np.random.default_rng(0).uniform(-1, 1, (BATCH, 3, 224, 224)).astype(np.float32)).cuda()
+    flops = graphs.graph_flops(layers, BATCH, 224, 224)
+    gbytes = graphs.graph_bytes(layers, BATCH, 224, 224)
+    res = {"workload": "MobileNetV2-shape graph b32 224x224 fp32 (53 conv/dw layers, GAP, IP 1280->1000), "
+                       "native graph executor from the .param/.bin form"}
+    # eager launches on torch's default (legacy) stream, and the steady-state
+    # path on a side stream where repeated calls replay a recorded hipGraph
+    for label, stream in (("eager", None), ("replay", torch.cuda.Stream())):
+        out = g.run(x)
+        ctx = torch.cuda.stream(stream) if stream is not None else None
+        if ctx:
+            ctx.__enter__()
+
+        def fn():
+            g.run(x, out=out, stream=stream)
+
+        for _ in range(max(warmup, 3)):
+            fn()
+        dt = timed(torch, fn, steps)
+        if ctx:
+            ctx.__exit__(None, None, None)
+        res[label] = {"ms_per_step": dt * 1e3, "images_per_sec": BATCH / dt, "tflops": flops / dt / 1e12}
+    best = min(res["eager"]["ms_per_step"], res["replay"]["ms_per_step"]) / 1e3
+    res["ms_per_step"] = best * 1e3
+    res["images_per_sec"] = BATCH / best
+    res["roofline"] = {"bound": "hbm", "kernel": "whole graph (layer-by-layer algorithmic bytes: every layer reads "
+                                                 "its input and weights once and writes its output once)",
+                       "achieved": round(gbytes / best / 1e9, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                       "frac": round(gbytes / best / 1e9 / PEAK_HBM_GBS, 4), "traffic": None,
+                       "bytes_per_step": int(gbytes)}
+    lib = compile_model(m, "mbv2", workdir)
+    if lib is not None:
+        lib.mbv2.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+        xh = x[0].cpu().numpy().copy()
+        oh = np.empty(1000, np.float32)
+        lat = host_entry_latency(lib.mbv2, (xh.ctypes.data, oh.ctypes.data), max(steps, 20))
+        res["dropin_entry"] = {"what": "generated int mbv2(const float*, float*) on host buffers, one image "
+                                       "(H2D + 57 kernels or their replay + D2H, synchronous)",
+                               "ms_per_call": lat * 1e3, "images_per_sec": 1 / lat}
+    if cpu:
+        from oracle import refcpu
+        x1 = x[:1].cpu().numpy()
+
+        def one_image(threads):
+            blobs = {"data": x1}
+            for L in layers:
+                src = blobs[L["src"]]
+                n, c, h, w = src.shape if src.ndim == 4 else (src.shape[0], src.shape[1], 1, 1)
+                if L["kind"] == "conv":
+                    p = L["pad"]
+                    gg = refcpu.geom(n, c, h, w, L["k"], (L["kernel"],) * 2, (L["stride"],) * 2, (1, 1), (p,) * 4)
+                    y = refcpu.conv2d_f32(gg, src, L["w"], L["b"], threads=threads)
+                    if L["residual"]:
+                        y = refcpu.add_f32(y, blobs[L["residual"]])
+                    if L["act"] == 1:
+                        y = refcpu.relu_f32(y)
+                elif L["kind"] == "dw":
+                    gg = refcpu.geom(n, c, h, w, c, (3, 3), (L["stride"],) * 2, (1, 1), (1, 1, 1, 1))
+                    y = refcpu.relu_f32(refcpu.dwconv2d_f32(gg, src, L["w"], L["b"], threads=threads))
+                elif L["kind"] == "gap":
+                    y = refcpu.global_avgpool_f32(src)
+                else:
+                    y = refcpu.innerproduct_f32(src.reshape(n, -1), L["w"], L["b"], threads=threads)
+                blobs[L["dst"]] = y
+
+        res["cpu_baseline"] = cpu_pair(one_image, 1.0, "images/s", "(1 image through the whole graph)",
+                                       target_s, share)
+    return res
 
 
 def main():
@@ -174,6 +440,9 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=3.0,
+                    help="length of each bounded CPU-baseline sample (per config and thread count)")
+    ap.add_argument("--only-config3", action="store_true", help="skip the secondary configurations")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="first run a plain device copy of this many MiB (hipMemcpy D2D) so that "
                          "rocprofv3 FETCH_SIZE/WRITE_SIZE can be scaled against known bytes")
@@ -198,27 +467,22 @@ def main():
             nhip.check(nhip.load().nhip_memcpy_d2d(nhip._ptr(dst), nhip._ptr(src), nbytes, nhip._stream()))
         torch.cuda.synchronize()
         del src, dst
+    cpu = not args.no_cpu_baseline
+    model, host_cpus, share = cpu_info()
+
+    # ---- config 3: the headline
     stages = stage_stack(nhip, workloads, torch, BATCH)
     for _ in range(args.warmup):
         run_step(stages)
     torch.cuda.synchronize()
-
-    variant = os.environ.get("NHIP_WINOGRAD_VARIANT", "")
-    fused_convs = [(c, hw) for c, hw in workloads.RESNET18_STAGES
-                   if variant == "2" or (variant != "1" and fused_stage(c, hw))]
+    fused_convs = [(c, hw) for c, hw in workloads.RESNET18_STAGES if fused_stage(c, hw)]
     kernel = "wino_fused" if fused_convs else "wino_gemm"
     kernel_convs = fused_convs or list(workloads.RESNET18_STAGES)
-    # The timed region: exactly K steps, no per-launch instrumentation.
-    torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
         run_step(stages)
     torch.cuda.synchronize()
     t1 = time.perf_counter()
-    # The same K steps again with HIP events on every launch of the roofline
-    # kernel (stamped by its dispatches on the launch stream): its average
-    # duration.  The events cost ~5% of a step, so the throughput above is
-    # taken without them.
     nhip.timer_start(kernel)
     torch.cuda.synchronize()
     t2 = time.perf_counter()
@@ -234,14 +498,23 @@ def main():
     wino_flops = sum(2 * workloads.winograd_flops(BATCH, c, c, hw, hw) for c, hw in workloads.RESNET18_STAGES)
     kernel_flops = sum(2 * workloads.winograd_flops(BATCH, c, c, hw, hw) for c, hw in kernel_convs)
     value = direct_flops / (ms_per_step / 1e3) / 1e12
-    # two convs per stage; each runs as one or two batch parts (one kernel launch each)
     per_step = launches // args.steps
     assert launches % args.steps == 0 and per_step in (2 * len(kernel_convs), 4 * len(kernel_convs)), \
         (launches, args.steps, kernel_convs)
     kernel_s_per_step = kernel_ms / args.steps / 1e3
     achieved = kernel_flops / kernel_s_per_step / 1e12
-    int8 = int8_secondary(nhip, workloads, torch, args.steps, args.warmup)
-    mbv2 = mobilenetv2_secondary(nhip, torch, args.steps, args.warmup)
+
+    secondary = {}
+    with tempfile.TemporaryDirectory() as workdir:
+        if not args.only_config3:
+            secondary["config1_conv"] = config1(nhip, workloads, torch, args.steps, args.warmup, workdir, share, cpu,
+                                                args.cpu_seconds)
+            secondary["config2_innerproduct"] = config2(nhip, workloads, torch, args.steps, args.warmup, share, cpu,
+                                                        args.cpu_seconds)
+            secondary["config4_int8"] = config4(nhip, workloads, torch, args.steps, args.warmup, share, cpu,
+                                                args.cpu_seconds)
+            secondary["config5_mobilenetv2"] = config5(nhip, torch, args.steps, args.warmup, workdir, share, cpu,
+                                                       args.cpu_seconds)
     result = {
         "metric": METRIC,
         "value": round(value, 3),
@@ -262,8 +535,7 @@ def main():
             "images_per_sec": round(BATCH / (ms_per_step / 1e3), 1),
             "frac_fp32_mfma_peak_direct_equivalent": round(value / PEAK_FP32_TFLOPS, 4),
             "winograd_executed_tflops": round(wino_flops / (ms_per_step / 1e3) / 1e12, 3),
-            "int8": {k: (round(v, 4) if isinstance(v, float) else v) for k, v in int8.items()},
-            "mobilenetv2": {k: (round(v, 4) if isinstance(v, float) else v) for k, v in mbv2.items()},
+            **rounded(secondary),
         },
         "roofline": {
             "bound": "mfma",
@@ -280,8 +552,15 @@ def main():
             "ms_per_step_instrumented": round(ms_per_step_instrumented, 4),
         },
     }
-    if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline(workloads)
+    if cpu:
+        pair = cpu_config3(workloads, share, args.cpu_seconds * 2)
+        result["cpu_baseline"] = {
+            "value": pair["all"]["value"], "unit": "TFLOP/s", "cores": share, "kind": "port",
+            "sample": f"{pair['all']['sample']}, OpenMP {share} threads (this job's CPU share of the host's "
+                      f"{host_cpus} logical CPUs, {model}); one image per call as the reference's entry runs",
+            "one_thread": pair["one"]["value"],
+            "one_thread_sample": pair["one"]["sample"],
+            "cpu_model": model, "host_logical_cpus": host_cpus}
     print(json.dumps(result), flush=True)
 
 

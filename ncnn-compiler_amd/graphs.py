@@ -90,6 +90,34 @@ def graph_flops(layers, n, h, w):
     return total
 
 
+def graph_bytes(layers, n, h, w):
+    """Algorithmic HBM bytes of the graph run layer by layer (fp32): every
+    layer reads its input(s) and weights once and writes its output once (a
+    residual operand is read once more)."""
+    shapes = {"data": (3, h, w)}
+    total = 0.0
+    for L in layers:
+        c, hh, ww = shapes[L["src"]]
+        inp = n * c * hh * ww
+        if L["kind"] in ("conv", "dw"):
+            k = L["k"] if L["kind"] == "conv" else L["c"]
+            ker = L.get("kernel", 3)
+            pad = L.get("pad", 1)
+            oh = (hh + 2 * pad - ker) // L["stride"] + 1
+            ow = (ww + 2 * pad - ker) // L["stride"] + 1
+            out = n * k * oh * ow
+            wts = L["w"].size + L["b"].size
+            total += 4.0 * (inp + wts + out + (out if L.get("residual") else 0))
+            shapes[L["dst"]] = (k, oh, ow)
+        elif L["kind"] == "gap":
+            total += 4.0 * (inp + n * c)
+            shapes[L["dst"]] = (c, 1, 1)
+        elif L["kind"] == "ip":
+            total += 4.0 * (n * L["w"].shape[1] + L["w"].size + L["b"].size + n * L["w"].shape[0])
+            shapes[L["dst"]] = (L["w"].shape[0], 1, 1)
+    return total
+
+
 class DeviceGraph:
     """Runs a layer list on the GPU through the libnhip C ABI.
 
