@@ -402,6 +402,150 @@ __global__ __launch_bounds__(kThreads, 1) void wino_fused_kernel(FusedArgs a) {
   write_out<8, ACT, FINAL>(a, bk, lds, lane, wave);
 }
 
+// ---- LDS-DMA variant --------------------------------------------------------
+// The same 32 tiles x 32 output channels x 36 transform points per
+// workgroup, with 4 waves that each own a 16 x 16 MFMA block and also move
+// the operands: buffer_load_dwordx4 ... lds copies V and U slices from
+// memory straight into LDS (lane l's 16 bytes land at the wave-uniform LDS
+// base in M0 plus 16*l), so no registers hold data in flight.  Two LDS slots
+// of 36 KB (chunks of 4 input channels) keep each workgroup at 74 KB and 175
+// registers per lane, so two workgroups share a CU: while one waits at its
+// per-chunk barrier or for its next chunk, the other's waves issue MFMAs
+// (the chunk loop of a co-resident pair measured ~92% MFMA-busy).  The
+// copies are issued from inline assembly: the compiler does not see them,
+// so it inserts no waits of its own before the LDS reads; the kernel waits
+// with explicit vmcnt counts (a wave's copies complete in issue order) and a
+// workgroup barrier per chunk.  Chosen where the launch has enough
+// workgroups for two per CU (measured: 64@56 at batch 32, 392 workgroups,
+// 45.0 -> 37.3 us; with fewer workgroups the register-staged kernel, one
+// workgroup of 8 waves per CU, is faster).
+namespace dma {
+constexpr int kThreads = 256;
+constexpr int kCB = 4;                                // input channels per chunk
+constexpr int kSlots = 2;                             // chunk slots per workgroup
+constexpr int kVElems = 36 * kTB * kCB;               // [36][2 pairs][32 tiles][2]
+constexpr int kUElems = 36 * kKB * kCB;               // [36][2 pairs][32 channels][2]
+constexpr int kSlotElems = kVElems + kUElems;
+constexpr int kLdsBytes = kSlots * kSlotElems * (int)sizeof(float);  // 73728
+constexpr int kInstrV = kVElems * 4 / 1024;           // 1 KB copies per chunk: 18 for V
+constexpr int kInstrU = kUElems * 4 / 1024;           // and 18 for U
+constexpr int kPerWave = (kInstrV + kInstrU) / 4;     // 9 per wave and chunk
+static_assert(kLdsBytes >= kKB * kTB * 16 * (int)sizeof(float), "the staged output tiles fit in the slots");
+static_assert((kInstrV + kInstrU) % 4 == 0, "whole copies per wave");
+
+// One 1 KB copy: lane l's 16 bytes from the buffer at voff + soff to LDS
+// byte address lds_base + 16*l.
+__device__ __forceinline__ void copy16(uint32_t lds_base, uint32_t voff, v4i rsrc, uint32_t soff) {
+  asm volatile(
+      "s_mov_b32 m0, %0\n\t"
+      "s_nop 0\n\t"
+      "buffer_load_dwordx4 %1, %2, %3 offen lds" ::"s"(lds_base),
+      "v"(voff), "s"(rsrc), "s"(soff)
+      : "memory", "m0");
+}
+
+// Wait until at most 9 * chunks of this wave's copies are outstanding.
+__device__ __forceinline__ void wait_copies(int chunks) {
+  static_assert(kPerWave == 9 && kSlots == 2, "the counts below are 9 copies per chunk, at most one chunk ahead");
+  if (chunks >= 1) asm volatile("s_waitcnt vmcnt(9)" ::: "memory");
+  else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+}
+
+__device__ __forceinline__ v4i raw_rsrc(const void* base, uint32_t bytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  return v4i{(int)(uint32_t)a, (int)(uint32_t)(a >> 32) & 0xffff, (int)bytes, 0x00020000};
+}
+}  // namespace dma
+
+// Two workgroups per CU: at least 2 waves per SIMD (<= 256 registers).
+template <int ACT, bool FINAL>
+__global__ __launch_bounds__(dma::kThreads, 2) void wino_fused_dma_kernel(FusedArgs a) {
+  extern __shared__ __attribute__((aligned(16))) float lds[];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const Block bk = block_of(a, dma::kCB);
+  const uint32_t lds0 = (uint32_t)(uintptr_t)lds;
+
+  // Copy sources.  V[xi][c/2][t][2]: copy j of a chunk covers xi = 2j, 2j+1
+  // (lane bit 5), pairs 0, 1 of the chunk (lane bit 4), tiles t0 + 2*(l%16)
+  // and +1.  U[c/8][xi][pair][k][2] likewise over k0 .. k0 + 31.
+  const v4i vrs = dma::raw_rsrc(a.V, a.v_bytes), urs = dma::raw_rsrc(a.U, a.u_bytes);
+  const int hp = a.c_pad / 2;
+  const uint32_t v_lane =
+      (uint32_t)((((lane >> 5) * hp + ((lane >> 4) & 1)) * a.t_pad + bk.t0 + 2 * (lane & 15)) * 8);
+  const uint32_t u_lane = (uint32_t)(((((lane >> 5) * 4 + ((lane >> 4) & 1)) * a.m_pad) + bk.k0 + 2 * (lane & 15)) * 8);
+  auto issue = [&](int c4, int slot) {  // chunk c4 (global 4-channel index) into slot
+    const uint32_t sb = lds0 + (uint32_t)(slot * dma::kSlotElems * 4);
+#pragma unroll
+    for (int m = 0; m < dma::kPerWave; ++m) {
+      const int q = wave + 4 * m;
+      if (q < dma::kInstrV) {
+        const uint32_t so = (uint32_t)(((2 * q) * hp + 2 * c4) * a.t_pad * 8);
+        dma::copy16(sb + (uint32_t)(q * 1024), v_lane, vrs, so);
+      } else {
+        const int j = q - dma::kInstrV;
+        const uint32_t so = (uint32_t)((((c4 >> 1) * 36 + 2 * j) * 4 + (c4 & 1) * 2) * a.m_pad * 8);
+        dma::copy16(sb + (uint32_t)(dma::kVElems * 4 + j * 1024), u_lane, urs, so);
+      }
+    }
+  };
+
+  const int li = lane & 15, q = lane >> 4;
+  const int wk = wave & 1, wt = wave >> 1;
+  // lane (li, q) supplies reduction index q (channel q of the chunk):
+  // A = U[xi][q/2][k = wk*16 + li][q%2], B = V[xi][q/2][t = wt*16 + li][q%2]
+  const int a_off = dma::kVElems + ((q >> 1) * 32 + wk * 16 + li) * 2 + (q & 1);
+  const int b_off = ((q >> 1) * 32 + wt * 16 + li) * 2 + (q & 1);
+  constexpr int kXiStride = 2 * 32 * 2;  // floats per transform point in a slot part
+
+  v4f acc[36];
+#pragma unroll
+  for (int xi = 0; xi < 36; ++xi) acc[xi] = v4f{0.f, 0.f, 0.f, 0.f};
+
+  const int n = bk.n;
+  for (int c = 0; c < min(dma::kSlots, n); ++c) issue(bk.ch_begin + c, c);
+  dma::wait_copies(min(dma::kSlots, n) - 1);
+  __syncthreads();  // chunk 0 in slot 0
+
+  constexpr int kG = 6, kGroups = 36 / kG;
+  static_assert(kGroups % 2 == 0, "a chunk's first group lands in register buffer 0");
+  float av[2][kG], bv[2][kG];
+  auto read_group = [&](const float* slot, int g, int buf) {
+#pragma unroll
+    for (int j = 0; j < kG; ++j) {
+      av[buf][j] = slot[a_off + (g * kG + j) * kXiStride];
+      bv[buf][j] = slot[b_off + (g * kG + j) * kXiStride];
+    }
+  };
+  if (n > 0) read_group(lds, 0, 0);
+  for (int i = 0; i < n; ++i) {
+    const float* slot = lds + (i % dma::kSlots) * dma::kSlotElems;
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int g = 0; g < kGroups; ++g) {
+      if (g + 1 < kGroups) {
+        read_group(slot, g + 1, (g + 1) & 1);
+      } else {
+        // chunk i is read (its operands are in registers): wait for this
+        // wave's copies of chunk i + 1, then the barrier hands slot i & 3
+        // back to the copies (chunk i + 4) and publishes chunk i + 1
+        dma::wait_copies(max(0, min(dma::kSlots - 1, n - 1 - i) - 1));
+        __syncthreads();
+        if (i + dma::kSlots < n) issue(bk.ch_begin + i + dma::kSlots, i % dma::kSlots);
+        if (i + 1 < n) read_group(lds + ((i + 1) % dma::kSlots) * dma::kSlotElems, 0, 0);
+      }
+#pragma unroll
+      for (int j = 0; j < kG; ++j)
+        acc[g * kG + j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[g & 1][j], bv[g & 1][j], acc[g * kG + j], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  // every copy has landed and every slot is read (the last barrier above)
+  y_to_lds(acc, lds, wk, wt, li, q);
+  __syncthreads();
+  write_out<4, ACT, FINAL>(a, bk, lds, lane, wave);
+}
+
 // out = act(sum_s part[s] + bias[k] (+ residual)), parts [splits][N][K][OH][OW];
 // VEC = 4 when OH*OW % 4 == 0 (a float4 never crosses a channel plane).
 template <int VEC, int ACT>
@@ -430,7 +574,13 @@ __global__ void wino_fused_reduce(const float* __restrict__ part, int splits, in
 }
 
 template <int ACT, bool FINAL>
-int launch_kernel(const FusedArgs& a, int64_t blocks, hipStream_t s) {
+int launch_kernel(const FusedArgs& a, int64_t blocks, bool dma, hipStream_t s) {
+  if (dma) {
+    NHIP_TRY(ensure_dynamic_lds(reinterpret_cast<const void*>(&wino_fused_dma_kernel<ACT, FINAL>), dma::kLdsBytes));
+    NHIP_LAUNCH("wino_fused", (wino_fused_dma_kernel<ACT, FINAL>), dim3((unsigned)blocks), dim3(dma::kThreads),
+                dma::kLdsBytes, s, a);
+    return check_launch("wino_fused");
+  }
   NHIP_TRY(ensure_dynamic_lds(reinterpret_cast<const void*>(&wino_fused_kernel<ACT, FINAL>), kLdsBytes));
   NHIP_LAUNCH("wino_fused", (wino_fused_kernel<ACT, FINAL>), dim3((unsigned)blocks), dim3(kThreads),
               kLdsBytes, s, a);
@@ -447,6 +597,7 @@ int launch_reduce(const float* parts, int splits, int64_t total, int ohw, int K,
 
 struct FusedShape {
   int th, tw, nt, nk, nch, splits, per;
+  bool dma;  // the LDS-DMA kernel (two workgroups per CU) rather than the register-staged one
 };
 
 // Tile blocks of 32 consecutive tiles; channel splits: the fewest that
@@ -458,12 +609,18 @@ FusedShape fused_shape(const nhip_conv_plan* p, int n, int oh, int ow) {
   f.tw = (int)ceil_div(ow, 4);
   f.nt = (int)ceil_div((int64_t)n * f.th * f.tw, kTB);
   f.nk = (int)ceil_div(p->g.k, kKB);
-  f.nch = p->c_pad / kCB;
-  const int64_t cus = cu_count();
   const int64_t blocks = (int64_t)f.nt * f.nk;
+  // The LDS-DMA kernel from 1.5 workgroups per CU without a channel split;
+  // NHIP_WINO_FUSED=dma / reg forces one (tuning and tests).
+  const char* force = setting("NHIP_WINO_FUSED");
+  f.dma = force ? std::strcmp(force, "dma") == 0 : 2 * blocks >= 3 * (int64_t)cu_count();
+  const int cb = f.dma ? dma::kCB : kCB;  // channels per chunk
+  f.nch = p->c_pad / cb;
+  const int64_t cus = cu_count() * (f.dma ? 2 : 1);  // workgroup slots
   f.splits = 1;
   int64_t best = ceil_div(blocks, cus) * f.nch;
-  for (int s = 2; s <= 8 && ceil_div(f.nch, s) >= 4; s *= 2) {
+  const int min_chunks = 32 / cb;  // at least 32 channels per split
+  for (int s = 2; s <= 8 && ceil_div(f.nch, s) >= min_chunks; s *= 2) {
     const int64_t cost = ceil_div(blocks * s, cus) * ceil_div(f.nch, s);
     if (cost < best) {
       best = cost;
@@ -519,13 +676,13 @@ int launch_fused(const nhip_conv_plan* p, FusedArgs& a, const FusedShape& f, con
   const int64_t blocks = (int64_t)f.nt * f.nk * f.splits;
   if (f.splits == 1) {
     switch (p->g.act) {
-      case NHIP_ACT_NONE: return launch_kernel<NHIP_ACT_NONE, true>(a, blocks, s);
-      case NHIP_ACT_RELU: return launch_kernel<NHIP_ACT_RELU, true>(a, blocks, s);
-      case NHIP_ACT_SIGMOID: return launch_kernel<NHIP_ACT_SIGMOID, true>(a, blocks, s);
+      case NHIP_ACT_NONE: return launch_kernel<NHIP_ACT_NONE, true>(a, blocks, f.dma, s);
+      case NHIP_ACT_RELU: return launch_kernel<NHIP_ACT_RELU, true>(a, blocks, f.dma, s);
+      case NHIP_ACT_SIGMOID: return launch_kernel<NHIP_ACT_SIGMOID, true>(a, blocks, f.dma, s);
       default: return fail(NHIP_STATUS_UNSUPPORTED, "winograd GEMM: unsupported activation");
     }
   }
-  NHIP_TRY((launch_kernel<NHIP_ACT_NONE, false>(a, blocks, s)));
+  NHIP_TRY((launch_kernel<NHIP_ACT_NONE, false>(a, blocks, f.dma, s)));
   const int64_t total = (int64_t)n * p->g.k * oh * ow;
   const int ohw = oh * ow;
 #define NHIP_REDUCE(V_)                                                                                       \

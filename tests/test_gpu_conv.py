@@ -116,14 +116,18 @@ WINO_CASES = [
 ]
 
 
-@pytest.fixture(params=["auto", "1", "2"])
+@pytest.fixture(params=["auto", "1", "2", "2dma"])
 def wino_variant(request, nhip_env):
     """Winograd implementations: the default per-shape choice (auto), the
-    three-kernel path (1) and the GEMM with the output transform fused (2)."""
+    three-kernel path (1), the GEMM with the output transform fused (2) with
+    its register-staged kernel, and the same with the LDS-DMA kernel
+    (2dma)."""
     if request.param == "auto":
         nhip_env.delenv("NHIP_WINOGRAD_VARIANT", raising=False)
+        nhip_env.delenv("NHIP_WINO_FUSED", raising=False)
     else:
-        nhip_env.setenv("NHIP_WINOGRAD_VARIANT", request.param)
+        nhip_env.setenv("NHIP_WINO_FUSED", "dma" if request.param == "2dma" else "reg")
+        nhip_env.setenv("NHIP_WINOGRAD_VARIANT", request.param[0])
     return request.param
 
 
@@ -158,9 +162,11 @@ def _random_wino_cases(count, seed):
     return cases
 
 
+@pytest.mark.parametrize("kernel", ["reg", "dma"])
 @pytest.mark.parametrize("case", _random_wino_cases(16, 7), ids=lambda c: "x".join(map(str, c[:5])))
-def test_winograd_fused_random_shapes(case, nhip_env):
+def test_winograd_fused_random_shapes(case, kernel, nhip_env):
     nhip_env.setenv("NHIP_WINOGRAD_VARIANT", "2")  # the fused GEMM whatever the tile count
+    nhip_env.setenv("NHIP_WINO_FUSED", kernel)  # register-staged or LDS-DMA kernel
     n, c, h, w, k, pad, with_res = case
     rng = np.random.default_rng(hash(case) % (2 ** 32))
     x = rng.uniform(-1, 1, (n, c, h, w)).astype(np.float32)
@@ -241,11 +247,12 @@ def test_resnet_stage_full_batch(stage, nhip_env):
         assert_close(igemm[i:i + 1], exp[i:i + 1], IGEMM_RTOL, f"igemm image {i}")
 
 
-@pytest.mark.parametrize("variant", ["2", "1"])
-def test_batch_is_independent_images(variant, nhip_env):  # 1 = three-kernel path, 2 = fused
+@pytest.mark.parametrize("variant", ["2", "1", "2dma"])
+def test_batch_is_independent_images(variant, nhip_env):  # 1 = three-kernel path, 2 = fused (2dma: LDS-DMA kernel)
     """The [N,C,H,W] batch equals N single-image calls (the reference ABI),
     bit for bit for a fixed kernel variant."""
-    nhip_env.setenv("NHIP_WINOGRAD_VARIANT", variant)
+    nhip_env.setenv("NHIP_WINOGRAD_VARIANT", variant[0])
+    nhip_env.setenv("NHIP_WINO_FUSED", "dma" if variant == "2dma" else "reg")
     c, k = 32, 32
     x = RNG.uniform(-1, 1, (4, c, 10, 10)).astype(np.float32)
     wt = workloads.he_normal(RNG, (k, c, 3, 3), c * 9)
