@@ -237,6 +237,25 @@ int nhip_innerproduct_workspace_size(nhip_ip_t plan, int32_t m,
 int nhip_innerproduct_f32_forward(nhip_ip_t plan, const float* input,
                                   float* output, int32_t m, void* workspace,
                                   uint64_t workspace_bytes, void* stream);
+/* a10 + a4 — global average pooling feeding an fp32 InnerProduct, fused
+ * (ConvertPooling global average NCNNToTosa.cpp:1880-1990, then
+ * ConvertInnerProduct :5254-5392): output[n][num_output] = InnerProduct of
+ * the per-channel means of input [n][C][h][w], C = num_input.  Each mean is
+ * the plane summed in order and divided by h*w, as the reference and
+ * nhip_global_avgpool_f32 compute it.  Planes of at most 6400 pixels
+ * (h*w larger: NHIP_STATUS_CONSTRAINT_VIOLATION; run the two ops).  Needs
+ * the workspace this reports for the same n, h, w. */
+int nhip_global_avgpool_innerproduct_f32_workspace_size(nhip_ip_t plan,
+                                                        int32_t n, int32_t h,
+                                                        int32_t w,
+                                                        uint64_t* bytes);
+int nhip_global_avgpool_innerproduct_f32_forward(nhip_ip_t plan,
+                                                 const float* input,
+                                                 float* output, int32_t n,
+                                                 int32_t c, int32_t h,
+                                                 int32_t w, void* workspace,
+                                                 uint64_t workspace_bytes,
+                                                 void* stream);
 /* a4 int8 — InnerProduct with int8_scale_term (NCNNToTosa.cpp:5300-5390):
  * out = act((float)(sum_k q(x)*q(W)) * r[j] + bias[j]), fp32 output.
  * weight: host [num_output][num_input], int8 when weight_is_i8 else fp32

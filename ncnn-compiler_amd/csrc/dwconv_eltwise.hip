@@ -227,6 +227,76 @@ __global__ __launch_bounds__(256) void dw3x3_f32_kernel(DwArgs a, uint32_t x_byt
   }
 }
 
+// 3x3 depthwise, stride S (1 or 2), dilation 1, any padding, for planes of
+// at most kDwPlaneMax pixels: a workgroup takes `ppb` whole planes (image x
+// channel).  In NCHW those planes are one contiguous block of the input and
+// one of the output, so the block comes into LDS through 16-byte loads
+// (every lane's load a full vector, the whole wave 1 KB), lanes then take
+// consecutive outputs (consecutive LDS words: no bank conflicts), and the
+// results, staged in LDS, leave as 16-byte stores.  The host picks ppb so
+// that every block starts on a 16-byte boundary of x and y.  Summation
+// order of the CPU loop nest: acc = 0, += x*w over (kh, kw), then + bias.
+constexpr int kDwPlaneMax = 1024;
+
+template <int S>
+__global__ __launch_bounds__(256) void dw3x3_planes_kernel(DwArgs a, FastDiv ohw_div, FastDiv ow_div) {
+  extern __shared__ float lds[];
+  const int hw = a.H * a.W, ohw = a.OH * a.OW;
+  const int p0 = blockIdx.x * a.ppb;
+  const int np = min(a.ppb, a.planes - p0);
+  float* xin = lds;                // [ppb][hw]
+  float* yout = xin + a.ppb * hw;  // [ppb][ohw]
+  float* wl = yout + a.ppb * ohw;  // [ppb][10]: the plane's 9 weights, then its bias
+  const float* xs = a.x + (int64_t)p0 * hw;
+  const int nin = np * hw, nin4 = nin >> 2;
+  for (int v0 = threadIdx.x; v0 < nin4; v0 += 1024) {  // four loads in flight per lane
+    v4f t[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      if (v0 + 256 * u < nin4) t[u] = reinterpret_cast<const v4f*>(xs)[v0 + 256 * u];
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      if (v0 + 256 * u < nin4) reinterpret_cast<v4f*>(xin)[v0 + 256 * u] = t[u];
+  }
+  for (int e = (nin4 << 2) + threadIdx.x; e < nin; e += 256) xin[e] = xs[e];
+  for (int e = threadIdx.x; e < np * 10; e += 256) {
+    const int pi = e / 10, t = e - pi * 10;
+    const int c = (p0 + pi) % a.C;
+    wl[e] = t < 9 ? a.w[c * 9 + t] : a.bias[c];
+  }
+  __syncthreads();
+  const int nout = np * ohw;
+  for (int o = threadIdx.x; o < nout; o += 256) {
+    const int pi = fdiv(o, ohw_div);
+    const int r = o - pi * ohw;
+    const int oy = fdiv(r, ow_div);
+    const int ox = r - oy * a.OW;
+    const float* src = xin + pi * hw;
+    const float* wp = wl + pi * 10;
+    const int y0 = oy * S - a.pt, x0 = ox * S - a.pl;
+    float acc = 0.f;
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+#pragma unroll
+      for (int j = 0; j < 3; ++j) {
+        const int y = y0 + i, x = x0 + j;
+        const bool ok = (unsigned)y < (unsigned)a.H && (unsigned)x < (unsigned)a.W;
+        const float v = ok ? src[ok ? y * a.W + x : 0] : 0.f;
+        acc = acc + v * wp[i * 3 + j];
+      }
+    }
+    acc = acc + wp[9];
+    if (a.act == NHIP_ACT_RELU) acc = acc < 0.f ? 0.f : acc;
+    yout[o] = acc;
+  }
+  __syncthreads();
+  float* ys = a.y + (int64_t)p0 * ohw;
+  const int nout4 = nout >> 2;
+  for (int v = threadIdx.x; v < nout4; v += 256)
+    reinterpret_cast<v4f*>(ys)[v] = reinterpret_cast<const v4f*>(yout)[v];
+  for (int e = (nout4 << 2) + threadIdx.x; e < nout; e += 256) ys[e] = yout[e];
+}
+
 // ---------------------------------------------------------------------------
 
 __device__ __forceinline__ int8_t quantize_i8(float x, float scale) {
@@ -346,6 +416,39 @@ __global__ __launch_bounds__(256) void gap_f32_kernel(const float* x, float* y, 
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
   if (lane == 0) y[plane] = s / (float)hw;
+}
+
+// Global average pooling for planes of at most kGapPlaneMax pixels: a
+// workgroup takes `ppb` whole planes, one contiguous block of the input,
+// brings it into LDS with 16-byte loads (four in flight per lane) and one
+// lane sums each plane in element order, the CPU loop's order: s = 0,
+// s += x[e] for e = 0 .. h*w-1, mean = s / (h*w).
+constexpr int kGapPlaneMax = 256;
+
+__global__ __launch_bounds__(256) void gap_planes_kernel(const float* x, float* y, int64_t planes, int hw,
+                                                         int ppb) {
+  extern __shared__ float lds[];
+  const int64_t p0 = (int64_t)blockIdx.x * ppb;
+  const int np = (int)min((int64_t)ppb, planes - p0);
+  const float* xs = x + p0 * hw;
+  const int nin = np * hw, nin4 = nin >> 2;
+  for (int v0 = threadIdx.x; v0 < nin4; v0 += 1024) {
+    v4f t[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      if (v0 + 256 * u < nin4) __builtin_memcpy(&t[u], xs + 4 * (v0 + 256 * u), 16);  // 4-byte aligned source
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      if (v0 + 256 * u < nin4) reinterpret_cast<v4f*>(lds)[v0 + 256 * u] = t[u];
+  }
+  for (int e = (nin4 << 2) + threadIdx.x; e < nin; e += 256) lds[e] = xs[e];
+  __syncthreads();
+  for (int pi = threadIdx.x; pi < np; pi += 256) {
+    const float* src = lds + pi * hw;
+    float s = 0.f;
+    for (int e = 0; e < hw; ++e) s = s + src[e];
+    y[p0 + pi] = s / (float)hw;
+  }
 }
 
 __global__ void quantize_f32_i8_kernel(const float* x, int8_t* y, int64_t n, int c,
@@ -476,9 +579,35 @@ int launch_dwconv_f32(const nhip_conv_plan* p, const float* in, float* out,
   a.act = p->g.act;
   const bool k3 = a.kh == 3 && a.kw == 3 && a.dh == 1 && a.dw == 1 && a.sh == a.sw && (a.sh == 1 || a.sh == 2);
   const uint64_t x_bytes = (uint64_t)a.planes * h * w * sizeof(float);
+  const int hw = h * w, ohw = oh * ow;
+  // VEC: rows the window kernel reads and writes as 16-byte vectors (it
+  // assumes the left pad of 1)
+  const bool vec = w % 4 == 0 && ow % 4 == 0 && a.pl == 1;
+  // Small planes whose rows are not vector-aligned (7x7, 14x14, stride 2 to
+  // 14 or 7): whole planes per workgroup through LDS, when x and y are
+  // 16-byte aligned.  Measured at batch 32: 960@7 8.2 us against 10.4,
+  // 576@14 12.0 against 17.3, 192@28 stride 2 8.0 against 12.8; with
+  // vector rows (192@28 stride 1) the window kernel is faster, 9.8 against
+  // 14.3.  NHIP_DW_PLANES=0 switches it off (tuning and tests).
+  if (k3 && !vec && hw <= kDwPlaneMax && x_bytes < (1ull << 31) &&
+      ((reinterpret_cast<uintptr_t>(in) | reinterpret_cast<uintptr_t>(out)) & 15) == 0 &&
+      setting_int("NHIP_DW_PLANES", 1) != 0) {
+    // about 8 KB of input and at most 48 KB of LDS per workgroup, ppb * hw
+    // and ppb * ohw multiples of 4 (every block 16-byte aligned)
+    const int step = (hw % 4 == 0 && ohw % 4 == 0) ? 1 : (hw % 2 == 0 && ohw % 2 == 0) ? 2 : 4;
+    const int want = std::max(1, std::min(2048 / hw, 12288 / (hw + ohw + 10)));
+    a.ppb = std::max(step, want / step * step);
+    const size_t lds = (size_t)a.ppb * (hw + ohw + 10) * sizeof(float);
+    const dim3 grid((unsigned)ceil_div(a.planes, a.ppb));
+    if (a.sh == 1)
+      NHIP_LAUNCH("dw3x3_planes_f32", (dw3x3_planes_kernel<1>), grid, dim3(256), lds, s, a, fast_div(ohw),
+                  fast_div(ow));
+    else
+      NHIP_LAUNCH("dw3x3_planes_f32", (dw3x3_planes_kernel<2>), grid, dim3(256), lds, s, a, fast_div(ohw),
+                  fast_div(ow));
+    return check_launch("dw3x3_planes_f32");
+  }
   if (k3 && x_bytes < (1ull << 31)) {
-    // VEC needs aligned rows and the left pad of 1 that the vector offsets assume
-    const bool vec = w % 4 == 0 && ow % 4 == 0 && a.pl == 1;
     const int R = a.sh == 1 ? 4 : 2;
     const int64_t threads = (int64_t)a.planes * ceil_div(oh, R) * ((ow + 3) / 4);
     const dim3 grid((unsigned)ceil_div(threads, 256));
@@ -547,8 +676,15 @@ int nhip_global_avgpool_f32(const float* input, float* output, int32_t n, int32_
     return fail(NHIP_STATUS_INVALID_SHAPE, "global_avgpool: invalid shape");
   if (n == 0) return ok();
   const int64_t planes = (int64_t)n * c;
+  const int hw = h * w;
+  if ((int64_t)h * w <= kGapPlaneMax) {
+    const int ppb = std::max(1, 4096 / hw);  // 16 KB of input per workgroup
+    NHIP_LAUNCH("global_avgpool_f32", gap_planes_kernel, dim3((unsigned)ceil_div(planes, ppb)), dim3(256),
+                (size_t)ppb * hw * sizeof(float), as_stream(stream), input, output, planes, hw, ppb);
+    return check_launch("global_avgpool_f32");
+  }
   NHIP_LAUNCH("global_avgpool_f32", gap_f32_kernel, dim3((unsigned)ceil_div(planes, 4)), dim3(256), 0,
-                     as_stream(stream), input, output, planes, h * w);
+                     as_stream(stream), input, output, planes, hw);
   return check_launch("global_avgpool_f32");
 }
 

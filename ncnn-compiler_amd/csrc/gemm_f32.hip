@@ -398,8 +398,19 @@ __global__ void ip_splitk_reduce(const float* part, const float* bias,
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (idx >= (int64_t)m * n) return;
   const int i = (int)(idx / n), j = (int)(idx - (int64_t)i * n);
+  // splits are added in order; the loads of 8 splits are issued together
+  const float* src = part + (int64_t)i * ldp + j;
+  const int64_t stride = (int64_t)m * ldp;
   float s = 0.f;
-  for (int z = 0; z < splits; ++z) s += part[((int64_t)z * m + i) * ldp + j];
+  int z = 0;
+  for (; z + 8 <= splits; z += 8) {
+    float v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = src[(z + u) * stride];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) s += v[u];
+  }
+  for (; z < splits; ++z) s += src[z * stride];
   out[idx] = apply_act(s + bias[j], act);
 }
 
@@ -516,6 +527,154 @@ uint64_t innerproduct_workspace(const nhip_ip_plan* p, int m) {
   const int splits = ip_splits(p, m);
   if (splits == 1) return 0;
   return (uint64_t)splits * m * p->n_pad * sizeof(float);
+}
+
+// ------------------- global average pooling + InnerProduct -----------------
+// The MobileNet / ResNet head: ConvertPooling's global average
+// (NCNNToTosa.cpp:1880-1990, the mean of every [H,W] plane) feeding
+// ConvertInnerProduct (:5254-5392), in one pass over the input.  A
+// workgroup of 16 waves owns 16 images x 256 outputs x one slice of ks <= 64
+// channels.  The slice of one image is one contiguous run of ks planes: ipp
+// images at a time come into LDS through 16-byte loads, one lane per plane
+// sums it in element order (the CPU loop's order, so the means equal
+// nhip_global_avgpool_f32's bit for bit), then the LDS holds the weight
+// slice, v_mfma_f32_16x16x4_f32 multiplies, and the workgroup writes a
+// split-K partial [split][n][n_out]; ip_splitk_reduce adds the splits in
+// order, the bias and the activation.  The ceil(n_out / 256) workgroups of
+// a slice (4 for 1000 outputs) read its planes, mostly from L2; the head is
+// two launches instead of three.
+namespace {
+constexpr int kGapRows = 16, kGapCols = 256, kGapMaxK = 64, kGapThreads = 1024;
+constexpr int kGapStage = 25600;  // floats of LDS: staged planes, then the weight slice
+static_assert(kGapCols * (kGapMaxK + 4) <= kGapStage, "the weight slice fits the staging area");
+static_assert(kGapThreads / 64 * 16 == kGapCols, "one 16-output MFMA block per wave");
+
+struct GapIpArgs {
+  const float* x;   // [n][C][hw]
+  const float* w;   // [n_pad][k_pad], zero padded
+  float* part;      // [splits][n][n_out]
+  int n, C, hw, n_out, n_pad, k_pad, ks, ipp;
+};
+
+__global__ __launch_bounds__(kGapThreads) void gap_ip_kernel(GapIpArgs a) {
+  __shared__ __attribute__((aligned(16))) float S[kGapStage];
+  __shared__ float P[kGapRows][kGapMaxK + 4];  // pooled [image][channel of the slice]
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int c0 = blockIdx.x * kGapCols, z = blockIdx.y, img0 = blockIdx.z * kGapRows;
+  const int k0 = z * a.ks;
+  const int kv = min(a.ks, a.C - k0);  // channels of the slice inside the tensor
+  const int L = kv * a.hw, L4 = L >> 2, Ls = (L + 3) & ~3;  // floats of one image's run, its LDS stride
+  for (int e = tid; e < kGapRows * (kGapMaxK + 4); e += kGapThreads) (&P[0][0])[e] = 0.f;
+  for (int i0 = 0; i0 < kGapRows && img0 + i0 < a.n; i0 += a.ipp) {
+    const int ni = min(a.ipp, a.n - img0 - i0);
+    const float* src = a.x + ((int64_t)(img0 + i0) * a.C + k0) * a.hw;
+    const int64_t img_stride = (int64_t)a.C * a.hw;
+    // runs of ni images: 16-byte loads (4-byte aligned sources), four in flight per lane
+    for (int v0 = tid; v0 < ni * L4; v0 += 4 * kGapThreads) {
+      v4f t[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int v = v0 + u * kGapThreads, i = v / max(L4, 1), q = v - i * L4;
+        if (v < ni * L4) __builtin_memcpy(&t[u], src + i * img_stride + 4 * q, 16);
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int v = v0 + u * kGapThreads, i = v / max(L4, 1), q = v - i * L4;
+        if (v < ni * L4) *reinterpret_cast<v4f*>(&S[i * Ls + 4 * q]) = t[u];
+      }
+    }
+    const int rem = L - 4 * L4;
+    for (int e = tid; e < ni * rem; e += kGapThreads) {
+      const int i = e / rem, j = e - i * rem;
+      S[i * Ls + 4 * L4 + j] = src[i * img_stride + 4 * L4 + j];
+    }
+    __syncthreads();
+    if (tid < ni * a.ks) {
+      const int i = tid / a.ks, j = tid - i * a.ks;
+      if (j < kv) {
+        const float* pl = S + i * Ls + j * a.hw;
+        float sum = 0.f;
+        for (int e = 0; e < a.hw; ++e) sum = sum + pl[e];
+        P[i0 + i][j] = sum / (float)a.hw;
+      }
+    }
+    __syncthreads();
+  }
+  // weight slice [256 outputs][ks channels], 16-byte loads (k_pad and ks are multiples of 4)
+  float (*Ws)[kGapMaxK + 4] = reinterpret_cast<float (*)[kGapMaxK + 4]>(S);
+  const int kq = a.ks / 4;
+  for (int e = tid; e < kGapCols * kq; e += kGapThreads) {
+    const int col = e / kq, q4 = e - col * kq, k = k0 + 4 * q4;
+    v4f v = v4f{0.f, 0.f, 0.f, 0.f};
+    if (c0 + col < a.n_pad && k < a.k_pad) v = *reinterpret_cast<const v4f*>(a.w + (int64_t)(c0 + col) * a.k_pad + k);
+    *reinterpret_cast<v4f*>(&Ws[col][4 * q4]) = v;
+  }
+  __syncthreads();
+  // one C[16 images][16 outputs] block per wave: lane (li, q) supplies
+  // A = P[li][4s + q] and B = Ws[16 wave + li][4s + q]; register r holds
+  // C[image 4q + r][output li]
+  const int li = lane & 15, q = lane >> 4;
+  v4f acc = v4f{0.f, 0.f, 0.f, 0.f};
+  for (int s = 0; s < kq; ++s)
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(P[li][4 * s + q], Ws[wave * 16 + li][4 * s + q], acc, 0, 0, 0);
+  float* dst = a.part + (int64_t)z * a.n * a.n_out;
+  const int col = c0 + wave * 16 + li;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int img = img0 + 4 * q + r;
+    if (img < a.n && col < a.n_out) dst[(int64_t)img * a.n_out + col] = acc[r];
+  }
+}
+
+// Channels per split: about one workgroup per CU, 16 to 64 channels per
+// slice, at most 16 splits (each split's partial is n x n_out floats), and
+// at least one image's slice in the staging area (4 <= ks).
+int gap_ip_ks(const nhip_ip_plan* p, int n, int hw) {
+  const int64_t others = ceil_div(p->n_out, kGapCols) * ceil_div(n, kGapRows);
+  const int64_t splits = std::min<int64_t>(16, std::max<int64_t>(1, cu_count() / others));
+  int ks = (int)round_up(ceil_div(p->k_in, splits), 4);
+  ks = std::min(std::max(ks, 16), kGapMaxK);
+  const int fit = (kGapStage / hw) / 4 * 4;  // run stride rounds up to 4 floats
+  return std::min(ks, fit);
+}
+
+// Images per staging pass: the largest power of two up to 16 whose runs fit.
+int gap_ip_ipp(int ks, int hw) {
+  const int run = (int)round_up((int64_t)ks * hw, 4);
+  int ipp = kGapRows;
+  while (ipp > 1 && ipp * run > kGapStage) ipp /= 2;
+  return ipp;
+}
+}  // namespace
+
+bool gap_innerproduct_supported(int hw) { return hw >= 1 && hw <= kGapStage / 4; }
+
+uint64_t gap_innerproduct_workspace(const nhip_ip_plan* p, int n, int hw) {
+  if (!gap_innerproduct_supported(hw)) return 0;
+  const int splits = (int)ceil_div(p->k_in, gap_ip_ks(p, n, hw));
+  return (uint64_t)splits * n * p->n_out * sizeof(float);
+}
+
+int launch_gap_innerproduct_f32(const nhip_ip_plan* p, const float* in, float* out, int n, int hw, void* ws,
+                                uint64_t ws_bytes, hipStream_t s) {
+  if (!gap_innerproduct_supported(hw))
+    return fail(NHIP_STATUS_CONSTRAINT_VIOLATION,
+                "global_avgpool_innerproduct: planes of at most " + std::to_string(kGapStage / 4) + " pixels");
+  const int ks = gap_ip_ks(p, n, hw);
+  const int splits = (int)ceil_div(p->k_in, ks);
+  const uint64_t need = (uint64_t)splits * n * p->n_out * sizeof(float);
+  if (ws == nullptr || ws_bytes < need)
+    return fail(NHIP_STATUS_OUTPUT_CAPACITY_INSUFFICIENT,
+                "global_avgpool_innerproduct: workspace of " + std::to_string(need) + " bytes required");
+  GapIpArgs a{in, p->weight, static_cast<float*>(ws), n, p->k_in, hw, p->n_out, p->n_pad, p->k_pad, ks,
+              gap_ip_ipp(ks, hw)};
+  const dim3 grid((unsigned)ceil_div(p->n_out, kGapCols), (unsigned)splits, (unsigned)ceil_div(n, kGapRows));
+  NHIP_LAUNCH("gap_innerproduct_f32", gap_ip_kernel, grid, dim3(kGapThreads), 0, s, a);
+  NHIP_TRY(check_launch("gap_innerproduct_f32"));
+  const int64_t total = (int64_t)n * p->n_out;
+  NHIP_LAUNCH("ip_splitk_reduce", ip_splitk_reduce, dim3((unsigned)ceil_div(total, 256)), dim3(256), 0, s,
+              static_cast<const float*>(ws), p->bias, out, n, p->n_out, p->n_out, splits, p->act);
+  return check_launch("ip_splitk_reduce");
 }
 
 int launch_innerproduct_f32(const nhip_ip_plan* p, const float* in,

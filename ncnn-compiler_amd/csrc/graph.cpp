@@ -614,9 +614,10 @@ struct Op {
   enum class View { Same, Flatten, Reshape, Squeeze } view = View::Same;
   std::vector<int64_t> reshape;  // (w, h, c) targets, -1 infer, 0 absent
   std::vector<int64_t> squeeze_axes;
-  // Depthwise -> 1x1 fusion (nhip_dwconv2d_pw_f32_*): on the depthwise op,
-  // the index of the convolution that is its output's only consumer; on
-  // that convolution, the depthwise op's index.
+  // Depthwise -> 1x1 fusion (nhip_dwconv2d_pw_f32_*), and global average
+  // pooling -> InnerProduct (nhip_global_avgpool_innerproduct_f32_*): on
+  // the first op, the index of the op that is its output's only consumer;
+  // on that op, the first op's index.
   int fuse_into = -1, fuse_from = -1;
 };
 
@@ -697,6 +698,38 @@ void mark_dw_pw_pairs(nhip_graph& g) {
         c.fuse_from = (int)i;
         break;
       }
+    }
+  }
+}
+
+// Global average pooling whose output reaches exactly one fp32
+// InnerProduct, directly or through at most two views (Flatten, Reshape,
+// Squeeze), and is no graph output: the pair runs as one fused launch.
+void mark_gap_ip_pairs(nhip_graph& g) {
+  std::vector<int> uses(g.blobs.size(), 0);
+  std::vector<int> consumer(g.blobs.size(), -1);
+  for (size_t j = 0; j < g.ops.size(); ++j) {
+    for (int b : g.ops[j].in) {
+      ++uses[b];
+      consumer[b] = (int)j;
+    }
+    if (g.ops[j].residual >= 0) ++uses[g.ops[j].residual];
+  }
+  for (int b : g.outputs) ++uses[b];
+  for (size_t i = 0; i < g.ops.size(); ++i) {
+    Op& gap = g.ops[i];
+    if (gap.kind != OpKind::Gap || g.blobs[gap.in[0]].dtype != NHIP_DTYPE_F32) continue;
+    int b = gap.out;
+    for (int hop = 0; hop < 3 && b >= 0; ++hop) {
+      if (uses[b] != 1 || consumer[b] < 0) break;
+      Op& c = g.ops[consumer[b]];
+      if (c.kind == OpKind::IP && c.in.size() == 1 && c.in[0] == b) {
+        gap.fuse_into = consumer[b];
+        c.fuse_from = (int)i;
+        break;
+      }
+      if (c.kind != OpKind::Alias || c.in.size() != 1) break;
+      b = c.out;
     }
   }
 }
@@ -1184,6 +1217,7 @@ int build(nhip_graph& g, std::vector<Layer>& layers, const int64_t* input_shapes
     if (op.kind != OpKind::Input && !consumed.count(op.out)) g.outputs.push_back(op.out);
   if (g.inputs.empty() || g.outputs.empty()) return fail(NHIP_STATUS_CONSTRAINT_VIOLATION, "graph needs inputs and outputs");
   mark_dw_pw_pairs(g);
+  mark_gap_ip_pairs(g);
   return ok();
 }
 
@@ -1199,6 +1233,14 @@ int ensure(void** buf, uint64_t* cap, uint64_t bytes) {
   return ok();
 }
 
+// A marked pooling -> InnerProduct pair runs fused when the pooled planes
+// fit nhip_global_avgpool_innerproduct_f32 (at most 6400 pixels).
+bool gap_ip_fusable(const nhip_graph& g, const std::vector<Shape>& sh, const Op& ip) {
+  if (ip.fuse_from < 0) return false;
+  const Shape& a = sh[g.ops[ip.fuse_from].in[0]];
+  return a.rank == 3 && a.d[1] > 0 && a.d[2] > 0 && a.d[1] * a.d[2] <= 6400;
+}
+
 int run_ops(nhip_graph& g, int n, const std::vector<Shape>& sh, const void* const* inputs, void* const* outputs,
             void* stream) {
   std::vector<char*> ptr(g.blobs.size(), nullptr);
@@ -1212,13 +1254,27 @@ int run_ops(nhip_graph& g, int n, const std::vector<Shape>& sh, const void* cons
     uint64_t w = 0;
     if (op.kind == OpKind::ConvF32 || op.kind == OpKind::ConvInt8)
       TRY(nhip_conv2d_workspace_size(op.conv, n, (int32_t)a.d[1], (int32_t)a.d[2], &w));
-    else if (op.kind == OpKind::IP || op.kind == OpKind::IPInt8)
+    else if (op.kind == OpKind::IP || op.kind == OpKind::IPInt8) {
       TRY(nhip_innerproduct_workspace_size(op.ip, (int32_t)(a.rank == 2 ? n * a.d[0] : n), &w));
+      if (op.kind == OpKind::IP && gap_ip_fusable(g, sh, op)) {  // fused or not, as the switch says at run time
+        const Shape& pa = sh[g.ops[op.fuse_from].in[0]];
+        uint64_t wf = 0;
+        TRY(nhip_global_avgpool_innerproduct_f32_workspace_size(op.ip, n, (int32_t)pa.d[1], (int32_t)pa.d[2], &wf));
+        w = std::max(w, wf);
+      }
+    }
     ws_need = std::max(ws_need, w);
   }
   TRY(ensure(&g.ws, &g.ws_cap, std::max<uint64_t>(ws_need, 256)));
   for (size_t i = 0; i < g.inputs.size(); ++i) ptr[g.inputs[i]] = (char*)inputs[i];
-  std::vector<char> fused(g.ops.size(), 0);  // depthwise ops folded into their 1x1 consumer
+  std::vector<char> fused(g.ops.size(), 0);  // ops folded into their consumer
+  // Pooling -> InnerProduct runs fused only with NHIP_GAP_IP=1.  Measured on
+  // the MobileNetV2 head at batch 32 (1280@7x7 -> 1000): fused 13.5 us +
+  // the split-K reduce against 4.0 us pooling + 9.8 us InnerProduct + 1.7 us
+  // reduce unfused - pooling wants every CU on the 8 MB input, the GEMM an
+  // output split, and one kernel gets either re-read planes or large split-K
+  // partials.
+  const bool gap_ip = nhip::setting_int("NHIP_GAP_IP", 0) != 0;
   for (size_t oi = 0; oi < g.ops.size(); ++oi) {
     const Op& op = g.ops[oi];
     if (op.kind == OpKind::Input) continue;
@@ -1230,6 +1286,20 @@ int run_ops(nhip_graph& g, int n, const std::vector<Shape>& sh, const void* cons
         fused[oi] = 1;
         continue;
       }
+    }
+    if (op.kind == OpKind::Gap && op.fuse_into >= 0 && gap_ip && gap_ip_fusable(g, sh, g.ops[op.fuse_into])) {
+      // runs inside its InnerProduct
+      fused[oi] = 1;
+      continue;
+    }
+    if (op.kind == OpKind::IP && op.fuse_from >= 0 && fused[op.fuse_from]) {
+      const Op& gp = g.ops[op.fuse_from];
+      const Shape& a = sh[gp.in[0]];
+      ptr[op.out] = (char*)g.blobs[op.out].buf;
+      TRY(nhip_global_avgpool_innerproduct_f32_forward(op.ip, (const float*)ptr[gp.in[0]], (float*)ptr[op.out], n,
+                                                       (int32_t)a.d[0], (int32_t)a.d[1], (int32_t)a.d[2], g.ws,
+                                                       g.ws_cap, stream));
+      continue;
     }
     if (op.kind == OpKind::ConvF32 && op.fuse_from >= 0 && fused[op.fuse_from]) {
       const Op& d = g.ops[op.fuse_from];

@@ -72,6 +72,23 @@ int resident_blocks(const void* kernel, int threads, size_t lds);
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 inline int64_t round_up(int64_t a, int64_t b) { return ceil_div(a, b) * b; }
 
+// ---- division by a divisor fixed at launch ------------------------------------
+// n / d for 0 <= n < 2^31 and 1 <= d < 2^31 as (umulhi(n, m) + n) >> s, with
+// s = ceil(log2 d) and m = floor(2^32 (2^s - d) / d) + 1 (Granlund and
+// Montgomery, "Division by invariant integers using multiplication", PLDI
+// 1994, section 4); n < 2^31 keeps the sum inside 32 bits.
+struct FastDiv {
+  uint32_t m, s;
+};
+inline FastDiv fast_div(uint32_t d) {
+  uint32_t s = 0;
+  while ((uint64_t(1) << s) < d) ++s;
+  return FastDiv{(uint32_t)((((uint64_t(1) << s) - d) << 32) / d + 1), s};
+}
+__device__ __forceinline__ int fdiv(int n, FastDiv f) {
+  return (int)((__umulhi((uint32_t)n, f.m) + (uint32_t)n) >> f.s);
+}
+
 // ---- MFMA operand / accumulator types ---------------------------------------
 typedef float v4f __attribute__((ext_vector_type(4)));
 typedef float v16f __attribute__((ext_vector_type(16)));
@@ -190,4 +207,10 @@ int launch_innerproduct_f32(const nhip_ip_plan* p, const float* in,
                             float* out, int m, void* ws, uint64_t ws_bytes,
                             hipStream_t s);
 uint64_t innerproduct_workspace(const nhip_ip_plan* p, int m);
+// Global average pooling of [n][k_in][hw] feeding the InnerProduct, fused
+// (gemm_f32.hip), for planes of 1 .. 6400 pixels.
+bool gap_innerproduct_supported(int hw);
+int launch_gap_innerproduct_f32(const nhip_ip_plan* p, const float* in, float* out, int n, int hw, void* ws,
+                                uint64_t ws_bytes, hipStream_t s);
+uint64_t gap_innerproduct_workspace(const nhip_ip_plan* p, int n, int hw);
 }  // namespace nhip

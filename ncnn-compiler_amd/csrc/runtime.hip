@@ -947,6 +947,36 @@ int nhip_innerproduct_f32_forward(nhip_ip_t p, const float* input, float* output
   return launch_innerproduct_f32(p, input, output, m, workspace, workspace_bytes, as_stream(stream));
 }
 
+int nhip_global_avgpool_innerproduct_f32_workspace_size(nhip_ip_t p, int32_t n, int32_t h, int32_t w,
+                                                        uint64_t* bytes) {
+  if (!p || !bytes) return fail(NHIP_STATUS_NULL_POINTER, "gap_innerproduct_workspace_size: null pointer");
+  if (p->q8) return fail(NHIP_STATUS_CONSTRAINT_VIOLATION, "gap_innerproduct: int8 plan");
+  if (n < 0 || h <= 0 || w <= 0) return fail(NHIP_STATUS_INVALID_SHAPE, "gap_innerproduct: invalid shape");
+  if ((int64_t)h * w > std::numeric_limits<int32_t>::max() || !gap_innerproduct_supported(h * w))
+    return fail(NHIP_STATUS_CONSTRAINT_VIOLATION, "gap_innerproduct: planes of at most 6400 pixels");
+  *bytes = n == 0 ? 0 : gap_innerproduct_workspace(p, n, h * w);
+  return ok();
+}
+
+int nhip_global_avgpool_innerproduct_f32_forward(nhip_ip_t p, const float* input, float* output, int32_t n,
+                                                 int32_t c, int32_t h, int32_t w, void* workspace,
+                                                 uint64_t workspace_bytes, void* stream) {
+  if (!p) return fail(NHIP_STATUS_NULL_POINTER, "gap_innerproduct_forward: null plan");
+  if (p->q8) return fail(NHIP_STATUS_CONSTRAINT_VIOLATION, "gap_innerproduct_forward: int8 plan");
+  if (n < 0 || c <= 0 || h <= 0 || w <= 0) return fail(NHIP_STATUS_INVALID_SHAPE, "gap_innerproduct: invalid shape");
+  if (c != p->k_in)
+    return fail(NHIP_STATUS_INVALID_SHAPE, "gap_innerproduct: input has " + std::to_string(c) +
+                                               " channels, weights expect " + std::to_string(p->k_in));
+  if ((int64_t)n * c * h * w > std::numeric_limits<int32_t>::max() ||
+      (int64_t)n * p->n_out > std::numeric_limits<int32_t>::max())
+    return fail(NHIP_STATUS_SHAPE_ARITHMETIC_OVERFLOW, "gap_innerproduct: tensor too large");
+  if (!gap_innerproduct_supported(h * w))
+    return fail(NHIP_STATUS_CONSTRAINT_VIOLATION, "gap_innerproduct: planes of at most 6400 pixels");
+  if (n == 0) return ok();
+  if (!input || !output) return fail(NHIP_STATUS_NULL_POINTER, "gap_innerproduct_forward: null pointer");
+  return launch_gap_innerproduct_f32(p, input, output, n, h * w, workspace, workspace_bytes, as_stream(stream));
+}
+
 int nhip_innerproduct_destroy(nhip_ip_t p) {
   if (p) {
     if (p->q8) free_plan(p->q8);

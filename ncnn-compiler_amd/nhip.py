@@ -44,7 +44,8 @@ EXPORTS = (
     "nhip_conv_destroy", "nhip_innerproduct_f32_create",
     "nhip_innerproduct_int8_create", "nhip_innerproduct_int8_forward",
     "nhip_innerproduct_workspace_size", "nhip_innerproduct_f32_forward",
-    "nhip_innerproduct_destroy", "nhip_relu_f32", "nhip_relu_i8",
+    "nhip_innerproduct_destroy", "nhip_global_avgpool_innerproduct_f32_workspace_size",
+    "nhip_global_avgpool_innerproduct_f32_forward", "nhip_relu_f32", "nhip_relu_i8",
     "nhip_add_f32", "nhip_global_avgpool_f32", "nhip_quantize_f32_i8",
     "nhip_requantize_i32_i8", "nhip_dequantize_i32_f32",
 )
@@ -125,6 +126,8 @@ def load():
         "nhip_innerproduct_workspace_size": [_P, i32, ctypes.POINTER(u64)],
         "nhip_innerproduct_f32_forward": [_P, _P, _P, i32, _P, u64, _P],
         "nhip_innerproduct_destroy": [_P],
+        "nhip_global_avgpool_innerproduct_f32_workspace_size": [_P, i32, i32, i32, ctypes.POINTER(u64)],
+        "nhip_global_avgpool_innerproduct_f32_forward": [_P, _P, _P, i32, i32, i32, i32, _P, u64, _P],
         "nhip_relu_f32": [_P, _P, i64, _P],
         "nhip_relu_i8": [_P, _P, i64, _P],
         "nhip_add_f32": [_P, _P, _P, i64, i32, _P],
@@ -485,6 +488,27 @@ class InnerProductF32(_Plan):
             nbytes = workspace.numel()
         check(load().nhip_innerproduct_f32_forward(self.handle, _ptr(x), _ptr(out), m, _ptr(workspace),
                                                    nbytes, _stream(stream)))
+        return out
+
+    def gap_workspace_size(self, n, h, w) -> int:
+        b = ctypes.c_uint64()
+        check(load().nhip_global_avgpool_innerproduct_f32_workspace_size(self.handle, n, h, w, ctypes.byref(b)))
+        return b.value
+
+    def forward_pooled(self, x, out=None, workspace=None, stream=None):
+        """Global average pooling of x [n, C, H, W] fused with this
+        InnerProduct (C = num_input) -> [n, num_output]."""
+        torch = _torch()
+        x = _dev(x, torch.float32)
+        n, c, h, w = x.shape
+        if out is None:
+            out = torch.empty((n, self.num_output), dtype=torch.float32, device=x.device)
+        if workspace is None:
+            workspace, nbytes = _workspace(self.gap_workspace_size(n, h, w), x.device)
+        else:
+            nbytes = workspace.numel()
+        check(load().nhip_global_avgpool_innerproduct_f32_forward(self.handle, _ptr(x), _ptr(out), n, c, h, w,
+                                                                  _ptr(workspace), nbytes, _stream(stream)))
         return out
 
 

@@ -5,7 +5,8 @@ Depthwise runs the reference's exact operation order (zero-init sum over
 kh, kw, then + bias, NCNNToTosa.cpp:3376-3503) with no fused multiply-add, so
 it is checked bit for bit.  InnerProduct (NCNNToTosa.cpp:5254-5392) is an
 MFMA GEMM: max relative error <= 1e-4.  Quantize / requantize / dequantize
-are bit-exact; global average pooling sums in a different order (1e-6).
+are bit-exact; global average pooling is checked to 1e-6 (planes of up to
+256 pixels are summed in the oracle's order and match it bit for bit).
 """
 import numpy as np
 import pytest
@@ -68,6 +69,46 @@ def test_depthwise_bit_exact(case, act, bias):
     if act == 1:
         exp = refcpu.relu_f32(exp)
     np.testing.assert_array_equal(got, exp)
+
+
+PLANE_CASES = [
+    # (n, c, h, w, stride, pad): 3x3 depthwise on planes of at most 1024
+    # pixels, the whole-plane LDS kernel - the MobileNetV2 layers at batch 32,
+    # blocks that end part-way (channel counts no multiple of the planes per
+    # block), odd plane sizes, 1x1 planes, asymmetric padding
+    (32, 960, 7, 7, 1, (1, 1, 1, 1)),
+    (32, 576, 14, 14, 2, (1, 1, 1, 1)),
+    (32, 384, 14, 14, 1, (1, 1, 1, 1)),
+    (32, 192, 28, 28, 2, (1, 1, 1, 1)),
+    (3, 37, 7, 7, 1, (1, 1, 1, 1)),
+    (1, 5, 1, 1, 1, (1, 1, 1, 1)),
+    (2, 7, 9, 13, 2, (0, 1, 0, 1)),
+    (2, 11, 32, 32, 2, (1, 1, 1, 1)),
+    (1, 3, 5, 31, 1, (2, 0, 1, 2)),
+]
+
+
+@pytest.mark.parametrize("case", PLANE_CASES, ids=lambda c: "x".join(map(str, c[:4])) + f"s{c[4]}")
+@pytest.mark.parametrize("planes", ["1", "0"])
+def test_depthwise_small_planes_bit_exact(case, planes, nhip_env):
+    """The whole-plane kernel (NHIP_DW_PLANES=1, default) and the row kernel
+    (=0) against the oracle, bit for bit; a 4-byte-offset input view (not
+    16-byte aligned) takes the row kernel and gives the same bits."""
+    nhip_env.setenv("NHIP_DW_PLANES", planes)
+    n, c, h, w, st, pad = case
+    x = RNG.uniform(-1, 1, (n, c, h, w)).astype(np.float32)
+    wt = workloads.he_normal(RNG, (c, 1, 3, 3), 9)
+    b = RNG.normal(0, 0.05, c).astype(np.float32)
+    d = nhip.conv_desc(c, c, (3, 3), (st, st), (1, 1), pad, bias=True, act=1, group=c)
+    plan = nhip.DwConv2dF32(d, wt, b)
+    got = host(plan.forward(dev(x)))
+    g = refcpu.geom(n, c, h, w, c, (3, 3), (st, st), (1, 1), pad)
+    exp = refcpu.relu_f32(refcpu.dwconv2d_f32(g, x, wt, b))
+    np.testing.assert_array_equal(got, exp)
+    buf = torch.empty(x.size + 1, dtype=torch.float32, device="cuda")
+    xv = buf[1:].view(x.shape)
+    xv.copy_(dev(x))
+    np.testing.assert_array_equal(host(plan.forward(xv)), exp)
 
 
 def test_innerproduct_config2():
