@@ -74,9 +74,10 @@ def timed(torch, fn, steps):
     return (time.perf_counter() - t0) / steps
 
 
-def kernel_time(nhip, torch, fn, steps, name):
+def kernel_time(nhip, torch, fn, steps, name, required=True):
     """(launches per call, seconds per launch) of the kernels whose name
-    contains `name`, from HIP events on their own dispatches."""
+    contains `name`, from HIP events on their own dispatches; (0, 0.0) when
+    none ran and `required` is false."""
     torch.cuda.synchronize()
     nhip.timer_start(name)
     for _ in range(steps):
@@ -84,7 +85,9 @@ def kernel_time(nhip, torch, fn, steps, name):
     torch.cuda.synchronize()
     launches, ms = nhip.timer_stop()
     if launches == 0:
-        return 0, 0.0
+        if not required:
+            return 0, 0.0
+        raise RuntimeError(f"no kernel launch named like {name!r} was timed")
     return launches / steps, ms / 1e3 / launches
 
 
@@ -93,7 +96,7 @@ def dominant(nhip, torch, fn, steps, names):
     (name, launches per call, seconds per launch)."""
     best = None
     for nm in names:
-        per, sec = kernel_time(nhip, torch, fn, steps, nm)
+        per, sec = kernel_time(nhip, torch, fn, steps, nm, required=False)
         if per and (best is None or per * sec > best[1] * best[2]):
             best = (nm, per, sec)
     return best
@@ -261,7 +264,7 @@ def config1(nhip, workloads, torch, steps, warmup, workdir, share, cpu, target_s
     wflops = workloads.winograd_flops(1, 64, 64, 56, 56)
     kernels = {}
     for k in ("wino_input_transform", "wino_gemm", "wino_output_transform", "wino_fused"):
-        kp, ks = kernel_time(nhip, torch, fn, n, k)
+        kp, ks = kernel_time(nhip, torch, fn, n, k, required=False)
         if kp:
             kernels[k] = round(kp * ks * 1e6, 2)
     res = {"workload": "conv fp32 1x64x56x56 -> 64, 3x3 s1 p1, bias + ReLU (Winograd F(4,3), device buffers)",
@@ -308,7 +311,8 @@ def config2(nhip, workloads, torch, steps, warmup, share, cpu, target_s):
     per, sec = kernel_time(nhip, torch, fn, n, "innerproduct_f32")
     res = {"workload": "InnerProduct fp32 256x2048 -> 1000 + bias (device buffers)",
            "ms_per_step": dt * 1e3, "tflops": flops / dt / 1e12,
-           "roofline": roofline("mfma", "innerproduct_f32 (MFMA GEMM, split-K partials)", flops / per, sec, per)}
+           "roofline": roofline("mfma", "innerproduct_f32 (MFMA GEMM fed by direct-to-LDS loads, split-K partials)",
+                                flops / per, sec, per)}
     if cpu:
         from oracle import refcpu
         res["cpu_baseline"] = cpu_pair(lambda t: refcpu.innerproduct_f32(x, w, b, threads=t), flops / 1e12,

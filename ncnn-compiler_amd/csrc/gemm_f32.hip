@@ -46,6 +46,7 @@ struct GemmArgs {
   // conv geometry
   const int* ktab;
   int C, H, W, OW, OHW, sh, sw, pt, pl;
+  int pointwise;         // 1x1, stride 1, no padding: reduction index k is channel k (no ktab lookup)
   // epilogue
   float* d;              // conv: out NCHW; IP: out [M][ldd]
   int ldd;
@@ -174,8 +175,13 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_kernel(GemmArgs g) {
       const int kbase = kt * BK + kg * KPT;
 #pragma unroll
       for (int u = 0; u < KPT; ++u) {
-        const int t = g.ktab[kbase + u];  // wave-uniform
-        const int c = t >> 16, dy = (t >> 8) & 255, dx = t & 255;
+        int c = kbase + u, dy = 0, dx = 0;
+        if (!g.pointwise) {  // wave-uniform table entry
+          const int t = g.ktab[kbase + u];
+          c = t >> 16;
+          dy = (t >> 8) & 255;
+          dx = t & 255;
+        }
         const int y = iy0 + dy, x = ix0 + dx;
         const bool in = pix_ok && c < g.C && (unsigned)y < (unsigned)g.H && (unsigned)x < (unsigned)g.W;
         st.b[u] = buf_load_f32(img_rs, in ? (uint32_t)((((img_plane0 + c) * g.H + y) * g.W + x) * (int)sizeof(float))
@@ -457,6 +463,7 @@ IgemmCfg igemm_config(const nhip_conv_plan* p, int64_t npix) {
 
 uint64_t conv_igemm_f32_workspace(const nhip_conv_plan* p, int n, int oh, int ow) {
   if (pointwise_selected(p, n, oh, ow)) return 0;
+  if (pw_dma_supported(p, n, oh, ow)) return conv_pw_dma_workspace(p, n, oh, ow);
   const int64_t npix = (int64_t)n * oh * ow;
   const IgemmCfg c = igemm_config(p, npix);
   return c.splits > 1 ? (uint64_t)c.splits * p->g.k * npix * sizeof(float) : 0;
@@ -467,6 +474,7 @@ int launch_conv_igemm_f32(const nhip_conv_plan* p, const float* in,
                           int w, int oh, int ow, void* ws, uint64_t ws_bytes,
                           hipStream_t s) {
   if (pointwise_selected(p, n, h, w)) return launch_conv_pointwise_f32(p, in, residual, out, n, h, w, s);
+  if (pw_dma_supported(p, n, h, w)) return launch_conv_pw_dma(p, in, residual, out, n, h, w, ws, ws_bytes, s);
   GemmArgs g{};
   g.a = p->weight;
   g.lda = p->kred_pad;
@@ -485,6 +493,8 @@ int launch_conv_igemm_f32(const nhip_conv_plan* p, const float* in,
   g.sw = p->g.sw;
   g.pt = p->g.pt;
   g.pl = p->g.pl;
+  g.pointwise = p->g.kh == 1 && p->g.kw == 1 && p->g.sh == 1 && p->g.sw == 1 && p->g.pt == 0 && p->g.pl == 0 &&
+                p->g.pb == 0 && p->g.pr == 0;
   g.d = out;
   g.bias = p->bias;
   g.residual = residual;
@@ -525,8 +535,10 @@ static int ip_splits(const nhip_ip_plan* p, int m) {
 
 uint64_t innerproduct_workspace(const nhip_ip_plan* p, int m) {
   const int splits = ip_splits(p, m);
-  if (splits == 1) return 0;
-  return (uint64_t)splits * m * p->n_pad * sizeof(float);
+  const uint64_t own = splits == 1 ? 0 : (uint64_t)splits * m * p->n_pad * sizeof(float);
+  // the direct-to-LDS kernel runs when the input is 16-byte aligned; this
+  // kernel otherwise: room for either
+  return ip_dma_supported(p, nullptr, m) ? std::max(own, innerproduct_dma_workspace(p, m)) : own;
 }
 
 // ------------------- global average pooling + InnerProduct -----------------
@@ -680,6 +692,7 @@ int launch_gap_innerproduct_f32(const nhip_ip_plan* p, const float* in, float* o
 int launch_innerproduct_f32(const nhip_ip_plan* p, const float* in,
                             float* out, int m, void* ws, uint64_t ws_bytes,
                             hipStream_t s) {
+  if (ip_dma_supported(p, in, m)) return launch_innerproduct_dma(p, in, out, m, ws, ws_bytes, s);
   GemmArgs g{};
   g.a = in;
   g.lda = p->k_in;

@@ -207,6 +207,17 @@ int launch_innerproduct_f32(const nhip_ip_plan* p, const float* in,
                             float* out, int m, void* ws, uint64_t ws_bytes,
                             hipStream_t s);
 uint64_t innerproduct_workspace(const nhip_ip_plan* p, int m);
+// fp32 GEMMs fed by direct-to-LDS loads (gemm_dma.hip): the InnerProduct
+// and the 1x1 stride-1 unpadded convolution.  `in` may be null for the
+// workspace query (alignment is then not part of the answer).
+bool ip_dma_supported(const nhip_ip_plan* p, const float* in, int m);
+uint64_t innerproduct_dma_workspace(const nhip_ip_plan* p, int m);
+int launch_innerproduct_dma(const nhip_ip_plan* p, const float* in, float* out, int m, void* ws, uint64_t ws_bytes,
+                            hipStream_t s);
+bool pw_dma_supported(const nhip_conv_plan* p, int n, int h, int w);
+uint64_t conv_pw_dma_workspace(const nhip_conv_plan* p, int n, int h, int w);
+int launch_conv_pw_dma(const nhip_conv_plan* p, const float* in, const float* residual, float* out, int n, int h,
+                       int w, void* ws, uint64_t ws_bytes, hipStream_t s);
 // Global average pooling of [n][k_in][hw] feeding the InnerProduct, fused
 // (gemm_f32.hip), for planes of 1 .. 6400 pixels.
 bool gap_innerproduct_supported(int hw);

@@ -34,6 +34,7 @@
 #include <cstdlib>
 #include <cstring>
 
+#include "lds_dma.h"
 #include "nhip_internal.h"
 
 namespace nhip {
@@ -433,27 +434,11 @@ constexpr int kPerWave = (kInstrV + kInstrU) / 4;     // 9 per wave and chunk
 static_assert(kLdsBytes >= kKB * kTB * 16 * (int)sizeof(float), "the staged output tiles fit in the slots");
 static_assert((kInstrV + kInstrU) % 4 == 0, "whole copies per wave");
 
-// One 1 KB copy: lane l's 16 bytes from the buffer at voff + soff to LDS
-// byte address lds_base + 16*l.
-__device__ __forceinline__ void copy16(uint32_t lds_base, uint32_t voff, v4i rsrc, uint32_t soff) {
-  asm volatile(
-      "s_mov_b32 m0, %0\n\t"
-      "s_nop 0\n\t"
-      "buffer_load_dwordx4 %1, %2, %3 offen lds" ::"s"(lds_base),
-      "v"(voff), "s"(rsrc), "s"(soff)
-      : "memory", "m0");
-}
-
 // Wait until at most 9 * chunks of this wave's copies are outstanding.
 __device__ __forceinline__ void wait_copies(int chunks) {
   static_assert(kPerWave == 9 && kSlots == 2, "the counts below are 9 copies per chunk, at most one chunk ahead");
   if (chunks >= 1) asm volatile("s_waitcnt vmcnt(9)" ::: "memory");
   else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-}
-
-__device__ __forceinline__ v4i raw_rsrc(const void* base, uint32_t bytes) {
-  const uint64_t a = reinterpret_cast<uint64_t>(base);
-  return v4i{(int)(uint32_t)a, (int)(uint32_t)(a >> 32) & 0xffff, (int)bytes, 0x00020000};
 }
 }  // namespace dma
 
@@ -469,7 +454,7 @@ __global__ __launch_bounds__(dma::kThreads, 2) void wino_fused_dma_kernel(FusedA
   // Copy sources.  V[xi][c/2][t][2]: copy j of a chunk covers xi = 2j, 2j+1
   // (lane bit 5), pairs 0, 1 of the chunk (lane bit 4), tiles t0 + 2*(l%16)
   // and +1.  U[c/8][xi][pair][k][2] likewise over k0 .. k0 + 31.
-  const v4i vrs = dma::raw_rsrc(a.V, a.v_bytes), urs = dma::raw_rsrc(a.U, a.u_bytes);
+  const v4i vrs = ::nhip::dma::raw_rsrc(a.V, a.v_bytes), urs = ::nhip::dma::raw_rsrc(a.U, a.u_bytes);
   const int hp = a.c_pad / 2;
   const uint32_t v_lane =
       (uint32_t)((((lane >> 5) * hp + ((lane >> 4) & 1)) * a.t_pad + bk.t0 + 2 * (lane & 15)) * 8);
@@ -481,11 +466,11 @@ __global__ __launch_bounds__(dma::kThreads, 2) void wino_fused_dma_kernel(FusedA
       const int q = wave + 4 * m;
       if (q < dma::kInstrV) {
         const uint32_t so = (uint32_t)(((2 * q) * hp + 2 * c4) * a.t_pad * 8);
-        dma::copy16(sb + (uint32_t)(q * 1024), v_lane, vrs, so);
+        ::nhip::dma::copy16(sb + (uint32_t)(q * 1024), v_lane, vrs, so);
       } else {
         const int j = q - dma::kInstrV;
         const uint32_t so = (uint32_t)((((c4 >> 1) * 36 + 2 * j) * 4 + (c4 & 1) * 2) * a.m_pad * 8);
-        dma::copy16(sb + (uint32_t)(dma::kVElems * 4 + j * 1024), u_lane, urs, so);
+        ::nhip::dma::copy16(sb + (uint32_t)(dma::kVElems * 4 + j * 1024), u_lane, urs, so);
       }
     }
   };
