@@ -34,14 +34,16 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kRow = 64 + 16;  // quantize tile row stride (bytes)
 
+// Branch-free: both roundings are formed and selected, and NaN (which
+// fminf / fmaxf would turn into +-127) selects 0 at the end.
 __device__ __forceinline__ int8_t quantize_i8(float x, float scale) {
 #pragma clang fp contract(off)
   const float s = x * scale;
-  if (s != s) return 0;
   float r = (s >= 0.0f) ? floorf(s + 0.5f) : ceilf(s - 0.5f);
   r = fminf(r, 127.0f);
   r = fmaxf(r, -127.0f);
-  return (int8_t)(int)r;
+  const int q = (int)r;
+  return (int8_t)(s != s ? 0 : q);
 }
 
 // x [N][C][HW] (fp32 or int8) -> y [N][HW][c_pad] int8, zero channel padding.
@@ -106,6 +108,8 @@ struct Int8Args {
   int OH, R;           // output rows per workgroup
   int FH, FW, FS;      // input footprint rows / columns / LDS bytes per pixel
   int fp_bytes;        // LDS bytes of the footprint (multiple of 16)
+  int rb_off;             // LDS byte offset of the footprint kernel's reciprocals and biases
+  FastDiv cpp_div, fw_div;  // footprint copy: 16-byte channel chunks per pixel, window width
 };
 
 // D[i = out channel][j = pixel] over the (kh, kw, c) reduction.
@@ -243,34 +247,35 @@ __global__ __launch_bounds__(kThreads) void conv_int8_kernel(Int8Args g) {
   // with one vector store (bytes or floats), falling back to element stores
   // where the run crosses an image or the tile edge or is misaligned.
   __syncthreads();
-  const bool q8 = g.term > 100;
+  const bool q8 = g.term > 100, relu = g.act == NHIP_ACT_RELU;
   float* tf = reinterpret_cast<float*>(smem);
   int8_t* tq = smem;
-#pragma unroll
-  for (int b = 0; b < TN; ++b) {
-    const int jl = wn * (BN / 2) + b * 32 + li;
-#pragma unroll
-    for (int a = 0; a < TM; ++a)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int il = wm * (BM / 2) + a * 32 + (r & 3) + 8 * (r >> 2) + 4 * lh;
-        const int i = i0 + il;
-        float f;
-        {
+  // One wave-uniform branch on the output kind; the per-value arithmetic
+  // is branch-free.
+  auto dequant = [&](int a, int b, int r, int il) {  // il: row of the tile
 #pragma clang fp contract(off)
-          f = (float)acc[a][b][r];
-          f = f * g.recip[i];
-          f = f + g.bias[i];
-        }
-        if (q8) {
-          int8_t q = quantize_i8(f, g.os);
-          if (g.act == NHIP_ACT_RELU && q < 0) q = 0;
-          tq[il * ES + jl] = q;
-        } else {
-          if (g.act == NHIP_ACT_RELU) f = f < 0.0f ? 0.0f : f;
-          tf[il * ES + jl] = f;
-        }
-      }
+    float f = (float)acc[a][b][r];
+    f = f * g.recip[i0 + il];
+    return f + g.bias[i0 + il];
+  };
+#define NHIP_I8_EPI(STORE)                                                                 \
+  for (int b = 0; b < TN; ++b) {                                                          \
+    const int jl = wn * (BN / 2) + b * 32 + li;                                           \
+    _Pragma("unroll") for (int a = 0; a < TM; ++a) _Pragma("unroll") for (int r = 0; r < 16; ++r) { \
+      const int il = wm * (BM / 2) + a * 32 + (r & 3) + 8 * (r >> 2) + 4 * lh;            \
+      const float f = dequant(a, b, r, il);                                              \
+      STORE;                                                                              \
+    }                                                                                     \
+  }
+  if (q8) {
+#pragma unroll
+    NHIP_I8_EPI({
+      const int8_t q = quantize_i8(f, g.os);
+      tq[il * ES + jl] = (relu && q < 0) ? (int8_t)0 : q;
+    })
+  } else {
+#pragma unroll
+    NHIP_I8_EPI(tf[il * ES + jl] = (relu && f < 0.0f) ? 0.0f : f)
   }
   __syncthreads();
   constexpr int RUNS = BN / 16;  // 16-pixel runs per row
@@ -334,41 +339,6 @@ __global__ __launch_bounds__(kThreads) void conv_int8_fp_kernel(Int8Args g) {
   const int i0 = blockIdx.y * BM;
   const int npx = min(g.R, g.OH - oy0) * g.OW;  // valid pixels of this workgroup
 
-  // ---- footprint -> LDS, four 16-byte loads in flight per thread
-  {
-    const __amdgpu_buffer_rsrc_t rs = make_rsrc(g.x, g.x_bytes);
-    const int cpp = g.c_pad / 16;
-    const int total = g.FH * g.FW * cpp;
-    const int iy_base = oy0 * g.sh - g.pt;
-    for (int base = 0; base < total; base += 4 * kThreads) {
-      v4i v[4];
-      int dst[4];
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int e = base + q * kThreads + tid;
-        const int pix = e / cpp, ch = e - pix * cpp;
-        const int fy = pix / g.FW, fx = pix - fy * g.FW;
-        const int iy = iy_base + fy, ix = fx - g.pl;
-        const bool in = e < total && (unsigned)iy < (unsigned)g.H && (unsigned)ix < (unsigned)g.W;
-        v[q] = __builtin_bit_cast(
-            v4i, buf_load_b128(rs, in ? (uint32_t)(((img * g.H + iy) * g.W + ix) * g.c_pad + ch * 16) : kBufOOB));
-        dst[q] = e < total ? pix * g.FS + ch * 16 : -1;
-      }
-#pragma unroll
-      for (int q = 0; q < 4; ++q)
-        if (dst[q] >= 0) *reinterpret_cast<v4i*>(foot + dst[q]) = v[q];
-    }
-  }
-
-  // per-lane window origin (bytes) of each of the wave's pixel columns
-  int fbase[TN];
-#pragma unroll
-  for (int b = 0; b < TN; ++b) {
-    const int pc = min(wn * (BN / 2) + b * 32 + li, npx - 1);
-    const int py = pc / g.OW, px = pc - py * g.OW;
-    fbase[b] = (py * g.sh * g.FW + px * g.sw) * g.FS;
-  }
-
   struct Stage {
     v4i a[A_LD];
   };
@@ -388,6 +358,54 @@ __global__ __launch_bounds__(kThreads) void conv_int8_fp_kernel(Int8Args g) {
       *reinterpret_cast<v4i*>(As(buf) + row * ROW + ch * 16) = st.a[u];
     }
   };
+
+  // The first two weight stages, the footprint and this workgroup's
+  // reciprocals and biases are all requested before anything waits, so
+  // their latencies overlap instead of adding up.
+  const int n = g.kred_pad / BK;
+  Stage s0, s1;
+  gload(s0, 0);
+  if (n > 1) gload(s1, 1);
+  float* rb = reinterpret_cast<float*>(dsm + g.rb_off);  // [BM] reciprocals, then [BM] biases
+  if (tid < BM) {
+    rb[tid] = g.recip[i0 + tid];
+    rb[BM + tid] = g.bias[i0 + tid];
+  }
+
+  // ---- footprint -> LDS, eight 16-byte loads in flight per thread
+  {
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(g.x, g.x_bytes);
+    const int cpp = g.c_pad / 16;
+    const int total = g.FH * g.FW * cpp;
+    const int iy_base = oy0 * g.sh - g.pt;
+    for (int base = 0; base < total; base += 8 * kThreads) {
+      v4i v[8];
+      int dst[8];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const int e = base + q * kThreads + tid;
+        const int pix = fdiv(e, g.cpp_div), ch = e - pix * cpp;
+        const int fy = fdiv(pix, g.fw_div), fx = pix - fy * g.FW;
+        const int iy = iy_base + fy, ix = fx - g.pl;
+        const bool in = e < total && (unsigned)iy < (unsigned)g.H && (unsigned)ix < (unsigned)g.W;
+        v[q] = __builtin_bit_cast(
+            v4i, buf_load_b128(rs, in ? (uint32_t)(((img * g.H + iy) * g.W + ix) * g.c_pad + ch * 16) : kBufOOB));
+        dst[q] = e < total ? pix * g.FS + ch * 16 : -1;
+      }
+#pragma unroll
+      for (int q = 0; q < 8; ++q)
+        if (dst[q] >= 0) *reinterpret_cast<v4i*>(foot + dst[q]) = v[q];
+    }
+  }
+
+  // per-lane window origin (bytes) of each of the wave's pixel columns
+  int fbase[TN];
+#pragma unroll
+  for (int b = 0; b < TN; ++b) {
+    const int pc = min(wn * (BN / 2) + b * 32 + li, npx - 1);
+    const int py = pc / g.OW, px = pc - py * g.OW;
+    fbase[b] = (py * g.sh * g.FW + px * g.sw) * g.FS;
+  }
 
   v16i acc[TM][TN];
 #pragma unroll
@@ -419,13 +437,9 @@ __global__ __launch_bounds__(kThreads) void conv_int8_fp_kernel(Int8Args g) {
     }
   };
 
-  const int n = g.kred_pad / BK;
   {
-    Stage s0, s1;
-    gload(s0, 0);
-    if (n > 1) gload(s1, 1);
     lstore(s0, 0);
-    __syncthreads();  // footprint and first A stage visible
+    __syncthreads();  // footprint, first A stage, reciprocals and biases visible
     int i = 0;
     for (; i + 1 < n; i += 2) {
       if (i + 2 < n) gload(s0, i + 2);
@@ -442,35 +456,26 @@ __global__ __launch_bounds__(kThreads) void conv_int8_fp_kernel(Int8Args g) {
 
   // ---- epilogue (as conv_int8_kernel), staged in LDS over the footprint
   __syncthreads();
-  const bool q8 = g.term > 100;
+  const bool q8 = g.term > 100, relu = g.act == NHIP_ACT_RELU;
   float* tf = reinterpret_cast<float*>(dsm);
   int8_t* tq = dsm;
-#pragma unroll
-  for (int b = 0; b < TN; ++b) {
-    const int jl = wn * (BN / 2) + b * 32 + li;
-#pragma unroll
-    for (int a = 0; a < TM; ++a)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int il = wm * (BM / 2) + a * 32 + (r & 3) + 8 * (r >> 2) + 4 * lh;
-        const int i = i0 + il;
-        float f;
-        {
+  auto dequant = [&](int a, int b, int r, int il) {
 #pragma clang fp contract(off)
-          f = (float)acc[a][b][r];
-          f = f * g.recip[i];
-          f = f + g.bias[i];
-        }
-        if (q8) {
-          int8_t q = quantize_i8(f, g.os);
-          if (g.act == NHIP_ACT_RELU && q < 0) q = 0;
-          tq[il * ES + jl] = q;
-        } else {
-          if (g.act == NHIP_ACT_RELU) f = f < 0.0f ? 0.0f : f;
-          tf[il * ES + jl] = f;
-        }
-      }
+    float f = (float)acc[a][b][r];
+    f = f * rb[il];
+    return f + rb[BM + il];
+  };
+  if (q8) {
+#pragma unroll
+    NHIP_I8_EPI({
+      const int8_t q = quantize_i8(f, g.os);
+      tq[il * ES + jl] = (relu && q < 0) ? (int8_t)0 : q;
+    })
+  } else {
+#pragma unroll
+    NHIP_I8_EPI(tf[il * ES + jl] = (relu && f < 0.0f) ? 0.0f : f)
   }
+#undef NHIP_I8_EPI
   __syncthreads();
   constexpr int RUNS = BN / 16;
   for (int q = tid; q < BM * RUNS; q += kThreads) {
@@ -555,17 +560,24 @@ int launch_conv_int8(const nhip_conv_plan* p, const void* in, int in_is_i8,
       g.FW = (ow - 1) * p->g.sw + max_dx + 1;
       g.FS = p->c_pad + 16;
       g.fp_bytes = (int)round_up((int64_t)g.FH * g.FW * g.FS, 16);
-      const int bm = p->m_pad % 128 == 0 && p->m_pad >= 256 ? 128 : 64;
+      g.cpp_div = fast_div((uint32_t)(p->c_pad / 16));
+      g.fw_div = fast_div((uint32_t)g.FW);
+      int bm = p->m_pad % 128 == 0 && p->m_pad >= 256 ? 128 : 64;
+      // NHIP_INT8_FP_BM=64/128 overrides (tuning switch, ignored when invalid)
+      if (const int v = setting_int("NHIP_INT8_FP_BM", 0); (v == 64 || v == 128) && p->m_pad % v == 0) bm = v;
       // K stage: the widest of 384 / 192 / 128 bytes that divides the
       // reduction (fewer stages: fewer global-load round trips and barriers
       // per workgroup; config 4: 3 stages of 384 bytes, 16.3 against 17.2 us
       // with 128-byte stages); NHIP_INT8_FP_BK overrides (tuning switch,
       // ignored when invalid).
-      auto lds_for = [&](int bk) {
+      // operands (footprint + two weight stages) or the epilogue's staging,
+      // then bm reciprocals and bm biases past both
+      auto rb_at = [&](int bk) {
         const int64_t oper = (int64_t)g.fp_bytes + 2LL * bm * (bk + 16);
         const int64_t epi = (int64_t)bm * (128 + 16) * 4;
-        return std::max(oper, epi);
+        return round_up(std::max(oper, epi), 16);
       };
+      auto lds_for = [&](int bk) { return rb_at(bk) + 2LL * bm * 4; };
       // Eligible when the window fits beside 128-byte stages in 64 KB; wider
       // stages may take up to 80 KB (still two workgroups per CU).
       constexpr int64_t kMaxLds = 80 * 1024;
@@ -580,13 +592,15 @@ int launch_conv_int8(const nhip_conv_plan* p, const void* in, int in_is_i8,
         if ((c == 128 || c == 192 || c == 384) && p->kred_pad % c == 0 && lds_for(c) <= kMaxLds) bk = c;
       }
       const int64_t lds = lds_for(bk);
+      g.rb_off = (int)rb_at(bk);
       if (lds_for(128) <= 64 * 1024) {
         const dim3 grid((unsigned)(n * ceil_div(oh, g.R)), (unsigned)(p->m_pad / bm));
-#define NHIP_FP_CASE(BM_, BK_)                                                                             \
-  if (bm == BM_ && bk == BK_) {                                                                           \
-    NHIP_TRY(ensure_dynamic_lds(reinterpret_cast<const void*>(&conv_int8_fp_kernel<BM_, BK_>), (int)kMaxLds)); \
-    NHIP_LAUNCH("conv_int8_fp", (conv_int8_fp_kernel<BM_, BK_>), grid, dim3(kThreads), (unsigned)lds, s, g); \
-    return check_launch("conv_int8_fp");                                                                  \
+#define NHIP_FP_CASE(BM_, BK_)                                                                                   \
+  if (bm == BM_ && bk == BK_) {                                                                                 \
+    const auto kernel = conv_int8_fp_kernel<BM_, BK_>;                                                          \
+    NHIP_TRY(ensure_dynamic_lds(reinterpret_cast<const void*>(kernel), (int)kMaxLds));                          \
+    NHIP_LAUNCH("conv_int8_fp", kernel, grid, dim3(kThreads), (unsigned)lds, s, g);                              \
+    return check_launch("conv_int8_fp");                                                                        \
   }
         NHIP_FP_CASE(64, 128)
         NHIP_FP_CASE(64, 192)

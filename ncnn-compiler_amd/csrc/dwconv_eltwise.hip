@@ -299,14 +299,16 @@ __global__ __launch_bounds__(256) void dw3x3_planes_kernel(DwArgs a, FastDiv ohw
 
 // ---------------------------------------------------------------------------
 
+// Branch-free: both roundings are formed and selected, and NaN (which
+// fminf / fmaxf would turn into +-127) selects 0 at the end.
 __device__ __forceinline__ int8_t quantize_i8(float x, float scale) {
 #pragma clang fp contract(off)
   const float s = x * scale;
-  if (s != s) return 0;
   float r = (s >= 0.0f) ? floorf(s + 0.5f) : ceilf(s - 0.5f);
   r = fminf(r, 127.0f);
   r = fmaxf(r, -127.0f);
-  return (int8_t)(int)r;
+  const int q = (int)r;
+  return (int8_t)(s != s ? 0 : q);
 }
 
 // int8 ConvolutionDepthWise (NCNNToTosa.cpp:3257-3376): the input band is

@@ -106,11 +106,17 @@ CASES = [
     (2, 32, 16, 16, 40, (3, 3), (2, 2), (1, 1), (0, 0, 0, 0), 101, 1, False, False),
     (1, 64, 8, 12, 64, (3, 3), (1, 1), (1, 1), (1, 2, 1, 2), 1, 0, True, True),
     (2, 96, 7, 20, 32, (3, 3), (1, 1), (1, 1), (1, 1, 1, 1), 102, 1, False, True),
+    # 5x5 taps over 64 channels: K stages cross taps, K padding past the 25th
+    (1, 64, 9, 11, 24, (5, 5), (1, 1), (1, 1), (2, 2, 2, 2), 101, 1, False, False),
 ]
 
 
 @pytest.mark.parametrize("case", CASES, ids=lambda c: "x".join(map(str, c[:5])) + f"-t{c[9]}")
-def test_int8_shapes_bit_exact(case):
+@pytest.mark.parametrize("footprint", ["1", "0"])
+def test_int8_shapes_bit_exact(case, footprint, nhip_env):
+    """footprint: the whole-row footprint kernel where the shape allows it
+    (NHIP_INT8_FOOTPRINT=1, default) or the im2col-gather kernel (=0)."""
+    nhip_env.setenv("NHIP_INT8_FOOTPRINT", footprint)
     n, c, h, w, k, ker, st, dl, pad, term, act, wf32, scalar = case
     rng = np.random.default_rng(hash(case) % (2 ** 32))
     x = rng.uniform(-1.5, 1.5, (n, c, h, w)).astype(np.float32)
