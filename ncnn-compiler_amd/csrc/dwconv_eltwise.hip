@@ -8,6 +8,7 @@
 // round every fp32 step separately to match the reference bit for bit.
 #include <algorithm>
 
+#include "lds_dma.h"
 #include "nhip_internal.h"
 
 namespace nhip {
@@ -228,73 +229,153 @@ __global__ __launch_bounds__(256) void dw3x3_f32_kernel(DwArgs a, uint32_t x_byt
 }
 
 // 3x3 depthwise, stride S (1 or 2), dilation 1, any padding, for planes of
-// at most kDwPlaneMax pixels: a workgroup takes `ppb` whole planes (image x
-// channel).  In NCHW those planes are one contiguous block of the input and
-// one of the output, so the block comes into LDS through 16-byte loads
-// (every lane's load a full vector, the whole wave 1 KB), lanes then take
-// consecutive outputs (consecutive LDS words: no bank conflicts), and the
-// results, staged in LDS, leave as 16-byte stores.  The host picks ppb so
-// that every block starts on a 16-byte boundary of x and y.  Summation
-// order of the CPU loop nest: acc = 0, += x*w over (kh, kw), then + bias.
+// at most kDwPlaneMax pixels, streamed: the (image, channel) planes are cut
+// into chunks of `ppb` whole planes, in NCHW one contiguous block of the
+// input and one of the output each.  A persistent workgroup walks the
+// chunks blockIdx.x, + gridDim.x, ...; while it computes chunk k, chunk
+// k + 1 is on its way into the other of two LDS slots through direct-to-LDS
+// copies (1 KB per wave copy, no registers), so the HBM reads of one chunk
+// overlap the arithmetic and the stores of the previous one.  Stride 1: a
+// lane takes one output row (at most kDwRowMax outputs), its three input
+// rows go from LDS into registers in one go (the zero halo decided once per
+// column) and the row's outputs are formed from registers.  Stride 2: lanes
+// take consecutive outputs (consecutive LDS words), each read from LDS.
+// (Measured at batch 32: row lanes 8.2 against 11.1 us at 384@14, 11.0
+// against 14.6 at 576@14; output lanes 7.7 against 13.0 at 576@14 stride 2,
+// 9.5 against 15.2 at 192@28 stride 2.)  The results are staged in LDS and
+// leave as 16-byte stores.  The host picks ppb so that every output block
+// starts on a 16-byte boundary.  Summation order of the CPU loop nest:
+// acc = 0, += x*w over (kh, kw), then + bias.
 constexpr int kDwPlaneMax = 1024;
+constexpr int kDwRowMax = 16;
+
+struct DwStream {
+  uint32_t x_bytes;
+  int chunks;      // ceil(planes / ppb)
+  int slot;        // floats per input slot (whole 4 KB: 4 waves x 1 KB copies)
+  int copies;      // 1 KB copies per wave and chunk
+  FastDiv oh_div, ohw_div, ow_div;
+};
 
 template <int S>
-__global__ __launch_bounds__(256) void dw3x3_planes_kernel(DwArgs a, FastDiv ohw_div, FastDiv ow_div) {
-  extern __shared__ float lds[];
+__global__ __launch_bounds__(256) void dw3x3_stream_kernel(DwArgs a, DwStream st) {
+  extern __shared__ __attribute__((aligned(16))) float lds[];
   const int hw = a.H * a.W, ohw = a.OH * a.OW;
-  const int p0 = blockIdx.x * a.ppb;
-  const int np = min(a.ppb, a.planes - p0);
-  float* xin = lds;                // [ppb][hw]
-  float* yout = xin + a.ppb * hw;  // [ppb][ohw]
-  float* wl = yout + a.ppb * ohw;  // [ppb][10]: the plane's 9 weights, then its bias
-  const float* xs = a.x + (int64_t)p0 * hw;
-  const int nin = np * hw, nin4 = nin >> 2;
-  for (int v0 = threadIdx.x; v0 < nin4; v0 += 1024) {  // four loads in flight per lane
-    v4f t[4];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  float* yout = lds + 2 * st.slot;  // [ppb][ohw]
+  float* wl = yout + a.ppb * ohw;   // [ppb][10]: the plane's 9 weights, then its bias
+  const uint32_t lds0 = (uint32_t)(uintptr_t)lds;
+  const v4i rs = dma::raw_rsrc(a.x, st.x_bytes);
+  // chunk c into slot: wave w copies bytes [1 KB (w + 4 i), + 1 KB) of the chunk
+  auto issue = [&](int c, int slot) {
+    const uint32_t src = (uint32_t)((int64_t)c * a.ppb * hw * 4);
+    const uint32_t end = (uint32_t)min((int64_t)(c + 1) * a.ppb * hw * 4, (int64_t)st.x_bytes);
+    for (int i = 0; i < st.copies; ++i) {
+      const uint32_t off = (uint32_t)((wave + 4 * i) * 1024 + lane * 16);
+      dma::copy16(lds0 + (uint32_t)(slot * st.slot * 4) + (uint32_t)((wave + 4 * i) * 1024),
+                  src + off < end ? src + off : kBufOOB, rs, 0);
+    }
+  };
+  // the chunk's per-plane weights and bias (ppb * 10 <= 4 * 256 values),
+  // requested together with its copy and written to LDS after the wait
+  float wv[4];
+  auto fetch_w = [&](int c) {
+    const int p0 = c * a.ppb, np = min(a.ppb, a.planes - p0);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int e = tid + 256 * u;
+      const int pi = e / 10, t = e - pi * 10;
+      const int ch = (p0 + min(pi, np - 1)) % a.C;
+      wv[u] = e < np * 10 ? (t < 9 ? a.w[ch * 9 + t] : a.bias[ch]) : 0.f;
+    }
+  };
+  int k = 0;
+  if ((int)blockIdx.x < st.chunks) {
+    issue(blockIdx.x, 0);
+    fetch_w(blockIdx.x);
+  }
+  for (int c = blockIdx.x; c < st.chunks; c += gridDim.x, ++k) {
+    const int p0 = c * a.ppb, np = min(a.ppb, a.planes - p0);
+    dma::wait_vmcnt<0>();  // chunk c and its weights have landed (and earlier stores are done)
+    __syncthreads();       // ... for every wave; slot (k + 1) % 2 and the staging are free
 #pragma unroll
     for (int u = 0; u < 4; ++u)
-      if (v0 + 256 * u < nin4) t[u] = reinterpret_cast<const v4f*>(xs)[v0 + 256 * u];
+      if (tid + 256 * u < np * 10) wl[tid + 256 * u] = wv[u];
+    if (c + (int)gridDim.x < st.chunks) {
+      issue(c + gridDim.x, (k + 1) & 1);
+      fetch_w(c + gridDim.x);
+    }
+    __syncthreads();
+    const float* xin = lds + (k & 1) * st.slot;
+    const int nout = np * ohw, rows = np * a.OH;
+    if constexpr (S == 2) {
+      for (int o = tid; o < nout; o += 256) {
+        const int pi = fdiv(o, st.ohw_div);
+        const int r = o - pi * ohw;
+        const int oy = fdiv(r, st.ow_div);
+        const int ox = r - oy * a.OW;
+        const float* src = xin + pi * hw;
+        const float* wp = wl + pi * 10;
+        const int y0 = oy * S - a.pt, x0 = ox * S - a.pl;
+        float acc = 0.f;
 #pragma unroll
-    for (int u = 0; u < 4; ++u)
-      if (v0 + 256 * u < nin4) reinterpret_cast<v4f*>(xin)[v0 + 256 * u] = t[u];
-  }
-  for (int e = (nin4 << 2) + threadIdx.x; e < nin; e += 256) xin[e] = xs[e];
-  for (int e = threadIdx.x; e < np * 10; e += 256) {
-    const int pi = e / 10, t = e - pi * 10;
-    const int c = (p0 + pi) % a.C;
-    wl[e] = t < 9 ? a.w[c * 9 + t] : a.bias[c];
-  }
-  __syncthreads();
-  const int nout = np * ohw;
-  for (int o = threadIdx.x; o < nout; o += 256) {
-    const int pi = fdiv(o, ohw_div);
-    const int r = o - pi * ohw;
-    const int oy = fdiv(r, ow_div);
-    const int ox = r - oy * a.OW;
-    const float* src = xin + pi * hw;
-    const float* wp = wl + pi * 10;
-    const int y0 = oy * S - a.pt, x0 = ox * S - a.pl;
-    float acc = 0.f;
+        for (int i = 0; i < 3; ++i) {
 #pragma unroll
-    for (int i = 0; i < 3; ++i) {
-#pragma unroll
-      for (int j = 0; j < 3; ++j) {
-        const int y = y0 + i, x = x0 + j;
-        const bool ok = (unsigned)y < (unsigned)a.H && (unsigned)x < (unsigned)a.W;
-        const float v = ok ? src[ok ? y * a.W + x : 0] : 0.f;
-        acc = acc + v * wp[i * 3 + j];
+          for (int j = 0; j < 3; ++j) {
+            const int y = y0 + i, x = x0 + j;
+            const bool ok = (unsigned)y < (unsigned)a.H && (unsigned)x < (unsigned)a.W;
+            const float v = ok ? src[ok ? y * a.W + x : 0] : 0.f;
+            acc = acc + v * wp[i * 3 + j];
+          }
+        }
+        acc = acc + wp[9];
+        if (a.act == NHIP_ACT_RELU) acc = acc < 0.f ? 0.f : acc;
+        yout[o] = acc;
       }
     }
-    acc = acc + wp[9];
-    if (a.act == NHIP_ACT_RELU) acc = acc < 0.f ? 0.f : acc;
-    yout[o] = acc;
+    constexpr int IC = (kDwRowMax - 1) * S + 3;  // input columns of a row of outputs
+    for (int rr = tid; rr < rows && S == 1; rr += 256) {
+      const int pi = fdiv(rr, st.oh_div), oy = rr - pi * a.OH;
+      const float* src = xin + pi * hw;
+      const float* wp = wl + pi * 10;
+      float win[3][IC];
+#pragma unroll
+      for (int i = 0; i < 3; ++i) {
+        const int y = oy * S - a.pt + i;
+        const bool yok = (unsigned)y < (unsigned)a.H;
+#pragma unroll
+        for (int c = 0; c < IC; ++c) {
+          const int x = c - a.pl;
+          const bool ok = yok && (unsigned)x < (unsigned)a.W && c < (a.OW - 1) * S + 3;
+          win[i][c] = ok ? src[ok ? y * a.W + x : 0] : 0.f;
+        }
+      }
+      float wr[10];
+#pragma unroll
+      for (int t = 0; t < 10; ++t) wr[t] = wp[t];
+      float* dst = yout + rr * a.OW;
+#pragma unroll
+      for (int ox = 0; ox < kDwRowMax; ++ox) {
+        if (ox < a.OW) {
+          float acc = 0.f;
+#pragma unroll
+          for (int i = 0; i < 3; ++i)
+#pragma unroll
+            for (int j = 0; j < 3; ++j) acc = acc + win[i][ox * S + j] * wr[i * 3 + j];
+          acc = acc + wr[9];
+          if (a.act == NHIP_ACT_RELU) acc = acc < 0.f ? 0.f : acc;
+          dst[ox] = acc;
+        }
+      }
+    }
+    __syncthreads();
+    float* ys = a.y + (int64_t)p0 * ohw;
+    const int nout4 = nout >> 2;
+    for (int v = tid; v < nout4; v += 256)
+      reinterpret_cast<v4f*>(ys)[v] = reinterpret_cast<const v4f*>(yout)[v];
+    for (int e = (nout4 << 2) + tid; e < nout; e += 256) ys[e] = yout[e];
   }
-  __syncthreads();
-  float* ys = a.y + (int64_t)p0 * ohw;
-  const int nout4 = nout >> 2;
-  for (int v = threadIdx.x; v < nout4; v += 256)
-    reinterpret_cast<v4f*>(ys)[v] = reinterpret_cast<const v4f*>(yout)[v];
-  for (int e = (nout4 << 2) + threadIdx.x; e < nout; e += 256) ys[e] = yout[e];
 }
 
 // ---------------------------------------------------------------------------
@@ -586,27 +667,34 @@ int launch_dwconv_f32(const nhip_conv_plan* p, const float* in, float* out,
   // assumes the left pad of 1)
   const bool vec = w % 4 == 0 && ow % 4 == 0 && a.pl == 1;
   // Small planes whose rows are not vector-aligned (7x7, 14x14, stride 2 to
-  // 14 or 7): whole planes per workgroup through LDS, when x and y are
-  // 16-byte aligned.  Measured at batch 32: 960@7 8.2 us against 10.4,
-  // 576@14 12.0 against 17.3, 192@28 stride 2 8.0 against 12.8; with
-  // vector rows (192@28 stride 1) the window kernel is faster, 9.8 against
-  // 14.3.  NHIP_DW_PLANES=0 switches it off (tuning and tests).
-  if (k3 && !vec && hw <= kDwPlaneMax && x_bytes < (1ull << 31) &&
-      ((reinterpret_cast<uintptr_t>(in) | reinterpret_cast<uintptr_t>(out)) & 15) == 0 &&
-      setting_int("NHIP_DW_PLANES", 1) != 0) {
-    // about 8 KB of input and at most 48 KB of LDS per workgroup, ppb * hw
-    // and ppb * ohw multiples of 4 (every block 16-byte aligned)
-    const int step = (hw % 4 == 0 && ohw % 4 == 0) ? 1 : (hw % 2 == 0 && ohw % 2 == 0) ? 2 : 4;
-    const int want = std::max(1, std::min(2048 / hw, 12288 / (hw + ohw + 10)));
+  // 14 or 7): the streamed whole-plane kernel, when y is 16-byte aligned.
+  // NHIP_DW_PLANES=0 switches it off (tuning and tests), =2 takes it for
+  // vector-aligned rows too.
+  const int planes_mode = setting_int("NHIP_DW_PLANES", 1);
+  if (k3 && (!vec || planes_mode == 2) && planes_mode != 0 && hw <= kDwPlaneMax && ow <= kDwRowMax &&
+      x_bytes < (1ull << 31) && (reinterpret_cast<uintptr_t>(out) & 15) == 0) {
+    // at most one output row per lane and 16 KB of input per chunk, ppb *
+    // ohw a multiple of 4 (every output block 16-byte aligned); ppb * 10
+    // weights fit the four per lane staged with the copy
+    const int step = ohw % 4 == 0 ? 1 : (ohw % 2 == 0 ? 2 : 4);
+    const int want = std::max(1, a.sh == 1 ? std::min({256 / oh, 4096 / hw, 100}) : std::min(2048 / hw, 100));
     a.ppb = std::max(step, want / step * step);
-    const size_t lds = (size_t)a.ppb * (hw + ohw + 10) * sizeof(float);
-    const dim3 grid((unsigned)ceil_div(a.planes, a.ppb));
+    DwStream st{};
+    st.x_bytes = (uint32_t)x_bytes;
+    st.chunks = (int)ceil_div(a.planes, a.ppb);
+    st.copies = (int)ceil_div((int64_t)a.ppb * hw * 4, 4096);
+    st.slot = st.copies * 1024;  // floats: 4 waves x copies x 1 KB
+    st.oh_div = fast_div(oh);
+    st.ohw_div = fast_div(ohw);
+    st.ow_div = fast_div(ow);
+    const size_t lds = ((size_t)2 * st.slot + (size_t)a.ppb * (ohw + 10)) * sizeof(float);
+    // persistent grid: NHIP_DW_WGS_PER_CU (default 4) workgroups per CU
+    const int per_cu = std::max(1, setting_int("NHIP_DW_WGS_PER_CU", 4));
+    const dim3 grid((unsigned)std::min<int64_t>(st.chunks, (int64_t)per_cu * cu_count()));
     if (a.sh == 1)
-      NHIP_LAUNCH("dw3x3_planes_f32", (dw3x3_planes_kernel<1>), grid, dim3(256), lds, s, a, fast_div(ohw),
-                  fast_div(ow));
+      NHIP_LAUNCH("dw3x3_planes_f32", (dw3x3_stream_kernel<1>), grid, dim3(256), lds, s, a, st);
     else
-      NHIP_LAUNCH("dw3x3_planes_f32", (dw3x3_planes_kernel<2>), grid, dim3(256), lds, s, a, fast_div(ohw),
-                  fast_div(ow));
+      NHIP_LAUNCH("dw3x3_planes_f32", (dw3x3_stream_kernel<2>), grid, dim3(256), lds, s, a, st);
     return check_launch("dw3x3_planes_f32");
   }
   if (k3 && x_bytes < (1ull << 31)) {

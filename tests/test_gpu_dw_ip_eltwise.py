@@ -89,11 +89,13 @@ PLANE_CASES = [
 
 
 @pytest.mark.parametrize("case", PLANE_CASES, ids=lambda c: "x".join(map(str, c[:4])) + f"s{c[4]}")
-@pytest.mark.parametrize("planes", ["1", "0"])
+@pytest.mark.parametrize("planes", ["1", "2", "0"])
 def test_depthwise_small_planes_bit_exact(case, planes, nhip_env):
-    """The whole-plane kernel (NHIP_DW_PLANES=1, default) and the row kernel
-    (=0) against the oracle, bit for bit; a 4-byte-offset input view (not
-    16-byte aligned) takes the row kernel and gives the same bits."""
+    """The streamed whole-plane kernel (NHIP_DW_PLANES=1, default: rows that
+    are not 16-byte vectors; =2: every shape it takes) and the window kernel
+    (=0) against the oracle, bit for bit, also from a 4-byte-offset input
+    view (direct-to-LDS copies from an address that is not 16-byte
+    aligned)."""
     nhip_env.setenv("NHIP_DW_PLANES", planes)
     n, c, h, w, st, pad = case
     x = RNG.uniform(-1, 1, (n, c, h, w)).astype(np.float32)
