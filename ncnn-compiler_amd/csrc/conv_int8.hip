@@ -562,9 +562,9 @@ int launch_conv_int8(const nhip_conv_plan* p, const void* in, int in_is_i8,
       g.fp_bytes = (int)round_up((int64_t)g.FH * g.FW * g.FS, 16);
       g.cpp_div = fast_div((uint32_t)(p->c_pad / 16));
       g.fw_div = fast_div((uint32_t)g.FW);
-      int bm = p->m_pad % 128 == 0 && p->m_pad >= 256 ? 128 : 64;
-      // NHIP_INT8_FP_BM=64/128 overrides (tuning switch, ignored when invalid)
-      if (const int v = setting_int("NHIP_INT8_FP_BM", 0); (v == 64 || v == 128) && p->m_pad % v == 0) bm = v;
+      // 64 output channels per workgroup (a 128-channel block's epilogue
+      // staging alone would take 72 KB and leave one workgroup per CU)
+      const int bm = 64;
       // K stage: the widest of 384 / 192 / 128 bytes that divides the
       // reduction (fewer stages: fewer global-load round trips and barriers
       // per workgroup; config 4: 3 stages of 384 bytes, 16.3 against 17.2 us
@@ -605,9 +605,6 @@ int launch_conv_int8(const nhip_conv_plan* p, const void* in, int in_is_i8,
         NHIP_FP_CASE(64, 128)
         NHIP_FP_CASE(64, 192)
         NHIP_FP_CASE(64, 384)
-        NHIP_FP_CASE(128, 128)
-        NHIP_FP_CASE(128, 192)
-        NHIP_FP_CASE(128, 384)
 #undef NHIP_FP_CASE
       }
     }

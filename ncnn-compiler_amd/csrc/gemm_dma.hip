@@ -413,12 +413,13 @@ static DmaCfg pw_dma_cfg(const nhip_conv_plan* p, int64_t npix) {
   return dma_config(p->g.k, (int)npix, (int)ceil_div(p->g.c, kBK));
 }
 
-// Taken for launches of at most 1.5 workgroups per CU.  Measured on the
+// Taken for launches of at most 2.5 workgroups per CU.  Measured on the
 // MobileNetV2 7x7 layers at batch 32 against the register-prefetch implicit
-// GEMM: 160->960 12.3 us against 16.5 (375 workgroups), 576->160 15.2
-// against 17.6 (150), 960->160 + residual 21.5 against 23.5 (300); at 500
-// workgroups it measured slower (960->320 27.1 against 25.2, 320->1280 32.2
-// against 27.0).  NHIP_GEMM_DMA=2 takes it for every supported shape (tests).
+// GEMM: 160->960 12.3 us against 16.5 (375 workgroups, no split),
+// 576->160 15.2 against 17.6 (300: 4 splits), 960->160 + residual 21.5
+// against 23.5 (600: 8 splits); at 1000 workgroups it measured slower
+// (960->320 27.1 against 25.2, 320->1280 32.2 against 27.0).
+// NHIP_GEMM_DMA=2 takes it for every supported shape (tests).
 bool pw_dma_supported(const nhip_conv_plan* p, int n, int h, int w) {
   const ConvGeom& g = p->g;
   if (g.kh != 1 || g.kw != 1 || g.sh != 1 || g.sw != 1 || g.pt || g.pb || g.pl || g.pr) return false;
@@ -431,7 +432,7 @@ bool pw_dma_supported(const nhip_conv_plan* p, int n, int h, int w) {
   if (mode == 2) return true;
   const DmaCfg c = pw_dma_cfg(p, npix);
   const int64_t wgs = ceil_div(g.k, c.bm) * ceil_div(npix, kBN) * c.splits;
-  return 2 * wgs <= 3LL * cu_count();
+  return 2 * wgs <= 5LL * cu_count();
 }
 
 uint64_t conv_pw_dma_workspace(const nhip_conv_plan* p, int n, int h, int w) {

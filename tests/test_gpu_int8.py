@@ -106,6 +106,8 @@ CASES = [
     (2, 32, 16, 16, 40, (3, 3), (2, 2), (1, 1), (0, 0, 0, 0), 101, 1, False, False),
     (1, 64, 8, 12, 64, (3, 3), (1, 1), (1, 1), (1, 2, 1, 2), 1, 0, True, True),
     (2, 96, 7, 20, 32, (3, 3), (1, 1), (1, 1), (1, 1, 1, 1), 102, 1, False, True),
+    # 260 output channels: five 64-channel blocks of the footprint kernel
+    (1, 32, 9, 14, 260, (3, 3), (1, 1), (1, 1), (1, 1, 1, 1), 101, 1, False, False),
     # 5x5 taps over 64 channels: K stages cross taps, K padding past the 25th
     (1, 64, 9, 11, 24, (5, 5), (1, 1), (1, 1), (2, 2, 2, 2), 101, 1, False, False),
 ]
