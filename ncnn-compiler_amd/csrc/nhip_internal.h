@@ -214,6 +214,11 @@ bool ip_dma_supported(const nhip_ip_plan* p, const float* in, int m);
 uint64_t innerproduct_dma_workspace(const nhip_ip_plan* p, int m);
 int launch_innerproduct_dma(const nhip_ip_plan* p, const float* in, float* out, int m, void* ws, uint64_t ws_bytes,
                             hipStream_t s);
+// conv_smallk.hip: fp32 convolutions with a reduction of at most 32 and at
+// most 32 output channels (network stems), one MFMA block per 32 pixels.
+bool smallk_supported(const nhip_conv_plan* p, int n, int h, int w, int oh, int ow);
+int launch_conv_smallk(const nhip_conv_plan* p, const float* in, const float* residual, float* out, int n, int h,
+                       int w, int oh, int ow, hipStream_t s);
 bool pw_dma_supported(const nhip_conv_plan* p, int n, int h, int w);
 uint64_t conv_pw_dma_workspace(const nhip_conv_plan* p, int n, int h, int w);
 int launch_conv_pw_dma(const nhip_conv_plan* p, const float* in, const float* residual, float* out, int n, int h,
