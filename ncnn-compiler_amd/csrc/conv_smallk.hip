@@ -207,15 +207,22 @@ void launch_steps(const SmallkArgs& a, int act, dim3 grid, hipStream_t s) {
 // Shapes taken: a plain (groups 1) fp32 convolution on the implicit-GEMM
 // plan whose reduction is at most 32 long with at most 32 output channels,
 // except 1x1 stride-1 unpadded ones (the pointwise kernels' shapes), and
-// 32-bit buffer offsets.  NHIP_CONV_SMALLK=0 turns it off.
+// 32-bit buffer offsets; by default only from four 32-pixel blocks per CU
+// (measured on the 224x224 stem: 26.4 against 35.7 us at batch 32, 11.1
+// against 13.1 at batch 8, equal at batch 2, 9.7 against 8.6 us for one
+// image, where the implicit GEMM's smaller tiles spread better).
+// NHIP_CONV_SMALLK=0 turns it off, =2 takes it for every shape it supports
+// (tests).
 bool smallk_supported(const nhip_conv_plan* p, int n, int h, int w, int oh, int ow) {
   const ConvGeom& g = p->g;
   if (p->kind != PlanKind::ConvF32 || p->algorithm != NHIP_CONV_ALGO_IMPLICIT_GEMM) return false;
-  if (setting_int("NHIP_CONV_SMALLK", 1) == 0) return false;
+  const int mode = setting_int("NHIP_CONV_SMALLK", 1);
+  if (mode == 0) return false;
   if (p->kred > 32 || p->kred_pad > 32 || g.k > 32) return false;
   if (g.kh == 1 && g.kw == 1 && g.sh == 1 && g.sw == 1 && !g.pt && !g.pb && !g.pl && !g.pr) return false;
   const int64_t xb = (int64_t)n * g.c * h * w * 4, ob = (int64_t)n * g.k * oh * ow * 4;
-  return xb < (int64_t(1) << 31) && ob < (int64_t(1) << 31) && oh > 0 && ow > 0;
+  if (!(xb < (int64_t(1) << 31) && ob < (int64_t(1) << 31) && oh > 0 && ow > 0)) return false;
+  return mode == 2 || ceil_div((int64_t)n * oh * ow, 32) >= 4LL * cu_count();
 }
 
 int launch_conv_smallk(const nhip_conv_plan* p, const float* in, const float* residual, float* out, int n, int h,
@@ -252,10 +259,13 @@ int launch_conv_smallk(const nhip_conv_plan* p, const float* in, const float* re
   // about eight blocks per wave (the gathers of one in flight behind the
   // other; measured on the 224x224 stem at batch 32: 25.0 us against
   // 28.2-29.8 with one to six blocks per wave, each wave's start-up loads
-  // then being spread over fewer blocks), at most 16 waves per CU;
-  // NHIP_SMALLK_BPW sets the blocks per wave (tuning)
+  // then being spread over fewer blocks), but never fewer than four waves
+  // per CU while there are blocks for them (one image of the stem is 392
+  // blocks), at most 16 waves per CU; NHIP_SMALLK_BPW sets the blocks per
+  // wave (tuning)
   const int bpw = std::max(1, setting_int("NHIP_SMALLK_BPW", 8));
-  const int64_t waves = std::min<int64_t>(ceil_div(a.nblk, bpw), 16LL * cu_count());
+  const int64_t waves = std::min<int64_t>(
+      std::min<int64_t>(a.nblk, std::max<int64_t>(ceil_div(a.nblk, bpw), 4LL * cu_count())), 16LL * cu_count());
   const dim3 grid((unsigned)ceil_div(waves, kThreads / 64));
   if (p->kred_pad <= 16) launch_steps<8>(a, p->g.act, grid, s);
   else launch_steps<16>(a, p->g.act, grid, s);
