@@ -82,29 +82,50 @@ __device__ __forceinline__ v4f load4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
 // are consecutive in one image); out of range past the last pixel.  DW: xo
 // are the three input rows of the depthwise window (byte offset of (n, 0,
 // row, DW*ox), out of range for rows outside the image) and lok / rok say
-// whether the window's left / right halo column lies inside the image.
+// whether the window's left / right halo column lies inside the image; eo
+// is the lane's share of the halo loads (see XChunk), out of range if none.
 template <bool SCALAR, int DW>
 struct Geo {
   uint32_t xo[DW ? 3 : (SCALAR ? 4 : 1)], oo[SCALAR ? 4 : 1];
+  uint32_t eo;
   bool lok, rok;
 };
 
 // One chunk of input in registers: four 16-byte pixel vectors (one per
-// k-step of 4 channels), or the lane's depthwise window rows for one k-step.
+// k-step of 4 channels), or the lane's depthwise window rows for one k-step:
+// the 16-byte centre vectors (columns DW*ox .. DW*ox + 3, and + 4 .. + 7 at
+// stride 2) of rows 0..2, and one halo value e.  A row of 16 lanes (one
+// channel) covers 64 consecutive output pixels, so a lane's halo columns are
+// the end columns of its neighbours' centre vectors, moved across by DPP;
+// only the two ends of the lane row load them: lanes 0, 1, 2 the left halo of
+// rows 0, 1, 2 of lane 0's window, and at stride 1 lanes 13, 14, 15 the right
+// halo of rows 0, 1, 2 of lane 15's.  Four loads per k-step at stride 1
+// (nine with a load per halo column), seven at stride 2.
 template <int DW>
 struct XChunk {
   v4f x[4];
 };
 template <>
 struct XChunk<1> {
-  float l[3], r[3];
   v4f m[3];
+  float e;
 };
 template <>
 struct XChunk<2> {
-  float l[3];
   v4f m[3], m2[3];
+  float e;
 };
+
+// v of lane l - N (SHR) or l + N (SHL) within the lane's row of 16 (DPP
+// row_shr / row_shl; 0 past the row's end).
+template <int N>
+__device__ __forceinline__ float row_shr(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x110 + N, 0xf, 0xf, true));
+}
+template <int N>
+__device__ __forceinline__ float row_shl(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x100 + N, 0xf, 0xf, true));
+}
 
 // LDS: W[k0 + 16t + j][c] at (c*16 + j)*KT + t + c/4 (c < c4, j < 16,
 // t < KT): the A fragments of one k-step (KT floats per lane, lane
@@ -236,6 +257,27 @@ __global__ __launch_bounds__(kThreads, 2) void pw_conv_kernel(PwArgs a) {
       }
       g.oo[v] = ok ? (uint32_t)(n * a.K * a.P + p) * 4u : kBufOOB;
     }
+    g.eo = kBufOOB;
+    if constexpr (DW != 0) {
+      // the lane's halo load: the left halo of row jl of lane 0's window
+      // (jl <= 2) or, stride 1, the right halo of row jl - 13 of lane 15's
+      // (jl >= 13)
+      const int side = jl <= 2 ? 0 : (DW == 1 && jl >= 13) ? 1 : -1;
+      if (side >= 0) {
+        const int u = p0 + (WC == 1 ? wave * 64 : 0) + 60 * side;  // lane 0's or lane 15's first pixel
+        int dn = (int)((float)u * inv_p);
+        int p = u - dn * a.P;
+        if (p < 0) { --dn; p += a.P; }
+        if (p >= a.P) { ++dn; p -= a.P; }
+        const int n = n0 + dn;
+        const bool ok = q0 + (u - p0) < a.np;
+        const int oy = p / a.OW, ox = p - oy * a.OW;
+        const int iy = DW * oy - 1 + (side ? jl - 13 : jl);
+        const int ix = side ? ox + 4 : DW * ox - 1;
+        if (ok && (unsigned)iy < (unsigned)a.H && (unsigned)ix < (unsigned)a.W)
+          g.eo = (uint32_t)((n * a.C * a.H + iy) * a.W + ix) * 4u;
+      }
+    }
     return g;
   };
   auto load_px = [&](__amdgpu_buffer_rsrc_t r, const uint32_t* base, uint32_t add, bool on) {
@@ -265,13 +307,10 @@ __global__ __launch_bounds__(kThreads, 2) void pw_conv_kernel(PwArgs a) {
       for (int i = 0; i < 3; ++i) {
         const bool row = on && g.xo[i] != kBufOOB;
         const uint32_t b = g.xo[i] + add;
-        xb.l[i] = buf_load_f32(xr, (row && g.lok) ? b - 4u : kBufOOB);
         xb.m[i] = load4(xr, row ? b : kBufOOB);
-        if constexpr (DW == 1)
-          xb.r[i] = buf_load_f32(xr, (row && g.rok) ? b + 16u : kBufOOB);
-        else
-          xb.m2[i] = load4(xr, row ? b + 16u : kBufOOB);
+        if constexpr (DW == 2) xb.m2[i] = load4(xr, row ? b + 16u : kBufOOB);
       }
+      xb.e = buf_load_f32(xr, (on && g.eo != kBufOOB) ? g.eo + add : kBufOOB);
     }
   };
 
@@ -281,8 +320,9 @@ __global__ __launch_bounds__(kThreads, 2) void pw_conv_kernel(PwArgs a) {
 #pragma unroll
     for (int v = 0; v < 4; ++v) acc[t][v] = v4f{0.f, 0.f, 0.f, 0.f};
 
-  // depthwise outputs of the lane's channel at its four pixels
-  auto depthwise = [&](const XChunk<DW>& xb, int c) {
+  // depthwise outputs of the lane's channel at its four pixels (lok / rok:
+  // the halo columns of the computed tile's window lie inside the image)
+  auto depthwise = [&](const XChunk<DW>& xb, int c, bool lok, bool rok) {
     v4f d = {0.f, 0.f, 0.f, 0.f};
     if constexpr (DW != 0) {
 #pragma clang fp contract(off)
@@ -290,6 +330,24 @@ __global__ __launch_bounds__(kThreads, 2) void pw_conv_kernel(PwArgs a) {
       float w[10];
 #pragma unroll
       for (int t = 0; t < 10; ++t) w[t] = wq[t];
+      // halo columns: the neighbour lane's end column, or at the ends of the
+      // lane row the halo loads of lanes 0..2 / 13..15 (all lanes run the
+      // moves: the loop is not divergent here)
+      float hl[3], hr[3];
+#pragma unroll
+      for (int i = 0; i < 3; ++i) {
+        float last;  // the lane's last window column of row i
+        if constexpr (DW == 1) last = xb.m[i][3];
+        else last = xb.m2[i][3];
+        const float from_left = row_shr<1>(last);
+        const float edge_l = i == 0 ? xb.e : i == 1 ? row_shl<1>(xb.e) : row_shl<2>(xb.e);
+        hl[i] = lok ? (jl == 0 ? edge_l : from_left) : 0.f;
+        if constexpr (DW == 1) {
+          const float from_right = row_shl<1>(xb.m[i][0]);
+          const float edge_r = i == 2 ? xb.e : i == 1 ? row_shr<1>(xb.e) : row_shr<2>(xb.e);
+          hr[i] = rok ? (jl == 15 ? edge_r : from_right) : 0.f;
+        }
+      }
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
         float acc = 0.f;
@@ -297,10 +355,10 @@ __global__ __launch_bounds__(kThreads, 2) void pw_conv_kernel(PwArgs a) {
         for (int i = 0; i < 3; ++i) {
           // window row i: columns DW*ox - 1 + (0 .. 4*DW + 1)
           float row[4 * DW + 2];
-          row[0] = xb.l[i];
+          row[0] = hl[i];
 #pragma unroll
           for (int e = 0; e < 4; ++e) row[1 + e] = xb.m[i][e];
-          if constexpr (DW == 1) row[5] = xb.r[i];
+          if constexpr (DW == 1) row[5] = hr[i];
           else
 #pragma unroll
             for (int e = 0; e < 4; ++e) row[5 + e] = xb.m2[i][e];
@@ -315,14 +373,14 @@ __global__ __launch_bounds__(kThreads, 2) void pw_conv_kernel(PwArgs a) {
     return d;
   };
 
-  auto compute = [&](const XChunk<DW>& xb, int j) {
+  auto compute = [&](const XChunk<DW>& xb, int j, const Geo<SCALAR, DW>& g) {
 #pragma unroll
     for (int s = 0; s < SPC; ++s) {
       const int cs = chunk_c0(j) + 4 * s;  // first channel of the k-step
       if (cs >= a.c4) break;
       v4f bx;
       if constexpr (DW == 0) bx = xb.x[s];
-      else bx = depthwise(xb, cs + cl);
+      else bx = depthwise(xb, cs + cl, g.lok, g.rok);
       float av[KT];
       const float* wp = ws + ((cs >> 2) * 64 + lane) * KT + (cs >> 2);
 #pragma unroll
@@ -434,7 +492,7 @@ __global__ __launch_bounds__(kThreads, 2) void pw_conv_kernel(PwArgs a) {
       if constexpr (RES)
         if (!res_early && last) issue_res(gc);
       issue_next(xb[(b + NB - 1) % NB]);
-      compute(xb[b], j);
+      compute(xb[b], j, gc);
       if (last) {
         epilogue(gc);
         ++i;
@@ -651,17 +709,14 @@ bool dwpw_supported(const nhip_conv_plan* dw, const nhip_conv_plan* pw, int n, i
   }
   int oh = 0, ow = 0;
   if (!dw_shape_ok(dw, h, w, &oh, &ow)) return false;
-  // Measured on the MobileNetV2 pairs (batch 32): a lane forms one row of
-  // four depthwise outputs per channel from 9 loads, twice the standalone
-  // depthwise kernel's loads per output, and every output-channel slice
-  // recomputes the depthwise values.  That pays when the 1x1 conv's channels
-  // fit one slice (K <= 32) and the depthwise output is a quarter of its
-  // input (stride 2: 96@112 -> 24 in 55.2 us against ~57 us for the two
-  // layers, 144@56 -> 32 in 24.4 against ~25) or the planes are wide
-  // (stride 1, 56 columns and up: 32@112 -> 16 in 35.8 against 37.7 us,
-  // 144@56 -> 24 with residual 42.9 against 44.9); at 28 columns stride 1
-  // measured slower (192@28 -> 32: 25.2 against 22.4).
-  if (!every && (pw->g.k > 32 || (dw->g.sh != 2 && !(dw->g.sh == 1 && ow >= 56)))) return false;
+  // Measured on the MobileNetV2 pairs (batch 32): every output-channel
+  // slice recomputes the depthwise values, which pays when the 1x1 conv's
+  // channels fit one slice (K <= 32): stride 2 (96@112 -> 24 in 32.4 us
+  // against ~57 us for the two layers, 144@56 -> 32 in 21.3 against ~25)
+  // and stride 1 from 28 output columns (32@112 -> 16 in 26.1 against 35.4
+  // us, 144@56 -> 24 with residual 36.9 against 40.6, 192@28 -> 32 with
+  // residual 20.5 against 23.4).
+  if (!every && (pw->g.k > 32 || (dw->g.sh != 2 && !(dw->g.sh == 1 && ow >= 28)))) return false;
   const ConvGeom& g = pw->g;
   if (pw->kind != PlanKind::ConvF32 || g.c != dw->g.c || g.kh != 1 || g.kw != 1 || g.sh != 1 || g.sw != 1 || g.pt ||
       g.pb || g.pl || g.pr || pw->algorithm != NHIP_CONV_ALGO_IMPLICIT_GEMM)
