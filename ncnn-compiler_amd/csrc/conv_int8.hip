@@ -32,7 +32,6 @@ namespace nhip {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kRow = 64 + 16;  // quantize tile row stride (bytes)
 
 // Branch-free: both roundings are formed and selected, and NaN (which
 // fminf / fmaxf would turn into +-127) selects 0 at the end.
@@ -48,46 +47,38 @@ __device__ __forceinline__ int8_t quantize_i8(float x, float scale) {
 
 // x [N][C][HW] (fp32 or int8) -> y [N][HW][c_pad] int8, zero channel padding.
 // Workgroup = 64 pixels x one 64-channel slab of one image (grid x: pixel
-// blocks, y: slabs, z: images); each thread issues its 16 loads before any
-// LDS write, then the slab leaves as 16-byte rows.
+// blocks, y: slabs, z: images); thread (pixel, q) quantizes channels 16q ..
+// 16q + 15 of the slab at its pixel (each load instruction: 64 consecutive
+// pixels of one channel) and writes them as one 16-byte NHWC vector, with
+// no LDS transpose; the four 16-byte pieces of a pixel's 64 bytes come from
+// the four waves of the workgroup.
 __global__ __launch_bounds__(kThreads) void quantize_nchw_to_nhwc(
     const void* __restrict__ x, int in_is_i8, int8_t* __restrict__ y, int C,
     int HW, int c_pad, float scale) {
-  __shared__ __attribute__((aligned(16))) int8_t tile[64 * kRow];
   const int img = blockIdx.z;
-  const int p0 = blockIdx.x * 64;
-  const int c0 = blockIdx.y * 64;
-  const int tid = threadIdx.x;
-  const int px = tid & 63, cc = tid >> 6;
-  const int p = p0 + px;
+  const int p = blockIdx.x * 64 + (threadIdx.x & 63);
+  const int cw = blockIdx.y * 64 + (threadIdx.x >> 6) * 16;
+  if (p >= HW || cw >= c_pad) return;
   const float* xf = static_cast<const float*>(x) + (int64_t)img * C * HW;
   const int8_t* xi = static_cast<const int8_t*>(x) + (int64_t)img * C * HW;
   int8_t v[16];
   if (in_is_i8) {
 #pragma unroll
-    for (int u = 0; u < 16; ++u) {
-      const int c = c0 + cc + 4 * u;
-      v[u] = (c < C && p < HW) ? xi[(int64_t)c * HW + p] : (int8_t)0;
-    }
+    for (int u = 0; u < 16; ++u) v[u] = cw + u < C ? xi[(int64_t)(cw + u) * HW + p] : (int8_t)0;
   } else {
     float f[16];
 #pragma unroll
-    for (int u = 0; u < 16; ++u) {
-      const int c = c0 + cc + 4 * u;
-      f[u] = (c < C && p < HW) ? xf[(int64_t)c * HW + p] : 0.0f;
-    }
+    for (int u = 0; u < 16; ++u) f[u] = cw + u < C ? xf[(int64_t)(cw + u) * HW + p] : 0.0f;
 #pragma unroll
     for (int u = 0; u < 16; ++u) v[u] = quantize_i8(f[u], scale);
   }
+  int4 out;
+  int* o = reinterpret_cast<int*>(&out);
 #pragma unroll
-  for (int u = 0; u < 16; ++u) tile[px * kRow + cc + 4 * u] = v[u];
-  __syncthreads();
-  const int wp = tid >> 2, chunk = tid & 3;
-  const int pw = p0 + wp;
-  const int cw = c0 + chunk * 16;
-  if (pw < HW && cw < c_pad)
-    *reinterpret_cast<int4*>(y + ((int64_t)img * HW + pw) * c_pad + cw) =
-        *reinterpret_cast<const int4*>(&tile[wp * kRow + chunk * 16]);
+  for (int q = 0; q < 4; ++q)
+    o[q] = (int)((uint32_t)(uint8_t)v[4 * q] | ((uint32_t)(uint8_t)v[4 * q + 1] << 8) |
+                 ((uint32_t)(uint8_t)v[4 * q + 2] << 16) | ((uint32_t)(uint8_t)v[4 * q + 3] << 24));
+  *reinterpret_cast<int4*>(y + ((int64_t)img * HW + p) * c_pad + cw) = out;
 }
 
 struct Int8Args {
