@@ -33,16 +33,18 @@ namespace {
 
 constexpr int kThreads = 256;
 
-// Branch-free: both roundings are formed and selected, and NaN (which
-// fminf / fmaxf would turn into +-127) selects 0 at the end.
-__device__ __forceinline__ int8_t quantize_i8(float x, float scale) {
+// Round half away from zero of s = x * scale, saturated to [lo, 127] (lo =
+// -127, or 0 for a ReLU that follows), NaN -> 0.  Branch-free:
+// trunc(s + copysign(0.5, s)) forms the same fp32 sum as floor(s + 0.5) for
+// s >= 0 and ceil(s - 0.5) for s < 0, and truncation equals that floor /
+// ceil since the sum has the sign of s (s = -0.0 gives 0 both ways); one
+// median-of-three saturates; NaN selects 0 before the conversion.
+// max(clamp(q, -127, 127), 0) = clamp(q, 0, 127), so the ReLU is the bound.
+__device__ __forceinline__ int8_t quantize_i8(float x, float scale, float lo = -127.0f) {
 #pragma clang fp contract(off)
   const float s = x * scale;
-  float r = (s >= 0.0f) ? floorf(s + 0.5f) : ceilf(s - 0.5f);
-  r = fminf(r, 127.0f);
-  r = fmaxf(r, -127.0f);
-  const int q = (int)r;
-  return (int8_t)(s != s ? 0 : q);
+  const float r = __builtin_amdgcn_fmed3f(truncf(s + copysignf(0.5f, s)), lo, 127.0f);
+  return (int8_t)(int)(s != s ? 0.0f : r);
 }
 
 // x [N][C][HW] (fp32 or int8) -> y [N][HW][c_pad] int8, zero channel padding.
@@ -239,6 +241,7 @@ __global__ __launch_bounds__(kThreads) void conv_int8_kernel(Int8Args g) {
   // where the run crosses an image or the tile edge or is misaligned.
   __syncthreads();
   const bool q8 = g.term > 100, relu = g.act == NHIP_ACT_RELU;
+  const float qlo = relu ? 0.0f : -127.0f;  // requantized ReLU: the saturation's lower bound
   float* tf = reinterpret_cast<float*>(smem);
   int8_t* tq = smem;
   // One wave-uniform branch on the output kind; the per-value arithmetic
@@ -261,8 +264,7 @@ __global__ __launch_bounds__(kThreads) void conv_int8_kernel(Int8Args g) {
   if (q8) {
 #pragma unroll
     NHIP_I8_EPI({
-      const int8_t q = quantize_i8(f, g.os);
-      tq[il * ES + jl] = (relu && q < 0) ? (int8_t)0 : q;
+      tq[il * ES + jl] = quantize_i8(f, g.os, qlo);
     })
   } else {
 #pragma unroll
@@ -448,6 +450,7 @@ __global__ __launch_bounds__(kThreads) void conv_int8_fp_kernel(Int8Args g) {
   // ---- epilogue (as conv_int8_kernel), staged in LDS over the footprint
   __syncthreads();
   const bool q8 = g.term > 100, relu = g.act == NHIP_ACT_RELU;
+  const float qlo = relu ? 0.0f : -127.0f;  // requantized ReLU: the saturation's lower bound
   float* tf = reinterpret_cast<float*>(dsm);
   int8_t* tq = dsm;
   auto dequant = [&](int a, int b, int r, int il) {
@@ -459,8 +462,7 @@ __global__ __launch_bounds__(kThreads) void conv_int8_fp_kernel(Int8Args g) {
   if (q8) {
 #pragma unroll
     NHIP_I8_EPI({
-      const int8_t q = quantize_i8(f, g.os);
-      tq[il * ES + jl] = (relu && q < 0) ? (int8_t)0 : q;
+      tq[il * ES + jl] = quantize_i8(f, g.os, qlo);
     })
   } else {
 #pragma unroll
