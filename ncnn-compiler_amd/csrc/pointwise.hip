@@ -715,8 +715,14 @@ bool dwpw_supported(const nhip_conv_plan* dw, const nhip_conv_plan* pw, int n, i
   // against ~57 us for the two layers, 144@56 -> 32 in 21.3 against ~25)
   // and stride 1 from 28 output columns (32@112 -> 16 in 26.1 against 35.4
   // us, 144@56 -> 24 with residual 36.9 against 40.6, 192@28 -> 32 with
-  // residual 20.5 against 23.4).
-  if (!every && (pw->g.k > 32 || (dw->g.sh != 2 && !(dw->g.sh == 1 && ow >= 28)))) return false;
+  // residual 20.5 against 23.4).  With few pixels the fused kernel's
+  // workgroups are too few to cover its per-chunk latency: the whole graph
+  // ran 0.336 ms unfused against 0.381 fused at batch 1, 0.413 against
+  // 0.428 at batch 8, even at 16 and 0.79 against 0.81 at 32, so pairs are
+  // fused from 24576 output pixels (a batch-32 28x28 plane set).
+  if (!every && (pw->g.k > 32 || (dw->g.sh != 2 && !(dw->g.sh == 1 && ow >= 28)) ||
+                 (int64_t)n * oh * ow < 24576))
+    return false;
   const ConvGeom& g = pw->g;
   if (pw->kind != PlanKind::ConvF32 || g.c != dw->g.c || g.kh != 1 || g.kw != 1 || g.sh != 1 || g.sw != 1 || g.pt ||
       g.pb || g.pl || g.pr || pw->algorithm != NHIP_CONV_ALGO_IMPLICIT_GEMM)
