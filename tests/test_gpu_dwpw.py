@@ -142,10 +142,12 @@ def test_dw_pw_unsupported_shapes():
 def test_graph_executor_fuses_depthwise_into_project(nhip_env):
     """A graph with two dw -> 1x1 pairs (the first feeding a residual add)
     runs each pair as one launch, bit-identical to NHIP_DWPW=0; by default
-    only the stride-2 pair with 24 output channels is fused."""
+    only the stride-2 pair with 24 output channels is fused, and only while
+    its launch has at least 24576 output pixels (6 images of 64x64 do, one
+    image does not)."""
     m = ncnn_format.Model()
     c, k = 48, 48
-    m.input("data", c, 16, 16)
+    m.input("data", c, 128, 128)
     wd = workloads.he_normal(RNG, (c, 1, 3, 3), 9)
     m.conv("dw1", "data", "d1", wd, RNG.normal(0, .05, c).astype(np.float32), act=1, depthwise=True)
     wp = workloads.he_normal(RNG, (k, c, 1, 1), c)
@@ -156,7 +158,7 @@ def test_graph_executor_fuses_depthwise_into_project(nhip_env):
     wp2 = workloads.he_normal(RNG, (24, k, 1, 1), k)
     m.conv("pw2", "d2", "out", wp2, RNG.normal(0, .05, 24).astype(np.float32), pad=0)
     g = nhip.Graph(m.param_text(), bytes(m.payload))
-    x = dev(RNG.uniform(-1, 1, (3, c, 16, 16)).astype(np.float32))
+    x = dev(RNG.uniform(-1, 1, (6, c, 128, 128)).astype(np.float32))
     nhip.timer_start("dwpw")
     fused = host(g.run(x)[0])
     assert nhip.timer_stop()[0] == 2
@@ -170,3 +172,7 @@ def test_graph_executor_fuses_depthwise_into_project(nhip_env):
     default = host(g.run(x)[0])
     assert nhip.timer_stop()[0] == 1
     np.testing.assert_array_equal(default, separate)
+    nhip.timer_start("dwpw")
+    one = host(g.run(x[:1].contiguous())[0])
+    assert nhip.timer_stop()[0] == 0
+    np.testing.assert_array_equal(one, separate[:1])
