@@ -341,7 +341,7 @@ def config4(nhip, workloads, torch, steps, warmup, share, cpu, target_s):
     qper, qsec = kernel_time(nhip, torch, fn, n, "quantize")
     res = {"workload": "int8 conv 32x128x28x28 3x3 requant(term 101)+relu, fp32 input",
            "ms_per_step": dt * 1e3, "tops": ops / dt / 1e12, "images_per_sec": BATCH / dt,
-           "roofline": roofline("mfma_int8", "conv_int8 (int8 MFMA GEMM, exact requantize epilogue)", ops / per,
+           "roofline": roofline("mfma_int8", "conv_int8_rw (int8 MFMA GEMM, weights in registers, exact requantize epilogue)", ops / per,
                                 sec, per)}
     if qper:
         # quantize pass: reads the fp32 input once, writes the int8 NHWC image

@@ -33,20 +33,6 @@ namespace {
 
 constexpr int kThreads = 256;
 
-// Round half away from zero of s = x * scale, saturated to [lo, 127] (lo =
-// -127, or 0 for a ReLU that follows), NaN -> 0.  Branch-free:
-// trunc(s + copysign(0.5, s)) forms the same fp32 sum as floor(s + 0.5) for
-// s >= 0 and ceil(s - 0.5) for s < 0, and truncation equals that floor /
-// ceil since the sum has the sign of s (s = -0.0 gives 0 both ways); one
-// median-of-three saturates; NaN selects 0 before the conversion.
-// max(clamp(q, -127, 127), 0) = clamp(q, 0, 127), so the ReLU is the bound.
-__device__ __forceinline__ int8_t quantize_i8(float x, float scale, float lo = -127.0f) {
-#pragma clang fp contract(off)
-  const float s = x * scale;
-  const float r = __builtin_amdgcn_fmed3f(truncf(s + copysignf(0.5f, s)), lo, 127.0f);
-  return (int8_t)(int)(s != s ? 0.0f : r);
-}
-
 // x [N][C][HW] (fp32 or int8) -> y [N][HW][c_pad] int8, zero channel padding.
 // Workgroup = 64 pixels x one 64-channel slab of one image (grid x: pixel
 // blocks, y: slabs, z: images); thread (pixel, q) quantizes channels 16q ..
@@ -63,28 +49,26 @@ __global__ __launch_bounds__(kThreads) void quantize_nchw_to_nhwc(
   if (p >= HW || cw >= c_pad) return;
   const float* xf = static_cast<const float*>(x) + (int64_t)img * C * HW;
   const int8_t* xi = static_cast<const int8_t*>(x) + (int64_t)img * C * HW;
-  int8_t v[16];
+  int v[16];
   if (in_is_i8) {
 #pragma unroll
-    for (int u = 0; u < 16; ++u) v[u] = cw + u < C ? xi[(int64_t)(cw + u) * HW + p] : (int8_t)0;
+    for (int u = 0; u < 16; ++u) v[u] = cw + u < C ? xi[(int64_t)(cw + u) * HW + p] : 0;
   } else {
     float f[16];
 #pragma unroll
     for (int u = 0; u < 16; ++u) f[u] = cw + u < C ? xf[(int64_t)(cw + u) * HW + p] : 0.0f;
 #pragma unroll
-    for (int u = 0; u < 16; ++u) v[u] = quantize_i8(f[u], scale);
+    for (int u = 0; u < 16; ++u) v[u] = quantize_q(f[u], scale);
   }
   int4 out;
   int* o = reinterpret_cast<int*>(&out);
 #pragma unroll
-  for (int q = 0; q < 4; ++q)
-    o[q] = (int)((uint32_t)(uint8_t)v[4 * q] | ((uint32_t)(uint8_t)v[4 * q + 1] << 8) |
-                 ((uint32_t)(uint8_t)v[4 * q + 2] << 16) | ((uint32_t)(uint8_t)v[4 * q + 3] << 24));
+  for (int q = 0; q < 4; ++q) o[q] = (int)pack_i8x4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
   *reinterpret_cast<int4*>(y + ((int64_t)img * HW + p) * c_pad + cw) = out;
 }
 
 struct Int8Args {
-  const int8_t* w;     // [m_pad][kred_pad]
+  const int8_t* w;     // [m_pad][kred_pad]; register-weight kernel: fragment order (weight_i8_frag)
   int kred_pad;
   int m;               // num_output
   const int8_t* x;     // NHWC [N][H][W][c_pad]
@@ -103,6 +87,10 @@ struct Int8Args {
   int fp_bytes;        // LDS bytes of the footprint (multiple of 16)
   int rb_off;             // LDS byte offset of the footprint kernel's reciprocals and biases
   FastDiv cpp_div, fw_div;  // footprint copy: 16-byte channel chunks per pixel, window width
+  // register-weight kernel only
+  uint32_t out_bytes;     // size of out (< 2^31)
+  int kred, KW, dh, dw;   // unpadded reduction bytes, kernel width, dilations
+  int vec;                // output stores: 0 single elements, 1 four pixels, 2 sixteen int8 pixels
 };
 
 // D[i = out channel][j = pixel] over the (kh, kw, c) reduction.
@@ -241,7 +229,7 @@ __global__ __launch_bounds__(kThreads) void conv_int8_kernel(Int8Args g) {
   // where the run crosses an image or the tile edge or is misaligned.
   __syncthreads();
   const bool q8 = g.term > 100, relu = g.act == NHIP_ACT_RELU;
-  const float qlo = relu ? 0.0f : -127.0f;  // requantized ReLU: the saturation's lower bound
+  const int qlo = relu ? 0 : -127;  // requantized ReLU: the saturation's lower bound
   float* tf = reinterpret_cast<float*>(smem);
   int8_t* tq = smem;
   // One wave-uniform branch on the output kind; the per-value arithmetic
@@ -450,7 +438,7 @@ __global__ __launch_bounds__(kThreads) void conv_int8_fp_kernel(Int8Args g) {
   // ---- epilogue (as conv_int8_kernel), staged in LDS over the footprint
   __syncthreads();
   const bool q8 = g.term > 100, relu = g.act == NHIP_ACT_RELU;
-  const float qlo = relu ? 0.0f : -127.0f;  // requantized ReLU: the saturation's lower bound
+  const int qlo = relu ? 0 : -127;  // requantized ReLU: the saturation's lower bound
   float* tf = reinterpret_cast<float*>(dsm);
   int8_t* tq = dsm;
   auto dequant = [&](int a, int b, int r, int il) {
@@ -492,6 +480,172 @@ __global__ __launch_bounds__(kThreads) void conv_int8_fp_kernel(Int8Args g) {
           *reinterpret_cast<v4f*>(dst + o + e) = *reinterpret_cast<const v4f*>(&tf[il * ES + jl + e]);
       } else {
         for (int e = 0; e < 16 && jl + e < npx; ++e) dst[o + e] = tf[il * ES + jl + e];
+      }
+    }
+  }
+}
+
+// Register-weight variant.  Each wave keeps its 32 output channels' whole
+// reduction (KS 32-byte k steps, 16 bytes per lane and step) in registers,
+// loaded once at the start in k order from the fragment-order copy of the
+// weights (each step one contiguous 1 KB load per wave, where the row-major
+// weights would touch 32 cache lines), so no weight passes through LDS and
+// the K loop has no barrier: the MFMAs of step s wait only for step s's
+// weights.  The workgroup (4 waves, 128 channels) shares one footprint
+// window of R whole output rows (at most 32*TN pixels) in LDS, as in
+// conv_int8_fp_kernel.  The MFMA operands are swapped against the other
+// kernels (A = pixels, B = weights), so the 32x32 result block is
+// D[pixel][channel]: lane (c, h) holds channel c and, in registers 4g..4g+3,
+// the four consecutive pixels 8g+4h .. 8g+4h+3.  The epilogue stores from
+// registers with no LDS staging: two lane-half swaps give each lane 16
+// consecutive int8 results of its channel (one 16-byte store), or four fp32
+// results go out as one 16-byte vector.  Same arithmetic as the other
+// kernels; the integer sums are exact in any order.
+template <int KS, int TN>
+__global__ __launch_bounds__(kThreads) void conv_int8_rw_kernel(Int8Args g) {
+  extern __shared__ __attribute__((aligned(16))) int8_t dsm[];
+  int8_t* foot = dsm;
+  int* koff_tab = reinterpret_cast<int*>(dsm + g.fp_bytes);  // [KS][2] LDS byte offsets of each k chunk
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int li = lane & 31, lh = lane >> 5;
+  const int rgs = (g.OH + g.R - 1) / g.R;
+  const int img = blockIdx.x / rgs, oy0 = (blockIdx.x % rgs) * g.R;
+  const int ch0 = blockIdx.y * 128 + wave * 32;
+  const int npx = min(g.R, g.OH - oy0) * g.OW;
+
+  // ---- footprint loads first (at most 8 per thread, checked on the host),
+  // then the weights in k order, then the epilogue scalars; nothing waits yet
+  const __amdgpu_buffer_rsrc_t rs = make_rsrc(g.x, g.x_bytes);
+  const int cpp = g.c_pad / 16;
+  const int total = g.FH * g.FW * cpp;
+  const int iy_base = oy0 * g.sh - g.pt;
+  v4i fv[8];
+  int fdst[8];
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    const int e = q * kThreads + tid;
+    const int pix = fdiv(e, g.cpp_div), ch = e - pix * cpp;
+    const int fy = fdiv(pix, g.fw_div), fx = pix - fy * g.FW;
+    const int iy = iy_base + fy, ix = fx - g.pl;
+    const bool in = e < total && (unsigned)iy < (unsigned)g.H && (unsigned)ix < (unsigned)g.W;
+    fv[q] = __builtin_bit_cast(
+        v4i, buf_load_b128(rs, in ? (uint32_t)(((img * g.H + iy) * g.W + ix) * g.c_pad + ch * 16) : kBufOOB));
+    // 24-bit products (window < 2^24 bytes) keep this 32-bit: a 64-bit
+    // multiply-add here pairs a register with a weight load's destination
+    // and forces an early wait for it
+    fdst[q] = e < total ? (int)__umul24(pix, g.FS) + ch * 16 : -1;
+  }
+  v4i wr[KS];
+  {
+    // fragment order: this wave's k step s is 1 KB at ((ch0/32)*KS + s) KB
+    const int8_t* wp = g.w + ((int64_t)(ch0 / 32) * KS) * 1024 + lane * 16;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) wr[s] = *reinterpret_cast<const v4i*>(wp + s * 1024);
+  }
+  const float rc = g.recip[ch0 + li], bs = g.bias[ch0 + li];
+  // k chunk q (16 bytes at reduction index 16q, order (kh, kw, c)) -> its
+  // byte offset in the window; computed, not loaded, so that nothing here
+  // waits for the loads in flight
+  if (tid < 2 * KS) {
+    const int kidx = tid * 16, r = kidx / g.c_pad, c0 = kidx - r * g.c_pad;
+    const int kh = r / g.KW, kw = r - kh * g.KW;
+    // K padding (past kred): the weights there are zero, any window byte will do
+    koff_tab[tid] = kidx < g.kred ? (kh * g.dh * g.FW + kw * g.dw) * g.FS + c0 : 0;
+  }
+#pragma unroll
+  for (int q = 0; q < 8; ++q)
+    if (fdst[q] >= 0) *reinterpret_cast<v4i*>(foot + fdst[q]) = fv[q];
+
+  // per-lane window origin (bytes) of each of the wave's pixel rows of D
+  int fbase[TN];
+#pragma unroll
+  for (int b = 0; b < TN; ++b) {
+    const int pc = min(b * 32 + li, npx - 1);
+    const int py = pc / g.OW, px = pc - py * g.OW;
+    fbase[b] = (py * g.sh * g.FW + px * g.sw) * g.FS;
+  }
+  __syncthreads();  // footprint and k offsets visible
+
+  v16i acc[TN];
+#pragma unroll
+  for (int b = 0; b < TN; ++b)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[b][r] = 0;
+#pragma unroll
+  for (int s = 0; s < KS; ++s) {
+    const int koff = koff_tab[s * 2 + lh];
+    v4i xf[TN];
+#pragma unroll
+    for (int b = 0; b < TN; ++b) xf[b] = *reinterpret_cast<const v4i*>(foot + fbase[b] + koff);
+#pragma unroll
+    for (int b = 0; b < TN; ++b) acc[b] = __builtin_amdgcn_mfma_i32_32x32x32_i8(xf[b], wr[s], acc[b], 0, 0, 0);
+  }
+
+  // ---- epilogue from registers: channel ch0 + li, pixels 8g + 4lh + q
+  const bool q8 = g.term > 100, relu = g.act == NHIP_ACT_RELU;
+  const int qlo = relu ? 0 : -127;  // requantized ReLU: the saturation's lower bound
+  const int ch = ch0 + li;
+  const bool chan_ok = ch < g.m;
+  const int es = q8 ? 1 : 4;
+  const uint32_t base = (uint32_t)((((int64_t)img * g.m + ch) * g.OHW + (int64_t)oy0 * g.OW) * es);
+  const __amdgpu_buffer_rsrc_t orr = make_rsrc(g.out, g.out_bytes);
+  auto dequant = [&](int b, int r) {
+#pragma clang fp contract(off)
+    float v = (float)acc[b][r];
+    v = v * rc;
+    return v + bs;
+  };
+#pragma unroll
+  for (int b = 0; b < TN; ++b) {
+    if (q8) {
+      uint32_t wd[4];  // pixels 8g + 4lh .. + 3 as bytes
+#pragma unroll
+      for (int gi = 0; gi < 4; ++gi)
+        wd[gi] = pack_i8x4(quantize_q(dequant(b, 4 * gi), g.os, qlo), quantize_q(dequant(b, 4 * gi + 1), g.os, qlo),
+                           quantize_q(dequant(b, 4 * gi + 2), g.os, qlo), quantize_q(dequant(b, 4 * gi + 3), g.os, qlo));
+      if (g.vec == 2) {
+        // swap words between lane halves so that lane (c, h) holds pixels
+        // 16h .. 16h + 15 of the block: one 16-byte store per lane
+        const auto s02 = __builtin_amdgcn_permlane32_swap(wd[0], wd[2], false, false);
+        const auto s13 = __builtin_amdgcn_permlane32_swap(wd[1], wd[3], false, false);
+        const v4i y{(int)s02[0], (int)s02[1], (int)s13[0], (int)s13[1]};
+        const int p0 = b * 32 + 16 * lh;
+        __builtin_amdgcn_raw_buffer_store_b128(y, orr, chan_ok && p0 < npx ? base + p0 : kBufOOB, 0, 0);
+      } else if (g.vec == 1) {
+#pragma unroll
+        for (int gi = 0; gi < 4; ++gi) {
+          const int p0 = b * 32 + 8 * gi + 4 * lh;
+          __builtin_amdgcn_raw_buffer_store_b32((int)wd[gi], orr, chan_ok && p0 < npx ? base + p0 : kBufOOB, 0, 0);
+        }
+      } else {
+#pragma unroll
+        for (int gi = 0; gi < 4; ++gi)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const int p = b * 32 + 8 * gi + 4 * lh + q;
+            __builtin_amdgcn_raw_buffer_store_b8((char)(wd[gi] >> (8 * q)), orr,
+                                                 chan_ok && p < npx ? base + p : kBufOOB, 0, 0);
+          }
+      }
+    } else {
+#pragma unroll
+      for (int gi = 0; gi < 4; ++gi) {
+        const int p0 = b * 32 + 8 * gi + 4 * lh;
+        float f[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          f[q] = dequant(b, 4 * gi + q);
+          f[q] = (relu && f[q] < 0.0f) ? 0.0f : f[q];
+        }
+        if (g.vec >= 1) {
+          const v4i y{__float_as_int(f[0]), __float_as_int(f[1]), __float_as_int(f[2]), __float_as_int(f[3])};
+          __builtin_amdgcn_raw_buffer_store_b128(y, orr, chan_ok && p0 < npx ? base + 4 * p0 : kBufOOB, 0, 0);
+        } else {
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            __builtin_amdgcn_raw_buffer_store_b32(__float_as_int(f[q]), orr,
+                                                  chan_ok && p0 + q < npx ? base + 4 * (p0 + q) : kBufOOB, 0, 0);
+        }
       }
     }
   }
@@ -539,6 +693,62 @@ int launch_conv_int8(const nhip_conv_plan* p, const void* in, int in_is_i8,
   g.term = p->scale_term;
   g.act = p->g.act;
   g.out = out;
+  const int64_t out_bytes = (int64_t)n * p->g.k * oh * ow * (p->scale_term > 100 ? 1 : 4);
+  g.out_bytes = (uint32_t)std::min<int64_t>(out_bytes, INT32_MAX);
+  // Register-weight kernel: a reduction of 36 k steps (1152 bytes: 128
+  // channels at 3x3), whole 128-channel blocks and a footprint window of at
+  // most 2048 16-byte chunks.  NHIP_INT8_RW=0 turns it off, =2 takes two
+  // 32-pixel blocks per wave instead of four (tuning and comparison
+  // switches).
+  {
+    const int mode = setting_int("NHIP_INT8_RW", 1);
+    const int tn = mode == 2 ? 2 : 4;
+    const int R = ow > 0 ? std::min(32 * tn / ow, oh) : 0;
+    constexpr int KS = kRwKred / 32;
+    if (mode != 0 && R >= 1 && p->weight_i8_frag != nullptr && p->m_pad % 128 == 0 && p->kred_pad == kRwKred &&
+        out_bytes < INT32_MAX) {
+      Int8Args r = g;
+      r.w = p->weight_i8_frag;
+      r.OH = oh;
+      r.R = R;
+      r.FH = (R - 1) * p->g.sh + (p->g.kh - 1) * p->g.dh + 1;
+      r.FW = (ow - 1) * p->g.sw + (p->g.kw - 1) * p->g.dw + 1;
+      r.FS = p->c_pad + 16;
+      r.fp_bytes = (int)round_up((int64_t)r.FH * r.FW * r.FS, 16);
+      r.cpp_div = fast_div((uint32_t)(p->c_pad / 16));
+      r.fw_div = fast_div((uint32_t)r.FW);
+      r.kred = p->kred;
+      r.KW = p->g.kw;
+      r.dh = p->g.dh;
+      r.dw = p->g.dw;
+      // Store mode: whole 16-pixel int8 runs (16-byte aligned and all valid
+      // or all past the workgroup's pixels) when OHW and R*OW are multiples
+      // of 16; whole 4-pixel groups when they are multiples of 4; else
+      // single elements.
+      {
+        const uintptr_t oa = reinterpret_cast<uintptr_t>(out);
+        const bool q8 = p->scale_term > 100;
+        const int64_t run = (int64_t)R * ow, ohw = (int64_t)oh * ow;
+        if (q8 && ohw % 16 == 0 && run % 16 == 0 && oa % 16 == 0)
+          r.vec = 2;
+        else if (ohw % 4 == 0 && run % 4 == 0 && oa % (q8 ? 4 : 16) == 0)
+          r.vec = 1;
+        else
+          r.vec = 0;
+      }
+      const int64_t chunks = (int64_t)r.FH * r.FW * (p->c_pad / 16);
+      const int64_t lds = r.fp_bytes + 2 * KS * 4;
+      if (chunks <= 8 * kThreads && lds <= 64 * 1024) {
+        const dim3 grid((unsigned)(n * ceil_div(oh, R)), (unsigned)(p->m_pad / 128));
+        if (tn == 4) {
+          NHIP_LAUNCH("conv_int8_rw", (conv_int8_rw_kernel<KS, 4>), grid, dim3(kThreads), (unsigned)lds, s, r);
+        } else {
+          NHIP_LAUNCH("conv_int8_rw", (conv_int8_rw_kernel<KS, 2>), grid, dim3(kThreads), (unsigned)lds, s, r);
+        }
+        return check_launch("conv_int8_rw");
+      }
+    }
+  }
   // Footprint kernel when a workgroup's input window fits in LDS (whole rows
   // of at most 128 output pixels); NHIP_INT8_FOOTPRINT=0 turns it off (a
   // tuning and comparison switch).

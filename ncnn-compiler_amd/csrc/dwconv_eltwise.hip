@@ -380,20 +380,6 @@ __global__ __launch_bounds__(256) void dw3x3_stream_kernel(DwArgs a, DwStream st
 
 // ---------------------------------------------------------------------------
 
-// Round half away from zero of s = x * scale, saturated to [lo, 127] (lo =
-// -127, or 0 for a ReLU that follows), NaN -> 0.  Branch-free:
-// trunc(s + copysign(0.5, s)) forms the same fp32 sum as floor(s + 0.5) for
-// s >= 0 and ceil(s - 0.5) for s < 0, and truncation equals that floor /
-// ceil since the sum has the sign of s (s = -0.0 gives 0 both ways); one
-// median-of-three saturates; NaN selects 0 before the conversion.
-// max(clamp(q, -127, 127), 0) = clamp(q, 0, 127), so the ReLU is the bound.
-__device__ __forceinline__ int8_t quantize_i8(float x, float scale, float lo = -127.0f) {
-#pragma clang fp contract(off)
-  const float s = x * scale;
-  const float r = __builtin_amdgcn_fmed3f(truncf(s + copysignf(0.5f, s)), lo, 127.0f);
-  return (int8_t)(int)(s != s ? 0.0f : r);
-}
-
 // int8 ConvolutionDepthWise (NCNNToTosa.cpp:3257-3376): the input band is
 // quantized (fp32 input) or copied (int8 input) into LDS as int8, the window
 // sum is exact int32, and the epilogue is the int8 convolution's:
@@ -455,7 +441,7 @@ __global__ __launch_bounds__(256) void dwconv_int8_kernel(DwI8Args a) {
     f = f * a.recip[c];
     f = f + a.bias[c];
     if (a.term > 100) {
-      static_cast<int8_t*>(a.y)[o] = quantize_i8(f, a.os, a.act == NHIP_ACT_RELU ? 0.0f : -127.0f);
+      static_cast<int8_t*>(a.y)[o] = quantize_i8(f, a.os, a.act == NHIP_ACT_RELU ? 0 : -127);
     } else {
       if (a.act == NHIP_ACT_RELU) f = f < 0.f ? 0.f : f;
       static_cast<float*>(a.y)[o] = f;

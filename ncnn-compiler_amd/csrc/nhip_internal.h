@@ -89,6 +89,35 @@ __device__ __forceinline__ int fdiv(int n, FastDiv f) {
   return (int)((__umulhi((uint32_t)n, f.m) + (uint32_t)n) >> f.s);
 }
 
+// ---- int8 quantization (reference quantizeSignedI8, NCNNToTosa.cpp:322-389) --
+// Round half away from zero of s = x * scale, saturated to [lo, 127] (lo =
+// -127, or 0 for a ReLU that follows), NaN -> 0.  s + copysign(0.5, s) forms
+// the same fp32 sum as floor(s + 0.5) for s >= 0 and ceil(s - 0.5) for s < 0,
+// and truncating it toward zero equals that floor / ceil since the sum has
+// the sign of s (s = -0.0 gives 0 both ways).  v_cvt_i32_f32 truncates toward
+// zero, saturates out-of-range values and infinities to the int32 limits and
+// converts NaN to 0 (GCN/CDNA ISA), so it is issued directly (a C++ cast of
+// such values is undefined) and one integer median-of-three saturates.
+// max(clamp(q, -127, 127), 0) = clamp(q, 0, 127), so a ReLU is the bound.
+// The caller's multiply stays separately rounded: no contraction here.
+__device__ __forceinline__ int quantize_q(float x, float scale, int lo = -127) {
+#pragma clang fp contract(off)
+  const float s = x * scale;
+  const float t = s + __builtin_copysignf(0.5f, s);
+  int q;
+  asm("v_cvt_i32_f32 %0, %1" : "=v"(q) : "v"(t));
+  return max(min(q, 127), lo);
+}
+__device__ __forceinline__ int8_t quantize_i8(float x, float scale, int lo = -127) {
+  return (int8_t)quantize_q(x, scale, lo);
+}
+// Four quantized values (low bytes of a, b, c, d) as one little-endian word.
+__device__ __forceinline__ uint32_t pack_i8x4(int a, int b, int c, int d) {
+  const uint32_t lo = __builtin_amdgcn_perm((uint32_t)b, (uint32_t)a, 0x0c0c0400u);
+  const uint32_t hi = __builtin_amdgcn_perm((uint32_t)d, (uint32_t)c, 0x0c0c0400u);
+  return __builtin_amdgcn_perm(hi, lo, 0x05040100u);
+}
+
 // ---- MFMA operand / accumulator types ---------------------------------------
 typedef float v4f __attribute__((ext_vector_type(4)));
 typedef float v16f __attribute__((ext_vector_type(16)));
@@ -147,6 +176,12 @@ struct nhip_conv_plan {
   // int8: weights int8 [m_pad][kh*kw*c_pad] (k = (kh, kw, c) order),
   // reciprocal r[c] = ws==0 ? 0 : 1/(ws*is), bias, scales.
   int8_t* weight_i8 = nullptr;
+  // The same int8 weights in MFMA fragment order for the register-weight
+  // kernel, [m_pad/32][kred_pad/32][64 lanes][16 bytes]: lane l of k step s
+  // of block b holds row 32b + l%32, bytes 32s + 16(l/32) .. +15, so one
+  // wave's load of a k step is 1 KB contiguous.  Only when that kernel can
+  // take the plan (kred_pad == kRwKred, m_pad a multiple of 128).
+  int8_t* weight_i8_frag = nullptr;
   float* recip = nullptr;
   float input_scale = 1.0f, output_scale = 1.0f;
   int32_t scale_term = 0;
@@ -162,6 +197,9 @@ struct nhip_ip_plan {
 };
 
 namespace nhip {
+// Reduction length (bytes) of the int8 register-weight kernel: 36 k steps of
+// 32 bytes (128 channels at 3x3).
+constexpr int kRwKred = 36 * 32;
 // Kernel launchers (defined in the .hip files).
 int launch_conv_igemm_f32(const nhip_conv_plan* p, const float* in,
                           const float* residual, float* out, int n, int h,

@@ -350,6 +350,7 @@ void free_plan(nhip_conv_plan* p) {
   (void)hipFree(p->bias);
   (void)hipFree(p->ktab);
   (void)hipFree(p->weight_i8);
+  (void)hipFree(p->weight_i8_frag);
   (void)hipFree(p->recip);
   delete p;
 }
@@ -692,6 +693,16 @@ int nhip_conv2d_int8_create(const nhip_conv_desc* d, const void* weight, int32_t
     kt[q] = (c0 << 16) | ((kh * d->dilation_h) << 8) | (kw * d->dilation_w);
   }
   int st = upload(&p->weight_i8, wq, "hipMalloc(int8 weight)");
+  if (st == NHIP_STATUS_SUCCESS && p->kred_pad == nhip::kRwKred && p->m_pad % 128 == 0) {
+    std::vector<int8_t> wf(wq.size());
+    const int ks = p->kred_pad / 32;
+    for (int b = 0; b < p->m_pad / 32; ++b)
+      for (int s = 0; s < ks; ++s)
+        for (int l = 0; l < 64; ++l)
+          std::copy_n(wq.begin() + (size_t)(32 * b + l % 32) * p->kred_pad + 32 * s + 16 * (l / 32), 16,
+                      wf.begin() + (((size_t)b * ks + s) * 64 + l) * 16);
+    st = upload(&p->weight_i8_frag, wf, "hipMalloc(int8 fragment-order weight)");
+  }
   if (st == NHIP_STATUS_SUCCESS) st = upload(&p->recip, rc, "hipMalloc(int8 reciprocal)");
   if (st == NHIP_STATUS_SUCCESS) st = upload(&p->ktab, kt, "hipMalloc(int8 ktab)");
   if (st == NHIP_STATUS_SUCCESS) st = upload_bias(p, d->bias_term ? bias : nullptr, K, p->m_pad);

@@ -138,6 +138,54 @@ def test_int8_shapes_bit_exact(case, footprint, nhip_env):
     np.testing.assert_array_equal(got, exp)
 
 
+RW_CASES = [
+    # Reductions of exactly 1152 bytes (the register-weight kernel's):
+    # (n, c, h, w, k, kernel, stride, dil, pad, term, act, scalar ws?)
+    (2, 128, 28, 28, 128, (3, 3), (1, 1), (1, 1), (1, 1, 1, 1), 101, 1, False),  # config 4 at batch 2
+    # 100 of 128 channels, 11 columns (byte stores), fp32 output
+    (1, 120, 13, 11, 100, (3, 3), (1, 1), (1, 1), (1, 1, 1, 1), 1, 0, False),
+    # two channel blocks, stride 2, asymmetric padding, scalar scale
+    (2, 128, 15, 17, 256, (3, 3), (2, 2), (1, 1), (0, 1, 1, 0), 102, 1, True),
+    # 250 of 256 channels, dilation 2, 40 columns (3 or 1 rows per workgroup)
+    (1, 113, 10, 40, 250, (3, 3), (1, 1), (2, 2), (2, 2, 2, 2), 2, 1, True),
+    # a 1x1 convolution over 1152 channels: every k step inside one tap
+    (1, 1152, 5, 5, 128, (1, 1), (1, 1), (1, 1), (0, 0, 0, 0), 101, 0, False),
+    # 7x7 planes: 49 pixels per workgroup, byte stores of int8 results
+    (3, 128, 7, 7, 128, (3, 3), (1, 1), (1, 1), (1, 1, 1, 1), 101, 0, False),
+    # 32 columns: four whole 32-pixel blocks per wave
+    (1, 128, 9, 32, 128, (3, 3), (1, 1), (1, 1), (1, 1, 1, 1), 1, 1, False),
+]
+
+
+@pytest.mark.parametrize("case", RW_CASES, ids=lambda c: "x".join(map(str, c[:5])) + f"-t{c[9]}")
+@pytest.mark.parametrize("rw", ["1", "2", "0"])
+def test_int8_register_weight_kernel_bit_exact(case, rw, nhip_env):
+    """The register-weight kernel (NHIP_INT8_RW=1, default: four 32-pixel
+    blocks per wave; =2: two) against the oracle, bit for bit, and with it
+    off (=0: the footprint kernel)."""
+    nhip_env.setenv("NHIP_INT8_RW", rw)
+    n, c, h, w, k, ker, st, dl, pad, term, act, scalar = case
+    rng = np.random.default_rng(hash(case) % (2 ** 32))
+    x = rng.uniform(-1.5, 1.5, (n, c, h, w)).astype(np.float32)
+    ws = (np.float32(rng.uniform(20, 200)) * np.ones(1, np.float32) if scalar
+          else rng.uniform(20, 200, k).astype(np.float32))
+    ws_full = np.broadcast_to(ws, (k,)) if ws.size == 1 else ws
+    wfloat = rng.uniform(-0.6, 0.6, (k, c) + ker).astype(np.float32)
+    w_i8 = np.stack([refcpu.quantize_f32_i8(wfloat[o], ws_full[o:o + 1]) for o in range(k)])
+    b = rng.normal(0, 0.3, k).astype(np.float32)
+    is_, os_ = 60.0, 25.0 / np.sqrt(c * ker[0] * ker[1] / 128.0)
+    d = nhip.conv_desc(c, k, ker, st, dl, pad, act=act, int8_scale_term=term)
+    conv = nhip.Conv2dInt8(d, w_i8, b, ws, is_, os_)
+    xd = dev(x)
+    exp = oracle(d, x, w_i8, b, ws, is_, os_)
+    for rep in range(2):  # the second call reuses the plan and the workspace
+        got = host(conv.forward(xd))
+        assert got.dtype == exp.dtype
+        np.testing.assert_array_equal(got, exp, err_msg=f"call {rep}")
+    if term > 100:  # not degenerate: many levels, not all saturated
+        assert len(np.unique(got)) > 32
+
+
 def test_rounding_ties_and_saturation_on_device():
     # x*is lands exactly on .5 and on the 0.49999997 trap; acc passes through
     # a 1x1 identity so the output requantize sees the same values.
