@@ -257,20 +257,25 @@ def config1(nhip, workloads, torch, steps, warmup, workdir, share, cpu, target_s
     n = max(steps * 10, 100)
     dt = timed(torch, fn, n)
     flops = workloads.conv_flops(1, 64, 64, 56, 56)
-    # one image = 196 Winograd tiles: the three-kernel path (input transform,
-    # batched GEMM, output transform) or the fused GEMM, whichever the
-    # library picks; the roofline is the GEMM's
-    name, per, sec = dominant(nhip, torch, fn, n, ["wino_gemm", "wino_fused"])
-    wflops = workloads.winograd_flops(1, 64, 64, 56, 56)
+    # the library's choice for one image (the plan is Winograd, as the
+    # automatic choice makes it): the one-kernel implicit GEMM with the
+    # reduction split over each workgroup's waves (196 blocks of 32x32, at
+    # most one per CU), else the Winograd kernels; the roofline is the
+    # dominant kernel's, in the FLOPs it executes
+    name, per, sec = dominant(nhip, torch, fn, n, ["conv_kq", "wino_gemm", "wino_fused"])
     kernels = {}
-    for k in ("wino_input_transform", "wino_gemm", "wino_output_transform", "wino_fused"):
+    for k in ("conv_kq", "wino_input_transform", "wino_gemm", "wino_output_transform", "wino_fused"):
         kp, ks = kernel_time(nhip, torch, fn, n, k, required=False)
         if kp:
             kernels[k] = round(kp * ks * 1e6, 2)
-    res = {"workload": "conv fp32 1x64x56x56 -> 64, 3x3 s1 p1, bias + ReLU (Winograd F(4,3), device buffers)",
+    if name == "conv_kq":
+        rl = roofline("mfma", "conv_kq (implicit GEMM, 2*C*K*9*OH*OW)", flops / per, sec, per)
+    else:
+        wflops = workloads.winograd_flops(1, 64, 64, 56, 56)
+        rl = roofline("mfma", f"{name} (executed 2*36*T*C*K, T=196 tiles)", wflops / per, sec, per)
+    res = {"workload": "conv fp32 1x64x56x56 -> 64, 3x3 s1 p1, bias + ReLU (device buffers)",
            "ms_per_step": dt * 1e3, "tflops_direct_equivalent": flops / dt / 1e12, "images_per_sec": 1 / dt,
-           "kernel_us_per_step": kernels,
-           "roofline": roofline("mfma", f"{name} (executed 2*36*T*C*K, T=196 tiles)", wflops / per, sec, per)}
+           "kernel_us_per_step": kernels, "roofline": rl}
     m = ncnn_format.Model()
     m.input("data", 64, 56, 56)
     m.conv("conv", "data", "output", w, b, act=1)

@@ -168,6 +168,11 @@ struct nhip_conv_plan {
   // pairs, [c_pad/8][36][4][m_pad][2], so one chunk's slice for 32 output
   // channels is four contiguous 256-byte runs per transform point.
   float* weight_fused = nullptr;
+  // Winograd plans of 32 or 64 input channels: the weights also row-major,
+  // [m_pad][rows_ld] with k = c*9 + kh*3 + kw, for the one-kernel path of
+  // small launches (conv_kq.hip).
+  float* weight_rows = nullptr;
+  int32_t rows_ld = 0;
   float* bias = nullptr;      // [m_pad] zero-filled past k (always present)
   int32_t m_pad = 0, kred = 0, kred_pad = 0, c_pad = 0;
   // im2col gather table: one packed int per reduction index
@@ -255,6 +260,12 @@ int launch_innerproduct_dma(const nhip_ip_plan* p, const float* in, float* out, 
 // conv_smallk.hip: fp32 convolutions with a reduction of at most 32 and at
 // most 32 output channels (network stems), one MFMA block per 32 pixels.
 bool smallk_supported(const nhip_conv_plan* p, int n, int h, int w, int oh, int ow);
+// conv_kq.hip: fp32 3x3 convolutions with few output pixels (32 or 64
+// input channels), one workgroup per 32x32 block, the reduction over its
+// four waves (no workspace).
+bool kq_supported(const nhip_conv_plan* p, int n, int h, int w, int oh, int ow);
+int launch_conv_kq(const nhip_conv_plan* p, const float* in, const float* residual, float* out, int n, int h, int w,
+                   int oh, int ow, hipStream_t s);
 int launch_conv_smallk(const nhip_conv_plan* p, const float* in, const float* residual, float* out, int n, int h,
                        int w, int oh, int ow, hipStream_t s);
 bool pw_dma_supported(const nhip_conv_plan* p, int n, int h, int w);

@@ -347,6 +347,7 @@ void free_plan(nhip_conv_plan* p) {
   if (!p) return;
   (void)hipFree(p->weight);
   (void)hipFree(p->weight_fused);
+  (void)hipFree(p->weight_rows);
   (void)hipFree(p->bias);
   (void)hipFree(p->ktab);
   (void)hipFree(p->weight_i8);
@@ -553,6 +554,13 @@ int nhip_conv2d_f32_create(const nhip_conv_desc* d, const float* weight, const f
   if (algo == NHIP_CONV_ALGO_WINOGRAD) {
     p->c_pad = (int)round_up(C, 16);
     st = winograd_prepack_weights(p, weight);
+    if (st == NHIP_STATUS_SUCCESS && (C == 32 || C == 64)) {
+      p->rows_ld = (int)round_up(C * 9, 16);
+      std::vector<float> wr((size_t)p->m_pad * p->rows_ld, 0.f);
+      for (int k = 0; k < K; ++k)
+        std::copy(weight + (size_t)k * C * 9, weight + (size_t)(k + 1) * C * 9, wr.begin() + (size_t)k * p->rows_ld);
+      st = upload(&p->weight_rows, wr, "hipMalloc(conv row-major weight)");
+    }
   } else {
     const int khw = d->kernel_h * d->kernel_w;
     p->kred = C * khw;

@@ -99,6 +99,41 @@ def test_implicit_gemm_no_bias_sigmoid_and_residual():
     assert_close(got, exp, IGEMM_RTOL, "residual")
 
 
+KQ_CASES = [
+    # (n, c, h, w, k, stride, dilation, pad(t,b,l,r), residual, act)
+    (1, 64, 56, 56, 64, (1, 1), (1, 1), (1, 1, 1, 1), False, 1),   # config 1
+    (1, 32, 13, 11, 40, (1, 1), (1, 1), (1, 1, 1, 1), True, 0),    # 40 of 64 channels, 143 pixels
+    (2, 32, 9, 17, 70, (2, 1), (1, 1), (0, 2, 1, 1), False, 1),    # stride 2 x 1, asymmetric padding, 2 images
+    (1, 64, 12, 10, 32, (1, 1), (2, 2), (2, 2, 2, 2), True, 1),    # dilation 2
+    (3, 32, 5, 5, 96, (2, 2), (1, 1), (1, 1, 1, 1), False, 0),     # blocks spanning images
+]
+
+
+@pytest.mark.parametrize("case", KQ_CASES, ids=lambda c: "x".join(map(str, c[:5])))
+@pytest.mark.parametrize("kq", ["2", "0"])
+def test_conv_kq_matches_oracle(case, kq, nhip_env):
+    """The one-block-per-32x32 kernel with the reduction split over its
+    waves (NHIP_CONV_KQ=2: every shape it takes; by default launches of at
+    most two blocks per CU) and the tiled implicit GEMM (=0)."""
+    nhip_env.setenv("NHIP_CONV_KQ", kq)
+    n, c, h, w, k, st, dl, pad, with_res, act = case
+    rng = np.random.default_rng(hash(case) % (2 ** 32))
+    x = rng.uniform(-1, 1, (n, c, h, w)).astype(np.float32)
+    wt = workloads.he_normal(rng, (k, c, 3, 3), c * 9)
+    b = rng.normal(0, 0.05, k).astype(np.float32)
+    oh = (h + pad[0] + pad[1] - dl[0] * 2 - 1) // st[0] + 1
+    ow = (w + pad[2] + pad[3] - dl[1] * 2 - 1) // st[1] + 1
+    res = rng.uniform(-1, 1, (n, k, oh, ow)).astype(np.float32) if with_res else None
+    d = nhip.conv_desc(c, k, (3, 3), st, dl, pad, bias=True, act=act, algorithm=nhip.ALGO_IMPLICIT_GEMM)
+    plan = nhip.Conv2dF32(d, wt, b)
+    exp = oracle_conv(x, wt, b, st, dl, pad, act, residual=res)
+    out = torch.full(exp.shape, float("nan"), dtype=torch.float32, device="cuda")
+    for rep in range(2):  # into the same output twice
+        got = host(plan.forward(dev(x), residual=None if res is None else dev(res), out=out))
+        assert_close(got, exp, IGEMM_RTOL, f"conv kq={kq} {case} call {rep}")
+        assert max_rel_err(got, exp) <= IGEMM_RTOL
+
+
 WINO_CASES = [
     # (n, c, h, w, k, pad)
     (1, 16, 4, 4, 16, (1, 1, 1, 1)),
