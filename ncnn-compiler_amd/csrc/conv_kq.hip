@@ -1,18 +1,21 @@
-// fp32 3x3 convolution for launches with few output pixels (a single image:
-// the 1x64x56x56 layer is 231 MFLOP, 2 us of MFMA issue spread over the
-// GPU), one kernel instead of the Winograd path's three launches or the
-// tiled implicit GEMM's 49 workgroups.  Same operation as the implicit GEMM
-// (reference ConvertConvolution, NCNNToTosa.cpp:1316-1529).
+// fp32 convolution for launches with few output blocks, one kernel with the
+// reduction split over each workgroup's waves.  3x3 (32 or 64 input
+// channels): a single image (the 1x64x56x56 layer is 231 MFLOP, 2 us of
+// MFMA issue spread over the GPU) instead of the Winograd path's three
+// launches or the tiled implicit GEMM's 49 workgroups.  1x1: layers with at
+// most one 32x32 block per CU (MobileNetV2's 960 -> 160 at 7x7, batch 32),
+// instead of a split-K GEMM and its reduce launch.  Same operation as the
+// implicit GEMM (reference ConvertConvolution, NCNNToTosa.cpp:1316-1529).
 //
 // A workgroup owns one 32x32 block of (output channel, output pixel) and
-// splits the reduction over its four waves: k = c*9 + kh*3 + kw (the plan's
-// weight order), lane half h of wave w takes input channels
-// (2w + h)*CH .. + CH - 1 with all nine taps (C = 8*CH), so every k step
-// of a lane is one (channel, tap) pair known at compile time.  Each lane
-// loads its 9*CH weights (one contiguous row segment, 16-byte loads) and
-// its pixel's 9*CH input values (zero padding through out-of-range buffer
-// offsets; the channel plane offset is wave-uniform) into registers before
-// the first v_mfma_f32_32x32x2_f32, so a wave waits once; the four partial
+// splits the reduction over its WAVES waves: k = c*TAPS + kh*3 + kw (the
+// plan's weight order), lane half h of wave w takes input channels
+// (2w + h)*CH .. + CH - 1 with all their taps (C = 2*WAVES*CH), so every k
+// step of a lane is one (channel, tap) pair known at compile time.  Each
+// lane loads its TAPS*CH weights (one contiguous row segment, 16-byte loads)
+// and its pixel's TAPS*CH input values (zero padding through out-of-range
+// buffer offsets; the channel plane offset is wave-uniform) into registers
+// before the first v_mfma_f32_32x32x2_f32, so a wave waits once; the partial
 // blocks are summed through LDS in wave order (deterministic), then bias,
 // residual and activation.
 #include <algorithm>
@@ -21,8 +24,6 @@
 
 namespace nhip {
 namespace {
-
-constexpr int kThreads = 256;
 
 struct KqArgs {
   const float* w;       // [m_pad][ldw], k = c*9 + kh*3 + kw
@@ -35,32 +36,32 @@ struct KqArgs {
   int sh, sw, pt, pl, dh, dw, act;
 };
 
-template <int CH>
-__global__ __launch_bounds__(kThreads) void conv_kq_kernel(KqArgs g) {
-  __shared__ float red[3][16][64];  // partial blocks of waves 1..3
+template <int CH, int TAPS, int WAVES>
+__global__ __launch_bounds__(64 * WAVES) void conv_kq_kernel(KqArgs g) {
+  __shared__ float red[WAVES - 1][16][64];  // partial blocks of waves 1..WAVES-1
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int li = lane & 31, lh = lane >> 5;
   const int mb = blockIdx.x % g.nmb, pb = blockIdx.x / g.nmb;
 
-  // this lane's pixel (B column li) and its nine tap offsets in the image
-  // of channel (2*wave + lh)*CH; out of range for taps in the padding
+  // this lane's pixel (B column li) and its tap offsets (3x3 or one) in
+  // the image of channel (2*wave + lh)*CH; out of range in the padding
   const int pix = pb * 32 + li;
   const bool pok = pix < g.npix;
   const int pp = pok ? pix : 0;
   const int img = pp / g.OHW, rem = pp - img * g.OHW;
   const int oy = rem / g.OW, ox = rem - oy * g.OW;
   const int plane = g.H * g.W;
-  uint32_t toff[9];
+  uint32_t toff[TAPS];
 #pragma unroll
-  for (int t = 0; t < 9; ++t) {
+  for (int t = 0; t < TAPS; ++t) {
     const int iy = oy * g.sh - g.pt + (t / 3) * g.dh, ix = ox * g.sw - g.pl + (t % 3) * g.dw;
     const bool ok = pok && (unsigned)iy < (unsigned)g.H && (unsigned)ix < (unsigned)g.W;
     toff[t] = ok ? (uint32_t)((((int64_t)img * g.C + lh * CH) * plane + iy * g.W + ix) * 4) : kBufOOB;
   }
 
   // weights: row 32*mb + li, k = 9*((2w + h)*CH) .. + 9*CH - 1, contiguous
-  constexpr int KS = 9 * CH;
+  constexpr int KS = TAPS * CH;
   static_assert(KS % 4 == 0, "a lane's weight segment is whole, 16-byte aligned float4s");
   v4f a[KS / 4];
   {
@@ -75,8 +76,8 @@ __global__ __launch_bounds__(kThreads) void conv_kq_kernel(KqArgs g) {
     for (int c = 0; c < CH; ++c) {
       const int soff = ((2 * wave * CH + c) * plane) * 4;  // wave-uniform channel plane
 #pragma unroll
-      for (int t = 0; t < 9; ++t)
-        b[c * 9 + t] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(xr, toff[t], soff, 0));
+      for (int t = 0; t < TAPS; ++t)
+        b[c * TAPS + t] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(xr, toff[t], soff, 0));
     }
   }
   __builtin_amdgcn_sched_barrier(0);  // every load issued before the first MFMA
@@ -93,7 +94,7 @@ __global__ __launch_bounds__(kThreads) void conv_kq_kernel(KqArgs g) {
   __syncthreads();
   if (wave != 0) return;
 #pragma unroll
-  for (int w = 0; w < 3; ++w)
+  for (int w = 0; w < WAVES - 1; ++w)
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[r] += red[w][r][lane];
   // D[channel][pixel]: register r of lane (li, lh) is channel
@@ -133,26 +134,46 @@ bool kq_weights(const nhip_conv_plan* p, const float** w, int* ld) {
   return *w != nullptr && *ld % 4 == 0;
 }
 
-// Whether the kernel takes the launch: a 3x3 fp32 convolution with 32 or 64
-// input channels (a lane's 9*C/8 weights then are whole 16-byte vectors),
-// activation none or ReLU, and few blocks: at most two 32x32 blocks per CU
-// on an implicit-GEMM plan (larger launches fill the GPU with the tiled
-// kernels), at most one on a Winograd plan (config 1, 1x64x56x56: 9.7 us
-// against 13.6 us for the Winograd path and 14.6 us for the tiled implicit
-// GEMM).  NHIP_CONV_KQ=0 never, =2 whenever it can.
+// Instances: (channels per lane half, waves) for a 1x1 convolution with C
+// input channels, C = 2*waves*CH (MobileNetV2's 7x7 and 14x14 layers);
+// {0, 0} when none.
+struct KqShape {
+  int ch, waves;
+};
+KqShape kq_1x1_shape(int c) {
+  for (int ch : {8, 12, 20, 40, 48, 72})
+    if (c == 8 * ch) return {ch, 4};
+  if (c == 960) return {60, 8};
+  return {0, 0};
+}
+
+// Whether the kernel takes the launch: a 3x3 convolution with 32 or 64 input
+// channels (a lane's 9*C/8 weights then are whole 16-byte vectors) or a 1x1
+// one with an instantiated channel count, activation none or ReLU, and few
+// blocks.  3x3: at most two 32x32 blocks per CU on an implicit-GEMM plan, at
+// most one on a Winograd plan (config 1, 1x64x56x56: 9.7 us against 13.6 us
+// for the Winograd path and 14.6 us for the tiled implicit GEMM).  1x1: at
+// most one per CU (MobileNetV2 at batch 32, 960 -> 160 + residual at 7x7:
+// 17.0 against 21.4 us; with more blocks the tiled kernels' operand reuse
+// wins: 960 -> 320, 26.7 against 25.0 us) and at least one per eight CUs
+// (MobileNetV2 at batch 1 puts its 7x7 and 14x14 projections, 10 to 21
+// blocks, on this kernel 11 us slower over the graph, its expansions, 60 to
+// 126 blocks, 5 us faster).  NHIP_CONV_KQ=0 never, =2 whenever it can.
 bool kq_supported(const nhip_conv_plan* p, int n, int h, int w, int oh, int ow) {
   const int mode = setting_int("NHIP_CONV_KQ", 1);
   if (mode == 0) return false;
   const ConvGeom& g = p->g;
   const float* wr = nullptr;
   int ld = 0;
-  if (p->kind != PlanKind::ConvF32 || !kq_weights(p, &wr, &ld) || g.kh != 3 || g.kw != 3 ||
-      (g.c != 32 && g.c != 64) || (g.act != NHIP_ACT_NONE && g.act != NHIP_ACT_RELU))
+  if (p->kind != PlanKind::ConvF32 || !kq_weights(p, &wr, &ld) || (g.act != NHIP_ACT_NONE && g.act != NHIP_ACT_RELU))
     return false;
+  const bool k3 = g.kh == 3 && g.kw == 3 && (g.c == 32 || g.c == 64);
+  const bool k1 = g.kh == 1 && g.kw == 1 && kq_1x1_shape(g.c).ch != 0;
+  if (!k3 && !k1) return false;
   const int64_t npix = (int64_t)n * oh * ow;
   const int64_t blocks = ceil_div(p->g.k, 32) * ceil_div(npix, 32);
-  const int per_cu = p->algorithm == NHIP_CONV_ALGO_IMPLICIT_GEMM ? 2 : 1;
-  if (mode != 2 && blocks > per_cu * (int64_t)cu_count()) return false;
+  const int per_cu = p->algorithm == NHIP_CONV_ALGO_IMPLICIT_GEMM && k3 ? 2 : 1;
+  if (mode != 2 && (blocks > per_cu * (int64_t)cu_count() || (k1 && blocks < cu_count() / 8))) return false;
   return (int64_t)n * g.c * h * w * 4 < INT32_MAX && npix * g.k * 4 < INT32_MAX;
 }
 
@@ -182,11 +203,28 @@ int launch_conv_kq(const nhip_conv_plan* p, const float* in, const float* residu
   a.dw = p->g.dw;
   a.act = p->g.act;
   const dim3 grid((unsigned)(a.nmb * ceil_div(a.npix, 32)));
-  if (p->g.c == 32)
-    NHIP_LAUNCH("conv_kq", conv_kq_kernel<4>, grid, dim3(kThreads), 0, s, a);
-  else
-    NHIP_LAUNCH("conv_kq", conv_kq_kernel<8>, grid, dim3(kThreads), 0, s, a);
-  return check_launch("conv_kq");
+  if (p->g.kh == 3) {
+    if (p->g.c == 32)
+      NHIP_LAUNCH("conv_kq", (conv_kq_kernel<4, 9, 4>), grid, dim3(256), 0, s, a);
+    else
+      NHIP_LAUNCH("conv_kq", (conv_kq_kernel<8, 9, 4>), grid, dim3(256), 0, s, a);
+    return check_launch("conv_kq");
+  }
+  const KqShape k = kq_1x1_shape(p->g.c);
+#define NHIP_KQ1(CH_, W_)                                                                       \
+  if (k.ch == CH_ && k.waves == W_) {                                                           \
+    NHIP_LAUNCH("conv_kq", (conv_kq_kernel<CH_, 1, W_>), grid, dim3(64 * W_), 0, s, a);         \
+    return check_launch("conv_kq");                                                             \
+  }
+  NHIP_KQ1(8, 4)
+  NHIP_KQ1(12, 4)
+  NHIP_KQ1(20, 4)
+  NHIP_KQ1(40, 4)
+  NHIP_KQ1(48, 4)
+  NHIP_KQ1(72, 4)
+  NHIP_KQ1(60, 8)
+#undef NHIP_KQ1
+  return fail(NHIP_STATUS_CONSTRAINT_VIOLATION, "conv_kq: unsupported shape");
 }
 
 }  // namespace nhip

@@ -260,9 +260,9 @@ int launch_innerproduct_dma(const nhip_ip_plan* p, const float* in, float* out, 
 // conv_smallk.hip: fp32 convolutions with a reduction of at most 32 and at
 // most 32 output channels (network stems), one MFMA block per 32 pixels.
 bool smallk_supported(const nhip_conv_plan* p, int n, int h, int w, int oh, int ow);
-// conv_kq.hip: fp32 3x3 convolutions with few output pixels (32 or 64
-// input channels), one workgroup per 32x32 block, the reduction over its
-// four waves (no workspace).
+// conv_kq.hip: fp32 3x3 (32 or 64 input channels) and 1x1 convolutions with
+// few output blocks, one workgroup per 32x32 block, the reduction over its
+// waves (no workspace).
 bool kq_supported(const nhip_conv_plan* p, int n, int h, int w, int oh, int ow);
 int launch_conv_kq(const nhip_conv_plan* p, const float* in, const float* residual, float* out, int n, int h, int w,
                    int oh, int ow, hipStream_t s);

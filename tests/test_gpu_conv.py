@@ -129,9 +129,52 @@ def test_conv_kq_matches_oracle(case, kq, nhip_env):
     exp = oracle_conv(x, wt, b, st, dl, pad, act, residual=res)
     out = torch.full(exp.shape, float("nan"), dtype=torch.float32, device="cuda")
     for rep in range(2):  # into the same output twice
+        nhip.timer_start("conv_kq")
         got = host(plan.forward(dev(x), residual=None if res is None else dev(res), out=out))
+        assert nhip.timer_stop()[0] == (1 if kq == "2" else 0)
         assert_close(got, exp, IGEMM_RTOL, f"conv kq={kq} {case} call {rep}")
         assert max_rel_err(got, exp) <= IGEMM_RTOL
+
+
+KQ1_CASES = [
+    # (n, c, h, w, k, stride, pad(t,b,l,r), residual, act): 1x1, C = 8*ch or 960
+    (32, 960, 7, 7, 160, (1, 1), (0, 0, 0, 0), True, 0),   # MobileNetV2's 960 -> 160 + residual
+    (1, 64, 5, 9, 40, (1, 1), (0, 0, 0, 0), False, 1),
+    (2, 96, 14, 14, 70, (1, 1), (0, 0, 0, 0), True, 0),
+    (3, 320, 6, 5, 33, (1, 1), (0, 0, 0, 0), False, 1),
+    (1, 576, 7, 7, 96, (1, 1), (0, 0, 0, 0), True, 0),
+    (2, 384, 3, 11, 64, (1, 1), (0, 0, 0, 0), False, 0),
+    (1, 160, 7, 7, 16, (1, 1), (0, 0, 0, 0), False, 1),
+    (2, 64, 9, 9, 32, (2, 2), (1, 0, 1, 0), False, 1),     # stride 2, padding
+]
+
+
+@pytest.mark.parametrize("case", KQ1_CASES, ids=lambda c: "x".join(map(str, c[:5])))
+@pytest.mark.parametrize("kq", ["2", "0"])
+def test_conv_kq_1x1_matches_oracle(case, kq, nhip_env):
+    """1x1 convolutions on the split-reduction kernel (NHIP_CONV_KQ=2:
+    every shape it takes, with the streaming pointwise kernel, which is
+    picked first, switched off; by default at most one 32x32 block per CU)
+    and off (=0: the pointwise, direct-to-LDS or tiled kernels)."""
+    nhip_env.setenv("NHIP_CONV_KQ", kq)
+    if kq == "2":
+        nhip_env.setenv("NHIP_POINTWISE", "0")
+    n, c, h, w, k, st, pad, with_res, act = case
+    rng = np.random.default_rng(hash(case) % (2 ** 32))
+    x = rng.uniform(-1, 1, (n, c, h, w)).astype(np.float32)
+    wt = workloads.he_normal(rng, (k, c, 1, 1), c)
+    b = rng.normal(0, 0.05, k).astype(np.float32)
+    oh = (h + pad[0] + pad[1] - 1) // st[0] + 1
+    ow = (w + pad[2] + pad[3] - 1) // st[1] + 1
+    res = rng.uniform(-1, 1, (n, k, oh, ow)).astype(np.float32) if with_res else None
+    d = nhip.conv_desc(c, k, (1, 1), st, (1, 1), pad, bias=True, act=act, algorithm=nhip.ALGO_IMPLICIT_GEMM)
+    plan = nhip.Conv2dF32(d, wt, b)
+    exp = oracle_conv(x, wt, b, st, (1, 1), pad, act, residual=res)
+    nhip.timer_start("conv_kq")
+    got = host(plan.forward(dev(x), residual=None if res is None else dev(res)))
+    assert nhip.timer_stop()[0] == (1 if kq == "2" else 0)
+    assert_close(got, exp, IGEMM_RTOL, f"1x1 kq={kq} {case}")
+    assert max_rel_err(got, exp) <= IGEMM_RTOL
 
 
 WINO_CASES = [

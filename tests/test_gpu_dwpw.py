@@ -36,8 +36,12 @@ def _gpu():
 def _every_pair(nhip_env):
     """NHIP_DWPW=2: fuse every pair the kernel can run; by default the library
     fuses only the stride-2 pairs with up to 32 output channels, where it
-    measured faster than the two layers."""
+    measured faster than the two layers.  NHIP_CONV_KQ=0 keeps the separate
+    1x1 layer on the pointwise GEMM kernel, whose reduction order the fused
+    kernel shares (the split-reduction kernel that small 1x1 launches take
+    sums in another order and has its own parity test)."""
     nhip_env.setenv("NHIP_DWPW", "2")
+    nhip_env.setenv("NHIP_CONV_KQ", "0")
 
 
 def dev(a):
