@@ -1,5 +1,6 @@
-"""Benchmark: the ResNet-18-shape 3x3 conv stack, batch 32, fp32 (BASELINE
-config 3) is the headline `value`; configs 1, 2, 4 and 5 are measured in the
+"""Benchmark: the ResNet-18-shape 3x3 conv stack, batch 32, fp32 (config 3,
+the third entry of BASELINE.json's `configs`) is the headline `value`;
+configs 1, 2, 4 and 5 (the other entries, in order) are measured in the
 same run and reported under `config`, each with the roofline of its dominant
 kernel and a CPU baseline.
 

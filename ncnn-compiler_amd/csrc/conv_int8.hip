@@ -770,7 +770,7 @@ int launch_conv_int8(const nhip_conv_plan* p, const void* in, int in_is_i8,
       const int bm = 64;
       // K stage: the widest of 384 / 192 / 128 bytes that divides the
       // reduction (fewer stages: fewer global-load round trips and barriers
-      // per workgroup; config 4: 3 stages of 384 bytes, 16.3 against 17.2 us
+      // per workgroup; 32x128x28x28 -> 128 channels: 3 stages of 384 bytes, 16.3 against 17.2 us
       // with 128-byte stages); NHIP_INT8_FP_BK overrides (tuning switch,
       // ignored when invalid).
       // operands (footprint + two weight stages) or the epilogue's staging,

@@ -151,7 +151,7 @@ KqShape kq_1x1_shape(int c) {
 // channels (a lane's 9*C/8 weights then are whole 16-byte vectors) or a 1x1
 // one with an instantiated channel count, activation none or ReLU, and few
 // blocks.  3x3: at most two 32x32 blocks per CU on an implicit-GEMM plan, at
-// most one on a Winograd plan (config 1, 1x64x56x56: 9.7 us against 13.6 us
+// most one on a Winograd plan (one image of 64x56x56, 64 output channels: 9.7 us against 13.6 us
 // for the Winograd path and 14.6 us for the tiled implicit GEMM).  1x1: at
 // most one per CU (MobileNetV2 at batch 32, 960 -> 160 + residual at 7x7:
 // 17.0 against 21.4 us; with more blocks the tiled kernels' operand reuse

@@ -5,7 +5,7 @@ weights, input/output blob names), so the same list drives the device
 runner here and the oracle chain in the tests.  Blob names follow ncnn's
 .param convention: every layer consumes and produces named blobs.
 
-MobileNetV2: width 1.0, 224x224 input, the standard
+MobileNetV2 (the benchmarked graph): width 1.0, 224x224 input, the standard
 (t, c, n, s) table, BN folded into the convolution biases, ReLU after the
 stem, every expand and every depthwise conv (the reference's Convolution and
 ConvolutionDepthWise importers accept no ReLU6, ImportConvolution.cpp:63-72,

@@ -101,7 +101,7 @@ def test_implicit_gemm_no_bias_sigmoid_and_residual():
 
 KQ_CASES = [
     # (n, c, h, w, k, stride, dilation, pad(t,b,l,r), residual, act)
-    (1, 64, 56, 56, 64, (1, 1), (1, 1), (1, 1, 1, 1), False, 1),   # config 1
+    (1, 64, 56, 56, 64, (1, 1), (1, 1), (1, 1, 1, 1), False, 1),   # the benchmarked single conv
     (1, 32, 13, 11, 40, (1, 1), (1, 1), (1, 1, 1, 1), True, 0),    # 40 of 64 channels, 143 pixels
     (2, 32, 9, 17, 70, (2, 1), (1, 1), (0, 2, 1, 1), False, 1),    # stride 2 x 1, asymmetric padding, 2 images
     (1, 64, 12, 10, 32, (1, 1), (2, 2), (2, 2, 2, 2), True, 1),    # dilation 2

@@ -38,7 +38,7 @@ def set_dma(env, mode):
 
 
 @pytest.mark.parametrize("m,k,n,act", [
-    (256, 2048, 1000, 0),   # config 2
+    (256, 2048, 1000, 0),   # the benchmarked InnerProduct
     (32, 1280, 1000, 0),    # MobileNetV2 head at batch 32 (split K)
     (1, 1280, 1000, 1),
     (7, 132, 65, 1),        # k not a multiple of 32, n past one tile

@@ -1,4 +1,4 @@
-"""GPU parity at graph level: the MobileNetV2-shape graph
+"""GPU parity at graph level: the MobileNetV2-shape graph (the benchmarked one)
 run through libnhip against the same layer list run through the CPU oracle,
 layer by layer in the reference's op order (conv + bias, add, relu; depthwise
 zero-init + bias; global average pool; InnerProduct zero-init + bias)."""

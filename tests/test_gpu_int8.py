@@ -141,7 +141,7 @@ def test_int8_shapes_bit_exact(case, footprint, nhip_env):
 RW_CASES = [
     # Reductions of exactly 1152 bytes (the register-weight kernel's):
     # (n, c, h, w, k, kernel, stride, dil, pad, term, act, scalar ws?)
-    (2, 128, 28, 28, 128, (3, 3), (1, 1), (1, 1), (1, 1, 1, 1), 101, 1, False),  # config 4 at batch 2
+    (2, 128, 28, 28, 128, (3, 3), (1, 1), (1, 1), (1, 1, 1, 1), 101, 1, False),  # the benchmarked int8 conv at batch 2
     # 100 of 128 channels, 11 columns (byte stores), fp32 output
     (1, 120, 13, 11, 100, (3, 3), (1, 1), (1, 1), (1, 1, 1, 1), 1, 0, False),
     # two channel blocks, stride 2, asymmetric padding, scalar scale
