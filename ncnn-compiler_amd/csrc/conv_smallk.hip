@@ -256,16 +256,12 @@ int launch_conv_smallk(const nhip_conv_plan* p, const float* in, const float* re
   a.npix = n * oh * ow;
   a.nblk = (int)ceil_div(a.npix, 32);
   if (a.npix == 0) return ok();
-  // about eight blocks per wave (the gathers of one in flight behind the
-  // other; measured on the 224x224 stem at batch 32: 25.0 us against
-  // 28.2-29.8 with one to six blocks per wave, each wave's start-up loads
-  // then being spread over fewer blocks), but never fewer than four waves
-  // per CU while there are blocks for them (one image of the stem is 392
-  // blocks), at most 16 waves per CU; NHIP_SMALLK_BPW sets the blocks per
-  // wave (tuning)
-  const int bpw = std::max(1, setting_int("NHIP_SMALLK_BPW", 8));
-  const int64_t waves = std::min<int64_t>(
-      std::min<int64_t>(a.nblk, std::max<int64_t>(ceil_div(a.nblk, bpw), 4LL * cu_count())), 16LL * cu_count());
+  // One wave per SIMD (grid-stride over the blocks), fewer only when there
+  // are fewer blocks: on the 224x224 stem at batch 32 (12544 blocks), 1024
+  // waves took 23.2 us, 1568 (two on half of the SIMDs) 26.0 us, 768 29.7 us;
+  // two-block-deep and three-block-deep gather rings were 1.2 and 2.3 us
+  // slower than the one-block-ahead pair of buffers kept here.
+  const int64_t waves = std::min<int64_t>(a.nblk, 4LL * cu_count());
   const dim3 grid((unsigned)ceil_div(waves, kThreads / 64));
   if (p->kred_pad <= 16) launch_steps<8>(a, p->g.act, grid, s);
   else launch_steps<16>(a, p->g.act, grid, s);
