@@ -94,6 +94,7 @@ CASES = [
     (4, 576, 7, 7, 160, False, nhip.ACT_NONE, "1,4"),  # MobileNetV2 576 -> 160 at 7x7 (forced)
     (2, 384, 14, 14, 64, True, nhip.ACT_NONE),      # MobileNetV2 384 -> 64 (+ residual) at 14x14
     (1, 960, 7, 7, 320, False, nhip.ACT_NONE, "2,4"),  # a 960-channel weight slice in LDS (forced)
+    (32, 576, 14, 14, 96, True, nhip.ACT_NONE),     # MobileNetV2 576 -> 96 + residual at batch 32 (six slices)
 ]
 
 
