@@ -173,6 +173,10 @@ struct nhip_conv_plan {
   // small launches (conv_kq.hip).
   float* weight_rows = nullptr;
   int32_t rows_ld = 0;
+  // Winograd plans of 256+ input channels: an implicit-GEMM plan of the same
+  // layer, for launches of so few tiles that the Winograd GEMM's 128-tile
+  // padding dominates (a single 7x7 or 14x14 image).
+  nhip_conv_plan* igemm_twin = nullptr;
   float* bias = nullptr;      // [m_pad] zero-filled past k (always present)
   int32_t m_pad = 0, kred = 0, kred_pad = 0, c_pad = 0;
   // im2col gather table: one packed int per reduction index
@@ -205,6 +209,8 @@ namespace nhip {
 // Reduction length (bytes) of the int8 register-weight kernel: 36 k steps of
 // 32 bytes (128 channels at 3x3).
 constexpr int kRwKred = 36 * 32;
+// Input channels from which a Winograd plan also holds an implicit-GEMM twin.
+constexpr int kWinoTwinMinC = 256;
 // Kernel launchers (defined in the .hip files).
 int launch_conv_igemm_f32(const nhip_conv_plan* p, const float* in,
                           const float* residual, float* out, int n, int h,

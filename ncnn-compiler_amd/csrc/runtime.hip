@@ -345,6 +345,7 @@ int upload_bias(nhip_conv_plan* p, const float* bias, int count, int padded) {
 
 void free_plan(nhip_conv_plan* p) {
   if (!p) return;
+  free_plan(p->igemm_twin);
   (void)hipFree(p->weight);
   (void)hipFree(p->weight_fused);
   (void)hipFree(p->weight_rows);
@@ -560,6 +561,11 @@ int nhip_conv2d_f32_create(const nhip_conv_desc* d, const float* weight, const f
       for (int k = 0; k < K; ++k)
         std::copy(weight + (size_t)k * C * 9, weight + (size_t)(k + 1) * C * 9, wr.begin() + (size_t)k * p->rows_ld);
       st = upload(&p->weight_rows, wr, "hipMalloc(conv row-major weight)");
+    }
+    if (st == NHIP_STATUS_SUCCESS && C >= kWinoTwinMinC) {
+      nhip_conv_desc d2 = *d;
+      d2.algorithm = NHIP_CONV_ALGO_IMPLICIT_GEMM;
+      st = nhip_conv2d_f32_create(&d2, weight, bias, &p->igemm_twin);
     }
   } else {
     const int khw = d->kernel_h * d->kernel_w;

@@ -287,7 +287,20 @@ int winograd_prepack_weights(nhip_conv_plan* p, const float* weight) {
                    "hipMemcpy(winograd U)");
 }
 
+// Launches of at most 32 tiles on a plan with an implicit-GEMM twin take the
+// twin: the Winograd GEMM pads the tiles to 128, and a single image of
+// 512@7 (4 tiles) took 46.6 us on it against 23.3 us on the implicit GEMM,
+// 256@14 22.8 against 17.0 us at one image (16 tiles) and 23.3 against 21.8
+// at two (32 tiles), where from 64 tiles on Winograd wins (23.9 against
+// 29.4).  Not when a Winograd variant is forced (NHIP_WINOGRAD_VARIANT);
+// NHIP_WINO_TWIN=0 switches the route off.
+static bool twin_selected(const nhip_conv_plan* p, int n, int oh, int ow) {
+  if (p->igemm_twin == nullptr || variant_requested() != 0 || setting_int("NHIP_WINO_TWIN", 1) == 0) return false;
+  return (int64_t)n * ceil_div(oh, 4) * ceil_div(ow, 4) <= 32;
+}
+
 uint64_t conv_winograd_f32_workspace(const nhip_conv_plan* p, int n, int oh, int ow) {
+  if (twin_selected(p, n, oh, ow)) return conv_igemm_f32_workspace(p->igemm_twin, n, oh, ow);
   const int th = (int)ceil_div(oh, 4), tw = (int)ceil_div(ow, 4);
   const int64_t t_pad = round_up((int64_t)n * th * tw, 128);
   if (fused_selected(p, n, oh, ow))  // V, then the GEMM's partial sums
@@ -310,6 +323,8 @@ int launch_conv_winograd_f32(const nhip_conv_plan* p, const float* in,
   // forced with NHIP_WINOGRAD_VARIANT)
   if (variant_requested() == 0 && kq_supported(p, n, h, w, oh, ow))
     return launch_conv_kq(p, in, residual, out, n, h, w, oh, ow, s);
+  if (twin_selected(p, n, oh, ow))
+    return launch_conv_igemm_f32(p->igemm_twin, in, residual, out, n, h, w, oh, ow, ws, ws_bytes, s);
   const bool fused = fused_selected(p, n, oh, ow);
   float* V = static_cast<float*>(ws);
   float* M = V + (int64_t)36 * ws_.c_pad * ws_.t_pad;

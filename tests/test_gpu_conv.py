@@ -177,6 +177,40 @@ def test_conv_kq_1x1_matches_oracle(case, kq, nhip_env):
     assert max_rel_err(got, exp) <= IGEMM_RTOL
 
 
+TWIN_CASES = [
+    # (n, c, h, w, k, residual): Winograd plans of 256+ input channels, launches of <= 32 tiles
+    (1, 512, 7, 7, 512, True),     # one image of ResNet-18's last stage (4 tiles)
+    (2, 256, 14, 14, 256, False),  # two images of the 256@14 stage (32 tiles)
+    (1, 256, 5, 9, 130, True),     # ragged extents, 130 output channels
+]
+
+
+@pytest.mark.parametrize("case", TWIN_CASES, ids=lambda c: "x".join(map(str, c[:5])))
+@pytest.mark.parametrize("twin", ["1", "0"])
+def test_winograd_plan_small_launch_twin(case, twin, nhip_env):
+    """A Winograd plan of 256+ input channels runs launches of at most 32
+    tiles on its implicit-GEMM twin (NHIP_WINO_TWIN=1, the default: no
+    Winograd kernel launched, the implicit GEMM's 1e-4 budget) and on the
+    Winograd kernels with the route off (=0, the Winograd budget)."""
+    nhip_env.delenv("NHIP_WINOGRAD_VARIANT", raising=False)
+    nhip_env.setenv("NHIP_WINO_TWIN", twin)
+    n, c, h, w, k, with_res = case
+    rng = np.random.default_rng(hash(case) % (2 ** 32))
+    x = rng.uniform(-1, 1, (n, c, h, w)).astype(np.float32)
+    wt = workloads.he_normal(rng, (k, c, 3, 3), c * 9)
+    b = rng.normal(0, 0.05, k).astype(np.float32)
+    res = rng.uniform(-1, 1, (n, k, h, w)).astype(np.float32) if with_res else None
+    plan = nhip.Conv2dF32(nhip.conv_desc(c, k, act=1, algorithm=nhip.ALGO_WINOGRAD), wt, b)
+    exp = oracle_conv(x, wt, b, (1, 1), (1, 1), (1, 1, 1, 1), act=1, residual=res)
+    nhip.timer_start("wino")
+    got = host(plan.forward(dev(x), residual=None if res is None else dev(res)))
+    launches = nhip.timer_stop()[0]
+    assert (launches == 0) == (twin == "1")
+    tol = IGEMM_RTOL if twin == "1" else WINO_RTOL
+    assert_close(got, exp, tol, f"twin={twin} {case}")
+    assert max_rel_err(got, exp) <= tol
+
+
 WINO_CASES = [
     # (n, c, h, w, k, pad)
     (1, 16, 4, 4, 16, (1, 1, 1, 1)),
