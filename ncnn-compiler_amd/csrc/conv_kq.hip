@@ -150,9 +150,11 @@ KqShape kq_1x1_shape(int c) {
 // Whether the kernel takes the launch: a 3x3 convolution with 32 or 64 input
 // channels (a lane's 9*C/8 weights then are whole 16-byte vectors) or a 1x1
 // one with an instantiated channel count, activation none or ReLU, and few
-// blocks.  3x3: at most two 32x32 blocks per CU on an implicit-GEMM plan, at
-// most one on a Winograd plan (one image of 64x56x56, 64 output channels: 9.7 us against 13.6 us
-// for the Winograd path and 14.6 us for the tiled implicit GEMM).  1x1: at
+// blocks.  3x3: at most two 32x32 blocks per CU, on either plan (one image
+// of 64x56x56, 64 output channels, 196 blocks: 9.7 us against 13.6 us for
+// the Winograd path and 14.6 us for the tiled implicit GEMM; two such
+// images, 392 blocks, 15.0 against 21.1 us on Winograd; at 784 blocks
+// Winograd wins with 64 channels, 25.6 against 26.5 us).  1x1: at
 // most one per CU (MobileNetV2 at batch 32, 960 -> 160 + residual at 7x7:
 // 17.0 against 21.4 us; with more blocks the tiled kernels' operand reuse
 // wins: 960 -> 320, 26.7 against 25.0 us) and at least one per eight CUs
@@ -172,7 +174,7 @@ bool kq_supported(const nhip_conv_plan* p, int n, int h, int w, int oh, int ow) 
   if (!k3 && !k1) return false;
   const int64_t npix = (int64_t)n * oh * ow;
   const int64_t blocks = ceil_div(p->g.k, 32) * ceil_div(npix, 32);
-  const int per_cu = p->algorithm == NHIP_CONV_ALGO_IMPLICIT_GEMM && k3 ? 2 : 1;
+  const int per_cu = k3 ? 2 : 1;
   if (mode != 2 && (blocks > per_cu * (int64_t)cu_count() || (k1 && blocks < cu_count() / 8))) return false;
   return (int64_t)n * g.c * h * w * 4 < INT32_MAX && npix * g.k * 4 < INT32_MAX;
 }

@@ -318,7 +318,7 @@ int launch_conv_winograd_f32(const nhip_conv_plan* p, const float* in,
   if (need > 0 && (ws == nullptr || ws_bytes < need))
     return fail(NHIP_STATUS_OUTPUT_CAPACITY_INSUFFICIENT,
                 "winograd conv: workspace of " + std::to_string(need) + " bytes required");
-  // Launches of at most one 32x32 block per CU: the one-kernel implicit
+  // Launches of at most two 32x32 blocks per CU: the one-kernel implicit
   // GEMM on the plan's row-major weights (unless a Winograd variant is
   // forced with NHIP_WINOGRAD_VARIANT)
   if (variant_requested() == 0 && kq_supported(p, n, h, w, oh, ow))
