@@ -85,7 +85,15 @@ int nhip_graph_infer_shapes(nhip_graph_t graph, const int64_t* input_shapes,
  * on; the calling thread's current device is restored afterwards.  On a
  * non-default stream, a call repeating the previous call's batch, shapes,
  * buffers and stream is recorded into a hipGraph, and later such calls
- * replay it. */
+ * replay it.
+ * A call on a stream the caller is capturing launches into the caller's
+ * graph.  Such a capture is only valid when the batch and shapes do not
+ * exceed those of a call already run on this graph: the executor's
+ * intermediate buffers cannot grow inside a capture, and the call then
+ * fails with NHIP_STATUS_CONSTRAINT_VIOLATION (launching nothing).  After a
+ * caller's capture, buffers superseded by a later, larger call are kept
+ * until nhip_graph_destroy, so the caller's graph stays replayable for the
+ * graph's lifetime. */
 int nhip_graph_run(nhip_graph_t graph, int32_t n, const int64_t* input_shapes,
                    const void* const* inputs, void* const* outputs,
                    void* stream);

@@ -656,8 +656,15 @@ struct nhip_graph {
   std::vector<const void*> exec_bufs;  // the internal buffers the recorded plan uses
   std::string seen_key;   // the previous call's key: a plan is recorded on its second call
   std::string nocap_key;  // a key whose capture failed: runs eagerly
+  // Once a call has run inside a caller's stream capture, the caller's graph
+  // may still reference the blob buffers and workspace of that call: buffers
+  // superseded by a later, larger call are kept here until destroy instead
+  // of being freed.
+  bool caller_captured = false;
+  std::vector<void*> retired;
   ~nhip_graph() {
     nhip::graph_exec_destroy(exec);
+    for (void* p : retired) nhip_free(p);
     for (auto& op : ops) {
       if (op.conv) nhip_conv_destroy(op.conv);
       if (op.ip) nhip_innerproduct_destroy(op.ip);
@@ -1233,6 +1240,29 @@ int ensure(void** buf, uint64_t* cap, uint64_t bytes) {
   return ok();
 }
 
+// Grows a blob buffer or the workspace of the executor.  Inside a stream
+// capture (the caller's or the executor's own recording) nothing may grow: a
+// hipFree or hipMalloc there would invalidate the capture, so the call fails
+// instead, naming the fix (run that batch and shape once before capturing).
+// After a caller's capture has been seen, superseded buffers are retired,
+// not freed, because the caller's graph may still replay over them.
+int grow(nhip_graph& g, void** buf, uint64_t* cap, uint64_t bytes, bool capturing) {
+  if (*cap >= bytes) return ok();
+  if (capturing)
+    return fail(NHIP_STATUS_CONSTRAINT_VIOLATION,
+                "graph_run: the stream is being captured and the executor's buffers would have to grow to " +
+                    std::to_string(bytes) + " bytes; run this batch size and these shapes once before capturing");
+  if (*buf) {
+    if (g.caller_captured) g.retired.push_back(*buf);
+    else TRY(nhip_free(*buf));
+  }
+  *buf = nullptr;
+  *cap = 0;
+  TRY(nhip_malloc(buf, bytes));
+  *cap = bytes;
+  return ok();
+}
+
 // A marked pooling -> InnerProduct pair runs fused when the pooled planes
 // fit nhip_global_avgpool_innerproduct_f32 (at most 6400 pixels).
 bool gap_ip_fusable(const nhip_graph& g, const std::vector<Shape>& sh, const Op& ip) {
@@ -1242,14 +1272,14 @@ bool gap_ip_fusable(const nhip_graph& g, const std::vector<Shape>& sh, const Op&
 }
 
 int run_ops(nhip_graph& g, int n, const std::vector<Shape>& sh, const void* const* inputs, void* const* outputs,
-            void* stream) {
+            void* stream, bool capturing) {
   std::vector<char*> ptr(g.blobs.size(), nullptr);
   // device buffers for computed blobs; the graph's inputs are the caller's
   uint64_t ws_need = 0;
   for (const Op& op : g.ops) {
     if (op.kind == OpKind::Input || op.kind == OpKind::Alias) continue;
     Blob& b = g.blobs[op.out];
-    TRY(ensure(&b.buf, &b.cap, (uint64_t)n * sh[op.out].elems() * esize(b.dtype)));
+    TRY(grow(g, &b.buf, &b.cap, (uint64_t)n * sh[op.out].elems() * esize(b.dtype), capturing));
     const Shape& a = sh[op.in[0]];
     uint64_t w = 0;
     if (op.kind == OpKind::ConvF32 || op.kind == OpKind::ConvInt8)
@@ -1265,7 +1295,7 @@ int run_ops(nhip_graph& g, int n, const std::vector<Shape>& sh, const void* cons
     }
     ws_need = std::max(ws_need, w);
   }
-  TRY(ensure(&g.ws, &g.ws_cap, std::max<uint64_t>(ws_need, 256)));
+  TRY(grow(g, &g.ws, &g.ws_cap, std::max<uint64_t>(ws_need, 256), capturing));
   for (size_t i = 0; i < g.inputs.size(); ++i) ptr[g.inputs[i]] = (char*)inputs[i];
   std::vector<char> fused(g.ops.size(), 0);  // ops folded into their consumer
   // Pooling -> InnerProduct runs fused only with NHIP_GAP_IP=1.  Measured on
@@ -1500,13 +1530,19 @@ class DeviceGuard {
 // every time stay eager and record nothing.  The legacy default stream
 // cannot be captured and runs eagerly, as do runs while the kernel timer
 // records per-launch events and runs on a stream the caller is capturing
-// itself (the launches then become part of the caller's graph);
+// itself (the launches then become part of the caller's graph; such a call
+// fails with status 3 if the executor's buffers would have to grow, and
+// from then on buffers that a larger call supersedes stay allocated until
+// the graph is destroyed, since the caller's graph may replay over them);
 // NHIP_GRAPH_REPLAY=0 turns replay off.  The graph's mutex is held.
 int run_with_replay(nhip_graph& g, int32_t n, const std::vector<Shape>& sh, const void* const* inputs,
                     void* const* outputs, void* stream) {
-  if (stream == nullptr || nhip::setting_int("NHIP_GRAPH_REPLAY", 1) == 0 || nhip::kernel_timer_active() ||
-      nhip::stream_capturing(stream))
-    return run_ops(g, n, sh, inputs, outputs, stream);
+  if (stream != nullptr && nhip::stream_capturing(stream)) {
+    g.caller_captured = true;  // from here on, superseded buffers are retired, not freed
+    return run_ops(g, n, sh, inputs, outputs, stream, true);
+  }
+  if (stream == nullptr || nhip::setting_int("NHIP_GRAPH_REPLAY", 1) == 0 || nhip::kernel_timer_active())
+    return run_ops(g, n, sh, inputs, outputs, stream, false);
   std::ostringstream key;
   key << n;
   for (int b : g.inputs) {
@@ -1532,7 +1568,7 @@ int run_with_replay(nhip_graph& g, int32_t n, const std::vector<Shape>& sh, cons
     g.exec = nullptr;
     g.exec_key.clear();
   }
-  TRY(run_ops(g, n, sh, inputs, outputs, stream));
+  TRY(run_ops(g, n, sh, inputs, outputs, stream, false));
   if (key.str() != g.seen_key || key.str() == g.nocap_key) {
     g.seen_key = key.str();
     return ok();
@@ -1542,7 +1578,7 @@ int run_with_replay(nhip_graph& g, int32_t n, const std::vector<Shape>& sh, cons
   g.exec_key.clear();
   bool recorded = false;
   if (nhip::graph_capture_begin(stream) == NHIP_STATUS_SUCCESS) {
-    const int st = run_ops(g, n, sh, inputs, outputs, stream);
+    const int st = run_ops(g, n, sh, inputs, outputs, stream, true);
     void* exec = nullptr;
     const int st2 = nhip::graph_capture_end(stream, &exec);
     if (st == NHIP_STATUS_SUCCESS && st2 == NHIP_STATUS_SUCCESS && exec) {

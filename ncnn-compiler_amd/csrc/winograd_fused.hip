@@ -512,8 +512,9 @@ __global__ __launch_bounds__(dma::kThreads, 2) void wino_fused_dma_kernel(FusedA
         read_group(slot, g + 1, (g + 1) & 1);
       } else {
         // chunk i is read (its operands are in registers): wait for this
-        // wave's copies of chunk i + 1, then the barrier hands slot i & 3
-        // back to the copies (chunk i + 4) and publishes chunk i + 1
+        // wave's copies of chunk i + 1 (vmcnt(0) here: at most one chunk is
+        // in flight), then the barrier hands slot i % kSlots back to the
+        // copies (chunk i + kSlots) and publishes chunk i + 1
         dma::wait_copies(max(0, min(dma::kSlots - 1, n - 1 - i) - 1));
         __syncthreads();
         if (i + dma::kSlots < n) issue(bk.ch_begin + i + dma::kSlots, i % dma::kSlots);

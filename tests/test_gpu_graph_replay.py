@@ -190,6 +190,69 @@ def test_calls_inside_a_callers_capture_run_eagerly_into_it(nhip_env):
     g.close()
 
 
+def test_larger_call_after_a_callers_capture_keeps_its_buffers(nhip_env):
+    """After a caller's capture at batch 2, a call at batch 4 grows the
+    executor's buffers; the buffers the caller's graph was captured with stay
+    allocated, so replaying it still gives the batch-2 result."""
+    nhip_env.delenv("NHIP_GRAPH_REPLAY", raising=False)
+    g = mobilenet_graph()
+    rng = np.random.default_rng(6)
+    xa = torch.from_numpy(rng.uniform(-1, 1, (2, 3, 224, 224)).astype(np.float32)).cuda()
+    xb = torch.from_numpy(rng.uniform(-1, 1, (4, 3, 224, 224)).astype(np.float32)).cuda()
+    ref_a = eager(g, xa, nhip_env)
+    g.close()
+    g = mobilenet_graph()
+    out_a = [torch.empty_like(ref_a)]
+    s = torch.cuda.current_stream()
+    g.run(xa, out=out_a, stream=s)  # sizes the buffers for batch 2
+    torch.cuda.synchronize()
+    cg = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(cg, stream=s):
+        g.run(xa, out=out_a, stream=s)
+    torch.cuda.synchronize()
+    out_b = g.run(xb, stream=s)  # grows every buffer past the captured ones
+    torch.cuda.synchronize()
+    ref_b = eager(mobilenet_graph(), xb, nhip_env)
+    assert torch.equal(out_b[0], ref_b)
+    for rep in range(3):
+        out_a[0].fill_(float("nan"))
+        scratch = torch.randn(1 << 22, device="cuda")  # allocations that could reuse freed memory
+        torch.cuda.synchronize()
+        cg.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out_a[0], ref_a), f"replay {rep} after the larger call"
+        del scratch
+    del cg
+    g.close()
+
+
+def test_capture_that_would_grow_buffers_fails_cleanly(nhip_env):
+    """A call inside a caller's capture on a graph whose buffers are too small
+    for it fails with status 3 and launches nothing; the capture stays valid
+    and the next call outside it runs normally."""
+    nhip_env.delenv("NHIP_GRAPH_REPLAY", raising=False)
+    g = mobilenet_graph()
+    x = torch.from_numpy(np.random.default_rng(7).uniform(-1, 1, (2, 3, 224, 224)).astype(np.float32)).cuda()
+    ref = eager(mobilenet_graph(), x, nhip_env)
+    out = [torch.empty_like(ref)]
+    s = torch.cuda.current_stream()
+    cg = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(cg, stream=s):
+        out[0].zero_()
+        with pytest.raises(nhip.NhipError) as err:
+            g.run(x, out=out, stream=s)  # never run before: every buffer would have to grow
+    assert err.value.status == 3
+    torch.cuda.synchronize()
+    cg.replay()
+    torch.cuda.synchronize()
+    assert torch.count_nonzero(out[0]) == 0
+    g.run(x, out=out, stream=s)
+    torch.cuda.synchronize()
+    assert torch.equal(out[0], ref)
+    del cg
+    g.close()
+
+
 def test_run_leaves_the_callers_current_device():
     g = mobilenet_graph()
     x = torch.zeros((1, 3, 224, 224), device="cuda")

@@ -52,8 +52,10 @@ def _noalloc(conv, x, res):
 
 
 @pytest.mark.parametrize("algo,stride,shapes", [
-    # Winograd: the fused GEMM (>= 256 tiles) then the three-kernel path
-    (nhip.ALGO_WINOGRAD, 1, [(8, 64, 56, 56), (2, 64, 20, 20)]),
+    # Winograd: the fused GEMM (392 tiles) then the three-kernel path (50
+    # tiles; 128 input channels keep it off the one-kernel 32/64-channel
+    # route, and below 256 channels there is no implicit-GEMM twin)
+    (nhip.ALGO_WINOGRAD, 1, [(8, 128, 28, 28), (2, 128, 20, 20)]),
     # implicit GEMM (3x3 stride 2), split-K partial sums in the scratch
     (nhip.ALGO_IMPLICIT_GEMM, 2, [(4, 256, 28, 28), (1, 256, 14, 14)]),
 ])
