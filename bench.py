@@ -204,10 +204,10 @@ def run_step(stages):
 
 
 def fused_stage(c, hw):
-    """The library's default Winograd path choice: the fused GEMM from 256
+    """The library's default Winograd path choice: the fused GEMM from 128
     tiles up (winograd.hip, fused_selected)."""
     t = -(-hw // 4)
-    return BATCH * t * t >= 256
+    return BATCH * t * t >= 128
 
 
 def measured_traffic(kernel):

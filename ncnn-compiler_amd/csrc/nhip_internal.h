@@ -164,9 +164,9 @@ struct nhip_conv_plan {
   // implicit GEMM fp32: weights [m_pad][kred_pad], k = (c, kh, kw) order;
   // Winograd: weights U[36][m_pad][c_pad].
   float* weight = nullptr;
-  // Winograd, fused kernel: the same U blocked by 8 channels in channel
-  // pairs, [c_pad/8][36][4][m_pad][2], so one chunk's slice for 32 output
-  // channels is four contiguous 256-byte runs per transform point.
+  // Winograd, fused kernel: the same U in 4-channel groups,
+  // [36][c_pad/4][m_pad][4], so 32 output channels of one group are 512
+  // contiguous bytes per transform point.
   float* weight_fused = nullptr;
   // Winograd plans of 32 or 64 input channels: the weights also row-major,
   // [m_pad][rows_ld] with k = c*9 + kh*3 + kw, for the one-kernel path of

@@ -33,8 +33,7 @@ uint64_t wino_gemm_out_parts_bytes(const nhip_conv_plan* p, int n, int oh, int o
 // (winograd_fused.hip), or the three-kernel path (M through HBM).
 // NHIP_WINOGRAD_VARIANT = 1 forces the three-kernel path, 2 the fused GEMM
 // (where its limits allow); unset or 0 chooses by shape: the fused GEMM from
-// 256 tiles up (on MI355X it measures faster there; with fewer tiles its
-// channel-split partial sums cost more than the M round trip saves).
+// 128 tiles up (four 32-tile blocks; below that the three-kernel path).
 static int variant_requested() {
   return setting_int("NHIP_WINOGRAD_VARIANT", 0);
 }
@@ -46,7 +45,7 @@ static bool fused_selected(const nhip_conv_plan* p, int n, int oh, int ow) {
   const int v = variant_requested();
   if (v == 1) return false;
   if (v == 2) return true;
-  return (int64_t)n * ceil_div(oh, 4) * ceil_div(ow, 4) >= 256;
+  return (int64_t)n * ceil_div(oh, 4) * ceil_div(ow, 4) >= 128;
 }
 
 namespace {
@@ -137,14 +136,14 @@ __device__ __forceinline__ void wino_in_patch(__amdgpu_buffer_rsrc_t rs, bool ok
 
 // Thread (c, t): the 6x6 transform of the zero-padded patch of channel c,
 // tile t.  Layouts:
-//   PAIRS  V[xi][c_pad/2][t_pad][2] (the fused GEMM's channel pairs); the two
-//          channels of a pair are neighbouring lanes, so a wave's stores for
-//          one point cover 256 contiguous bytes;
+//   QUADS  V[xi][c_pad/4][t_pad][4] (the fused GEMM's 4-channel groups); the
+//          four channels of a group are neighbouring lanes, so a wave's
+//          stores for one point cover 256 contiguous bytes;
 //   else   V[xi][c_pad][t_pad].
 // VEC (left padding 1, W % 4 == 0, 16-byte aligned input): columns 1..4 of a
 // patch row are the aligned run x = 4*tx .. +3, wholly inside the row or
 // wholly past its end, loaded as one 16-byte vector.
-template <bool PAIRS, bool VEC>
+template <bool QUADS, bool VEC>
 __global__ __launch_bounds__(256) void wino_input_transform(
     const float* __restrict__ x, uint32_t x_bytes, float* __restrict__ V, int C, int H, int W,
     int th, int tw, int T, int t_pad, int c_pad, int pt, int pl) {
@@ -154,13 +153,13 @@ __global__ __launch_bounds__(256) void wino_input_transform(
   const int64_t rem = idx;
   int c, t;
   float* vout;
-  if constexpr (PAIRS) {
-    const int e = (int)(rem & 1);
-    const int64_t q = rem >> 1;
-    const int cp = (int)(q / t_pad);
-    t = (int)(q - (int64_t)cp * t_pad);
-    c = 2 * cp + e;
-    vout = V + ((int64_t)cp * t_pad + t) * 2 + e;
+  if constexpr (QUADS) {
+    const int e = (int)(rem & 3);
+    const int64_t q = rem >> 2;
+    const int cq = (int)(q / t_pad);
+    t = (int)(q - (int64_t)cq * t_pad);
+    c = 4 * cq + e;
+    vout = V + ((int64_t)cq * t_pad + t) * 4 + e;
   } else {
     c = (int)(rem / t_pad);
     t = (int)(rem - (int64_t)c * t_pad);
@@ -248,8 +247,8 @@ __global__ __launch_bounds__(256) void wino_output_transform(
 }  // namespace
 
 // U[xi][k][c] = (G g_kc G^T)[xi], computed in double, stored fp32 with zero
-// padding to [36][m_pad][c_pad], and again blocked for the fused kernel as
-// [c_pad/8][36][4][m_pad][2] (channel c = 8*chunk + 2*pair + s).
+// padding to [36][m_pad][c_pad], and again in 4-channel groups for the fused
+// kernel as [36][c_pad/4][m_pad][4].
 int winograd_prepack_weights(nhip_conv_plan* p, const float* weight) {
   static const double G[6][3] = {
       {1.0 / 4, 0, 0},
@@ -277,11 +276,11 @@ int winograd_prepack_weights(nhip_conv_plan* p, const float* weight) {
   for (int xi = 0; xi < 36; ++xi)
     for (int k = 0; k < p->m_pad; ++k)
       for (int c = 0; c < p->c_pad; ++c)
-        Uf[((((size_t)(c / 8) * 36 + xi) * 4 + (c % 8) / 2) * p->m_pad + k) * 2 + c % 2] =
+        Uf[(((size_t)xi * (p->c_pad / 4) + c / 4) * p->m_pad + k) * 4 + c % 4] =
             U[((size_t)xi * p->m_pad + k) * p->c_pad + c];
-  NHIP_TRY(check_hip(hipMalloc(&p->weight_fused, Uf.size() * sizeof(float)), "hipMalloc(winograd U, blocked)"));
+  NHIP_TRY(check_hip(hipMalloc(&p->weight_fused, Uf.size() * sizeof(float)), "hipMalloc(winograd U, 4-channel groups)"));
   NHIP_TRY(check_hip(hipMemcpy(p->weight_fused, Uf.data(), Uf.size() * sizeof(float), hipMemcpyHostToDevice),
-                     "hipMemcpy(winograd U, blocked)"));
+                     "hipMemcpy(winograd U, 4-channel groups)"));
   NHIP_TRY(check_hip(hipMalloc(&p->weight, U.size() * sizeof(float)), "hipMalloc(winograd U)"));
   return check_hip(hipMemcpy(p->weight, U.data(), U.size() * sizeof(float), hipMemcpyHostToDevice),
                    "hipMemcpy(winograd U)");

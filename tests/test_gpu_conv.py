@@ -228,18 +228,23 @@ WINO_CASES = [
 ]
 
 
-@pytest.fixture(params=["auto", "1", "2", "2dma"])
+@pytest.fixture(params=["auto", "1", "2", "2split", "2ks"])
 def wino_variant(request, nhip_env):
     """Winograd implementations: the default per-shape choice (auto), the
     three-kernel path (1), the GEMM with the output transform fused (2) with
-    its register-staged kernel, and the same with the LDS-DMA kernel
-    (2dma)."""
+    each workgroup's halves taking alternate input-channel chunks of one
+    32-channel block, the same with the input channels split over two
+    workgroups per block and the parts summed by the reduce kernel
+    (2split), and the halves owning two 32-channel blocks (2ks)."""
+    nhip_env.delenv("NHIP_WINO_SPLITS", raising=False)
+    nhip_env.setenv("NHIP_WINO_KS", "1" if request.param == "2ks" else "0")
     if request.param == "auto":
         nhip_env.delenv("NHIP_WINOGRAD_VARIANT", raising=False)
-        nhip_env.delenv("NHIP_WINO_FUSED", raising=False)
+        nhip_env.delenv("NHIP_WINO_KS", raising=False)
     else:
-        nhip_env.setenv("NHIP_WINO_FUSED", "dma" if request.param == "2dma" else "reg")
         nhip_env.setenv("NHIP_WINOGRAD_VARIANT", request.param[0])
+        if request.param == "2split":
+            nhip_env.setenv("NHIP_WINO_SPLITS", "2")
     return request.param
 
 
@@ -274,11 +279,13 @@ def _random_wino_cases(count, seed):
     return cases
 
 
-@pytest.mark.parametrize("kernel", ["reg", "dma"])
+@pytest.mark.parametrize("mode", ["1", "4", "ks"])
 @pytest.mark.parametrize("case", _random_wino_cases(16, 7), ids=lambda c: "x".join(map(str, c[:5])))
-def test_winograd_fused_random_shapes(case, kernel, nhip_env):
+def test_winograd_fused_random_shapes(case, mode, nhip_env):
     nhip_env.setenv("NHIP_WINOGRAD_VARIANT", "2")  # the fused GEMM whatever the tile count
-    nhip_env.setenv("NHIP_WINO_FUSED", kernel)  # register-staged or LDS-DMA kernel
+    # one part, up to four channel splits + reduce, or workgroups of two channel blocks
+    nhip_env.setenv("NHIP_WINO_SPLITS", "1" if mode == "ks" else mode)
+    nhip_env.setenv("NHIP_WINO_KS", "1" if mode == "ks" else "0")
     n, c, h, w, k, pad, with_res = case
     rng = np.random.default_rng(hash(case) % (2 ** 32))
     x = rng.uniform(-1, 1, (n, c, h, w)).astype(np.float32)
@@ -359,12 +366,15 @@ def test_resnet_stage_full_batch(stage, nhip_env):
         assert_close(igemm[i:i + 1], exp[i:i + 1], IGEMM_RTOL, f"igemm image {i}")
 
 
-@pytest.mark.parametrize("variant", ["2", "1", "2dma"])
-def test_batch_is_independent_images(variant, nhip_env):  # 1 = three-kernel path, 2 = fused (2dma: LDS-DMA kernel)
+@pytest.mark.parametrize("variant", ["2", "1", "2split"])
+def test_batch_is_independent_images(variant, nhip_env):  # 1 = three-kernel path, 2 = fused (2split: channel splits)
     """The [N,C,H,W] batch equals N single-image calls (the reference ABI),
     bit for bit for a fixed kernel variant."""
     nhip_env.setenv("NHIP_WINOGRAD_VARIANT", variant[0])
-    nhip_env.setenv("NHIP_WINO_FUSED", "dma" if variant == "2dma" else "reg")
+    if variant == "2split":
+        nhip_env.setenv("NHIP_WINO_SPLITS", "2")
+    else:
+        nhip_env.delenv("NHIP_WINO_SPLITS", raising=False)
     c, k = 32, 32
     x = RNG.uniform(-1, 1, (4, c, 10, 10)).astype(np.float32)
     wt = workloads.he_normal(RNG, (k, c, 3, 3), c * 9)
