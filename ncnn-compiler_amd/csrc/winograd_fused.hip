@@ -27,7 +27,8 @@
 // Output transform.  Y = A^T M A is applied along q inside each wave,
 // Z_h[p][b] = sum_q M[p][q] A[q][b] (4 values per (channel, tile) pair),
 // then along p across the waves: Z goes through LDS (per round of 16
-// channels: 2 halves x 512 pairs x 6 rows x 4 floats, 96 KB) and thread
+// channels: 2 halves x 512 pairs x 6 rows x 4 floats, 112 KB with the
+// records padded against bank conflicts) and thread
 // tid < 512 of the workgroup sums the two halves and finishes its pair:
 // Y[a][b] = sum_p A^T[a][p] Z[p][b], + bias (+ residual), activation, four
 // row stores.
@@ -52,7 +53,11 @@ constexpr int kTB = 32;             // tiles per block
 constexpr int kKB = 32;             // output channels per block
 constexpr int kCB = 8;              // input channels per chunk
 constexpr int kPairs = kTB * kKB / 2;  // (channel, tile) pairs per epilogue round
-constexpr int kLdsBytes = 2 * kPairs * 24 * (int)sizeof(float);  // Z of both halves, 96 KB
+// Z record of one pair: 6 rows x 4 floats, padded to 28 floats so that the
+// 16-byte accesses of 16 consecutive lanes (records 112 bytes apart) fall on
+// distinct LDS banks.
+constexpr int kZRec = 28;
+constexpr int kLdsBytes = 2 * kPairs * kZRec * (int)sizeof(float);  // Z of both halves, 112 KB
 constexpr int kXcds = 8;            // MI355X: workgroup L runs on XCD L % 8
 
 struct FusedArgs {
@@ -108,36 +113,6 @@ __global__ __launch_bounds__(kThreads, 1) void wino_fused_kernel(FusedArgs a) {
   // KS with an odd number of 32-channel blocks: the last half has none
   const bool kvalid = k0 < a.m_pad;
 
-  // This thread's epilogue pairs (tid < 512): tile t0 + tid % 32 and, per
-  // round rr, channel kbase + tid / 32 + 16 rr (+ 32 for the second half's
-  // pair with KS).
-  const int OHW = a.OH * a.OW;
-  const bool own = tid < kPairs;
-  const int kk = kbase + ((tid >> 5) & 15), tt = t0 + (tid & 31);
-  const bool live_t = own && tt < a.T;
-  constexpr int NQ = KS ? 2 : 1;  // pairs per thread and round
-  int obase = 0, rows = 0, cols = 0;
-  float bias_r[2][NQ];
-#pragma unroll
-  for (int rr = 0; rr < 2; ++rr)
-#pragma unroll
-    for (int e = 0; e < NQ; ++e) bias_r[rr][e] = 0.f;
-  if (live_t) {
-    const int per_img = a.th * a.tw;
-    const int img = tt / per_img, rem = tt - img * per_img;
-    const int ty = rem / a.tw, tx = rem - ty * a.tw;
-    obase = (img * a.K + kk) * OHW + 4 * ty * a.OW + 4 * tx;
-    rows = min(4, a.OH - 4 * ty);
-    cols = min(4, a.OW - 4 * tx);
-    if (FINAL) {
-#pragma unroll
-      for (int rr = 0; rr < 2; ++rr)
-#pragma unroll
-        for (int e = 0; e < NQ; ++e)  // m_pad entries, zero past K
-          bias_r[rr][e] = kk + 16 * rr + 32 * e < a.m_pad ? a.bias[kk + 16 * rr + 32 * e] : 0.f;
-    }
-  }
-
   // Operand addressing: byte offsets, lane part in the per-lane offset,
   // the rest (point, chunk, block) in the scalar offset.
   const __amdgpu_buffer_rsrc_t ur = make_rsrc(a.U, a.u_bytes), vr = make_rsrc(a.V, a.v_bytes);
@@ -187,6 +162,38 @@ __global__ __launch_bounds__(kThreads, 1) void wino_fused_kernel(FusedArgs a) {
   for (int q = 0; q < 6; ++q) load(c, q);
 #pragma unroll
   for (int q = 0; q < 6; ++q) __builtin_amdgcn_sched_group_barrier(0x020, 2, 0);
+
+  // This thread's epilogue pairs (tid < 512), set up while the first
+  // chunk's operands are in flight: tile t0 + tid % 32 and, per
+  // round rr, channel kbase + tid / 32 + 16 rr (+ 32 for the second half's
+  // pair with KS).
+  const int OHW = a.OH * a.OW;
+  const bool own = tid < kPairs;
+  const int kk = kbase + ((tid >> 5) & 15), tt = t0 + (tid & 31);
+  const bool live_t = own && tt < a.T;
+  constexpr int NQ = KS ? 2 : 1;  // pairs per thread and round
+  int obase = 0, rows = 0, cols = 0;
+  float bias_r[2][NQ];
+#pragma unroll
+  for (int rr = 0; rr < 2; ++rr)
+#pragma unroll
+    for (int e = 0; e < NQ; ++e) bias_r[rr][e] = 0.f;
+  if (live_t) {
+    const int per_img = a.th * a.tw;
+    const int img = tt / per_img, rem = tt - img * per_img;
+    const int ty = rem / a.tw, tx = rem - ty * a.tw;
+    obase = (img * a.K + kk) * OHW + 4 * ty * a.OW + 4 * tx;
+    rows = min(4, a.OH - 4 * ty);
+    cols = min(4, a.OW - 4 * tx);
+    if (FINAL) {
+#pragma unroll
+      for (int rr = 0; rr < 2; ++rr)
+#pragma unroll
+        for (int e = 0; e < NQ; ++e)  // m_pad entries, zero past K
+          bias_r[rr][e] = kk + 16 * rr + 32 * e < a.m_pad ? a.bias[kk + 16 * rr + 32 * e] : 0.f;
+    }
+  }
+
   // The first chunk is peeled, so the loop is entered with the loads in
   // flight in the loop's own order: the compiler's wait counts at the loop
   // head are then exact (vmcnt(10) before each point) rather than vmcnt(0).
@@ -197,6 +204,17 @@ __global__ __launch_bounds__(kThreads, 1) void wino_fused_kernel(FusedArgs a) {
 
   const int tl = lane & 31, hi = lane >> 5;
   float* dst_part = a.out + (FINAL ? 0 : (int64_t)s * a.part_stride);
+  // Z_h[p][.] of accumulator register r: (sum_q M[p][q] A[q][b]) for b = 0..3.
+  auto zrow = [&](int r) {
+    const float m0 = acc[0][r], m1 = acc[1][r], m2 = acc[2][r], m3 = acc[3][r], m4 = acc[4][r], m5 = acc[5][r];
+    const float s12 = m1 + m2, d12 = m1 - m2, s34 = m3 + m4, d34 = m3 - m4;
+    return v4f{m0 + s12 + s34, d12 + 2.f * d34, s12 + 4.f * s34, d12 + 8.f * d34 + m5};
+  };
+  // Round 1's Z are computed here, before the first barrier, while the
+  // workgroup's slower waves are still in their loops.
+  v4f z_late[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) z_late[j] = zrow(8 + j);
 #pragma unroll
   for (int rr = 0; rr < 2; ++rr) {
     // Residual rows of this round's pairs, requested before the exchange.
@@ -223,10 +241,7 @@ __global__ __launch_bounds__(kThreads, 1) void wino_fused_kernel(FusedArgs a) {
     for (int j = 0; j < 8; ++j) {
       const int r = 8 * rr + j;
       const int row = (r & 3) + 8 * ((r >> 2) & 1) + 4 * hi;  // channel within the round's 16
-      const float m0 = acc[0][r], m1 = acc[1][r], m2 = acc[2][r], m3 = acc[3][r], m4 = acc[4][r], m5 = acc[5][r];
-      const float s12 = m1 + m2, d12 = m1 - m2, s34 = m3 + m4, d34 = m3 - m4;
-      *reinterpret_cast<v4f*>(zs + ((h * kPairs + row * 32 + tl) * 6 + p) * 4) =
-          v4f{m0 + s12 + s34, d12 + 2.f * d34, s12 + 4.f * s34, d12 + 8.f * d34 + m5};
+      *reinterpret_cast<v4f*>(zs + (h * kPairs + row * 32 + tl) * kZRec + p * 4) = rr ? z_late[j] : zrow(j);
     }
     __syncthreads();
 #pragma unroll
@@ -237,12 +252,12 @@ __global__ __launch_bounds__(kThreads, 1) void wino_fused_kernel(FusedArgs a) {
 #pragma unroll
       for (int pp = 0; pp < 6; ++pp) {
         if (KS) {  // the pair of half e
-          const v4f z0 = *reinterpret_cast<const v4f*>(zs + ((e * kPairs + tid) * 6 + pp) * 4);
+          const v4f z0 = *reinterpret_cast<const v4f*>(zs + (e * kPairs + tid) * kZRec + pp * 4);
 #pragma unroll
           for (int j = 0; j < 4; ++j) z[pp][j] = z0[j];
         } else {  // the two halves' partial sums of one pair
-          const v4f z0 = *reinterpret_cast<const v4f*>(zs + (tid * 6 + pp) * 4);
-          const v4f z1 = *reinterpret_cast<const v4f*>(zs + ((kPairs + tid) * 6 + pp) * 4);
+          const v4f z0 = *reinterpret_cast<const v4f*>(zs + tid * kZRec + pp * 4);
+          const v4f z1 = *reinterpret_cast<const v4f*>(zs + (kPairs + tid) * kZRec + pp * 4);
 #pragma unroll
           for (int j = 0; j < 4; ++j) z[pp][j] = z0[j] + z1[j];
         }

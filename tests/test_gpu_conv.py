@@ -282,9 +282,10 @@ def _random_wino_cases(count, seed):
 @pytest.mark.parametrize("mode", ["1", "4", "ks"])
 @pytest.mark.parametrize("case", _random_wino_cases(16, 7), ids=lambda c: "x".join(map(str, c[:5])))
 def test_winograd_fused_random_shapes(case, mode, nhip_env):
+    """Modes: one part; up to four input-channel splits summed by the
+    reduce kernel (4); workgroups of two 32-channel blocks (ks)."""
     nhip_env.setenv("NHIP_WINOGRAD_VARIANT", "2")  # the fused GEMM whatever the tile count
-    # one part, up to four channel splits + reduce, or workgroups of two channel blocks
-    nhip_env.setenv("NHIP_WINO_SPLITS", "1" if mode == "ks" else mode)
+    nhip_env.setenv("NHIP_WINO_SPLITS", mode[0] if mode != "ks" else "1")
     nhip_env.setenv("NHIP_WINO_KS", "1" if mode == "ks" else "0")
     n, c, h, w, k, pad, with_res = case
     rng = np.random.default_rng(hash(case) % (2 ** 32))
