@@ -31,7 +31,9 @@ roofline: the dominant kernel's algorithmic work per launch over its average
 duration.  For config 3 that is the Winograd GEMM with the output transform
 fused (wino_fused: executed FLOPs 2*36*T*C*K per launch, T tiles); traffic =
 its HBM bytes per launch from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE
-summary (profiles/wino_fused_traffic.json, copy-calibrated).
+summary (profiles/wino_fused_traffic.json, copy-calibrated), null when that
+summary was taken on another version of the kernel's source.  For config 5
+it is the streaming 1x1 kernel (pw_conv_f32) inside the graph, HBM-bound.
 
 cpu_baseline: the CPU oracle (a restatement of the reference's lowered loop
 nests, compiled like the reference's .so: -O3, no -march, no FP contraction,
@@ -210,14 +212,27 @@ def fused_stage(c, hw):
     return BATCH * t * t >= 128
 
 
+KERNEL_SOURCES = {"wino_fused": "ncnn-compiler_amd/csrc/winograd_fused.hip"}
+
+
+def source_sha256(kernel):
+    import hashlib
+    with open(os.path.join(ROOT, KERNEL_SOURCES[kernel]), "rb") as f:
+        return hashlib.sha256(f.read()).hexdigest()
+
+
 def measured_traffic(kernel):
     """HBM bytes per launch of `kernel`, from the committed rocprofv3
     FETCH_SIZE / WRITE_SIZE summary (profiles/<kernel>_traffic.json, averaged
-    over the stage shapes it runs, copy-calibrated); None if absent."""
+    over the stage shapes it runs, copy-calibrated); None if absent or if it
+    was measured on another version of the kernel's source (the summary
+    records the SHA-256 of the source file it was taken with)."""
     try:
         with open(os.path.join(ROOT, "profiles", f"{kernel}_traffic.json")) as f:
             d = json.load(f)
-        return int(d["bytes_per_launch"]) if d.get("kernel") == kernel else None
+        if d.get("kernel") != kernel or d.get("source_sha256") != source_sha256(kernel):
+            return None
+        return int(d["bytes_per_launch"])
     except (OSError, ValueError, KeyError):
         return None
 
@@ -366,6 +381,50 @@ def config4(nhip, workloads, torch, steps, warmup, share, cpu, target_s):
 
 
 # ------------------------------------------------------------ config 5
+def pw_kernel_layers(nhip, torch, layers, batch, name="pw_conv_f32"):
+    """The graph's 1x1 layers that run on the streaming 1x1 kernel: 1x1
+    convolutions not fused with a depthwise producer (a fused pair runs as
+    dwpw_fused_f32), each routed once through the layer ABI with the launch
+    timer on `name`.  Returns (launches, algorithmic HBM bytes) per graph
+    run: every such layer reads its input, weights and bias (and residual)
+    once and writes its output once."""
+    shapes = {"data": (3, 224, 224)}
+    producer = {}
+    launches, nbytes = 0, 0.0
+    for L in layers:
+        if L["kind"] not in ("conv", "dw"):
+            continue
+        c, h, w = shapes[L["src"]]
+        ker = L.get("kernel", 3)
+        pad = L.get("pad", 1)
+        oh, ow = (h + 2 * pad - ker) // L["stride"] + 1, (w + 2 * pad - ker) // L["stride"] + 1
+        k = L["k"] if L["kind"] == "conv" else L["c"]
+        shapes[L["dst"]] = (k, oh, ow)
+        producer[L["dst"]] = L
+        if L["kind"] != "conv" or ker != 1:
+            continue
+        pw = nhip.Conv2dF32(nhip.conv_desc(c, k, kernel=(1, 1), pad=(0, 0, 0, 0), act=L["act"]), L["w"], L["b"])
+        src = producer.get(L["src"])
+        if src is not None and src["kind"] == "dw" and not L.get("residual") == src["dst"]:
+            sc, sh, sw = shapes[src["src"]]
+            dw = nhip.DwConv2dF32(nhip.conv_desc(sc, sc, stride=(src["stride"],) * 2, act=src["act"], group=sc),
+                                  src["w"], src["b"])
+            if nhip.dwconv_pw_supported(dw, pw, batch, sh, sw):
+                continue
+        x = torch.zeros((batch, c, h, w), device="cuda")
+        res = torch.zeros((batch, k, oh, ow), device="cuda") if L.get("residual") else None
+        nhip.timer_start(name)
+        pw.forward(x, residual=res)
+        torch.cuda.synchronize()
+        n, _ = nhip.timer_stop()
+        if n:
+            launches += n
+            nbytes += 4.0 * (batch * c * h * w + L["w"].size + L["b"].size + batch * k * oh * ow
+                             * (2 if L.get("residual") else 1))
+        del x, res
+    return launches, nbytes
+
+
 def config5(nhip, torch, steps, warmup, workdir, share, cpu, target_s):
     import numpy as np
 
@@ -399,11 +458,18 @@ def config5(nhip, torch, steps, warmup, workdir, share, cpu, target_s):
     best = min(res["eager"]["ms_per_step"], res["replay"]["ms_per_step"]) / 1e3
     res["ms_per_step"] = best * 1e3
     res["images_per_sec"] = BATCH / best
-    res["roofline"] = {"bound": "hbm", "kernel": "whole graph (layer-by-layer algorithmic bytes: every layer reads "
-                                                 "its input and weights once and writes its output once)",
-                       "achieved": round(gbytes / best / 1e9, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                       "frac": round(gbytes / best / 1e9 / PEAK_HBM_GBS, 4), "traffic": None,
-                       "bytes_per_step": int(gbytes)}
+    res["graph_bytes"] = {"what": "layer-by-layer algorithmic bytes of the whole graph over the best step time",
+                          "bytes_per_step": int(gbytes), "achieved_gbs": round(gbytes / best / 1e9, 1),
+                          "frac_hbm_peak": round(gbytes / best / 1e9 / PEAK_HBM_GBS, 4)}
+    # dominant kernel: the streaming 1x1 kernel (expand / project layers),
+    # timed inside the graph (eager: the timer's events need eager launches)
+    pw_launches, pw_bytes = pw_kernel_layers(nhip, torch, layers, BATCH)
+    per, sec = kernel_time(nhip, torch, lambda: g.run(x, out=out), steps, "pw_conv_f32")
+    assert round(per) == pw_launches, (per, pw_launches)
+    res["roofline"] = roofline("hbm", "pw_conv_f32 (streaming 1x1 convolution: the expand and project layers not "
+                                      "fused with their depthwise; bytes = each layer's input, weights, output "
+                                      "(+ residual) once)", pw_bytes / per, sec, per)
+    res["roofline"]["step_share"] = round(per * sec / best, 4)
     lib = compile_model(m, "mbv2", workdir)
     if lib is not None:
         lib.mbv2.argtypes = [ctypes.c_void_p, ctypes.c_void_p]

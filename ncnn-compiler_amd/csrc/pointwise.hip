@@ -546,7 +546,7 @@ template <int KT, int ACT, bool RES, int WC, bool SCALAR, int DW>
 int launch_one(const PwArgs& a, int slices, size_t lds, hipStream_t s) {
   const auto kernel = pw_conv_kernel<KT, ACT, RES, WC, SCALAR, DW>;
   NHIP_TRY(ensure_dynamic_lds(reinterpret_cast<const void*>(kernel), kMaxLds));
-  NHIP_LAUNCH(DW ? "dwpw_conv_f32" : "pw_conv_f32", kernel, pw_grid(kernel, a, slices, lds), dim3(kThreads), lds,
+  NHIP_LAUNCH(DW ? "dwpw_fused_f32" : "pw_conv_f32", kernel, pw_grid(kernel, a, slices, lds), dim3(kThreads), lds,
               s, a);
   return check_launch("pw_conv_f32");
 }
