@@ -329,11 +329,16 @@ def config2(nhip, workloads, torch, steps, warmup, share, cpu, target_s):
     n = max(steps * 10, 100)
     dt = timed(torch, fn, n)
     flops = 2.0 * 256 * 1000 * 2048
+    # the one-workgroup-per-32x32-block kernel (reduction over the 16 waves
+    # of the workgroup, summed in LDS) when it takes the shape, else the tiled
+    # GEMM with split-K partials and a reduce launch
+    kq, _ = kernel_time(nhip, torch, fn, 2, "innerproduct_f32_kq", required=False)
     per, sec = kernel_time(nhip, torch, fn, n, "innerproduct_f32")
+    what = ("innerproduct_f32_kq (one workgroup per 32x32 output block, the 2048-long reduction over its 16 waves)"
+            if kq else "innerproduct_f32 (MFMA GEMM fed by direct-to-LDS loads, split-K partials)")
     res = {"workload": "InnerProduct fp32 256x2048 -> 1000 + bias (device buffers)",
            "ms_per_step": dt * 1e3, "tflops": flops / dt / 1e12,
-           "roofline": roofline("mfma", "innerproduct_f32 (MFMA GEMM fed by direct-to-LDS loads, split-K partials)",
-                                flops / per, sec, per)}
+           "roofline": roofline("mfma", what, flops / per, sec, per)}
     if cpu:
         from oracle import refcpu
         res["cpu_baseline"] = cpu_pair(lambda t: refcpu.innerproduct_f32(x, w, b, threads=t), flops / 1e12,

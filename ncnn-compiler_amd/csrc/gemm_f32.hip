@@ -696,6 +696,7 @@ int launch_gap_innerproduct_f32(const nhip_ip_plan* p, const float* in, float* o
 int launch_innerproduct_f32(const nhip_ip_plan* p, const float* in,
                             float* out, int m, void* ws, uint64_t ws_bytes,
                             hipStream_t s) {
+  if (ip_kq_supported(p, in, m)) return launch_ip_kq(p, in, out, m, s);
   if (ip_dma_supported(p, in, m)) return launch_innerproduct_dma(p, in, out, m, ws, ws_bytes, s);
   GemmArgs g{};
   g.a = in;

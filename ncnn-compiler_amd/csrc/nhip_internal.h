@@ -201,6 +201,10 @@ struct nhip_ip_plan {
   int32_t n_pad, k_pad;
   float* weight = nullptr;  // [n_pad][k_pad]
   float* bias = nullptr;    // [n_pad], zero past n_out
+  // The same weights in 4-k groups for the one-block-per-workgroup kernel
+  // (ip_kq.hip): [n_pad/32][k_kq/4][32][4], k_kq = k_in rounded up to 256;
+  // null for reductions beyond that kernel's range.
+  float* weight_kq = nullptr;
   // int8 InnerProduct: a 1x1 int8 convolution over m one-pixel images
   nhip_conv_plan* q8 = nullptr;
 };
@@ -256,6 +260,11 @@ int launch_innerproduct_f32(const nhip_ip_plan* p, const float* in,
                             float* out, int m, void* ws, uint64_t ws_bytes,
                             hipStream_t s);
 uint64_t innerproduct_workspace(const nhip_ip_plan* p, int m);
+// ip_kq.hip: one workgroup per 32 x 32 output block, the reduction split
+// over its 16 waves and summed in LDS (no workspace).
+int ip_kq_prepack(nhip_ip_plan* p, const float* weight);
+bool ip_kq_supported(const nhip_ip_plan* p, const float* in, int m);
+int launch_ip_kq(const nhip_ip_plan* p, const float* in, float* out, int m, hipStream_t s);
 // fp32 GEMMs fed by direct-to-LDS loads (gemm_dma.hip): the InnerProduct
 // and the 1x1 stride-1 unpadded convolution.  `in` may be null for the
 // workspace query (alignment is then not part of the answer).

@@ -902,10 +902,12 @@ int nhip_innerproduct_f32_create(int32_t num_output, int32_t num_input, const fl
   if (bias) std::copy(bias, bias + num_output, bv.begin());
   int st = upload(&p->weight, wp, "hipMalloc(ip weight)");
   if (st == NHIP_STATUS_SUCCESS) st = upload(&p->bias, bv, "hipMalloc(ip bias)");
+  if (st == NHIP_STATUS_SUCCESS) st = ip_kq_prepack(p, weight);
   if (st != NHIP_STATUS_SUCCESS) {
     std::string msg = g_last_error;
     (void)hipFree(p->weight);
     (void)hipFree(p->bias);
+    (void)hipFree(p->weight_kq);
     delete p;
     return fail(st, msg);
   }
@@ -1007,6 +1009,7 @@ int nhip_innerproduct_destroy(nhip_ip_t p) {
     if (p->q8) free_plan(p->q8);
     (void)hipFree(p->weight);
     (void)hipFree(p->bias);
+    (void)hipFree(p->weight_kq);
     delete p;
   }
   return ok();

@@ -44,10 +44,15 @@ def set_dma(env, mode):
     (7, 132, 65, 1),        # k not a multiple of 32, n past one tile
     (70, 2052, 3, 0),       # two row tiles, long reduction, 3 outputs
     (130, 36, 200, 1),      # three row tiles, one stage
+    (300, 1000, 130, 1),    # reduction not a multiple of 256, ragged blocks
 ])
-@pytest.mark.parametrize("dma", ["1", "128", "0"])
+@pytest.mark.parametrize("dma", ["kq", "1", "128", "0"])
 def test_innerproduct(m, k, n, act, dma, nhip_env):
-    set_dma(nhip_env, dma)
+    """Mode "kq" forces the one-workgroup-per-block kernel (csrc/ip_kq.hip,
+    reductions up to 2048; longer ones fall back to the tiled GEMMs); the
+    other modes switch it off."""
+    nhip_env.setenv("NHIP_IP_KQ", "1" if dma == "kq" else "0")
+    set_dma(nhip_env, "1" if dma == "kq" else dma)
     x = RNG.uniform(-1, 1, (m, k)).astype(np.float32)
     w = (RNG.standard_normal((n, k)) / np.sqrt(k)).astype(np.float32)
     b = RNG.normal(0, 0.01, n).astype(np.float32)
