@@ -8,16 +8,19 @@
 // implicit GEMM (reference ConvertConvolution, NCNNToTosa.cpp:1316-1529).
 //
 // A workgroup owns one 32x32 block of (output channel, output pixel) and
-// splits the reduction over its WAVES waves: k = c*TAPS + kh*3 + kw (the
-// plan's weight order), lane half h of wave w takes input channels
-// (2w + h)*CH .. + CH - 1 with all their taps (C = 2*WAVES*CH), so every k
-// step of a lane is one (channel, tap) pair known at compile time.  Each
-// lane loads its TAPS*CH weights (one contiguous row segment, 16-byte loads)
-// and its pixel's TAPS*CH input values (zero padding through out-of-range
-// buffer offsets; the channel plane offset is wave-uniform) into registers
-// before the first v_mfma_f32_32x32x2_f32, so a wave waits once; the partial
-// blocks are summed through LDS in wave order (deterministic), then bias,
-// residual and activation.
+// splits the reduction over its WAVES waves (8 for 3x3): k = c*TAPS +
+// kh*3 + kw, lane half h of wave w takes input channels (2w + h)*CH .. +
+// CH - 1 with all their taps (C = 2*WAVES*CH), so every k step of a lane is
+// one (channel, tap) pair known at compile time.  Each lane loads its
+// TAPS*CH weights and its pixel's TAPS*CH input values (zero padding through
+// out-of-range buffer offsets; the channel plane offset is wave-uniform)
+// into registers before the first v_mfma_f32_32x32x2_f32, so a wave waits
+// once.  The weights come from the plan's copy in groups of 2 (3x3) or 4
+// (1x1) reduction indices, [K/32][k/VW][32][VW]: a wave's load reads the 32
+// output channels of two groups from 2 x 32 x VW contiguous floats (from
+// row-major weights each lane read its own row, 64 cache lines a load).
+// The partial blocks are summed through LDS in wave order (deterministic)
+// by all threads, then bias, residual and activation.
 #include <algorithm>
 
 #include "nhip_internal.h"
@@ -26,19 +29,25 @@ namespace nhip {
 namespace {
 
 struct KqArgs {
-  const float* w;       // [m_pad][ldw], k = c*9 + kh*3 + kw
+  const float* w;       // [m_pad/32][kgroups][32][VW], k = c*TAPS + tap
   const float* bias;    // [m_pad]
   const float* x;       // [N][C][H][W]
   const float* res;     // [N][K][OH][OW] or null
   float* out;           // [N][K][OH][OW]
   uint32_t x_bytes, out_bytes;  // (< 2^31)
-  int ldw, C, K, H, W, OW, OHW, npix, nmb;
+  int kgroups, C, K, H, W, OW, OHW, npix, nmb;
   int sh, sw, pt, pl, dh, dw, act;
 };
 
+typedef float v2f __attribute__((ext_vector_type(2)));
+
+// Reduction indices per weight group: 2 for 3x3 (a lane's 9*CH weights are
+// whole float2s), 4 for 1x1 (its channel counts are multiples of 4).
+constexpr int kq_group(int taps) { return taps == 9 ? 2 : 4; }
+
 template <int CH, int TAPS, int WAVES>
 __global__ __launch_bounds__(64 * WAVES) void conv_kq_kernel(KqArgs g) {
-  __shared__ float red[WAVES - 1][16][64];  // partial blocks of waves 1..WAVES-1
+  extern __shared__ float red[];  // [WAVES][16][64]: every wave's partial block
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int li = lane & 31, lh = lane >> 5;
@@ -46,28 +55,43 @@ __global__ __launch_bounds__(64 * WAVES) void conv_kq_kernel(KqArgs g) {
 
   // this lane's pixel (B column li) and its tap offsets (3x3 or one) in
   // the image of channel (2*wave + lh)*CH; out of range in the padding
-  const int pix = pb * 32 + li;
-  const bool pok = pix < g.npix;
-  const int pp = pok ? pix : 0;
-  const int img = pp / g.OHW, rem = pp - img * g.OHW;
-  const int oy = rem / g.OW, ox = rem - oy * g.OW;
   const int plane = g.H * g.W;
   uint32_t toff[TAPS];
+  {
+    const int pix = pb * 32 + li;
+    const bool pok = pix < g.npix;
+    const int pp = pok ? pix : 0;
+    const int img = pp / g.OHW, rem = pp - img * g.OHW;
+    const int oy = rem / g.OW, ox = rem - oy * g.OW;
 #pragma unroll
-  for (int t = 0; t < TAPS; ++t) {
-    const int iy = oy * g.sh - g.pt + (t / 3) * g.dh, ix = ox * g.sw - g.pl + (t % 3) * g.dw;
-    const bool ok = pok && (unsigned)iy < (unsigned)g.H && (unsigned)ix < (unsigned)g.W;
-    toff[t] = ok ? (uint32_t)((((int64_t)img * g.C + lh * CH) * plane + iy * g.W + ix) * 4) : kBufOOB;
+    for (int t = 0; t < TAPS; ++t) {
+      const int iy = oy * g.sh - g.pt + (t / 3) * g.dh, ix = ox * g.sw - g.pl + (t % 3) * g.dw;
+      const bool ok = pok && (unsigned)iy < (unsigned)g.H && (unsigned)ix < (unsigned)g.W;
+      toff[t] = ok ? (uint32_t)((((int64_t)img * g.C + lh * CH) * plane + iy * g.W + ix) * 4) : kBufOOB;
+    }
   }
 
-  // weights: row 32*mb + li, k = 9*((2w + h)*CH) .. + 9*CH - 1, contiguous
+  // weights: row 32*mb + li, k = TAPS*((2w + h)*CH) .. + TAPS*CH - 1, in
+  // groups of VW (the plan's layout): one load of a wave reads the 32 rows
+  // of two groups, 2 x 32 x VW contiguous floats
   constexpr int KS = TAPS * CH;
-  static_assert(KS % 4 == 0, "a lane's weight segment is whole, 16-byte aligned float4s");
-  v4f a[KS / 4];
+  constexpr int VW = kq_group(TAPS);
+  static_assert(KS % VW == 0, "a lane's weight segment is whole groups");
+  float a[KS];
   {
-    const float* ap = g.w + (int64_t)(mb * 32 + li) * g.ldw + (2 * wave + lh) * KS;
+    const float* ap = g.w + ((int64_t)mb * g.kgroups + (2 * wave + lh) * (KS / VW)) * 32 * VW + li * VW;
 #pragma unroll
-    for (int q = 0; q < KS / 4; ++q) a[q] = *reinterpret_cast<const v4f*>(ap + 4 * q);
+    for (int q = 0; q < KS / VW; ++q) {
+      if constexpr (VW == 4) {
+        const v4f v = *reinterpret_cast<const v4f*>(ap + q * 32 * VW);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) a[4 * q + e] = v[e];
+      } else {
+        const v2f v = *reinterpret_cast<const v2f*>(ap + q * 32 * VW);
+        a[2 * q] = v[0];
+        a[2 * q + 1] = v[1];
+      }
+    }
   }
   float b[KS];
   {
@@ -85,53 +109,49 @@ __global__ __launch_bounds__(64 * WAVES) void conv_kq_kernel(KqArgs g) {
 #pragma unroll
   for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
 #pragma unroll
-  for (int s = 0; s < KS; ++s) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a[s / 4][s % 4], b[s], acc, 0, 0, 0);
+  for (int s = 0; s < KS; ++s) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a[s], b[s], acc, 0, 0, 0);
 
-  if (wave > 0) {
 #pragma unroll
-    for (int r = 0; r < 16; ++r) red[wave - 1][r][lane] = acc[r];
-  }
+  for (int r = 0; r < 16; ++r) red[(wave * 16 + r) * 64 + lane] = acc[r];
   __syncthreads();
-  if (wave != 0) return;
-#pragma unroll
-  for (int w = 0; w < WAVES - 1; ++w)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) acc[r] += red[w][r][lane];
-  // D[channel][pixel]: register r of lane (li, lh) is channel
-  // 32mb + (r&3) + 8(r>>2) + 4lh at pixel 32pb + li
+  // entry (r, l) of the block, r = e / 64, l = e % 64: the partials summed in
+  // wave order (deterministic); D[channel][pixel]: register r of lane
+  // (li, lh) is channel 32mb + (r&3) + 8(r>>2) + 4lh at pixel 32pb + li
   const __amdgpu_buffer_rsrc_t orr = make_rsrc(g.out, g.out_bytes);
   const __amdgpu_buffer_rsrc_t rr = make_rsrc(g.res, g.res ? g.out_bytes : 0);
-  uint32_t off[16];
-  float rv[16];
 #pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    const int o = mb * 32 + (r & 3) + 8 * (r >> 2) + 4 * lh;
-    off[r] = pok && o < g.K ? (uint32_t)((((int64_t)img * g.K + o) * g.OHW + rem) * 4) : kBufOOB;
-    rv[r] = g.res ? __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rr, off[r], 0, 0)) : 0.f;
-  }
+  for (int e = tid; e < 1024; e += 64 * WAVES) {
+    const int r = e >> 6, l = e & 63;
+    float v = 0.f;
 #pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    const int o = mb * 32 + (r & 3) + 8 * (r >> 2) + 4 * lh;
-    float v = acc[r] + g.bias[o];
-    if (g.res) v = v + rv[r];
-    if (g.act == NHIP_ACT_RELU) v = v < 0.f ? 0.f : v;
-    __builtin_amdgcn_raw_buffer_store_b32(__float_as_int(v), orr, off[r], 0, 0);
+    for (int w = 0; w < WAVES; ++w) v += red[(w * 16 + r) * 64 + l];
+    const int pix = pb * 32 + (l & 31);
+    const int o = mb * 32 + (r & 3) + 8 * (r >> 2) + 4 * (l >> 5);
+    if (pix < g.npix && o < g.K) {
+      const int img = pix / g.OHW, rem = pix - img * g.OHW;
+      const uint32_t off = (uint32_t)((((int64_t)img * g.K + o) * g.OHW + rem) * 4);
+      v = v + g.bias[o];
+      if (g.res) v = v + __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rr, off, 0, 0));
+      if (g.act == NHIP_ACT_RELU) v = v < 0.f ? 0.f : v;
+      __builtin_amdgcn_raw_buffer_store_b32(__float_as_int(v), orr, off, 0, 0);
+    }
   }
+}
+
+template <int CH, int TAPS, int WAVES>
+int launch_kq(const KqArgs& a, dim3 grid, hipStream_t s) {
+  constexpr int lds = WAVES * 16 * 64 * 4;
+  NHIP_TRY(ensure_dynamic_lds(reinterpret_cast<const void*>(&conv_kq_kernel<CH, TAPS, WAVES>), lds));
+  NHIP_LAUNCH("conv_kq", (conv_kq_kernel<CH, TAPS, WAVES>), grid, dim3(64 * WAVES), lds, s, a);
+  return check_launch("conv_kq");
 }
 
 }  // namespace
 
-// The row-major weights and their row stride: the implicit-GEMM plan's own,
-// or a Winograd plan's extra copy (32 or 64 input channels).
-bool kq_weights(const nhip_conv_plan* p, const float** w, int* ld) {
-  if (p->algorithm == NHIP_CONV_ALGO_IMPLICIT_GEMM) {
-    *w = p->weight;
-    *ld = p->kred_pad;
-  } else {
-    *w = p->weight_rows;
-    *ld = p->rows_ld;
-  }
-  return *w != nullptr && *ld % 4 == 0;
+// The grouped weights (made with the plan when the kernel can take it).
+bool kq_weights(const nhip_conv_plan* p, const float** w) {
+  *w = p->weight_kq;
+  return *w != nullptr && p->kq_vw == kq_group(p->g.kh * p->g.kw);
 }
 
 // Instances: (channels per lane half, waves) for a 1x1 convolution with C
@@ -147,14 +167,32 @@ KqShape kq_1x1_shape(int c) {
   return {0, 0};
 }
 
+int conv_kq_prepack(nhip_conv_plan* p, const float* weight, int c, int k, int kh, int kw) {
+  const bool k3 = kh == 3 && kw == 3 && (c == 32 || c == 64);
+  const bool k1 = kh == 1 && kw == 1 && kq_1x1_shape(c).ch != 0;
+  if (!k3 && !k1) return ok();
+  const int taps = kh * kw, kt = c * taps, vw = kq_group(taps);
+  const int mp = (int)round_up(k, 32);
+  std::vector<float> wg((size_t)mp * kt, 0.f);
+  for (int o = 0; o < k; ++o)
+    for (int j = 0; j < kt; ++j)
+      wg[(((size_t)(o / 32) * (kt / vw) + j / vw) * 32 + o % 32) * vw + j % vw] = weight[(size_t)o * kt + j];
+  p->kq_vw = vw;
+  NHIP_TRY(check_hip(hipMalloc(&p->weight_kq, wg.size() * sizeof(float)), "hipMalloc(conv grouped weight)"));
+  return check_hip(hipMemcpy(p->weight_kq, wg.data(), wg.size() * sizeof(float), hipMemcpyHostToDevice),
+                   "hipMemcpy(conv grouped weight)");
+}
+
 // Whether the kernel takes the launch: a 3x3 convolution with 32 or 64 input
-// channels (a lane's 9*C/8 weights then are whole 16-byte vectors) or a 1x1
+// channels (a lane's 9*C/16 weights then are whole float2 groups) or a 1x1
 // one with an instantiated channel count, activation none or ReLU, and few
 // blocks.  3x3: at most two 32x32 blocks per CU, on either plan (one image
-// of 64x56x56, 64 output channels, 196 blocks: 9.7 us against 13.6 us for
-// the Winograd path and 14.6 us for the tiled implicit GEMM; two such
-// images, 392 blocks, 15.0 against 21.1 us on Winograd; at 784 blocks
-// Winograd wins with 64 channels, 25.6 against 26.5 us).  1x1: at
+// of 64x56x56, 64 output channels, 196 blocks: 7.1 us in a kernel trace,
+// 7.6 us with 4 waves a block, 8.0 with 16; 9.7 us before the grouped
+// weights, against 13.6 us for the Winograd path and 14.6 us for the tiled
+// implicit GEMM; two such images, 392 blocks, 15.0 against 21.1 us on
+// Winograd; at 784 blocks Winograd wins with 64 channels, 25.6 against 26.5
+// us).  1x1: at
 // most one per CU (MobileNetV2 at batch 32, 960 -> 160 + residual at 7x7:
 // 17.0 against 21.4 us; with more blocks the tiled kernels' operand reuse
 // wins: 960 -> 320, 26.7 against 25.0 us) and at least one per eight CUs
@@ -166,8 +204,7 @@ bool kq_supported(const nhip_conv_plan* p, int n, int h, int w, int oh, int ow) 
   if (mode == 0) return false;
   const ConvGeom& g = p->g;
   const float* wr = nullptr;
-  int ld = 0;
-  if (p->kind != PlanKind::ConvF32 || !kq_weights(p, &wr, &ld) || (g.act != NHIP_ACT_NONE && g.act != NHIP_ACT_RELU))
+  if (p->kind != PlanKind::ConvF32 || !kq_weights(p, &wr) || (g.act != NHIP_ACT_NONE && g.act != NHIP_ACT_RELU))
     return false;
   const bool k3 = g.kh == 3 && g.kw == 3 && (g.c == 32 || g.c == 64);
   const bool k1 = g.kh == 1 && g.kw == 1 && kq_1x1_shape(g.c).ch != 0;
@@ -182,7 +219,8 @@ bool kq_supported(const nhip_conv_plan* p, int n, int h, int w, int oh, int ow) 
 int launch_conv_kq(const nhip_conv_plan* p, const float* in, const float* residual, float* out, int n, int h, int w,
                    int oh, int ow, hipStream_t s) {
   KqArgs a{};
-  if (!kq_weights(p, &a.w, &a.ldw)) return fail(NHIP_STATUS_CONSTRAINT_VIOLATION, "conv_kq: no row-major weights");
+  if (!kq_weights(p, &a.w)) return fail(NHIP_STATUS_CONSTRAINT_VIOLATION, "conv_kq: no grouped weights");
+  a.kgroups = p->g.c * p->g.kh * p->g.kw / p->kq_vw;
   a.bias = p->bias;
   a.x = in;
   a.res = residual;
@@ -205,19 +243,10 @@ int launch_conv_kq(const nhip_conv_plan* p, const float* in, const float* residu
   a.dw = p->g.dw;
   a.act = p->g.act;
   const dim3 grid((unsigned)(a.nmb * ceil_div(a.npix, 32)));
-  if (p->g.kh == 3) {
-    if (p->g.c == 32)
-      NHIP_LAUNCH("conv_kq", (conv_kq_kernel<4, 9, 4>), grid, dim3(256), 0, s, a);
-    else
-      NHIP_LAUNCH("conv_kq", (conv_kq_kernel<8, 9, 4>), grid, dim3(256), 0, s, a);
-    return check_launch("conv_kq");
-  }
+  if (p->g.kh == 3) return p->g.c == 32 ? launch_kq<2, 9, 8>(a, grid, s) : launch_kq<4, 9, 8>(a, grid, s);
   const KqShape k = kq_1x1_shape(p->g.c);
-#define NHIP_KQ1(CH_, W_)                                                                       \
-  if (k.ch == CH_ && k.waves == W_) {                                                           \
-    NHIP_LAUNCH("conv_kq", (conv_kq_kernel<CH_, 1, W_>), grid, dim3(64 * W_), 0, s, a);         \
-    return check_launch("conv_kq");                                                             \
-  }
+#define NHIP_KQ1(CH_, W_)                                        \
+  if (k.ch == CH_ && k.waves == W_) return launch_kq<CH_, 1, W_>(a, grid, s);
   NHIP_KQ1(8, 4)
   NHIP_KQ1(12, 4)
   NHIP_KQ1(20, 4)

@@ -168,11 +168,13 @@ struct nhip_conv_plan {
   // [36][c_pad/4][m_pad][4], so 32 output channels of one group are 512
   // contiguous bytes per transform point.
   float* weight_fused = nullptr;
-  // Winograd plans of 32 or 64 input channels: the weights also row-major,
-  // [m_pad][rows_ld] with k = c*9 + kh*3 + kw, for the one-kernel path of
-  // small launches (conv_kq.hip).
-  float* weight_rows = nullptr;
-  int32_t rows_ld = 0;
+  // Plans the one-kernel path of small launches can take (conv_kq.hip: 3x3
+  // with 32 or 64 input channels, on either algorithm, and 1x1 with its
+  // channel counts): the weights in groups of kq_vw reduction indices,
+  // [m_pad/32][C*KH*KW/kq_vw][32][kq_vw] with k = c*KH*KW + kh*KW + kw, so
+  // the 32 output channels of one group are contiguous.
+  float* weight_kq = nullptr;
+  int32_t kq_vw = 0;
   // Winograd plans of 256+ input channels: an implicit-GEMM plan of the same
   // layer, for launches of so few tiles that the Winograd GEMM's 128-tile
   // padding dominates (a single 7x7 or 14x14 image).
@@ -279,6 +281,8 @@ bool smallk_supported(const nhip_conv_plan* p, int n, int h, int w, int oh, int 
 // few output blocks, one workgroup per 32x32 block, the reduction over its
 // waves (no workspace).
 bool kq_supported(const nhip_conv_plan* p, int n, int h, int w, int oh, int ow);
+// The weight copy above for a plan the kernel can take (nothing otherwise).
+int conv_kq_prepack(nhip_conv_plan* p, const float* weight, int c, int k, int kh, int kw);
 int launch_conv_kq(const nhip_conv_plan* p, const float* in, const float* residual, float* out, int n, int h, int w,
                    int oh, int ow, hipStream_t s);
 int launch_conv_smallk(const nhip_conv_plan* p, const float* in, const float* residual, float* out, int n, int h,

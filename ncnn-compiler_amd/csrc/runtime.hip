@@ -348,7 +348,7 @@ void free_plan(nhip_conv_plan* p) {
   free_plan(p->igemm_twin);
   (void)hipFree(p->weight);
   (void)hipFree(p->weight_fused);
-  (void)hipFree(p->weight_rows);
+  (void)hipFree(p->weight_kq);
   (void)hipFree(p->bias);
   (void)hipFree(p->ktab);
   (void)hipFree(p->weight_i8);
@@ -555,13 +555,7 @@ int nhip_conv2d_f32_create(const nhip_conv_desc* d, const float* weight, const f
   if (algo == NHIP_CONV_ALGO_WINOGRAD) {
     p->c_pad = (int)round_up(C, 16);
     st = winograd_prepack_weights(p, weight);
-    if (st == NHIP_STATUS_SUCCESS && (C == 32 || C == 64)) {
-      p->rows_ld = (int)round_up(C * 9, 16);
-      std::vector<float> wr((size_t)p->m_pad * p->rows_ld, 0.f);
-      for (int k = 0; k < K; ++k)
-        std::copy(weight + (size_t)k * C * 9, weight + (size_t)(k + 1) * C * 9, wr.begin() + (size_t)k * p->rows_ld);
-      st = upload(&p->weight_rows, wr, "hipMalloc(conv row-major weight)");
-    }
+    if (st == NHIP_STATUS_SUCCESS) st = conv_kq_prepack(p, weight, C, K, 3, 3);
     if (st == NHIP_STATUS_SUCCESS && C >= kWinoTwinMinC) {
       nhip_conv_desc d2 = *d;
       d2.algorithm = NHIP_CONV_ALGO_IMPLICIT_GEMM;
@@ -581,6 +575,7 @@ int nhip_conv2d_f32_create(const nhip_conv_desc* d, const float* weight, const f
     }
     st = upload(&p->weight, wp, "hipMalloc(conv weight)");
     if (st == NHIP_STATUS_SUCCESS) st = upload(&p->ktab, kt, "hipMalloc(conv ktab)");
+    if (st == NHIP_STATUS_SUCCESS) st = conv_kq_prepack(p, weight, C, K, d->kernel_h, d->kernel_w);
   }
   if (st == NHIP_STATUS_SUCCESS) st = upload_bias(p, d->bias_term ? bias : nullptr, K, p->m_pad);
   if (st != NHIP_STATUS_SUCCESS) {
