@@ -364,11 +364,14 @@ def config4(nhip, workloads, torch, steps, warmup, share, cpu, target_s):
     dt = timed(torch, fn, n)
     ops = workloads.conv_flops(BATCH, 128, 128, 28, 28)
     per, sec = kernel_time(nhip, torch, fn, n, "conv_int8")
-    qper, qsec = kernel_time(nhip, torch, fn, n, "quantize")
+    qper, qsec = kernel_time(nhip, torch, fn, n, "quantize", required=False)
+    fq, _ = kernel_time(nhip, torch, fn, 2, "conv_int8_rw_fq", required=False)
+    what = ("conv_int8_rw_fq (fp32 input quantized into the LDS window, int8 MFMA GEMM, weights in registers, "
+            "exact requantize epilogue; one launch)" if fq else
+            "conv_int8_rw (int8 MFMA GEMM, weights in registers, exact requantize epilogue)")
     res = {"workload": "int8 conv 32x128x28x28 3x3 requant(term 101)+relu, fp32 input",
            "ms_per_step": dt * 1e3, "tops": ops / dt / 1e12, "images_per_sec": BATCH / dt,
-           "roofline": roofline("mfma_int8", "conv_int8_rw (int8 MFMA GEMM, weights in registers, exact requantize epilogue)", ops / per,
-                                sec, per)}
+           "roofline": roofline("mfma_int8", what, ops / per, sec, per)}
     if qper:
         # quantize pass: reads the fp32 input once, writes the int8 NHWC image
         qbytes = BATCH * 128 * 28 * 28 * 5

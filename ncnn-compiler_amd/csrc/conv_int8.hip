@@ -15,11 +15,13 @@
 // accumulation is exact in any order, which is what lets the reduction run
 // on v_mfma_i32_32x32x32_i8 in a different order from the CPU loop nest.
 //
-// Layout: the fp32/int8 NCHW input is first quantized into an NHWC int8
-// scratch image with channels padded to 16 (one pass over HBM).  The GEMM
-// then gathers 16-byte channel vectors per (pixel, kh, kw), reduction order
-// (kh, kw, c) — the OHWI order the reference itself transposes the weights
-// to (NCNNToTosa.cpp:1168-1176).
+// Layout: the GEMM gathers 16-byte channel vectors per (pixel, kh, kw),
+// reduction order (kh, kw, c) — the OHWI order the reference itself
+// transposes the weights to (NCNNToTosa.cpp:1168-1176) — from an NHWC int8
+// image with channels padded to 16.  The register-weight kernel builds that
+// layout for its own input window in LDS, quantizing fp32 input on the way
+// (NHIP_INT8_FUSED_QUANT=0 turns this off); the other kernels read a scratch
+// image that a separate pass quantizes (one pass over HBM).
 #include <algorithm>
 #include <cmath>
 #include <cstdio>
@@ -91,6 +93,12 @@ struct Int8Args {
   uint32_t out_bytes;     // size of out (< 2^31)
   int kred, KW, dh, dw;   // unpadded reduction bytes, kernel width, dilations
   int vec;                // output stores: 0 single elements, 1 four pixels, 2 sixteen int8 pixels
+  // register-weight kernel with the quantization fused into its window fill
+  const float* xf;        // fp32 NCHW input [N][C][H][W] (W % 4 == 0, 16-byte aligned)
+  uint32_t xf_bytes;      // size of xf (< 2^31)
+  int C;                  // input channels (% 4 == 0)
+  float in_scale;         // quantizeSignedI8 scale of the input
+  FastDiv xg_div, c4_div;  // window items: W/4 column groups, C/4 channel groups
 };
 
 // D[i = out channel][j = pixel] over the (kh, kw, c) reduction.
@@ -501,7 +509,16 @@ __global__ __launch_bounds__(kThreads) void conv_int8_fp_kernel(Int8Args g) {
 // consecutive int8 results of its channel (one 16-byte store), or four fp32
 // results go out as one 16-byte vector.  Same arithmetic as the other
 // kernels; the integer sums are exact in any order.
-template <int KS, int TN>
+//
+// FQ: the input arrives as fp32 NCHW and the window is filled by quantizing
+// it on the way into LDS (no NHWC int8 image, no separate launch).  Window
+// item i = (row fy, channel group c4 of 4, column group x4 of 4 pixels),
+// x4 fastest, so 7 consecutive threads read one 112-byte channel row: four
+// 16-byte loads (channels 4c4 .. 4c4 + 3), sixteen quantizations, and one
+// 4-byte LDS word (4 channels) per pixel.  Rows outside the image and the
+// window's columns outside it (the padding) are zero.  The items come in two
+// batches of at most 3 per thread, the first in flight with the weights.
+template <int KS, int TN, bool FQ = false>
 __global__ __launch_bounds__(kThreads) void conv_int8_rw_kernel(Int8Args g) {
   extern __shared__ __attribute__((aligned(16))) int8_t dsm[];
   int8_t* foot = dsm;
@@ -515,25 +532,76 @@ __global__ __launch_bounds__(kThreads) void conv_int8_rw_kernel(Int8Args g) {
 
   // ---- footprint loads first (at most 8 per thread, checked on the host),
   // then the weights in k order, then the epilogue scalars; nothing waits yet
-  const __amdgpu_buffer_rsrc_t rs = make_rsrc(g.x, g.x_bytes);
   const int cpp = g.c_pad / 16;
-  const int total = g.FH * g.FW * cpp;
   const int iy_base = oy0 * g.sh - g.pt;
-  v4i fv[8];
-  int fdst[8];
+  v4i fv[FQ ? 1 : 8];
+  int fdst[FQ ? 1 : 8];
+  // FQ items: 16 fp32 values (4 channels x 4 pixels) and the LDS byte
+  // offset of the first pixel's 4-channel word (-1: none, -2: zero row)
+  constexpr int kQB = 3;
+  v4f qv[FQ ? kQB : 1][4];
+  int qdst[FQ ? kQB : 1];
+  const int c4n = g.C / 4, xgn = g.W / 4;
+  const int items = FQ ? c4n * g.FH * xgn : 0;
+  auto fq_load = [&](int batch) {
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(g.xf, g.xf_bytes);
 #pragma unroll
-  for (int q = 0; q < 8; ++q) {
-    const int e = q * kThreads + tid;
-    const int pix = fdiv(e, g.cpp_div), ch = e - pix * cpp;
-    const int fy = fdiv(pix, g.fw_div), fx = pix - fy * g.FW;
-    const int iy = iy_base + fy, ix = fx - g.pl;
-    const bool in = e < total && (unsigned)iy < (unsigned)g.H && (unsigned)ix < (unsigned)g.W;
-    fv[q] = __builtin_bit_cast(
-        v4i, buf_load_b128(rs, in ? (uint32_t)(((img * g.H + iy) * g.W + ix) * g.c_pad + ch * 16) : kBufOOB));
-    // 24-bit products (window < 2^24 bytes) keep this 32-bit: a 64-bit
-    // multiply-add here pairs a register with a weight load's destination
-    // and forces an early wait for it
-    fdst[q] = e < total ? (int)__umul24(pix, g.FS) + ch * 16 : -1;
+    for (int q = 0; q < kQB; ++q) {
+      const int i = (batch * kQB + q) * kThreads + tid;
+      const int rest = fdiv(i, g.xg_div), x4 = i - rest * xgn;
+      const int fy = fdiv(rest, g.c4_div), c4 = rest - fy * c4n;
+      const int iy = iy_base + fy;
+      const bool row_in = (unsigned)iy < (unsigned)g.H;
+      qdst[q] = i < items ? (row_in ? (fy * g.FW + 4 * x4 + g.pl) * g.FS + 4 * c4 : -2) : -1;
+      const uint32_t off = ((uint32_t)((img * g.C + 4 * c4) * g.H + iy) * g.W + 4 * x4) * 4;
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        qv[q][j] = __builtin_bit_cast(
+            v4f, buf_load_b128(xr, i < items && row_in ? off + (uint32_t)(j * g.H * g.W * 4) : kBufOOB));
+    }
+  };
+  auto fq_store = [&](int batch) {
+#pragma unroll
+    for (int q = 0; q < kQB; ++q) {
+      if (qdst[q] == -1) continue;
+      int w4[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        w4[e] = (int)pack_i8x4(quantize_q(qv[q][0][e], g.in_scale), quantize_q(qv[q][1][e], g.in_scale),
+                               quantize_q(qv[q][2][e], g.in_scale), quantize_q(qv[q][3][e], g.in_scale));
+      if (qdst[q] == -2) {
+        // a row outside the image: its item's pixels and channels are zero
+        const int i = (batch * kQB + q) * kThreads + tid;
+        const int rest = fdiv(i, g.xg_div), x4 = i - rest * xgn;
+        const int fy = fdiv(rest, g.c4_div), c4 = rest - fy * c4n;
+        const int d0 = (fy * g.FW + 4 * x4 + g.pl) * g.FS + 4 * c4;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) *reinterpret_cast<int*>(foot + d0 + e * g.FS) = 0;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) *reinterpret_cast<int*>(foot + qdst[q] + e * g.FS) = w4[e];
+      }
+    }
+  };
+  if constexpr (FQ) {
+    fq_load(0);
+  } else {
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(g.x, g.x_bytes);
+    const int total = g.FH * g.FW * cpp;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const int e = q * kThreads + tid;
+      const int pix = fdiv(e, g.cpp_div), ch = e - pix * cpp;
+      const int fy = fdiv(pix, g.fw_div), fx = pix - fy * g.FW;
+      const int iy = iy_base + fy, ix = fx - g.pl;
+      const bool in = e < total && (unsigned)iy < (unsigned)g.H && (unsigned)ix < (unsigned)g.W;
+      fv[q] = __builtin_bit_cast(
+          v4i, buf_load_b128(rs, in ? (uint32_t)(((img * g.H + iy) * g.W + ix) * g.c_pad + ch * 16) : kBufOOB));
+      // 24-bit products (window < 2^24 bytes) keep this 32-bit: a 64-bit
+      // multiply-add here pairs a register with a weight load's destination
+      // and forces an early wait for it
+      fdst[q] = e < total ? (int)__umul24(pix, g.FS) + ch * 16 : -1;
+    }
   }
   v4i wr[KS];
   {
@@ -552,9 +620,23 @@ __global__ __launch_bounds__(kThreads) void conv_int8_rw_kernel(Int8Args g) {
     // K padding (past kred): the weights there are zero, any window byte will do
     koff_tab[tid] = kidx < g.kred ? (kh * g.dh * g.FW + kw * g.dw) * g.FS + c0 : 0;
   }
+  if constexpr (FQ) {
+    // the window's columns outside the image (left and right padding): zero
+    const int nh = g.FW - g.W, hz = g.FH * nh * cpp;
+    for (int e = tid; e < hz; e += kThreads) {
+      const int pos = e / cpp, ch = e - pos * cpp;
+      const int fy = pos / nh, h = pos - fy * nh;
+      const int fx = h < g.pl ? h : g.W + h;
+      *reinterpret_cast<v4i*>(foot + (fy * g.FW + fx) * g.FS + ch * 16) = v4i{0, 0, 0, 0};
+    }
+    fq_store(0);
+    fq_load(1);
+    fq_store(1);
+  } else {
 #pragma unroll
-  for (int q = 0; q < 8; ++q)
-    if (fdst[q] >= 0) *reinterpret_cast<v4i*>(foot + fdst[q]) = fv[q];
+    for (int q = 0; q < 8; ++q)
+      if (fdst[q] >= 0) *reinterpret_cast<v4i*>(foot + fdst[q]) = fv[q];
+  }
 
   // per-lane window origin (bytes) of each of the wave's pixel rows of D
   int fbase[TN];
@@ -665,10 +747,12 @@ int launch_conv_int8(const nhip_conv_plan* p, const void* in, int in_is_i8,
     return fail(NHIP_STATUS_OUTPUT_CAPACITY_INSUFFICIENT,
                 "int8 conv: workspace of " + std::to_string(need) + " bytes required");
   int8_t* xq = static_cast<int8_t*>(ws);
-  NHIP_LAUNCH("quantize_nchw_to_nhwc", quantize_nchw_to_nhwc,
-              dim3((unsigned)ceil_div((int64_t)h * w, 64), (unsigned)ceil_div(p->c_pad, 64), n), dim3(kThreads), 0, s,
-              in, in_is_i8, xq, p->g.c, h * w, p->c_pad, p->input_scale);
-  NHIP_TRY(check_launch("quantize_nchw_to_nhwc"));
+  auto quantize = [&]() {
+    NHIP_LAUNCH("quantize_nchw_to_nhwc", quantize_nchw_to_nhwc,
+                dim3((unsigned)ceil_div((int64_t)h * w, 64), (unsigned)ceil_div(p->c_pad, 64), n), dim3(kThreads), 0, s,
+                in, in_is_i8, xq, p->g.c, h * w, p->c_pad, p->input_scale);
+    return check_launch("quantize_nchw_to_nhwc");
+  };
 
   Int8Args g{};
   g.w = p->weight_i8;
@@ -738,8 +822,26 @@ int launch_conv_int8(const nhip_conv_plan* p, const void* in, int in_is_i8,
       }
       const int64_t chunks = (int64_t)r.FH * r.FW * (p->c_pad / 16);
       const int64_t lds = r.fp_bytes + 2 * KS * 4;
+      // Quantization fused into the window fill: fp32 input with whole
+      // 4-pixel column groups and 4-channel groups (16-byte loads), the
+      // window covering every input column, at most 6 items per thread
+      const int64_t fq_items = (int64_t)(p->g.c / 4) * r.FH * (w / 4);
+      const bool fq = !in_is_i8 && setting_int("NHIP_INT8_FUSED_QUANT", 1) != 0 && tn == 4 && w % 4 == 0 &&
+                      p->g.c % 4 == 0 && (reinterpret_cast<uintptr_t>(in) & 15) == 0 && p->g.pl + w <= r.FW &&
+                      fq_items <= 6 * kThreads && (int64_t)n * p->g.c * h * w * 4 < INT32_MAX;
       if (chunks <= 8 * kThreads && lds <= 64 * 1024) {
         const dim3 grid((unsigned)(n * ceil_div(oh, R)), (unsigned)(p->m_pad / 128));
+        if (fq) {
+          r.xf = static_cast<const float*>(in);
+          r.xf_bytes = (uint32_t)((int64_t)n * p->g.c * h * w * 4);
+          r.C = p->g.c;
+          r.in_scale = p->input_scale;
+          r.xg_div = fast_div((uint32_t)(w / 4));
+          r.c4_div = fast_div((uint32_t)(p->g.c / 4));
+          NHIP_LAUNCH("conv_int8_rw_fq", (conv_int8_rw_kernel<KS, 4, true>), grid, dim3(kThreads), (unsigned)lds, s, r);
+          return check_launch("conv_int8_rw_fq");
+        }
+        NHIP_TRY(quantize());
         if (tn == 4) {
           NHIP_LAUNCH("conv_int8_rw", (conv_int8_rw_kernel<KS, 4>), grid, dim3(kThreads), (unsigned)lds, s, r);
         } else {
@@ -749,6 +851,8 @@ int launch_conv_int8(const nhip_conv_plan* p, const void* in, int in_is_i8,
       }
     }
   }
+  // The other kernels read the NHWC int8 image.
+  NHIP_TRY(quantize());
   // Footprint kernel when a workgroup's input window fits in LDS (whole rows
   // of at most 128 output pixels); NHIP_INT8_FOOTPRINT=0 turns it off (a
   // tuning and comparison switch).

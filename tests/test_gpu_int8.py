@@ -4,6 +4,8 @@ dequantizeAccumulator :577-637, bias add :1294-1300, requantize :1309-1312,
 relu after, ImportConvolution.cpp:236-241), plus the reference's own
 known-answer cases (test/Conversion/NCNNToTosa/quantized-contractions.mlir,
 test/Numerical/fixtures/generate_int8_bins.py)."""
+import os
+
 import numpy as np
 import pytest
 
@@ -154,15 +156,24 @@ RW_CASES = [
     (3, 128, 7, 7, 128, (3, 3), (1, 1), (1, 1), (1, 1, 1, 1), 101, 0, False),
     # 32 columns: four whole 32-pixel blocks per wave
     (1, 128, 9, 32, 128, (3, 3), (1, 1), (1, 1), (1, 1, 1, 1), 1, 1, False),
+    # no padding: the window's columns are exactly the image's
+    (2, 128, 28, 28, 128, (3, 3), (1, 1), (1, 1), (0, 0, 0, 0), 1, 0, False),
+    # 124 of 128 window channels filled (4-channel groups), 16 columns
+    (1, 124, 12, 16, 128, (3, 3), (1, 1), (1, 1), (1, 1, 1, 1), 101, 1, True),
 ]
 
 
 @pytest.mark.parametrize("case", RW_CASES, ids=lambda c: "x".join(map(str, c[:5])) + f"-t{c[9]}")
-@pytest.mark.parametrize("rw", ["1", "2", "0"])
+@pytest.mark.parametrize("rw", ["1", "1q", "2", "0"])
 def test_int8_register_weight_kernel_bit_exact(case, rw, nhip_env):
     """The register-weight kernel (NHIP_INT8_RW=1, default: four 32-pixel
-    blocks per wave; =2: two) against the oracle, bit for bit, and with it
-    off (=0: the footprint kernel)."""
+    blocks per wave, with the input quantized inside its window fill where
+    the shape allows (fp32 input, width and channels multiples of 4); "1q":
+    the same with that fusion off, a separate quantize pass first; =2: two
+    blocks per wave) against the oracle, bit for bit, and with it off (=0:
+    the footprint kernel)."""
+    nhip_env.setenv("NHIP_INT8_FUSED_QUANT", "0" if rw == "1q" else "1")
+    rw = rw[0]
     nhip_env.setenv("NHIP_INT8_RW", rw)
     n, c, h, w, k, ker, st, dl, pad, term, act, scalar = case
     rng = np.random.default_rng(hash(case) % (2 ** 32))
@@ -178,8 +189,19 @@ def test_int8_register_weight_kernel_bit_exact(case, rw, nhip_env):
     conv = nhip.Conv2dInt8(d, w_i8, b, ws, is_, os_)
     xd = dev(x)
     exp = oracle(d, x, w_i8, b, ws, is_, os_)
+    # where the fused window fill takes the shape (4 output rows' window of
+    # at most 6 x 256 items of 4 channels x 4 pixels, covering every column)
+    oh = (h + pad[0] + pad[1] - dl[0] * (ker[0] - 1) - 1) // st[0] + 1
+    ow = (w + pad[2] + pad[3] - dl[1] * (ker[1] - 1) - 1) // st[1] + 1
+    rows = min(128 // ow, oh)
+    fh = (rows - 1) * st[0] + (ker[0] - 1) * dl[0] + 1
+    fw = (ow - 1) * st[1] + (ker[1] - 1) * dl[1] + 1
+    fused = (rw == "1" and w % 4 == 0 and c % 4 == 0 and pad[2] + w <= fw
+             and (c // 4) * fh * (w // 4) <= 6 * 256 and os.environ["NHIP_INT8_FUSED_QUANT"] == "1")
     for rep in range(2):  # the second call reuses the plan and the workspace
+        nhip.timer_start("conv_int8_rw_fq")
         got = host(conv.forward(xd))
+        assert nhip.timer_stop()[0] == (1 if fused else 0)
         assert got.dtype == exp.dtype
         np.testing.assert_array_equal(got, exp, err_msg=f"call {rep}")
     if term > 100:  # not degenerate: many levels, not all saturated
