@@ -151,6 +151,31 @@ def test_innerproduct_without_bias_zero_init_then_bias():
     assert got[0, 0] == 0.0
 
 
+@pytest.mark.parametrize("count", [1, 3, 4, 7, 1024, 4099, 65536 * 5 + 2, 1 << 22])
+@pytest.mark.parametrize("offset", [0, 1])
+def test_relu_and_add_vector_paths_bit_exact(count, offset):
+    """ReLU and add on 16-byte vectors (aligned buffers: four vectors in
+    flight per thread, the last count % 4 elements on the scalar kernel) and
+    on the scalar kernel alone (offset 1: views 4 bytes past an aligned
+    base), bit for bit against the oracle, signed zeros and NaN included."""
+    x = RNG.uniform(-1, 1, count).astype(np.float32)
+    y = RNG.uniform(-1, 1, count).astype(np.float32)
+    x[: min(count, 3)] = np.array([-0.0, np.nan, 0.0], np.float32)[: min(count, 3)]
+    def view(a):
+        buf = torch.empty(a.size + offset, dtype=torch.float32, device="cuda")
+        v = buf[offset:]
+        v.copy_(torch.from_numpy(a).cuda())
+        return v
+    got = host(nhip.relu(view(x), out=view(np.zeros_like(x))))
+    np.testing.assert_array_equal(got.view(np.uint32), refcpu.relu_f32(x).view(np.uint32))
+    for relu_after in (False, True):
+        exp = refcpu.add_f32(x, y)
+        if relu_after:
+            exp = refcpu.relu_f32(exp)
+        got = host(nhip.add(view(x), view(y), relu_after=relu_after, out=view(np.zeros_like(x))))
+        np.testing.assert_array_equal(got.view(np.uint32), exp.view(np.uint32))
+
+
 def test_relu_add_and_avgpool():
     x = RNG.uniform(-1, 1, (3, 5, 7, 9)).astype(np.float32)
     y = RNG.uniform(-1, 1, (3, 5, 7, 9)).astype(np.float32)
