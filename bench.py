@@ -518,6 +518,46 @@ def config5(nhip, torch, steps, warmup, workdir, share, cpu, target_s):
     return res
 
 
+def hbm_kernels(nhip, workloads, torch, steps, warmup):
+    """Bandwidth-bound kernels on their own at batch-32 MobileNetV2 shapes
+    (the graph fuses these layers, or runs them on small planes where launch
+    costs dominate): algorithmic bytes (each input read once, each output
+    written once) over the kernel's average launch time from HIP events."""
+    import numpy as np
+    rng = np.random.default_rng(0)
+    rows = []
+
+    def timed_kernel(what, fn, nbytes, name):
+        for _ in range(warmup):
+            fn()
+        per, sec = kernel_time(nhip, torch, fn, steps, name)
+        gbs = nbytes / sec / 1e9
+        rows.append({"kernel": what, "mb": round(nbytes / 1e6, 1), "avg_launch_us": round(sec * 1e6, 2),
+                     "gbs": round(gbs, 1), "frac_hbm": round(gbs / PEAK_HBM_GBS, 4)})
+
+    for shape in [(BATCH, 96, 112, 112), (BATCH, 144, 56, 56)]:
+        x = torch.from_numpy(rng.uniform(-1, 1, shape).astype(np.float32)).cuda()
+        z = torch.from_numpy(rng.uniform(-1, 1, shape).astype(np.float32)).cuda()
+        y = torch.empty_like(x)
+        nb = x.numel() * 4
+        tag = "x".join(map(str, shape))
+        timed_kernel(f"relu_f32 {tag}", lambda: nhip.relu(x, out=y), 2 * nb, "relu_f32")
+        timed_kernel(f"add_f32 {tag}", lambda: nhip.add(x, z, out=y), 3 * nb, "add_f32")
+        timed_kernel(f"add_f32 + relu {tag}", lambda: nhip.add(x, z, relu_after=True, out=y), 3 * nb, "add_f32")
+        c = shape[1]
+        for st in (1, 2):
+            w = workloads.he_normal(rng, (c, 1, 3, 3), 9)
+            b = rng.normal(0, 0.05, c).astype(np.float32)
+            d = nhip.DwConv2dF32(nhip.conv_desc(c, c, (3, 3), (st, st), (1, 1), (1, 1, 1, 1), act=nhip.ACT_RELU,
+                                                group=c), w, b)
+            oh = (shape[2] - 1) // st + 1
+            o = torch.empty((shape[0], c, oh, oh), device="cuda")
+            timed_kernel(f"dw3x3s{st}_f32 + relu {tag}", lambda: d.forward(x, out=o), nb + o.numel() * 4, "dw3x3")
+    return {"what": "achieved HBM bandwidth of the depthwise and elementwise kernels, batch-32 MobileNetV2 "
+                    "shapes, fp32; bytes = inputs read once + outputs written once; time = HIP events around "
+                    "each launch", "peak_gbs": PEAK_HBM_GBS, "kernels": rows}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -527,6 +567,9 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=3.0,
                     help="length of each bounded CPU-baseline sample (per config and thread count)")
     ap.add_argument("--only-config3", action="store_true", help="skip the secondary configurations")
+    ap.add_argument("--hbm-kernels", action="store_true",
+                    help="instead of the bench line: the achieved HBM bandwidth of the depthwise and "
+                         "elementwise kernels at batch-32 MobileNetV2 shapes (one JSON line)")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="first run a plain device copy of this many MiB (hipMemcpy D2D) so that "
                          "rocprofv3 FETCH_SIZE/WRITE_SIZE can be scaled against known bytes")
@@ -551,6 +594,9 @@ def main():
             nhip.check(nhip.load().nhip_memcpy_d2d(nhip._ptr(dst), nhip._ptr(src), nbytes, nhip._stream()))
         torch.cuda.synchronize()
         del src, dst
+    if args.hbm_kernels:
+        print(json.dumps(hbm_kernels(nhip, workloads, torch, max(args.steps, 10), args.warmup)), flush=True)
+        return
     cpu = not args.no_cpu_baseline
     model, host_cpus, share = cpu_info()
 

@@ -738,7 +738,11 @@ int launch_dwconv_f32(const nhip_conv_plan* p, const float* in, float* out,
     return check_launch("dw3x3_planes_f32");
   }
   if (k3 && x_bytes < (1ull << 31)) {
-    const int R = a.sh == 1 ? 4 : 2;
+    // output rows per thread: 8 at stride 1 (10 input rows for 8 output
+    // rows), 1 at stride 2 (measured at batch 32: 96@112 s1 4.9-5.0 TB/s
+    // against 4.6-4.9 with 4 rows, 144@56 s1 5.8-5.9 against 5.6; s2 6.5
+    // and 5.3-5.5 against 6.4 and 5.1 with 2 rows)
+    const int R = a.sh == 1 ? 8 : 1;
     const int64_t threads = (int64_t)a.planes * ceil_div(oh, R) * ((ow + 3) / 4);
     const dim3 grid((unsigned)ceil_div(threads, 256));
 #define NHIP_DW3(S_, R_, V_)                                                                            \
@@ -746,10 +750,10 @@ int launch_dwconv_f32(const nhip_conv_plan* p, const float* in, float* out,
     NHIP_LAUNCH("dw3x3s" #S_ "_f32", (dw3x3_f32_kernel<S_, R_, V_>), grid, dim3(256), 0, s, a, (uint32_t)x_bytes); \
     return check_launch("dw3x3_f32");                                                                   \
   }
-    NHIP_DW3(1, 4, true)
-    NHIP_DW3(1, 4, false)
-    NHIP_DW3(2, 2, true)
-    NHIP_DW3(2, 2, false)
+    NHIP_DW3(1, 8, true)
+    NHIP_DW3(1, 8, false)
+    NHIP_DW3(2, 1, true)
+    NHIP_DW3(2, 1, false)
 #undef NHIP_DW3
   }
   int64_t lds = 0;
