@@ -1297,6 +1297,36 @@ int run_ops(nhip_graph& g, int n, const std::vector<Shape>& sh, const void* cons
   }
   TRY(grow(g, &g.ws, &g.ws_cap, std::max<uint64_t>(ws_need, 256), capturing));
   for (size_t i = 0; i < g.inputs.size(); ++i) ptr[g.inputs[i]] = (char*)inputs[i];
+  // Outputs written in place: a graph output computed by an op goes
+  // straight into the caller's buffer (no copy after the last op) when that
+  // buffer is 256-byte aligned (as the kernels' own buffers are) and overlaps
+  // none of the graph's inputs (which later ops may still read).  Views and
+  // pass-through inputs, and a blob listed twice after its first listing,
+  // are copied as before.
+  std::vector<char*> direct(g.blobs.size(), nullptr);
+  std::vector<char> copied(g.outputs.size(), 1);
+  {
+    std::vector<char> computed(g.blobs.size(), 0);
+    for (const Op& op : g.ops)
+      if (op.kind != OpKind::Input && op.kind != OpKind::Alias) computed[op.out] = 1;
+    for (size_t j = 0; j < g.outputs.size(); ++j) {
+      const int b = g.outputs[j];
+      char* o = static_cast<char*>(outputs[j]);
+      const uint64_t ob = (uint64_t)n * sh[b].elems() * esize(g.blobs[b].dtype);
+      bool ok = computed[b] && direct[b] == nullptr && (reinterpret_cast<uintptr_t>(o) & 255) == 0;
+      for (size_t i = 0; ok && i < g.inputs.size(); ++i) {
+        const int ib = g.inputs[i];
+        const char* in = static_cast<const char*>(inputs[i]);
+        const uint64_t inb = (uint64_t)n * sh[ib].elems() * esize(g.blobs[ib].dtype);
+        if (o < in + inb && in < o + ob) ok = false;
+      }
+      if (ok) {
+        direct[b] = o;
+        copied[j] = 0;
+      }
+    }
+  }
+  auto out_buf = [&](int b) { return direct[b] ? direct[b] : (char*)g.blobs[b].buf; };
   std::vector<char> fused(g.ops.size(), 0);  // ops folded into their consumer
   // Pooling -> InnerProduct runs fused only with NHIP_GAP_IP=1.  Measured on
   // the MobileNetV2 head at batch 32 (1280@7x7 -> 1000): fused 13.5 us +
@@ -1325,7 +1355,7 @@ int run_ops(nhip_graph& g, int n, const std::vector<Shape>& sh, const void* cons
     if (op.kind == OpKind::IP && op.fuse_from >= 0 && fused[op.fuse_from]) {
       const Op& gp = g.ops[op.fuse_from];
       const Shape& a = sh[gp.in[0]];
-      ptr[op.out] = (char*)g.blobs[op.out].buf;
+      ptr[op.out] = out_buf(op.out);
       TRY(nhip_global_avgpool_innerproduct_f32_forward(op.ip, (const float*)ptr[gp.in[0]], (float*)ptr[op.out], n,
                                                        (int32_t)a.d[0], (int32_t)a.d[1], (int32_t)a.d[2], g.ws,
                                                        g.ws_cap, stream));
@@ -1334,7 +1364,7 @@ int run_ops(nhip_graph& g, int n, const std::vector<Shape>& sh, const void* cons
     if (op.kind == OpKind::ConvF32 && op.fuse_from >= 0 && fused[op.fuse_from]) {
       const Op& d = g.ops[op.fuse_from];
       const Shape& a = sh[d.in[0]];
-      ptr[op.out] = (char*)g.blobs[op.out].buf;
+      ptr[op.out] = out_buf(op.out);
       TRY(nhip_dwconv2d_pw_f32_forward(d.conv, op.conv, (const float*)ptr[d.in[0]],
                                        op.residual >= 0 ? (const float*)ptr[op.residual] : nullptr,
                                        (float*)ptr[op.out], n, (int32_t)a.d[1], (int32_t)a.d[2], stream));
@@ -1344,7 +1374,7 @@ int run_ops(nhip_graph& g, int n, const std::vector<Shape>& sh, const void* cons
       ptr[op.out] = ptr[op.in[0]];
       continue;
     }
-    ptr[op.out] = (char*)g.blobs[op.out].buf;
+    ptr[op.out] = out_buf(op.out);
     const Shape& a = sh[op.in[0]];
     char* in = ptr[op.in[0]];
     char* out = ptr[op.out];
@@ -1413,6 +1443,7 @@ int run_ops(nhip_graph& g, int n, const std::vector<Shape>& sh, const void* cons
     }
   }
   for (size_t j = 0; j < g.outputs.size(); ++j) {
+    if (!copied[j]) continue;
     const int b = g.outputs[j];
     TRY(nhip_memcpy_d2d(outputs[j], ptr[b], (uint64_t)n * sh[b].elems() * esize(g.blobs[b].dtype), stream));
   }

@@ -127,6 +127,34 @@ def test_changing_outputs_stay_eager_and_correct(nhip_env):
         assert torch.equal(o, ref)
 
 
+def test_outputs_written_in_place_or_copied_agree(nhip_env):
+    """An aligned output buffer receives the last layer's result directly (no
+    copy after it); a view 4 bytes past an aligned base, and an output that
+    overlaps the input, are written by a copy after the last layer instead.
+    Each equals the eager result, recorded and replayed as well."""
+    nhip_env.delenv("NHIP_GRAPH_REPLAY", raising=False)
+    g = mobilenet_graph()
+    x = torch.from_numpy(np.random.default_rng(5).uniform(-1, 1, (2, 3, 224, 224)).astype(np.float32)).cuda()
+    ref = eager(g, x, nhip_env)
+    aligned = torch.empty_like(ref)
+    assert aligned.data_ptr() % 256 == 0
+    base = torch.empty(ref.numel() + 1, device="cuda")
+    misaligned = base[1:].view(ref.shape)
+    for out in (aligned, misaligned):
+        for call in range(4):  # eager, eager + recorded, replays
+            out.fill_(float("nan"))
+            g.run(x, out=[out])
+            torch.cuda.synchronize()
+            assert torch.equal(out, ref), f"call {call}, output at {out.data_ptr() % 256} mod 256"
+    # the output over the first bytes of the input: the input must survive
+    # until the last layer, so the result arrives by the final copy
+    xin = x.clone()
+    over = xin.view(-1)[: ref.numel()].view(ref.shape)
+    g.run(xin, out=[over])
+    torch.cuda.synchronize()
+    assert torch.equal(over, ref)
+
+
 def test_buffers_grown_by_a_larger_batch_invalidate_the_recorded_plan(nhip_env):
     """A recorded plan uses the executor's blob buffers; a call with a larger
     batch reallocates them, and the next call with the recorded key must not
