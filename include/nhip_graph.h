@@ -80,7 +80,10 @@ int nhip_graph_infer_shapes(nhip_graph_t graph, const int64_t* input_shapes,
 
 /* Batch execution on device memory: n images per input, inputs[i] and
  * outputs[j] are device pointers of n back-to-back blobs.  input_shapes as in
- * nhip_graph_infer_shapes.  Calls on one graph are serialised (it owns the
+ * nhip_graph_infer_shapes.  An output buffer that is 256-byte aligned and
+ * overlaps no input is written by the layer that computes it (no copy at the
+ * end); other outputs are copied there after the last layer.  Calls on one
+ * graph are serialised (it owns the
  * intermediate buffers).  Kernels run on the device the graph was loaded
  * on; the calling thread's current device is restored afterwards.  On a
  * non-default stream, a call repeating the previous call's batch, shapes,
