@@ -619,6 +619,9 @@ struct Op {
   // the first op, the index of the op that is its output's only consumer;
   // on that op, the first op's index.
   int fuse_into = -1, fuse_from = -1;
+  // a 1x1 convolution whose only consumer is a depthwise op: that op's index
+  // (the pair may run as one kernel, decided at run time)
+  int pwdw_dw = -1;
 };
 
 struct Blob {
@@ -706,6 +709,31 @@ void mark_dw_pw_pairs(nhip_graph& g) {
         break;
       }
     }
+  }
+}
+
+// Candidates for the 1x1 -> depthwise fusion (an inverted-residual block's
+// expand and depthwise): an fp32 convolution without residual, not itself the
+// consumer of a depthwise fusion, whose output blob is read by exactly one op,
+// a depthwise op taking it as input, and is no graph output.  Whether the
+// pair's shapes have a fused kernel is asked at run time.
+void mark_pw_dw_pairs(nhip_graph& g) {
+  std::vector<int> uses(g.blobs.size(), 0);
+  std::vector<int> consumer(g.blobs.size(), -1);
+  for (size_t j = 0; j < g.ops.size(); ++j) {
+    for (int b : g.ops[j].in) {
+      ++uses[b];
+      consumer[b] = (int)j;
+    }
+    if (g.ops[j].residual >= 0) ++uses[g.ops[j].residual];
+  }
+  for (int b : g.outputs) ++uses[b];
+  for (size_t i = 0; i < g.ops.size(); ++i) {
+    Op& c = g.ops[i];
+    if (c.kind != OpKind::ConvF32 || c.residual >= 0 || c.fuse_from >= 0 || uses[c.out] != 1 || consumer[c.out] < 0)
+      continue;
+    const Op& d = g.ops[consumer[c.out]];
+    if (d.kind == OpKind::DwF32 && d.in.size() == 1 && d.in[0] == c.out) c.pwdw_dw = consumer[c.out];
   }
 }
 
@@ -1224,6 +1252,7 @@ int build(nhip_graph& g, std::vector<Layer>& layers, const int64_t* input_shapes
     if (op.kind != OpKind::Input && !consumed.count(op.out)) g.outputs.push_back(op.out);
   if (g.inputs.empty() || g.outputs.empty()) return fail(NHIP_STATUS_CONSTRAINT_VIOLATION, "graph needs inputs and outputs");
   mark_dw_pw_pairs(g);
+  mark_pw_dw_pairs(g);
   mark_gap_ip_pairs(g);
   return ok();
 }
@@ -1335,9 +1364,30 @@ int run_ops(nhip_graph& g, int n, const std::vector<Shape>& sh, const void* cons
   // output split, and one kernel gets either re-read planes or large split-K
   // partials.
   const bool gap_ip = nhip::setting_int("NHIP_GAP_IP", 0) != 0;
+  std::vector<char> done(g.ops.size(), 0);  // depthwise ops run with their 1x1 producer
   for (size_t oi = 0; oi < g.ops.size(); ++oi) {
     const Op& op = g.ops[oi];
-    if (op.kind == OpKind::Input) continue;
+    if (op.kind == OpKind::Input || done[oi]) continue;
+    if (op.kind == OpKind::ConvF32 && op.pwdw_dw >= 0) {
+      // expand -> depthwise in one kernel, unless the depthwise runs fused
+      // into the 1x1 after it (that pair's kernel is preferred where it runs)
+      const Op& d = g.ops[op.pwdw_dw];
+      const Shape& a = sh[op.in[0]];
+      int32_t sup = 0;
+      if (d.fuse_into >= 0)
+        TRY(nhip_dwconv2d_pw_f32_supported(d.conv, g.ops[d.fuse_into].conv, n, (int32_t)a.d[1], (int32_t)a.d[2],
+                                           &sup));
+      if (!sup) {
+        TRY(nhip_conv1x1_dw_f32_supported(op.conv, d.conv, n, (int32_t)a.d[1], (int32_t)a.d[2], &sup));
+        if (sup) {
+          ptr[d.out] = out_buf(d.out);
+          TRY(nhip_conv1x1_dw_f32_forward(op.conv, d.conv, (const float*)ptr[op.in[0]], (float*)ptr[d.out], n,
+                                          (int32_t)a.d[1], (int32_t)a.d[2], stream));
+          done[op.pwdw_dw] = 1;
+          continue;
+        }
+      }
+    }
     if (op.kind == OpKind::DwF32 && op.fuse_into >= 0) {
       const Shape& a = sh[op.in[0]];
       int32_t sup = 0;

@@ -232,6 +232,12 @@ int launch_conv_pointwise_f32(const nhip_conv_plan* p, const float* in, const fl
 // A 3x3 depthwise convolution feeding a 1x1 convolution, in one pass
 // (pointwise.hip): dwpw_supported says whether the pair and shape qualify.
 bool dwpw_supported(const nhip_conv_plan* dw, const nhip_conv_plan* pw, int n, int h, int w);
+// expand_dw.hip: a 1x1 expand convolution and the 3x3 depthwise reading it,
+// one kernel for planes of at most 256 pixels (the expanded tensor never
+// reaches memory); pwdw_supported says whether the pair and shape qualify.
+bool pwdw_supported(const nhip_conv_plan* pw, const nhip_conv_plan* dw, int n, int h, int w);
+int launch_pwdw_f32(const nhip_conv_plan* pw, const nhip_conv_plan* dw, const float* in, float* out, int n, int h,
+                    int w, hipStream_t s);
 int launch_dwpw_f32(const nhip_conv_plan* dw, const nhip_conv_plan* pw, const float* in, const float* residual,
                     float* out, int n, int h, int w, hipStream_t s);
 int launch_conv_winograd_f32(const nhip_conv_plan* p, const float* in,

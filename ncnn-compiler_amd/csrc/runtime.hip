@@ -810,6 +810,37 @@ int nhip_dwconv2d_pw_f32_forward(nhip_conv_t dw, nhip_conv_t pw, const float* in
   });
 }
 
+int nhip_conv1x1_dw_f32_supported(nhip_conv_t pw, nhip_conv_t dw, int32_t n, int32_t h, int32_t w,
+                                  int32_t* supported) {
+  if (!pw || !dw || !supported) return fail(NHIP_STATUS_NULL_POINTER, "conv1x1_dw_supported: null pointer");
+  if (n < 0 || h <= 0 || w <= 0) return fail(NHIP_STATUS_INVALID_SHAPE, "conv1x1_dw_supported: invalid extent");
+  *supported = pwdw_supported(pw, dw, std::max(1, std::min<int32_t>(n, 65535)), h, w) ? 1 : 0;
+  return ok();
+}
+
+int nhip_conv1x1_dw_f32_forward(nhip_conv_t pw, nhip_conv_t dw, const float* input, float* output, int32_t n,
+                                int32_t h, int32_t w, void* stream) {
+  int oh = 0, ow = 0;
+  if (!pw) return fail(NHIP_STATUS_NULL_POINTER, "conv1x1_dw_forward: null plan");
+  NHIP_TRY(check_forward(dw, input, output, n, h, w, &oh, &ow));
+  if (dw->kind != PlanKind::DwConvF32 || pw->kind != PlanKind::ConvF32 || dw->g.c != pw->g.k)
+    return fail(NHIP_STATUS_CONSTRAINT_VIOLATION,
+                "conv1x1_dw_forward: needs an fp32 convolution and an fp32 depthwise plan over its outputs");
+  if (n == 0) return ok();
+  const int64_t in_img = (int64_t)pw->g.c * h * w, out_img = (int64_t)dw->g.k * oh * ow;
+  return for_each_subbatch(n, 4 * std::max(in_img, out_img), [&](int i0, int nb) {
+    // the grid's y extent is the batch
+    for (int j0 = 0; j0 < nb; j0 += 65535) {
+      const int nj = std::min(65535, nb - j0);
+      if (!pwdw_supported(pw, dw, nj, h, w))
+        return fail(NHIP_STATUS_UNSUPPORTED, "conv1x1_dw_forward: this pair or shape has no fused kernel");
+      NHIP_TRY(launch_pwdw_f32(pw, dw, input + (i0 + j0) * in_img, output + (i0 + j0) * out_img, nj, h, w,
+                               as_stream(stream)));
+    }
+    return ok();
+  });
+}
+
 int nhip_dwconv2d_int8_create(const nhip_conv_desc* d, const void* weight, int32_t weight_is_i8, const float* bias,
                               const float* weight_scale, int32_t weight_scale_count, float input_scale,
                               float output_scale, nhip_conv_t* plan) {

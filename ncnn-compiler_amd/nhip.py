@@ -40,6 +40,7 @@ EXPORTS = (
     "nhip_conv2d_int8_create", "nhip_conv2d_int8_forward",
     "nhip_dwconv2d_f32_create", "nhip_dwconv2d_f32_forward",
     "nhip_dwconv2d_pw_f32_supported", "nhip_dwconv2d_pw_f32_forward",
+    "nhip_conv1x1_dw_f32_supported", "nhip_conv1x1_dw_f32_forward",
     "nhip_dwconv2d_int8_create", "nhip_dwconv2d_int8_forward",
     "nhip_conv_destroy", "nhip_innerproduct_f32_create",
     "nhip_innerproduct_int8_create", "nhip_innerproduct_int8_forward",
@@ -117,6 +118,8 @@ def load():
         "nhip_dwconv2d_f32_forward": [_P, _P, _P, i32, i32, i32, _P],
         "nhip_dwconv2d_pw_f32_supported": [_P, _P, i32, i32, i32, ctypes.POINTER(i32)],
         "nhip_dwconv2d_pw_f32_forward": [_P, _P, _P, _P, _P, i32, i32, i32, _P],
+        "nhip_conv1x1_dw_f32_supported": [_P, _P, i32, i32, i32, ctypes.POINTER(i32)],
+        "nhip_conv1x1_dw_f32_forward": [_P, _P, _P, _P, i32, i32, i32, _P],
         "nhip_dwconv2d_int8_create": [D, _P, i32, _P, _P, i32, f32, f32, ctypes.POINTER(_P)],
         "nhip_dwconv2d_int8_forward": [_P, _P, i32, _P, i32, i32, i32, _P],
         "nhip_innerproduct_int8_create": [i32, i32, _P, i32, _P, _P, f32, i32, ctypes.POINTER(_P)],
@@ -387,6 +390,27 @@ def dwconv_pw_forward(dw: "DwConv2dF32", pw: "Conv2dF32", x, residual=None, out=
     res = None if residual is None else _dev(residual, torch.float32)
     check(load().nhip_dwconv2d_pw_f32_forward(dw.handle, pw.handle, _ptr(x), _ptr(res), _ptr(out), n, h, w,
                                                _stream(stream)))
+    return out
+
+
+def conv1x1_dw_supported(pw: "Conv2dF32", dw: "DwConv2dF32", n: int, h: int, w: int) -> bool:
+    """Whether a 1x1 convolution plan feeding a depthwise plan has the fused
+    kernel for n images of h x w (nhip_conv1x1_dw_f32_supported)."""
+    sup = ctypes.c_int32()
+    check(load().nhip_conv1x1_dw_f32_supported(pw.handle, dw.handle, n, h, w, ctypes.byref(sup)))
+    return bool(sup.value)
+
+
+def conv1x1_dw_forward(pw: "Conv2dF32", dw: "DwConv2dF32", x, out=None, stream=None):
+    """dw(pw(x)) in one pass without the 1x1 output in memory
+    (nhip_conv1x1_dw_f32_forward; the graph executor's fusion)."""
+    torch = _torch()
+    x = _dev(x, torch.float32)
+    n, c, h, w = x.shape
+    oh, ow = output_shape(dw.desc, h, w)
+    if out is None:
+        out = torch.empty((n, dw.desc.num_output, oh, ow), dtype=torch.float32, device=x.device)
+    check(load().nhip_conv1x1_dw_f32_forward(pw.handle, dw.handle, _ptr(x), _ptr(out), n, h, w, _stream(stream)))
     return out
 
 
