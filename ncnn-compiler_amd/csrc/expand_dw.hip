@@ -49,6 +49,7 @@ constexpr int kMaxC = 256;  // input channels: C/4 A registers per lane
 struct EdArgs {
   const float* x;   // [N][C][H][W]
   const float* w1;  // [m_pad][ldw1], k = c (1x1)
+  const float* w1q; // the same weights as [rows/32][C/4][32][4], or null
   const float* b1;  // [m_pad] (zero past K)
   const float* wd;  // [K][9]
   const float* bd;  // [K]
@@ -85,19 +86,20 @@ __device__ __forceinline__ void depthwise_strips(const float* es, const float* w
   const float inv_t = 1.f / (float)T, inv_ow = 1.f / (float)OW;
   const int OHW = OH * OW;
   for (int e = tid; e < nch * T; e += kThreads) {
+    // (24-bit multiplies: every product here is below 2^23)
     const int c = (int)(((float)e + 0.5f) * inv_t);
-    const int rem = e - c * T;
+    const int rem = e - __mul24(c, T);
     const int rb = (int)(((float)rem + 0.5f) * inv_ow);
-    const int ox = rem - rb * OW;
-    const float* ec = es + c * PS + ox * S;
+    const int ox = rem - __mul24(rb, OW);
+    const float* ec = es + __mul24(c, PS) + ox * S;
     float w[9];
 #pragma unroll
-    for (int t = 0; t < 9; ++t) w[t] = wds[c * 9 + t];
+    for (int t = 0; t < 9; ++t) w[t] = wds[__mul24(c, 9) + t];
     const float bias = bds[c];
     const int oy0 = rb * kStrip;
-    float* yc = yo + (int64_t)c * OHW + ox;
+    float* yc = yo + __mul24(c, OHW) + ox;
     auto row = [&](int r, float* v) {
-      const float* q = ec + min(r, H + 1) * PW;
+      const float* q = ec + __mul24(min(r, H + 1), PW);
       v[0] = q[0];
       v[1] = q[1];
       v[2] = q[2];
@@ -117,7 +119,7 @@ __device__ __forceinline__ void depthwise_strips(const float* es, const float* w
 #pragma unroll
       for (int kw = 0; kw < 3; ++kw) sum = __fadd_rn(sum, __fmul_rn(r2[kw], w[6 + kw]));
       sum = __fadd_rn(sum, bias);
-      if (oy0 + i < OH) yc[(oy0 + i) * OW] = act_of(sum, actd);
+      if (oy0 + i < OH) yc[__mul24(oy0 + i, OW)] = act_of(sum, actd);
 #pragma unroll
       for (int kw = 0; kw < 3; ++kw) {
         if (S == 1) {
@@ -160,13 +162,23 @@ __global__ __launch_bounds__(kThreads) void expand_dw_kernel(EdArgs a) {
   // float4, W1[k0 + 16 grp + l%16][16 q + 4 g ..+ 3], and four lanes read 64
   // contiguous bytes of a weight row (rows are 16-float aligned; rows past K
   // are the plan's zero padding up to m_pad)
+  // (grouped layout: lane group g's float4 of step q is group 4q + g of the
+  // row's 32-row block, so 16 lanes read 256 contiguous bytes)
   float av[NK];
   {
     const int row = k0 + 16 * grp + (lane & 15);
-    const float4* wr = reinterpret_cast<const float4*>(a.w1 + (int64_t)row * a.ldw1) + (lane >> 4);
+    const float4* wr;
+    int step;  // float4s from group q to group q + 1 of the lane
+    if (a.w1q) {
+      wr = reinterpret_cast<const float4*>(a.w1q) + ((int64_t)(row >> 5) * NK + (lane >> 4)) * 32 + (row & 31);
+      step = 4 * 32;
+    } else {
+      wr = reinterpret_cast<const float4*>(a.w1 + (int64_t)row * a.ldw1) + (lane >> 4);
+      step = 4;
+    }
 #pragma unroll
     for (int q = 0; q < NK / 4; ++q) {
-      const float4 v = wr[4 * q];
+      const float4 v = wr[q * step];
       av[4 * q] = v.x;
       av[4 * q + 1] = v.y;
       av[4 * q + 2] = v.z;
@@ -222,46 +234,53 @@ __global__ __launch_bounds__(kThreads) void expand_dw_kernel(EdArgs a) {
   for (int t = 0; t < TH; ++t) acc[t] = v4f{0.f, 0.f, 0.f, 0.f};
   const int t0 = half * TH;
   const float* xb = xs + 4 * (lane >> 4) * HW + (lane & 15) + 16 * t0;
+  // step j + 1's B values are read while step j's MFMAs run
+  float bv_cur[TH], bv_next[TH];
+#pragma unroll
+  for (int t = 0; t < TH; ++t) bv_cur[t] = xb[16 * t];
 #pragma unroll  // whole: av[j] stays in registers
   for (int j = 0; j < NK; ++j) {
-    const float* xr = xb + (16 * (j >> 2) + (j & 3)) * HW;
+    if (j + 1 < NK) {
+      const float* xr = xb + (16 * ((j + 1) >> 2) + ((j + 1) & 3)) * HW;
 #pragma unroll
-    for (int t = 0; t < TH; ++t) acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[j], xr[16 * t], acc[t], 0, 0, 0);
+      for (int t = 0; t < TH; ++t) bv_next[t] = xr[16 * t];
+    }
+#pragma unroll
+    for (int t = 0; t < TH; ++t) acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[j], bv_cur[t], acc[t], 0, 0, 0);
+    // scheduling order: the next step's LDS reads, then this step's MFMAs
+    // (left alone, the compiler reads each value right before its MFMA and
+    // waits for it there)
+    __builtin_amdgcn_sched_group_barrier(0x100, TH, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, TH, 0);
+#pragma unroll
+    for (int t = 0; t < TH; ++t) bv_cur[t] = bv_next[t];
   }
   __syncthreads();  // every wave done with the input planes
 
-  // ---- 3. expanded planes with a zero border (bias + act1 on the interior),
-  // PS floats apart: the four register rows of an MFMA result, 4 planes
-  // apart, fall on different LDS banks
+  // ---- 3. expanded planes, PS floats apart (the four register rows of an
+  // MFMA result, 4 planes apart, fall on different LDS banks): zeros first,
+  // then the interiors, bias + act1.  Planes past K come out zero (zero
+  // weight rows and bias) and are never read.
   float* es = xs;
+  for (int e = tid; e < kSlice * PS / 4; e += kThreads) reinterpret_cast<float4*>(es)[e] = float4{0.f, 0.f, 0.f, 0.f};
+  __syncthreads();
   {
-    // the border cells of the 64 planes, flat: top row, bottom row, then the
-    // two side cells of each interior row
-    const int nb = 2 * PW + 2 * a.H;
-    const float inv_nb = 1.f / (float)nb;  // e / nb exact as below (e < 64 nb)
-    for (int e = tid; e < kSlice * nb; e += kThreads) {
-      const int c = (int)(((float)e + 0.5f) * inv_nb);
-      const int b = e - c * nb, sb = b - 2 * PW;
-      const int pos = b < PW ? b : b < 2 * PW ? (a.H + 1) * PW + (b - PW) : (1 + (sb >> 1)) * PW + ((sb & 1) ? a.W + 1 : 0);
-      es[c * PS + pos] = 0.f;
-    }
-  }
-  {
-    const int k = k0 + chw;
     // p / W as (p + 1/2) / W in fp32, exact for p < 256: the quotient is at
     // least 1/(2W) >= 1/512 from an integer, the rounding error below 2^-15
     const float inv_w = 1.f / (float)a.W;
+    const bool relu = a.act1 == NHIP_ACT_RELU;
+    float* eb = es + __mul24(chw, PS) + PW + 1;  // interior origin of the lane's first plane
 #pragma unroll
     for (int t = 0; t < TH; ++t) {
       const int p = 16 * (t0 + t) + (lane & 15);
       if (p < HW) {
-        const int py = (int)(((float)p + 0.5f) * inv_w), px = p - py * a.W;
-        const int o = (py + 1) * PW + px + 1;
+        const int py = (int)(((float)p + 0.5f) * inv_w), px = p - __mul24(py, a.W);
+        float* ep = eb + __mul24(py, PW) + px;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           // the 1x1 layer's epilogue: sum + bias, then the activation
-          const float v = (k + r < a.K) ? act_of(__fadd_rn(acc[t][r], bv[r]), a.act1) : 0.f;
-          es[(chw + r) * PS + o] = v;
+          const float v = __fadd_rn(acc[t][r], bv[r]);
+          ep[r * PS] = (relu && v < 0.f) ? 0.f : v;
         }
       }
     }
@@ -345,6 +364,10 @@ int launch_pwdw_f32(const nhip_conv_plan* pw, const nhip_conv_plan* dw, const fl
   EdArgs a{};
   a.x = in;
   a.w1 = pw->weight;
+  // the grouped copy when its rows (K rounded up to 32) cover every 64-row slice
+  a.w1q = pw->weight_kq != nullptr && pw->kq_vw == 4 && round_up(pw->g.k, 32) == round_up(pw->g.k, 64)
+              ? pw->weight_kq
+              : nullptr;
   a.b1 = pw->bias;
   a.wd = dw->weight;
   a.bd = dw->bias;
