@@ -1,6 +1,5 @@
 // An inverted-residual block's 1x1 expand convolution and the 3x3 depthwise
-// convolution that reads it, in one kernel, for small planes (at most 256
-// pixels: MobileNetV2's 14x14 and 7x7 blocks).  Same operations as the two
+// convolution that reads it, in one kernel.  Same operations as the two
 // layers (reference ConvertConvolution, NCNNToTosa.cpp:1316-1529, and
 // ConvertDepthwiseConvolution, :3074-3503):
 //
@@ -9,28 +8,31 @@
 //
 // with e zero-padded by one pixel (padding 1), stride s = 1 or 2.
 //
-// A workgroup owns one image and a slice of 64 expanded channels, so the
-// whole plane of every channel it expands is its own: the depthwise halo is
-// in the workgroup and nothing is computed twice, and the expanded tensor
-// never reaches memory (at 14x14, batch 32, 96 -> 576 channels: 14.5 MB
+// A workgroup owns one image, a slice of SL = 32 or 64 expanded channels and
+// a strip of R output rows (the whole plane where it fits: MobileNetV2's
+// 14x14 and 7x7 blocks), so the expanded values its depthwise outputs read
+// are all its own: the strip's input rows plus a one-row halo are expanded
+// (the halo rows twice, by the two strips that need them) and the expanded
+// tensor never reaches memory (at 56x56, batch 32, 24 -> 144 channels: 58 MB
 // written and read back by the two separate layers).
-//   1. The image's input planes [C][HW], one contiguous block in NCHW, are
-//      copied into LDS as they lie (16-byte loads, eight in flight per
-//      thread), then 16 x PT zeros past the last plane; the 64 x 9 depthwise
-//      weights and biases beside them.  An MFMA column past HW reads the next
-//      plane's first pixels (or the zeros), and lands in a pixel that is not
-//      stored.
-//   2. Eight waves: wave w owns expanded channels 16 (w % 4) .. + 15 of the
-//      slice and half of the plane's 16-pixel tiles (w / 4 picks which):
-//      v_mfma_f32_16x16x4_f32, A = W1 (the wave's C/4 k-steps preloaded into
-//      registers from the plan's row-major weights, 16-byte loads), B = x
-//      from LDS.
+//   1. The strip's input rows of every channel come into LDS as they lie
+//      (16-byte loads, eight in flight per thread; the whole plane as one
+//      contiguous block), zero channels up to a multiple of 16, and zeros
+//      past the block; the depthwise weights and biases beside them.  An
+//      MFMA column past the strip reads the next channel's first pixels (or
+//      the zeros), and lands in a pixel that is not stored.
+//   2. Eight waves: wave w owns expanded channels 16 (w % G) .. + 15 of the
+//      slice (G = SL / 16 channel groups) and every (8 / G)-th run of TQ
+//      16-pixel tiles: v_mfma_f32_16x16x4_f32, A = W1 (the wave's k-steps
+//      preloaded into registers with 16-byte loads), B = x from LDS, the
+//      next k-step's B values read while the current step's MFMAs run.
 //      Register r of lane l of tile t is channel 4 (l / 16) + r of the
 //      wave's group, pixel 16 t + l % 16.  Two waves per SIMD keep one
 //      wave's LDS and memory latency behind the other's work in every
 //      phase.
 //   3. After a barrier the input's LDS holds the expanded planes instead,
-//      each (H + 2) x (W + 2) with a zero border: e + b1, act1.
+//      (rows of the strip's window) x (W + 2), zero outside the image: e + b1,
+//      act1.
 //   4. Every thread takes column strips of 7 outputs (channel, rows, column)
 //      and forms each depthwise sum in the reference's order (zero, += e * w
 //      over kh then kw, + bias, activation; separately rounded, no fused
@@ -43,8 +45,10 @@ namespace nhip {
 namespace {
 
 constexpr int kThreads = 512;
-constexpr int kSlice = 64;  // expanded channels per workgroup (4 channel groups x 16)
-constexpr int kMaxC = 256;  // input channels: C/4 A registers per lane
+constexpr int kWaves = kThreads / 64;
+constexpr int kMaxSlice = 64;  // expanded channels per workgroup, at most
+constexpr int kInFlight = 8;   // loads per thread issued before their LDS writes
+constexpr int kStrip = 7;      // depthwise outputs per lane task: a column strip of 7 rows
 
 struct EdArgs {
   const float* x;   // [N][C][H][W]
@@ -55,41 +59,43 @@ struct EdArgs {
   const float* bd;  // [K]
   float* y;         // [N][K][OH][OW]
   int C, K, H, W, OH, OW, s, ldw1, act1, actd;
-  int vec;          // x is 16-byte aligned: the block is copied in float4s
+  int R;            // output rows per strip (gridDim.z strips)
+  int vec;          // x is 16-byte aligned
 };
 
-constexpr int kInFlight = 8;  // loads per thread issued before their LDS writes
-
-// LDS floats from one expanded plane to the next: (H + 2) (W + 2) rounded up
+// LDS floats from one expanded plane to the next: rows x (W + 2) rounded up
 // to 4 more than a multiple of 16
-__host__ __device__ __forceinline__ int plane_stride(int h, int w) { return ((h + 2) * (w + 2) + 15) / 16 * 16 + 4; }
+__host__ __device__ __forceinline__ int plane_stride(int rows, int w) { return (rows * (w + 2) + 15) / 16 * 16 + 4; }
 
 __device__ __forceinline__ float act_of(float v, int act) { return (act == NHIP_ACT_RELU && v < 0.f) ? 0.f : v; }
 
-constexpr int kStrip = 7;  // depthwise outputs per lane task: a column strip of 7 rows
+// x / d for x >= 0 as (x + 1/2) * (1/d) in fp32: exact while quotient * d <
+// 2^21 (every use here; the LDS bounds the operands): (x + 1/2) / d is at
+// least 1/(2d) from an integer, the computed value within q * 2^-22 of it.
+__device__ __forceinline__ int div_small(int x, float inv_d) { return (int)(((float)x + 0.5f) * inv_d); }
 
 // The depthwise layer over the slice's padded planes (es: channel c at
-// c * PS, rows of PW floats, zero border).  A task is (channel, strip of
-// kStrip output rows, output column); consecutive threads take consecutive
-// columns, so each output row of a strip is one coalesced run.  The 3 x 3
-// window slides down the strip in registers: S new rows of 3 values per
-// output instead of 9.  Every output is the reference's sum: zero, += e * w
-// over (kh, kw) in order, + bias, activation, each step separately rounded.
-// Rows past OH (the last strip's) are formed from clamped rows and not stored.
+// c * PS, `rows` rows of PW floats, zero outside the image), for the strip's
+// `roh` output rows; yo is the strip's first output row of channel 0, OHW
+// the output's channel stride.  A task is (channel, run of kStrip output
+// rows, output column); consecutive threads take consecutive columns, so
+// each output row of a run is one coalesced store.  The 3 x 3 window slides
+// down the run in registers: S new rows of 3 values per output instead of 9.
+// Every output is the reference's sum: zero, += e * w over (kh, kw) in order,
+// + bias, activation, each step separately rounded.  Rows past roh (the last
+// run's) are formed from clamped rows and not stored.
 template <int S>
 __device__ __forceinline__ void depthwise_strips(const float* es, const float* wds, const float* bds, float* yo,
-                                                 int nch, int H, int PW, int PS, int OH, int OW, int actd, int tid) {
-  const int nrb = (OH + kStrip - 1) / kStrip;
+                                                 int nch, int rows, int PW, int PS, int roh, int OW, int OHW,
+                                                 int actd, int tid) {
+  const int nrb = (roh + kStrip - 1) / kStrip;
   const int T = nrb * OW;  // tasks per channel
-  // e / T and r / OW as (x + 1/2) / d in fp32: exact, the quotients are below
-  // 256 and at least 1/(2d) >= 1/512 from an integer
   const float inv_t = 1.f / (float)T, inv_ow = 1.f / (float)OW;
-  const int OHW = OH * OW;
   for (int e = tid; e < nch * T; e += kThreads) {
     // (24-bit multiplies: every product here is below 2^23)
-    const int c = (int)(((float)e + 0.5f) * inv_t);
+    const int c = div_small(e, inv_t);
     const int rem = e - __mul24(c, T);
-    const int rb = (int)(((float)rem + 0.5f) * inv_ow);
+    const int rb = div_small(rem, inv_ow);
     const int ox = rem - __mul24(rb, OW);
     const float* ec = es + __mul24(c, PS) + ox * S;
     float w[9];
@@ -99,7 +105,7 @@ __device__ __forceinline__ void depthwise_strips(const float* es, const float* w
     const int oy0 = rb * kStrip;
     float* yc = yo + __mul24(c, OHW) + ox;
     auto row = [&](int r, float* v) {
-      const float* q = ec + __mul24(min(r, H + 1), PW);
+      const float* q = ec + __mul24(min(r, rows - 1), PW);
       v[0] = q[0];
       v[1] = q[1];
       v[2] = q[2];
@@ -119,7 +125,7 @@ __device__ __forceinline__ void depthwise_strips(const float* es, const float* w
 #pragma unroll
       for (int kw = 0; kw < 3; ++kw) sum = __fadd_rn(sum, __fmul_rn(r2[kw], w[6 + kw]));
       sum = __fadd_rn(sum, bias);
-      if (oy0 + i < OH) yc[__mul24(oy0 + i, OW)] = act_of(sum, actd);
+      if (oy0 + i < roh) yc[__mul24(oy0 + i, OW)] = act_of(sum, actd);
 #pragma unroll
       for (int kw = 0; kw < 3; ++kw) {
         if (S == 1) {
@@ -135,23 +141,46 @@ __device__ __forceinline__ void depthwise_strips(const float* es, const float* w
   }
 }
 
-// PT = 16-pixel tiles of a plane (ceil(H*W / 16)); NK = C / 4 k-steps.
-template <int PT, int NK>
+// Strip geometry of workgroup z: output rows oy0 .. oy0 + roh - 1 read
+// expanded rows iy_lo .. iy_lo + rows - 1 (iy_lo = oy0 * s - 1), of which
+// the image holds iy_a .. iy_a + rows_in - 1.
+struct Strip {
+  int oy0, roh, iy_lo, rows, iy_a, rows_in;
+};
+__host__ __device__ __forceinline__ Strip strip_of(int z, int R, int OH, int H, int s) {
+  Strip t;
+  t.oy0 = z * R;
+  t.roh = min(R, OH - t.oy0);
+  t.iy_lo = t.oy0 * s - 1;
+  t.rows = (t.roh - 1) * s + 3;
+  t.iy_a = max(t.iy_lo, 0);
+  t.rows_in = min(t.iy_lo + t.rows - 1, H - 1) - t.iy_a + 1;
+  return t;
+}
+
+// TQ = 16-pixel tiles per wave; NK = C_pad / 4 k-steps (C_pad: C rounded up
+// to 16); SL = expanded channels per workgroup.
+template <int TQ, int NK, int SL>
 __global__ __launch_bounds__(kThreads) void expand_dw_kernel(EdArgs a) {
+  constexpr int G = SL / 16, WPG = kWaves / G;  // channel groups, waves per group
+  constexpr int CP = NK * 4;
   extern __shared__ __attribute__((aligned(16))) float lds[];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int k0 = blockIdx.x * kSlice, img = blockIdx.y;
+  const int k0 = blockIdx.x * SL, img = blockIdx.y;
+  const Strip st = strip_of(blockIdx.z, a.R, a.OH, a.H, a.s);
   const int HW = a.H * a.W, OHW = a.OH * a.OW;
-  const int PW = a.W + 2;  // padded expanded plane: (H + 2) x PW
-  const int PS = plane_stride(a.H, a.W);
-  // LDS: [input planes, later expanded planes][64 x 9 depthwise weights][64 biases]
-  const int tot = NK * 4 * HW;  // floats of the image's input block
-  const int region = max(tot + 16 * PT, kSlice * PS);
+  const int HWs = st.rows_in * a.W;  // pixels of the strip's input block, per channel
+  const int PW = a.W + 2;            // padded expanded rows
+  const int PS = plane_stride(st.rows, a.W);
+  // LDS: [input block, later expanded planes][SL x 9 depthwise weights][SL biases]
+  const int tot = CP * HWs;
+  constexpr int kSlack = 16 * WPG * TQ;  // zeros past the block
+  const int region = max(tot + kSlack, SL * PS);
   float* xs = lds;
   float* wds = lds + region;
-  float* bds = wds + kSlice * 9;
-  const int grp = wave & 3, half = wave >> 2;
+  float* bds = wds + SL * 9;
+  const int grp = wave % G, part = wave / G;
   const int chw = 16 * grp + 4 * (lane >> 4);  // slice channel of MFMA register 0
 
   // ---- 1. every global read of the phase is issued before the first LDS
@@ -160,10 +189,10 @@ __global__ __launch_bounds__(kThreads) void expand_dw_kernel(EdArgs a) {
   // k-step j of lane group g = l / 16 reduces input channel
   // 16 (j / 4) + 4 g + j % 4, so the A operand of steps 4q .. 4q + 3 is one
   // float4, W1[k0 + 16 grp + l%16][16 q + 4 g ..+ 3], and four lanes read 64
-  // contiguous bytes of a weight row (rows are 16-float aligned; rows past K
-  // are the plan's zero padding up to m_pad)
-  // (grouped layout: lane group g's float4 of step q is group 4q + g of the
-  // row's 32-row block, so 16 lanes read 256 contiguous bytes)
+  // contiguous bytes of a weight row (rows are 16-float aligned and zero
+  // past C; rows past K are the plan's zero padding up to m_pad).  Grouped
+  // layout: lane group g's float4 of step q is group 4q + g of the row's
+  // 32-row block, so 16 lanes read 256 contiguous bytes.
   float av[NK];
   {
     const int row = k0 + 16 * grp + (lane & 15);
@@ -188,93 +217,127 @@ __global__ __launch_bounds__(kThreads) void expand_dw_kernel(EdArgs a) {
   float bv[4];  // the 1x1 layer's bias for the lane's 4 channels
 #pragma unroll
   for (int r = 0; r < 4; ++r) bv[r] = a.b1[k0 + chw + r];
-  static_assert(kSlice * 9 <= 2 * kThreads && kSlice <= kThreads, "depthwise parameters: two per thread");
-  const int nch = min(kSlice, a.K - k0);
+  static_assert(kMaxSlice * 9 <= 2 * kThreads && kMaxSlice <= kThreads, "depthwise parameters: two per thread");
+  const int nch = min(SL, a.K - k0);
   const int e1 = tid + kThreads;
   const float wd0 = tid < nch * 9 ? a.wd[(int64_t)k0 * 9 + tid] : 0.f;
   const float wd1 = e1 < nch * 9 ? a.wd[(int64_t)k0 * 9 + e1] : 0.f;
   const float bd0 = tid < nch ? a.bd[k0 + tid] : 0.f;
-  const float* xi = a.x + (int64_t)img * a.C * HW;
-  if (a.vec) {
-    // C is a multiple of 4, so the block is whole float4s
-    const float4* src = reinterpret_cast<const float4*>(xi);
-    const int n4 = tot >> 2;
-    for (int base = tid; base < n4; base += kThreads * kInFlight) {
-      float4 v[kInFlight];
-      // every load issued (index clamped to the block), only in-range ones stored
+  const float* xi = a.x + (int64_t)img * a.C * HW + (int64_t)st.iy_a * a.W;
+  const int treal = a.C * HWs;  // input values; channels C .. CP - 1 are zeros
+  if (st.rows_in == a.H) {
+    // the whole plane: the image's channels are one contiguous block
+    if (a.vec && treal % 4 == 0) {
+      const float4* src = reinterpret_cast<const float4*>(xi);
+      const int n4 = treal >> 2;
+      for (int base = tid; base < n4; base += kThreads * kInFlight) {
+        float4 v[kInFlight];
+        // every load issued (index clamped to the block), only in-range ones stored
 #pragma unroll
-      for (int i = 0; i < kInFlight; ++i) v[i] = src[min(base + i * kThreads, n4 - 1)];
+        for (int i = 0; i < kInFlight; ++i) v[i] = src[min(base + i * kThreads, n4 - 1)];
 #pragma unroll
-      for (int i = 0; i < kInFlight; ++i)
-        if (base + i * kThreads < n4) reinterpret_cast<float4*>(xs)[base + i * kThreads] = v[i];
+        for (int i = 0; i < kInFlight; ++i)
+          if (base + i * kThreads < n4) reinterpret_cast<float4*>(xs)[base + i * kThreads] = v[i];
+      }
+    } else {
+      for (int base = tid; base < treal; base += kThreads * kInFlight) {
+        float v[kInFlight];
+#pragma unroll
+        for (int i = 0; i < kInFlight; ++i) v[i] = xi[min(base + i * kThreads, treal - 1)];
+#pragma unroll
+        for (int i = 0; i < kInFlight; ++i)
+          if (base + i * kThreads < treal) xs[base + i * kThreads] = v[i];
+      }
     }
   } else {
-    for (int base = tid; base < tot; base += kThreads * kInFlight) {
-      float v[kInFlight];
+    // a strip: rows iy_a .. of each channel, HWs contiguous values per
+    // channel; element e is (c, e - c * n)
+    if (a.vec && a.W % 4 == 0) {
+      const int n = HWs / 4, tn = a.C * n;
+      const float inv_n = 1.f / (float)n;
+      for (int base = tid; base < tn; base += kThreads * kInFlight) {
+        float4 v[kInFlight];
 #pragma unroll
-      for (int i = 0; i < kInFlight; ++i) v[i] = xi[min(base + i * kThreads, tot - 1)];
+        for (int i = 0; i < kInFlight; ++i) {
+          const int e = min(base + i * kThreads, tn - 1);
+          const int c = div_small(e, inv_n);
+          v[i] = reinterpret_cast<const float4*>(xi + (int64_t)c * HW)[e - c * n];
+        }
 #pragma unroll
-      for (int i = 0; i < kInFlight; ++i)
-        if (base + i * kThreads < tot) xs[base + i * kThreads] = v[i];
+        for (int i = 0; i < kInFlight; ++i)
+          if (base + i * kThreads < tn) reinterpret_cast<float4*>(xs)[base + i * kThreads] = v[i];
+      }
+    } else {
+      const int n = HWs, tn = a.C * n;
+      const float inv_n = 1.f / (float)n;
+      for (int base = tid; base < tn; base += kThreads * kInFlight) {
+        float v[kInFlight];
+#pragma unroll
+        for (int i = 0; i < kInFlight; ++i) {
+          const int e = min(base + i * kThreads, tn - 1);
+          const int c = div_small(e, inv_n);
+          v[i] = xi[(int64_t)c * HW + (e - c * n)];
+        }
+#pragma unroll
+        for (int i = 0; i < kInFlight; ++i)
+          if (base + i * kThreads < tn) xs[base + i * kThreads] = v[i];
+      }
     }
   }
-  if (tid < 16 * PT) xs[tot + tid] = 0.f;
-  wds[tid] = wd0;
-  if (e1 < kSlice * 9) wds[e1] = wd1;
-  if (tid < kSlice) bds[tid] = bd0;
-  // tiles of a half: half * TH .. half * TH + TH - 1; for odd PT the last one
-  // is past the plane (its reads stay in the LDS allocation, its pixels are
-  // not stored)
-  constexpr int TH = (PT + 1) / 2;
+  for (int i = treal + tid; i < tot + kSlack; i += kThreads) xs[i] = 0.f;
+  if (tid < SL * 9) wds[tid] = wd0;
+  if (e1 < SL * 9) wds[e1] = wd1;
+  if (tid < SL) bds[tid] = bd0;
   __syncthreads();
 
-  // ---- 2. expand: the wave's 16 channels x its half of the pixel tiles
-  v4f acc[TH];
+  // ---- 2. expand: the wave's 16 channels x its tiles part * TQ .. + TQ - 1
+  // (tiles past the strip compute values that are not stored; their reads
+  // stay inside the block and the zeros after it)
+  v4f acc[TQ];
 #pragma unroll
-  for (int t = 0; t < TH; ++t) acc[t] = v4f{0.f, 0.f, 0.f, 0.f};
-  const int t0 = half * TH;
-  const float* xb = xs + 4 * (lane >> 4) * HW + (lane & 15) + 16 * t0;
+  for (int t = 0; t < TQ; ++t) acc[t] = v4f{0.f, 0.f, 0.f, 0.f};
+  const int t0 = part * TQ;
+  const float* xb = xs + 4 * (lane >> 4) * HWs + (lane & 15) + 16 * t0;
   // step j + 1's B values are read while step j's MFMAs run
-  float bv_cur[TH], bv_next[TH];
+  float bv_cur[TQ], bv_next[TQ];
 #pragma unroll
-  for (int t = 0; t < TH; ++t) bv_cur[t] = xb[16 * t];
+  for (int t = 0; t < TQ; ++t) bv_cur[t] = xb[16 * t];
 #pragma unroll  // whole: av[j] stays in registers
   for (int j = 0; j < NK; ++j) {
     if (j + 1 < NK) {
-      const float* xr = xb + (16 * ((j + 1) >> 2) + ((j + 1) & 3)) * HW;
+      const float* xr = xb + (16 * ((j + 1) >> 2) + ((j + 1) & 3)) * HWs;
 #pragma unroll
-      for (int t = 0; t < TH; ++t) bv_next[t] = xr[16 * t];
+      for (int t = 0; t < TQ; ++t) bv_next[t] = xr[16 * t];
     }
 #pragma unroll
-    for (int t = 0; t < TH; ++t) acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[j], bv_cur[t], acc[t], 0, 0, 0);
+    for (int t = 0; t < TQ; ++t) acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[j], bv_cur[t], acc[t], 0, 0, 0);
     // scheduling order: the next step's LDS reads, then this step's MFMAs
     // (left alone, the compiler reads each value right before its MFMA and
     // waits for it there)
-    __builtin_amdgcn_sched_group_barrier(0x100, TH, 0);
-    __builtin_amdgcn_sched_group_barrier(0x008, TH, 0);
+    __builtin_amdgcn_sched_group_barrier(0x100, TQ, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, TQ, 0);
 #pragma unroll
-    for (int t = 0; t < TH; ++t) bv_cur[t] = bv_next[t];
+    for (int t = 0; t < TQ; ++t) bv_cur[t] = bv_next[t];
   }
-  __syncthreads();  // every wave done with the input planes
+  __syncthreads();  // every wave done with the input block
 
   // ---- 3. expanded planes, PS floats apart (the four register rows of an
   // MFMA result, 4 planes apart, fall on different LDS banks): zeros first,
-  // then the interiors, bias + act1.  Planes past K come out zero (zero
-  // weight rows and bias) and are never read.
+  // then the rows inside the image, bias + act1.  Planes past K come out
+  // zero (zero weight rows and bias) and are never read.
   float* es = xs;
-  for (int e = tid; e < kSlice * PS / 4; e += kThreads) reinterpret_cast<float4*>(es)[e] = float4{0.f, 0.f, 0.f, 0.f};
+  for (int e = tid; e < SL * PS / 4; e += kThreads) reinterpret_cast<float4*>(es)[e] = float4{0.f, 0.f, 0.f, 0.f};
   __syncthreads();
   {
-    // p / W as (p + 1/2) / W in fp32, exact for p < 256: the quotient is at
-    // least 1/(2W) >= 1/512 from an integer, the rounding error below 2^-15
     const float inv_w = 1.f / (float)a.W;
     const bool relu = a.act1 == NHIP_ACT_RELU;
-    float* eb = es + __mul24(chw, PS) + PW + 1;  // interior origin of the lane's first plane
+    // origin of the lane's first plane: window row of input row iy_a, column 1
+    float* eb = es + __mul24(chw, PS) + (st.iy_a - st.iy_lo) * PW + 1;
 #pragma unroll
-    for (int t = 0; t < TH; ++t) {
+    for (int t = 0; t < TQ; ++t) {
       const int p = 16 * (t0 + t) + (lane & 15);
-      if (p < HW) {
-        const int py = (int)(((float)p + 0.5f) * inv_w), px = p - __mul24(py, a.W);
+      if (p < HWs) {
+        const int py = div_small(p, inv_w), px = p - __mul24(py, a.W);
         float* ep = eb + __mul24(py, PW) + px;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
@@ -287,48 +350,139 @@ __global__ __launch_bounds__(kThreads) void expand_dw_kernel(EdArgs a) {
   }
   __syncthreads();
 
-  // ---- 4. depthwise 3x3 in the reference's order, in column strips
-  float* yo = a.y + ((int64_t)img * a.K + k0) * OHW;
+  // ---- 4. depthwise 3x3 in the reference's order, in column runs
+  float* yo = a.y + ((int64_t)img * a.K + k0) * OHW + (int64_t)st.oy0 * a.OW;
   if (a.s == 1)
-    depthwise_strips<1>(es, wds, bds, yo, nch, a.H, PW, PS, a.OH, a.OW, a.actd, tid);
+    depthwise_strips<1>(es, wds, bds, yo, nch, st.rows, PW, PS, st.roh, a.OW, OHW, a.actd, tid);
   else
-    depthwise_strips<2>(es, wds, bds, yo, nch, a.H, PW, PS, a.OH, a.OW, a.actd, tid);
+    depthwise_strips<2>(es, wds, bds, yo, nch, st.rows, PW, PS, st.roh, a.OW, OHW, a.actd, tid);
 }
 
-int lds_bytes(int C, int PT, int H, int W) {
-  const int region = std::max(C * H * W + 16 * PT, kSlice * plane_stride(H, W));
-  return (region + kSlice * 9 + kSlice) * (int)sizeof(float);
+// A launch configuration: SL expanded channels and R output rows per
+// workgroup, TQ tiles per wave.
+struct EdCfg {
+  int sl = 0, r = 0, tq = 0;
+};
+
+// Instantiated tile counts per wave, by slice width.
+constexpr int kTq64[] = {1, 2, 4, 7, 8};
+constexpr int kTq32[] = {4, 7, 8, 9};
+
+int lds_floats(int cp, int w, int rows, int rows_in, int sl, int tq) {
+  const int wpg = kWaves / (sl / 16);
+  return std::max(cp * rows_in * w + 16 * wpg * tq, sl * plane_stride(rows, w)) + sl * 10;
 }
 
-template <int PT, int NK>
-int launch_one(const EdArgs& a, int n, hipStream_t s) {
-  const int lds = lds_bytes(a.C, PT, a.H, a.W);
-  NHIP_TRY(ensure_dynamic_lds(reinterpret_cast<const void*>(&expand_dw_kernel<PT, NK>), lds));
-  NHIP_LAUNCH("expand_dw_f32", (expand_dw_kernel<PT, NK>), dim3((unsigned)ceil_div(a.K, kSlice), (unsigned)n),
-              dim3(kThreads), lds, s, a);
+// The configuration for an expand (c input channels, k outputs) + depthwise
+// (stride s) pair on h x w planes, or false.  Whole planes take the 64-wide
+// slice when it fits the LDS (one or two workgroups per CU: the 14x14 and
+// 7x7 shapes measured); other planes are cut into strips, the candidate
+// (slice, rows) that fits two workgroups per CU chosen for the least
+// expand work counted with its halo rows and slice padding, scaled up when
+// a 32-image batch would give fewer than two workgroups per CU (the choice
+// does not depend on the batch), strip heights that are whole 7-row
+// depthwise runs first (at 28x28: 7-row strips of 32 channels, 15.3 us at
+// stride 1 against 17.2 for 14-row strips and 19.3 for 5-row ones; 12.0 us
+// at stride 2, the fastest 11.5).  NHIP_PWDW_CFG="sl,r" forces one.
+bool ed_config(int c, int k, int h, int w, int s, EdCfg* out) {
+  const int cp = (int)round_up(c, 16);
+  const int oh = (h - 1) / s + 1;
+  const int nk = cp / 4;
+  int fsl = 0, fr = 0;
+  if (const char* env = setting("NHIP_PWDW_CFG")) std::sscanf(env, "%d,%d", &fsl, &fr);
+  double best = 0;
+  bool found = false;
+  // first pass: strips of whole 7-row depthwise runs (or the whole plane);
+  // second pass, if none fits: any strip height
+  for (int pass = 0; pass < 2 && !found; ++pass)
+  for (int sl : {64, 32}) {
+    if (fsl && sl != fsl) continue;
+    const bool nk_ok = sl == 64 ? (nk == 8 || nk == 16 || nk == 24 || nk == 40) : (nk == 4 || nk == 8);
+    if (!nk_ok) continue;
+    for (int r = oh; r >= 1; --r) {
+      if (fr && r != fr) continue;
+      if (pass == 0 && !fr && r != oh && r % kStrip != 0) continue;
+      const int rows = (r - 1) * s + 3;
+      const int rows_in = std::min(rows, h);
+      const int pt = (int)ceil_div(rows_in * w, 16);
+      const int wpg = kWaves / (sl / 16);
+      const int need = (int)ceil_div(pt, wpg);
+      int tq = 0;
+      if (sl == 64) {
+        for (int v : kTq64)
+          if (v >= need) {
+            tq = v;
+            break;
+          }
+      } else {
+        for (int v : kTq32)
+          if (v >= need) {
+            tq = v;
+            break;
+          }
+      }
+      if (!tq) continue;
+      const int64_t bytes = (int64_t)lds_floats(cp, w, rows, rows_in, sl, tq) * 4;
+      const bool whole = r == oh;
+      if (bytes > (whole ? 160 * 1024 : 80 * 1024)) continue;
+      const int strips = (int)ceil_div(oh, r);
+      const int64_t wgs = ceil_div(k, sl) * (int64_t)strips * 32;
+      double cost = (double)ceil_div(k, sl) * sl * strips * rows * std::max(1.0, 512.0 / (double)wgs);
+      // the whole plane with 64-wide slices where it fits (measured)
+      if (whole && sl == 64 && !fsl) cost = 0;
+      if (!found || cost < best) {
+        found = true;
+        best = cost;
+        *out = EdCfg{sl, r, tq};
+      }
+    }
+  }
+  return found;
+}
+
+template <int TQ, int NK, int SL>
+int launch_one(const EdArgs& a, int n, int strips, int lds, hipStream_t s) {
+  NHIP_TRY(ensure_dynamic_lds(reinterpret_cast<const void*>(&expand_dw_kernel<TQ, NK, SL>), lds));
+  NHIP_LAUNCH("expand_dw_f32", (expand_dw_kernel<TQ, NK, SL>),
+              dim3((unsigned)ceil_div(a.K, SL), (unsigned)n, (unsigned)strips), dim3(kThreads), lds, s, a);
   return check_launch("expand_dw_f32");
 }
 
-template <int PT>
-int launch_pt(const EdArgs& a, int n, hipStream_t s) {
-  switch (a.C / 4) {
-    case 8: return launch_one<PT, 8>(a, n, s);
-    case 16: return launch_one<PT, 16>(a, n, s);
-    case 24: return launch_one<PT, 24>(a, n, s);
-    case 40: return launch_one<PT, 40>(a, n, s);
-    default: return fail(NHIP_STATUS_UNSUPPORTED, "expand + depthwise: input channels outside the kernel's range");
+template <int SL, int NK>
+int launch_tq(const EdArgs& a, int tq, int n, int strips, int lds, hipStream_t s) {
+  if constexpr (SL == 64) {
+    switch (tq) {
+      case 1: return launch_one<1, NK, 64>(a, n, strips, lds, s);
+      case 2: return launch_one<2, NK, 64>(a, n, strips, lds, s);
+      case 4: return launch_one<4, NK, 64>(a, n, strips, lds, s);
+      case 7: return launch_one<7, NK, 64>(a, n, strips, lds, s);
+      case 8: return launch_one<8, NK, 64>(a, n, strips, lds, s);
+    }
+  } else {
+    switch (tq) {
+      case 4: return launch_one<4, NK, 32>(a, n, strips, lds, s);
+      case 7: return launch_one<7, NK, 32>(a, n, strips, lds, s);
+      case 8: return launch_one<8, NK, 32>(a, n, strips, lds, s);
+      case 9: return launch_one<9, NK, 32>(a, n, strips, lds, s);
+    }
   }
+  return fail(NHIP_STATUS_UNSUPPORTED, "expand + depthwise: no kernel for the tile count");
 }
 
 }  // namespace
 
 // Whether the fused kernel takes the pair: an fp32 1x1 stride-1 unpadded
-// convolution on the implicit-GEMM plan (32, 64, 96 or 160 input channels;
-// the 1x1 layers of MobileNetV2's 14x14 and 7x7 blocks) feeding a 3x3
-// depthwise convolution (stride 1 or 2, padding 1, dilation 1) over its
-// channels, activations none or ReLU, planes of at most 256 pixels.
-// NHIP_PWDW=0 never; by default planes of at most 196 pixels (14x14), the
-// shapes measured.
+// convolution on the implicit-GEMM plan (16, 24, 32, 64, 96 or 160 input
+// channels: the expand layers of MobileNetV2) feeding a 3x3 depthwise
+// convolution (stride 1 or 2, padding 1, dilation 1) over its channels,
+// activations none or ReLU, with a configuration that fits the LDS.
+// NHIP_PWDW=0 never; 2 every such pair; by default planes of at most 784
+// pixels.  Measured at batch 32 against the expand followed by the
+// depthwise -> 1x1 pair (or the three layers), expand + depthwise and then
+// the 1x1: 26.1 against 33.6 us at 14x14 (64 -> 384 -> 64), 28.4 against
+// 30.2 at 28x28 (32 -> 192 -> 32), 24.2 against 34.3 at 28x28 stride 2; at
+// 56x56 61.1 against 53.6 and at 112x112 77.5 against 67.9 (many strips,
+// each workgroup's phases serial: per-workgroup latency dominates).
 bool pwdw_supported(const nhip_conv_plan* pw, const nhip_conv_plan* dw, int n, int h, int w) {
   if (!pw || !dw || pw->kind != PlanKind::ConvF32 || dw->kind != PlanKind::DwConvF32) return false;
   const int mode = setting_int("NHIP_PWDW", 1);
@@ -338,22 +492,21 @@ bool pwdw_supported(const nhip_conv_plan* pw, const nhip_conv_plan* dw, int n, i
   if (pw->algorithm != NHIP_CONV_ALGO_IMPLICIT_GEMM || p.kh != 1 || p.kw != 1 || p.sh != 1 || p.sw != 1 || p.pt ||
       p.pb || p.pl || p.pr || pw->kred != p.c)
     return false;
-  if (!(p.c == 32 || p.c == 64 || p.c == 96 || p.c == 160) || p.c > kMaxC || pw->kred_pad % 4) return false;
+  if (!(p.c == 16 || p.c == 24 || p.c == 32 || p.c == 64 || p.c == 96 || p.c == 160)) return false;
+  // the row-major weights' rows hold C rounded up to 16 (zero past C)
+  if (pw->kred_pad < (int)round_up(p.c, 16) || pw->kred_pad % 4) return false;
   if (d.c != p.k || d.k != p.k || d.kh != 3 || d.kw != 3 || d.dh != 1 || d.dw != 1 || d.sh != d.sw ||
       (d.sh != 1 && d.sh != 2) || d.pt != 1 || d.pb != 1 || d.pl != 1 || d.pr != 1)
     return false;
   if ((p.act != NHIP_ACT_NONE && p.act != NHIP_ACT_RELU) || (d.act != NHIP_ACT_NONE && d.act != NHIP_ACT_RELU))
     return false;
-  if (h * w > (mode == 2 ? 256 : 196)) return false;
-  int pt = (int)ceil_div(h * w, 16);
-  for (int c : {2, 4, 8, 13, 16})
-    if (pt <= c) {
-      pt = c;
-      break;
-    }
-  if (lds_bytes(p.c, pt, h, w) > 160 * 1024) return false;
+  if (mode != 2 && h * w > 784) return false;
+  if (h < 1 || w < 1 || w > 4096 || h > 4096) return false;
+  EdCfg c;
+  if (!ed_config(p.c, p.k, h, w, d.sh, &c)) return false;
   const int oh = (h - 1) / d.sh + 1, ow = (w - 1) / d.sw + 1;
-  return (int64_t)n * p.c * h * w < INT32_MAX && (int64_t)n * p.k * oh * ow < INT32_MAX && n <= 65535;
+  return (int64_t)n * p.c * h * w < INT32_MAX && (int64_t)n * p.k * oh * ow < INT32_MAX && n <= 65535 &&
+         ceil_div(oh, c.r) <= 65535;
 }
 
 int launch_pwdw_f32(const nhip_conv_plan* pw, const nhip_conv_plan* dw, const float* in, float* out, int n, int h,
@@ -364,10 +517,6 @@ int launch_pwdw_f32(const nhip_conv_plan* pw, const nhip_conv_plan* dw, const fl
   EdArgs a{};
   a.x = in;
   a.w1 = pw->weight;
-  // the grouped copy when its rows (K rounded up to 32) cover every 64-row slice
-  a.w1q = pw->weight_kq != nullptr && pw->kq_vw == 4 && round_up(pw->g.k, 32) == round_up(pw->g.k, 64)
-              ? pw->weight_kq
-              : nullptr;
   a.b1 = pw->bias;
   a.wd = dw->weight;
   a.bd = dw->bias;
@@ -382,23 +531,35 @@ int launch_pwdw_f32(const nhip_conv_plan* pw, const nhip_conv_plan* dw, const fl
   a.ldw1 = pw->kred_pad;
   a.act1 = pw->g.act;
   a.actd = dw->g.act;
-  // 16-pixel tiles, rounded up to an instantiated count (the tiles past the
-  // plane hold zero pixels)
-  int pt = (int)ceil_div(h * w, 16);
-  for (int c : {2, 4, 8, 13, 16})
-    if (pt <= c) {
-      pt = c;
-      break;
-    }
   a.vec = (reinterpret_cast<uintptr_t>(in) & 15) == 0;
-  switch (pt) {
-    case 2: return launch_pt<2>(a, n, s);
-    case 4: return launch_pt<4>(a, n, s);
-    case 8: return launch_pt<8>(a, n, s);
-    case 13: return launch_pt<13>(a, n, s);
-    case 16: return launch_pt<16>(a, n, s);
-    default: return fail(NHIP_STATUS_UNSUPPORTED, "expand + depthwise: plane size outside the kernel's range");
+  EdCfg c;
+  if (!ed_config(a.C, a.K, h, w, a.s, &c)) return fail(NHIP_STATUS_UNSUPPORTED, "expand + depthwise: no configuration");
+  a.R = c.r;
+  // the grouped copy when its rows (K rounded up to 32) cover every slice and
+  // its channel groups are the kernel's (C a multiple of 16)
+  a.w1q = pw->weight_kq != nullptr && pw->kq_vw == 4 && a.C % 16 == 0 &&
+                  round_up(pw->g.k, 32) == round_up(pw->g.k, c.sl)
+              ? pw->weight_kq
+              : nullptr;
+  const int cp = (int)round_up(a.C, 16);
+  const int rows = (c.r - 1) * a.s + 3;
+  const int lds = lds_floats(cp, w, rows, std::min(rows, h), c.sl, c.tq) * (int)sizeof(float);
+  const int strips = (int)ceil_div(a.OH, c.r);
+  const int nk = cp / 4;
+  if (c.sl == 64) {
+    switch (nk) {
+      case 8: return launch_tq<64, 8>(a, c.tq, n, strips, lds, s);
+      case 16: return launch_tq<64, 16>(a, c.tq, n, strips, lds, s);
+      case 24: return launch_tq<64, 24>(a, c.tq, n, strips, lds, s);
+      case 40: return launch_tq<64, 40>(a, c.tq, n, strips, lds, s);
+    }
+  } else {
+    switch (nk) {
+      case 4: return launch_tq<32, 4>(a, c.tq, n, strips, lds, s);
+      case 8: return launch_tq<32, 8>(a, c.tq, n, strips, lds, s);
+    }
   }
+  return fail(NHIP_STATUS_UNSUPPORTED, "expand + depthwise: input channels outside the kernel's range");
 }
 
 }  // namespace nhip

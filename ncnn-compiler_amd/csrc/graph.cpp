@@ -1369,23 +1369,19 @@ int run_ops(nhip_graph& g, int n, const std::vector<Shape>& sh, const void* cons
     const Op& op = g.ops[oi];
     if (op.kind == OpKind::Input || done[oi]) continue;
     if (op.kind == OpKind::ConvF32 && op.pwdw_dw >= 0) {
-      // expand -> depthwise in one kernel, unless the depthwise runs fused
-      // into the 1x1 after it (that pair's kernel is preferred where it runs)
+      // expand -> depthwise in one kernel where that kernel takes the pair
+      // (its shape policy says where it is preferred); the depthwise's own
+      // fusion into the 1x1 after it is then not used
       const Op& d = g.ops[op.pwdw_dw];
       const Shape& a = sh[op.in[0]];
       int32_t sup = 0;
-      if (d.fuse_into >= 0)
-        TRY(nhip_dwconv2d_pw_f32_supported(d.conv, g.ops[d.fuse_into].conv, n, (int32_t)a.d[1], (int32_t)a.d[2],
-                                           &sup));
-      if (!sup) {
-        TRY(nhip_conv1x1_dw_f32_supported(op.conv, d.conv, n, (int32_t)a.d[1], (int32_t)a.d[2], &sup));
-        if (sup) {
-          ptr[d.out] = out_buf(d.out);
-          TRY(nhip_conv1x1_dw_f32_forward(op.conv, d.conv, (const float*)ptr[op.in[0]], (float*)ptr[d.out], n,
-                                          (int32_t)a.d[1], (int32_t)a.d[2], stream));
-          done[op.pwdw_dw] = 1;
-          continue;
-        }
+      TRY(nhip_conv1x1_dw_f32_supported(op.conv, d.conv, n, (int32_t)a.d[1], (int32_t)a.d[2], &sup));
+      if (sup) {
+        ptr[d.out] = out_buf(d.out);
+        TRY(nhip_conv1x1_dw_f32_forward(op.conv, d.conv, (const float*)ptr[op.in[0]], (float*)ptr[d.out], n,
+                                        (int32_t)a.d[1], (int32_t)a.d[2], stream));
+        done[op.pwdw_dw] = 1;
+        continue;
       }
     }
     if (op.kind == OpKind::DwF32 && op.fuse_into >= 0) {

@@ -1,7 +1,7 @@
 """GPU parity: a 1x1 Convolution feeding a 3x3 ConvolutionDepthWise run as one
 kernel (nhip_conv1x1_dw_f32_forward, the graph executor's fusion of an
-inverted-residual block's expand -> depthwise pair on planes of at most 256
-pixels).
+inverted-residual block's expand -> depthwise pair: whole planes, or row
+strips with a one-row halo).
 
 The fused result is checked against the two layers run separately and
 against the CPU oracle restating the reference's Convolution
@@ -50,6 +50,13 @@ CASES = [
     (2, 64, 12, 9, 100, 1, R, N0),     # 108 pixels: 7 tiles rounded up to 8
     (1, 96, 16, 16, 64, 2, R, R),      # 256 pixels, one slice
     (1, 96, 5, 3, 130, 1, N0, N0),     # 15 pixels: one tile of a plane
+    # row strips (planes the LDS cannot hold whole, or cut for more workgroups)
+    (2, 16, 28, 28, 96, 2, R, R),      # MobileNetV2 block 2's channels (16 -> 96, stride 2)
+    (2, 24, 20, 20, 144, 1, R, R),     # blocks 3 (24 -> 144; channels padded to 32)
+    (1, 24, 17, 13, 48, 2, R, N0),     # odd plane, stride 2
+    (2, 32, 28, 28, 192, 1, R, R),     # blocks 5-6 (32 -> 192 at 28x28)
+    (1, 32, 28, 28, 64, 2, N0, R),     # block 7's stride 2
+    (1, 160, 16, 16, 64, 2, R, R),     # too large for a whole plane: strips of 64-wide slices
 ]
 
 
@@ -84,9 +91,65 @@ def test_expand_dw_fused_matches_separate_and_oracle(case, nhip_env):
     assert max_rel_err(fused, y) <= RTOL
 
 
+# forced (slice width, rows per strip): every strip shape, first / middle /
+# last strips, strips shorter than the kernel's 7-row depthwise runs
+FORCED = [
+    ("32,1", (1, 16, 12, 12, 40, 2)),
+    ("32,2", (1, 16, 20, 16, 32, 2)),
+    ("32,3", (1, 24, 13, 12, 32, 1)),
+    ("32,5", (1, 32, 14, 8, 32, 2)),
+    ("64,3", (1, 64, 14, 14, 96, 1)),
+    ("64,2", (1, 96, 14, 14, 64, 2)),
+    ("32,9", (1, 24, 17, 12, 40, 1)),
+]
+
+
+def _layers(rng, c, k, st, act1, actd):
+    w1 = workloads.he_normal(rng, (k, c, 1, 1), c)
+    b1 = rng.normal(0, 0.05, k).astype(np.float32)
+    wd = workloads.he_normal(rng, (k, 1, 3, 3), 9)
+    bd = rng.normal(0, 0.05, k).astype(np.float32)
+    pw = nhip.Conv2dF32(nhip.conv_desc(c, k, (1, 1), (1, 1), (1, 1), (0, 0, 0, 0), act=act1,
+                                       algorithm=nhip.ALGO_IMPLICIT_GEMM), w1, b1)
+    dw = nhip.DwConv2dF32(nhip.conv_desc(k, k, (3, 3), (st, st), (1, 1), (1, 1, 1, 1), act=actd, group=k), wd, bd)
+    return pw, dw
+
+
+@pytest.mark.parametrize("cfg,case", FORCED, ids=[f[0].replace(",", "x") for f in FORCED])
+def test_expand_dw_forced_strip_configs(cfg, case, nhip_env):
+    nhip_env.setenv("NHIP_PWDW", "2")
+    nhip_env.setenv("NHIP_PWDW_CFG", cfg)
+    n, c, h, w, k, st = case
+    rng = np.random.default_rng(7)
+    pw, dw = _layers(rng, c, k, st, R, R)
+    assert nhip.conv1x1_dw_supported(pw, dw, n, h, w)
+    xd = dev(rng.uniform(-1, 1, (n, c, h, w)).astype(np.float32))
+    fused = host(nhip.conv1x1_dw_forward(pw, dw, xd))
+    separate = host(dw.forward(pw.forward(xd)))
+    assert_close(fused, separate, RTOL, f"forced {cfg} {case}")
+
+
+@pytest.mark.parametrize("h,w", [(14, 14), (7, 7), (20, 20)])
+def test_expand_dw_misaligned_input(h, w, nhip_env):
+    """An input that is not 16-byte aligned takes the 4-byte copies (whole
+    plane and strips)."""
+    nhip_env.setenv("NHIP_PWDW", "2")
+    rng = np.random.default_rng(11)
+    c, k = 32, 64
+    pw, dw = _layers(rng, c, k, 1, R, R)
+    x = rng.uniform(-1, 1, (2, c, h, w)).astype(np.float32)
+    buf = torch.zeros(x.size + 1, dtype=torch.float32, device="cuda")
+    xd = buf[1:].view(2, c, h, w)
+    xd.copy_(torch.from_numpy(x).cuda())
+    assert xd.data_ptr() % 16 != 0
+    fused = host(nhip.conv1x1_dw_forward(pw, dw, xd))
+    separate = host(dw.forward(pw.forward(dev(x))))
+    assert_close(fused, separate, RTOL, f"misaligned {h}x{w}")
+
+
 def test_expand_dw_not_taken_for_unsupported_pairs(nhip_env):
-    """Planes over 256 pixels, other channel counts and a 5x5 depthwise have
-    no fused kernel; the default also leaves planes over 196 pixels alone."""
+    """Other channel counts and a 5x5 depthwise have no fused kernel; the
+    default leaves planes over 784 pixels alone."""
     rng = np.random.default_rng(3)
 
     def plans(c, k, kernel=3):
@@ -101,14 +164,11 @@ def test_expand_dw_not_taken_for_unsupported_pairs(nhip_env):
 
     pw, dw = plans(64, 128)
     assert nhip.conv1x1_dw_supported(pw, dw, 2, 14, 14)
-    assert not nhip.conv1x1_dw_supported(pw, dw, 2, 16, 16)   # 256 pixels: only with NHIP_PWDW=2
-    assert not nhip.conv1x1_dw_supported(pw, dw, 2, 28, 28)
+    assert nhip.conv1x1_dw_supported(pw, dw, 2, 28, 28)
+    assert not nhip.conv1x1_dw_supported(pw, dw, 2, 29, 28)   # over 784 pixels: only with NHIP_PWDW=2
+    assert not nhip.conv1x1_dw_supported(pw, dw, 2, 56, 56)
     nhip_env.setenv("NHIP_PWDW", "2")
-    assert nhip.conv1x1_dw_supported(pw, dw, 2, 16, 16)
-    assert not nhip.conv1x1_dw_supported(pw, dw, 2, 17, 16)
-    pw160, dw160 = plans(160, 64)
-    assert not nhip.conv1x1_dw_supported(pw160, dw160, 1, 16, 16)  # 166 KB of LDS
-    assert nhip.conv1x1_dw_supported(pw160, dw160, 1, 14, 14)
+    assert nhip.conv1x1_dw_supported(pw, dw, 2, 56, 56)       # row strips
     pw2, dw2 = plans(48, 96)
     assert not nhip.conv1x1_dw_supported(pw2, dw2, 2, 14, 14)
     pw3, dw3 = plans(64, 64, kernel=5)
