@@ -193,9 +193,11 @@ int conv_kq_prepack(nhip_conv_plan* p, const float* weight, int c, int k, int kh
 // implicit GEMM; two such images, 392 blocks, 15.0 against 21.1 us on
 // Winograd; at 784 blocks Winograd wins with 64 channels, 25.6 against 26.5
 // us).  1x1: at
-// most one per CU (MobileNetV2 at batch 32, 960 -> 160 + residual at 7x7:
-// 17.0 against 21.4 us; with more blocks the tiled kernels' operand reuse
-// wins: 960 -> 320, 26.7 against 25.0 us) and at least one per eight CUs
+// most one per CU, two for reductions of 768+ channels, taken before the
+// pointwise kernel (MobileNetV2 at batch 32, 7x7: 576 -> 160 9.1 against
+// 16.1 us, 960 -> 160 + residual 13.3 against 13.2, 960 -> 320 18.9
+// against 21.3; at 14x14, 392 blocks, 384 -> 64 + residual 13.0 against
+// 11.4 us on the pointwise kernel) and at least one per eight CUs
 // (MobileNetV2 at batch 1 puts its 7x7 and 14x14 projections, 10 to 21
 // blocks, on this kernel 11 us slower over the graph, its expansions, 60 to
 // 126 blocks, 5 us faster).  NHIP_CONV_KQ=0 never, =2 whenever it can.
@@ -211,7 +213,9 @@ bool kq_supported(const nhip_conv_plan* p, int n, int h, int w, int oh, int ow) 
   if (!k3 && !k1) return false;
   const int64_t npix = (int64_t)n * oh * ow;
   const int64_t blocks = ceil_div(p->g.k, 32) * ceil_div(npix, 32);
-  const int per_cu = k3 ? 2 : 1;
+  // (1x1 with reductions of 768+ channels: up to two blocks per CU; the
+  // long reduction amortizes each block's fixed cost)
+  const int per_cu = k3 || g.c >= 768 ? 2 : 1;
   if (mode != 2 && (blocks > per_cu * (int64_t)cu_count() || (k1 && blocks < cu_count() / 8))) return false;
   return (int64_t)n * g.c * h * w * 4 < INT32_MAX && npix * g.k * 4 < INT32_MAX;
 }

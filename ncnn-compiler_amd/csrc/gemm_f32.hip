@@ -476,8 +476,8 @@ int launch_conv_igemm_f32(const nhip_conv_plan* p, const float* in,
   // (the short-reduction kernel needs no workspace; the size query above
   // keeps the implicit GEMM's, which is then unused)
   if (smallk_supported(p, n, h, w, oh, ow)) return launch_conv_smallk(p, in, residual, out, n, h, w, oh, ow, s);
-  if (pointwise_selected(p, n, h, w)) return launch_conv_pointwise_f32(p, in, residual, out, n, h, w, s);
   if (kq_supported(p, n, h, w, oh, ow)) return launch_conv_kq(p, in, residual, out, n, h, w, oh, ow, s);
+  if (pointwise_selected(p, n, h, w)) return launch_conv_pointwise_f32(p, in, residual, out, n, h, w, s);
   if (pw_dma_supported(p, n, h, w)) return launch_conv_pw_dma(p, in, residual, out, n, h, w, ws, ws_bytes, s);
   GemmArgs g{};
   g.a = p->weight;

@@ -101,7 +101,10 @@ CASES = [
 @pytest.mark.parametrize("case", CASES, ids=lambda c: "x".join(map(str, c[:5])) + ("r" if c[5] else "") + f"a{c[6]}")
 def test_pointwise_matches_oracle(case, nhip_env):
     """Cases with an eighth entry force that configuration (NHIP_PW_CFG):
-    the library leaves those shapes to the implicit GEMM by default."""
+    the library leaves those shapes to the implicit GEMM by default.
+    NHIP_CONV_KQ=0: the one-block-per-CU kernel, tried first, would take
+    some of these shapes (64 -> 384 at 14x14, 576 -> 160 at 7x7)."""
+    nhip_env.setenv("NHIP_CONV_KQ", "0")
     if len(case) > 7:
         nhip_env.setenv("NHIP_PW_CFG", case[7])
     run(*case[:7])
