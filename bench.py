@@ -390,15 +390,24 @@ def config4(nhip, workloads, torch, steps, warmup, share, cpu, target_s):
 
 # ------------------------------------------------------------ config 5
 def pw_kernel_layers(nhip, torch, layers, batch, name="pw_conv_f32"):
-    """The graph's 1x1 layers that run on the streaming 1x1 kernel: 1x1
-    convolutions not fused with a depthwise producer (a fused pair runs as
-    dwpw_fused_f32), each routed once through the layer ABI with the launch
-    timer on `name`.  Returns (launches, algorithmic HBM bytes) per graph
-    run: every such layer reads its input, weights and bias (and residual)
-    once and writes its output once."""
+    """The graph's 1x1 layers that run on the streaming 1x1 kernel, with the
+    executor's fusion decisions: an expand 1x1 whose depthwise consumer the
+    expand + depthwise kernel takes runs as expand_dw_f32 (that depthwise
+    then runs with it, not fused into the 1x1 after it); a 1x1 whose
+    depthwise producer runs fused into it is a dwpw_fused_f32 launch; every
+    other 1x1 goes once through the layer ABI with the launch timer on
+    `name`.  Returns (launches, algorithmic HBM bytes) per graph run for the
+    streaming kernel and (launches, bytes) for the expand + depthwise
+    kernel: each layer reads its input, weights and bias (and residual) once
+    and writes its output once (the fused pair: its input and the
+    depthwise's output)."""
     shapes = {"data": (3, 224, 224)}
-    producer = {}
+    producer, consumers = {}, {}
+    for L in layers:
+        consumers.setdefault(L["src"], []).append(L)
     launches, nbytes = 0, 0.0
+    ed_launches, ed_bytes = 0, 0.0
+    with_expand = set()  # depthwise layers run with their expand
     for L in layers:
         if L["kind"] not in ("conv", "dw"):
             continue
@@ -411,9 +420,23 @@ def pw_kernel_layers(nhip, torch, layers, batch, name="pw_conv_f32"):
         producer[L["dst"]] = L
         if L["kind"] != "conv" or ker != 1:
             continue
-        pw = nhip.Conv2dF32(nhip.conv_desc(c, k, kernel=(1, 1), pad=(0, 0, 0, 0), act=L["act"]), L["w"], L["b"])
+        pw = nhip.Conv2dF32(nhip.conv_desc(c, k, kernel=(1, 1), pad=(0, 0, 0, 0), act=L["act"],
+                                           algorithm=nhip.ALGO_IMPLICIT_GEMM), L["w"], L["b"])
+        cons = consumers.get(L["dst"], [])
+        if not L.get("residual") and len(cons) == 1 and cons[0]["kind"] == "dw":
+            D = cons[0]
+            dw = nhip.DwConv2dF32(nhip.conv_desc(k, k, stride=(D["stride"],) * 2, act=D["act"], group=k),
+                                  D["w"], D["b"])
+            if nhip.conv1x1_dw_supported(pw, dw, batch, h, w):
+                with_expand.add(D["dst"])
+                dh, dwid = (h - 1) // D["stride"] + 1, (w - 1) // D["stride"] + 1
+                ed_launches += 1
+                ed_bytes += 4.0 * (batch * c * h * w + L["w"].size + L["b"].size + D["w"].size + D["b"].size
+                                   + batch * k * dh * dwid)
+                continue
         src = producer.get(L["src"])
-        if src is not None and src["kind"] == "dw" and not L.get("residual") == src["dst"]:
+        if (src is not None and src["kind"] == "dw" and src["dst"] not in with_expand
+                and not L.get("residual") == src["dst"]):
             sc, sh, sw = shapes[src["src"]]
             dw = nhip.DwConv2dF32(nhip.conv_desc(sc, sc, stride=(src["stride"],) * 2, act=src["act"], group=sc),
                                   src["w"], src["b"])
@@ -430,7 +453,7 @@ def pw_kernel_layers(nhip, torch, layers, batch, name="pw_conv_f32"):
             nbytes += 4.0 * (batch * c * h * w + L["w"].size + L["b"].size + batch * k * oh * ow
                              * (2 if L.get("residual") else 1))
         del x, res
-    return launches, nbytes
+    return (launches, nbytes), (ed_launches, ed_bytes)
 
 
 def config5(nhip, torch, steps, warmup, workdir, share, cpu, target_s):
@@ -471,13 +494,23 @@ def config5(nhip, torch, steps, warmup, workdir, share, cpu, target_s):
                           "frac_hbm_peak": round(gbytes / best / 1e9 / PEAK_HBM_GBS, 4)}
     # dominant kernel: the streaming 1x1 kernel (expand / project layers),
     # timed inside the graph (eager: the timer's events need eager launches)
-    pw_launches, pw_bytes = pw_kernel_layers(nhip, torch, layers, BATCH)
+    (pw_launches, pw_bytes), (ed_launches, ed_bytes) = pw_kernel_layers(nhip, torch, layers, BATCH)
     per, sec = kernel_time(nhip, torch, lambda: g.run(x, out=out), steps, "pw_conv_f32")
     assert round(per) == pw_launches, (per, pw_launches)
-    res["roofline"] = roofline("hbm", "pw_conv_f32 (streaming 1x1 convolution: the expand and project layers not "
-                                      "fused with their depthwise; bytes = each layer's input, weights, output "
-                                      "(+ residual) once)", pw_bytes / per, sec, per)
+    res["roofline"] = roofline("hbm", "pw_conv_f32 (streaming 1x1 convolution: the 1x1 layers fused with no "
+                                      "depthwise; bytes = each layer's input, weights, output (+ residual) once)",
+                               pw_bytes / per, sec, per)
     res["roofline"]["step_share"] = round(per * sec / best, 4)
+    # the expand + depthwise kernel (the 28x28, 14x14 and 7x7 blocks), its
+    # share of the step and its bytes against HBM (it is bound by MFMA and
+    # per-workgroup latency rather than by HBM)
+    if ed_launches:
+        per_e, sec_e = kernel_time(nhip, torch, lambda: g.run(x, out=out), steps, "expand_dw_f32")
+        assert round(per_e) == ed_launches, (per_e, ed_launches)
+        res["roofline_expand_dw"] = roofline("hbm", "expand_dw_f32 (1x1 expand + 3x3 depthwise in one kernel; "
+                                                    "bytes = the expand's input and weights, the depthwise "
+                                                    "output, once)", ed_bytes / per_e, sec_e, per_e)
+        res["roofline_expand_dw"]["step_share"] = round(per_e * sec_e / best, 4)
     lib = compile_model(m, "mbv2", workdir)
     if lib is not None:
         lib.mbv2.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
