@@ -518,16 +518,28 @@ __global__ __launch_bounds__(kThreads) void conv_int8_fp_kernel(Int8Args g) {
 // 4-byte LDS word (4 channels) per pixel.  Rows outside the image and the
 // window's columns outside it (the padding) are zero.  The items come in two
 // batches of at most 3 per thread, the first in flight with the weights.
-template <int KS, int TN, bool FQ = false>
-__global__ __launch_bounds__(kThreads) void conv_int8_rw_kernel(Int8Args g) {
+//
+// KP = 2: eight waves, wave w holding channel block w % 4 and half w / 4 of
+// the reduction (18 k steps, 72 weight registers), so that two waves share
+// each SIMD and one's LDS reads and MFMA latency hide behind the other's
+// MFMAs.  After the K loop each wave hands its partner (same channels, other
+// half) the partial blocks the partner finishes through LDS (the window is
+// free by then) and takes the ones it finishes: blocks b with b % 2 == half.
+// Integer sums, so the result is the same in any order.
+template <int KS, int TN, bool FQ = false, int KP = 1>
+__global__ __launch_bounds__(kThreads * KP) void conv_int8_rw_kernel(Int8Args g) {
+  constexpr int NT = kThreads * KP;  // threads of the workgroup
+  constexpr int KSP = KS / KP;       // k steps per wave
+  static_assert(KS % KP == 0 && TN % KP == 0, "whole k steps and pixel blocks per half");
   extern __shared__ __attribute__((aligned(16))) int8_t dsm[];
   int8_t* foot = dsm;
   int* koff_tab = reinterpret_cast<int*>(dsm + g.fp_bytes);  // [KS][2] LDS byte offsets of each k chunk
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int cw = wave & 3, kp = KP == 1 ? 0 : __builtin_amdgcn_readfirstlane(wave >> 2);
   const int li = lane & 31, lh = lane >> 5;
   const int rgs = (g.OH + g.R - 1) / g.R;
   const int img = blockIdx.x / rgs, oy0 = (blockIdx.x % rgs) * g.R;
-  const int ch0 = blockIdx.y * 128 + wave * 32;
+  const int ch0 = blockIdx.y * 128 + cw * 32;
   const int npx = min(g.R, g.OH - oy0) * g.OW;
 
   // ---- footprint loads first (at most 8 per thread, checked on the host),
@@ -547,7 +559,7 @@ __global__ __launch_bounds__(kThreads) void conv_int8_rw_kernel(Int8Args g) {
     const __amdgpu_buffer_rsrc_t xr = make_rsrc(g.xf, g.xf_bytes);
 #pragma unroll
     for (int q = 0; q < kQB; ++q) {
-      const int i = (batch * kQB + q) * kThreads + tid;
+      const int i = (batch * kQB + q) * NT + tid;
       const int rest = fdiv(i, g.xg_div), x4 = i - rest * xgn;
       const int fy = fdiv(rest, g.c4_div), c4 = rest - fy * c4n;
       const int iy = iy_base + fy;
@@ -571,7 +583,7 @@ __global__ __launch_bounds__(kThreads) void conv_int8_rw_kernel(Int8Args g) {
                                quantize_q(qv[q][2][e], g.in_scale), quantize_q(qv[q][3][e], g.in_scale));
       if (qdst[q] == -2) {
         // a row outside the image: its item's pixels and channels are zero
-        const int i = (batch * kQB + q) * kThreads + tid;
+        const int i = (batch * kQB + q) * NT + tid;
         const int rest = fdiv(i, g.xg_div), x4 = i - rest * xgn;
         const int fy = fdiv(rest, g.c4_div), c4 = rest - fy * c4n;
         const int d0 = (fy * g.FW + 4 * x4 + g.pl) * g.FS + 4 * c4;
@@ -590,7 +602,7 @@ __global__ __launch_bounds__(kThreads) void conv_int8_rw_kernel(Int8Args g) {
     const int total = g.FH * g.FW * cpp;
 #pragma unroll
     for (int q = 0; q < 8; ++q) {
-      const int e = q * kThreads + tid;
+      const int e = q * NT + tid;
       const int pix = fdiv(e, g.cpp_div), ch = e - pix * cpp;
       const int fy = fdiv(pix, g.fw_div), fx = pix - fy * g.FW;
       const int iy = iy_base + fy, ix = fx - g.pl;
@@ -603,12 +615,12 @@ __global__ __launch_bounds__(kThreads) void conv_int8_rw_kernel(Int8Args g) {
       fdst[q] = e < total ? (int)__umul24(pix, g.FS) + ch * 16 : -1;
     }
   }
-  v4i wr[KS];
+  v4i wr[KSP];
   {
     // fragment order: this wave's k step s is 1 KB at ((ch0/32)*KS + s) KB
-    const int8_t* wp = g.w + ((int64_t)(ch0 / 32) * KS) * 1024 + lane * 16;
+    const int8_t* wp = g.w + ((int64_t)(ch0 / 32) * KS + kp * KSP) * 1024 + lane * 16;
 #pragma unroll
-    for (int s = 0; s < KS; ++s) wr[s] = *reinterpret_cast<const v4i*>(wp + s * 1024);
+    for (int s = 0; s < KSP; ++s) wr[s] = *reinterpret_cast<const v4i*>(wp + s * 1024);
   }
   const float rc = g.recip[ch0 + li], bs = g.bias[ch0 + li];
   // k chunk q (16 bytes at reduction index 16q, order (kh, kw, c)) -> its
@@ -623,7 +635,7 @@ __global__ __launch_bounds__(kThreads) void conv_int8_rw_kernel(Int8Args g) {
   if constexpr (FQ) {
     // the window's columns outside the image (left and right padding): zero
     const int nh = g.FW - g.W, hz = g.FH * nh * cpp;
-    for (int e = tid; e < hz; e += kThreads) {
+    for (int e = tid; e < hz; e += NT) {
       const int pos = e / cpp, ch = e - pos * cpp;
       const int fy = pos / nh, h = pos - fy * nh;
       const int fx = h < g.pl ? h : g.W + h;
@@ -654,13 +666,37 @@ __global__ __launch_bounds__(kThreads) void conv_int8_rw_kernel(Int8Args g) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[b][r] = 0;
 #pragma unroll
-  for (int s = 0; s < KS; ++s) {
-    const int koff = koff_tab[s * 2 + lh];
+  for (int s = 0; s < KSP; ++s) {
+    const int koff = koff_tab[(kp * KSP + s) * 2 + lh];
     v4i xf[TN];
 #pragma unroll
     for (int b = 0; b < TN; ++b) xf[b] = *reinterpret_cast<const v4i*>(foot + fbase[b] + koff);
 #pragma unroll
     for (int b = 0; b < TN; ++b) acc[b] = __builtin_amdgcn_mfma_i32_32x32x32_i8(xf[b], wr[s], acc[b], 0, 0, 0);
+  }
+  if constexpr (KP == 2) {
+    // exchange through LDS, 16-byte records [channel block][pixel block]
+    // [register quad][lane] (64 KB for TN = 4): every wave done with the
+    // window first
+    v4i* xch = reinterpret_cast<v4i*>(dsm);
+    __syncthreads();
+#pragma unroll
+    for (int b = 0; b < TN; ++b)
+      if (b % 2 != kp)
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4)
+          xch[((cw * TN + b) * 4 + r4) * 64 + lane] =
+              v4i{acc[b][4 * r4], acc[b][4 * r4 + 1], acc[b][4 * r4 + 2], acc[b][4 * r4 + 3]};
+    __syncthreads();
+#pragma unroll
+    for (int b = 0; b < TN; ++b)
+      if (b % 2 == kp)
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4) {
+          const v4i v = xch[((cw * TN + b) * 4 + r4) * 64 + lane];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) acc[b][4 * r4 + e] += v[e];
+        }
   }
 
   // ---- epilogue from registers: channel ch0 + li, pixels 8g + 4lh + q
@@ -679,6 +715,7 @@ __global__ __launch_bounds__(kThreads) void conv_int8_rw_kernel(Int8Args g) {
   };
 #pragma unroll
   for (int b = 0; b < TN; ++b) {
+    if (KP == 2 && b % 2 != kp) continue;  // the partner's block
     if (q8) {
       uint32_t wd[4];  // pixels 8g + 4lh .. + 3 as bytes
 #pragma unroll
@@ -838,6 +875,14 @@ int launch_conv_int8(const nhip_conv_plan* p, const void* in, int in_is_i8,
           r.in_scale = p->input_scale;
           r.xg_div = fast_div((uint32_t)(w / 4));
           r.c4_div = fast_div((uint32_t)(p->g.c / 4));
+          // NHIP_INT8_KSPLIT=1: four waves, each with the whole reduction
+          if (setting_int("NHIP_INT8_KSPLIT", 2) == 2) {
+            const auto kernel = conv_int8_rw_kernel<KS, 4, true, 2>;
+            const int lds2 = (int)std::max<int64_t>(lds, 4 * 4 * 16 * 64 * 4);  // + the exchange
+            NHIP_TRY(ensure_dynamic_lds(reinterpret_cast<const void*>(kernel), lds2));
+            NHIP_LAUNCH("conv_int8_rw_fq", kernel, grid, dim3(2 * kThreads), (unsigned)lds2, s, r);
+            return check_launch("conv_int8_rw_fq");
+          }
           NHIP_LAUNCH("conv_int8_rw_fq", (conv_int8_rw_kernel<KS, 4, true>), grid, dim3(kThreads), (unsigned)lds, s, r);
           return check_launch("conv_int8_rw_fq");
         }

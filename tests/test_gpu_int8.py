@@ -164,15 +164,18 @@ RW_CASES = [
 
 
 @pytest.mark.parametrize("case", RW_CASES, ids=lambda c: "x".join(map(str, c[:5])) + f"-t{c[9]}")
-@pytest.mark.parametrize("rw", ["1", "1q", "2", "0"])
+@pytest.mark.parametrize("rw", ["1", "1k", "1q", "2", "0"])
 def test_int8_register_weight_kernel_bit_exact(case, rw, nhip_env):
     """The register-weight kernel (NHIP_INT8_RW=1, default: four 32-pixel
     blocks per wave, with the input quantized inside its window fill where
-    the shape allows (fp32 input, width and channels multiples of 4); "1q":
-    the same with that fusion off, a separate quantize pass first; =2: two
-    blocks per wave) against the oracle, bit for bit, and with it off (=0:
-    the footprint kernel)."""
+    the shape allows (fp32 input, width and channels multiples of 4), then
+    eight waves splitting the reduction in two halves; "1k": the fused fill
+    on four waves with the whole reduction each (NHIP_INT8_KSPLIT=1); "1q":
+    the fusion off, a separate quantize pass first; =2: two blocks per wave)
+    against the oracle, bit for bit, and with it off (=0: the footprint
+    kernel)."""
     nhip_env.setenv("NHIP_INT8_FUSED_QUANT", "0" if rw == "1q" else "1")
+    nhip_env.setenv("NHIP_INT8_KSPLIT", "1" if rw == "1k" else "2")
     rw = rw[0]
     nhip_env.setenv("NHIP_INT8_RW", rw)
     n, c, h, w, k, ker, st, dl, pad, term, act, scalar = case
