@@ -175,3 +175,28 @@ def test_expand_dw_not_taken_for_unsupported_pairs(nhip_env):
     assert not nhip.conv1x1_dw_supported(pw3, dw3, 2, 14, 14)
     nhip_env.setenv("NHIP_PWDW", "0")
     assert not nhip.conv1x1_dw_supported(pw, dw, 2, 14, 14)
+
+
+def test_expand_dw_random_shapes(nhip_env):
+    """40 seeded random pairs (channels, planes of 1-30 rows and columns,
+    stride, activations, batch) with every plane the kernel takes: the fused
+    result within 1e-4 of the two layers."""
+    nhip_env.setenv("NHIP_PWDW", "2")
+    rng = np.random.default_rng(2024)
+    taken = 0
+    for _ in range(40):
+        c = int(rng.choice([16, 24, 32, 64, 96, 160]))
+        k = int(rng.integers(2, 100)) * 4
+        h, w = int(rng.integers(1, 31)), int(rng.integers(1, 31))
+        st = int(rng.integers(1, 3))
+        n = int(rng.integers(1, 4))
+        a1, ad = (R if rng.random() < 0.7 else N0), (R if rng.random() < 0.7 else N0)
+        pw, dw = _layers(rng, c, k, st, a1, ad)
+        if not nhip.conv1x1_dw_supported(pw, dw, n, h, w):
+            continue
+        taken += 1
+        xd = dev(rng.uniform(-1, 1, (n, c, h, w)).astype(np.float32))
+        fused = host(nhip.conv1x1_dw_forward(pw, dw, xd))
+        separate = host(dw.forward(pw.forward(xd)))
+        assert_close(fused, separate, RTOL, f"random pair c{c} k{k} {h}x{w} s{st} n{n}")
+    assert taken >= 30
