@@ -207,16 +207,17 @@ int nhip_dwconv2d_pw_f32_forward(nhip_conv_t dw, nhip_conv_t pw,
 
 /* No counterpart in the reference (it lowers every layer on its own): an fp32
  * 1x1 stride-1 unpadded Convolution (ConvertConvolution,
- * NCNNToTosa.cpp:1316-1529; implicit-GEMM plan, 32, 64, 96 or 160 input
- * channels) whose output only feeds a 3x3 fp32 ConvolutionDepthWise over its
- * channels (ConvertDepthwiseConvolution, :3074-3503; stride 1 or 2, padding
- * 1), run as one kernel without writing the 1x1 output — the expand ->
- * depthwise pair of an inverted-residual block on small planes, fused by the
- * graph executor.  Results equal nhip_conv2d_f32_forward followed by
- * nhip_dwconv2d_f32_forward within rounding (the 1x1 sum is formed in
- * another order; the depthwise sum in the reference's).  _supported sets
- * *supported to 1 when the pair and the input extent qualify (planes of at
- * most 196 pixels by default); _forward then takes input [n,C,h,w] of pw and
+ * NCNNToTosa.cpp:1316-1529; implicit-GEMM plan, 16, 24, 32, 64, 96 or 160
+ * input channels) whose output only feeds a 3x3 fp32 ConvolutionDepthWise
+ * over its channels (ConvertDepthwiseConvolution, :3074-3503; stride 1 or 2,
+ * padding 1), run as one kernel without writing the 1x1 output (whole planes
+ * or row strips with a one-row halo) — the expand -> depthwise pair of an
+ * inverted-residual block, fused by the graph executor.  Results equal
+ * nhip_conv2d_f32_forward followed by nhip_dwconv2d_f32_forward within
+ * rounding (the 1x1 sum is formed in another order; the depthwise sum in the
+ * reference's).  _supported sets *supported to 1 when the pair and the input
+ * extent qualify (planes of at most 784 pixels by default, any plane the LDS
+ * takes with NHIP_PWDW=2); _forward then takes input [n,C,h,w] of pw and
  * output of dw's shape, device pointers, no workspace. */
 int nhip_conv1x1_dw_f32_supported(nhip_conv_t pw, nhip_conv_t dw, int32_t n,
                                   int32_t h, int32_t w, int32_t* supported);

@@ -62,7 +62,7 @@ CASES = [
 
 @pytest.mark.parametrize("case", CASES, ids=lambda c: "x".join(map(str, c[:5])) + f"s{c[5]}")
 def test_expand_dw_fused_matches_separate_and_oracle(case, nhip_env):
-    nhip_env.setenv("NHIP_PWDW", "2")  # every plane size the kernel takes (default: up to 196 pixels)
+    nhip_env.setenv("NHIP_PWDW", "2")  # every plane the kernel takes (default: up to 784 pixels)
     n, c, h, w, k, st, act1, actd = case
     rng = np.random.default_rng(hash(case) % (2 ** 32))
     x = rng.uniform(-1, 1, (n, c, h, w)).astype(np.float32)
