@@ -72,3 +72,29 @@ def test_native_executor_mobilenetv2_matches_oracle(n):
             s.synchronize()
             check(out[0], what)
     g.close()
+
+
+@pytest.mark.parametrize("mode", ["1", "2"])
+@pytest.mark.parametrize("side", [160, 96])
+def test_native_executor_mobilenetv2_other_resolutions(nhip_env, side, mode):
+    """The MobileNetV2-shape graph declared at 160x160 (planes 80/40/20/10/5)
+    and 96x96 (48/24/12/6/3) through the native executor: the expand ->
+    depthwise pairs run fused as whole planes (up to 784 pixels, the default
+    NHIP_PWDW=1) or also as row strips (NHIP_PWDW=2, the 80x80, 40x40 and
+    48x48 planes), at plane sizes the 224x224 graph never produces.  Logits
+    within 1e-4 of the oracle, same top-1 class."""
+    nhip_env.setenv("NHIP_PWDW", mode)
+    layers = graphs.mobilenetv2_layers(seed=1)
+    m = ncnn_format.from_layer_list(layers, input_shape=(3, side, side))
+    g = nhip.Graph(m.param_text(), bytes(m.payload))
+    n = 3
+    x = np.random.default_rng(side).uniform(-1, 1, (n, 3, side, side)).astype(np.float32)
+    exp = oracle_forward(layers, x)["fc"]
+    got = g.run(torch.from_numpy(x).cuda())[0]
+    torch.cuda.synchronize()
+    got = got.cpu().numpy().reshape(n, -1)
+    g.close()
+    assert got.shape == (n, 1000)
+    assert_close(got, exp, 1e-4, f"native mobilenetv2 {side}x{side} NHIP_PWDW={mode}")
+    assert max_rel_err(got, exp) <= 1e-4
+    np.testing.assert_array_equal(got.argmax(1), exp.argmax(1))
