@@ -179,6 +179,11 @@ struct nhip_conv_plan {
   // layer, for launches of so few tiles that the Winograd GEMM's 128-tile
   // padding dominates (a single 7x7 or 14x14 image).
   nhip_conv_plan* igemm_twin = nullptr;
+  // 1x1 plans with at most 32 output channels: the weights channel-major,
+  // [C][32] (zero past K), the LDS layout of the depthwise -> 1x1 kernel.
+  float* weight_ck = nullptr;
+  // 3x3 depthwise plans: [C][12], the nine taps, the bias, two zeros.
+  float* weight_dw12 = nullptr;
   float* bias = nullptr;      // [m_pad] zero-filled past k (always present)
   int32_t m_pad = 0, kred = 0, kred_pad = 0, c_pad = 0;
   // im2col gather table: one packed int per reduction index
@@ -240,6 +245,12 @@ int launch_pwdw_f32(const nhip_conv_plan* pw, const nhip_conv_plan* dw, const fl
                     int w, hipStream_t s);
 int launch_dwpw_f32(const nhip_conv_plan* dw, const nhip_conv_plan* pw, const float* in, const float* residual,
                     float* out, int n, int h, int w, hipStream_t s);
+// dwpw_lds.hip: the pair with its input rows staged through LDS (up to 32
+// output channels, channels a multiple of 8); taken by launch_dwpw_f32 when
+// dwpw_lds_supported says so (NHIP_DWPW_LDS=0: never).
+bool dwpw_lds_supported(const nhip_conv_plan* dw, const nhip_conv_plan* pw, int n, int h, int w, int oh, int ow);
+int launch_dwpw_lds_f32(const nhip_conv_plan* dw, const nhip_conv_plan* pw, const float* in,
+                        const float* residual, float* out, int n, int h, int w, int oh, int ow, hipStream_t s);
 int launch_conv_winograd_f32(const nhip_conv_plan* p, const float* in,
                              const float* residual, float* out, int n, int h,
                              int w, int oh, int ow, void* ws,

@@ -684,6 +684,8 @@ bool dw_shape_ok(const nhip_conv_plan* dw, int h, int w, int* oh, int* ow) {
   if (dw->kind != PlanKind::DwConvF32 || g.kh != 3 || g.kw != 3 || g.dh != 1 || g.dw != 1 || g.sh != g.sw ||
       (g.sh != 1 && g.sh != 2) || g.pt != 1 || g.pb != 1 || g.pl != 1 || g.pr != 1)
     return false;
+  // the fused kernels apply no depthwise activation other than ReLU
+  if (g.act != NHIP_ACT_NONE && g.act != NHIP_ACT_RELU) return false;
   *oh = (h + 2 - 3) / g.sh + 1;
   *ow = (w + 2 - 3) / g.sw + 1;
   return w % 4 == 0 && *ow % 4 == 0 && *oh > 0;
@@ -730,6 +732,7 @@ bool dwpw_supported(const nhip_conv_plan* dw, const nhip_conv_plan* pw, int n, i
   if (pw->kind != PlanKind::ConvF32 || g.c != dw->g.c || g.kh != 1 || g.kw != 1 || g.sh != 1 || g.sw != 1 || g.pt ||
       g.pb || g.pl || g.pr || pw->algorithm != NHIP_CONV_ALGO_IMPLICIT_GEMM)
     return false;
+  if (dwpw_lds_supported(dw, pw, n, h, w, oh, ow)) return true;
   PwCfg c;
   const int64_t np = (int64_t)n * oh * ow;
   if (!pw_config(pw, np, oh * ow, dw->g.sh, &c)) return false;
@@ -741,6 +744,8 @@ int launch_dwpw_f32(const nhip_conv_plan* dw, const nhip_conv_plan* pw, const fl
                     float* out, int n, int h, int w, hipStream_t s) {
   int oh = 0, ow = 0;
   PwCfg c;
+  if (dw_shape_ok(dw, h, w, &oh, &ow) && dwpw_lds_supported(dw, pw, n, h, w, oh, ow))
+    return launch_dwpw_lds_f32(dw, pw, in, residual, out, n, h, w, oh, ow, s);
   if (!dw_shape_ok(dw, h, w, &oh, &ow) || !pw_config(pw, (int64_t)n * oh * ow, oh * ow, dw->g.sh, &c))
     return fail(NHIP_STATUS_CONSTRAINT_VIOLATION, "depthwise + pointwise: unsupported shape");
   PwArgs a{};

@@ -349,6 +349,8 @@ void free_plan(nhip_conv_plan* p) {
   (void)hipFree(p->weight);
   (void)hipFree(p->weight_fused);
   (void)hipFree(p->weight_kq);
+  (void)hipFree(p->weight_ck);
+  (void)hipFree(p->weight_dw12);
   (void)hipFree(p->bias);
   (void)hipFree(p->ktab);
   (void)hipFree(p->weight_i8);
@@ -576,6 +578,12 @@ int nhip_conv2d_f32_create(const nhip_conv_desc* d, const float* weight, const f
     st = upload(&p->weight, wp, "hipMalloc(conv weight)");
     if (st == NHIP_STATUS_SUCCESS) st = upload(&p->ktab, kt, "hipMalloc(conv ktab)");
     if (st == NHIP_STATUS_SUCCESS) st = conv_kq_prepack(p, weight, C, K, d->kernel_h, d->kernel_w);
+    if (st == NHIP_STATUS_SUCCESS && khw == 1 && K <= 32) {
+      std::vector<float> ck((size_t)C * 32, 0.f);
+      for (int k = 0; k < K; ++k)
+        for (int c = 0; c < C; ++c) ck[(size_t)c * 32 + k] = weight[(size_t)k * C + c];
+      st = upload(&p->weight_ck, ck, "hipMalloc(1x1 weight, channel-major)");
+    }
   }
   if (st == NHIP_STATUS_SUCCESS) st = upload_bias(p, d->bias_term ? bias : nullptr, K, p->m_pad);
   if (st != NHIP_STATUS_SUCCESS) {
@@ -760,6 +768,14 @@ int nhip_dwconv2d_f32_create(const nhip_conv_desc* d, const float* weight, const
   std::vector<float> wv(weight, weight + wcount);
   int st = upload(&p->weight, wv, "hipMalloc(dw weight)");
   if (st == NHIP_STATUS_SUCCESS) st = upload_bias(p, d->bias_term ? bias : nullptr, d->num_output, d->num_output);
+  if (st == NHIP_STATUS_SUCCESS && d->kernel_h == 3 && d->kernel_w == 3) {
+    std::vector<float> w12((size_t)d->num_output * 12, 0.f);
+    for (int c = 0; c < d->num_output; ++c) {
+      std::copy(weight + (size_t)c * 9, weight + (size_t)c * 9 + 9, w12.begin() + (size_t)c * 12);
+      w12[(size_t)c * 12 + 9] = d->bias_term ? bias[c] : 0.f;
+    }
+    st = upload(&p->weight_dw12, w12, "hipMalloc(dw weight, 12-float records)");
+  }
   if (st != NHIP_STATUS_SUCCESS) {
     std::string msg = g_last_error;
     free_plan(p);

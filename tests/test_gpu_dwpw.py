@@ -81,7 +81,12 @@ def oracle(x, stride, dw_act, pw_act, params, residual):
     return z
 
 
-def check_pair(n, c, h, w, k, stride, dw_act, pw_act, res):
+def check_pair(n, c, h, w, k, stride, dw_act, pw_act, res, env=None, lds=False, images=None):
+    """Fused launch against the two layers run separately (bit for bit) and
+    the oracle (on `images`, default all).  lds: the LDS-staged kernel is
+    expected to take the pair; the separate 1x1 layer then runs the
+    streaming kernel's sequential configuration (NHIP_PW_CFG=1,1), whose
+    per-output summation order that kernel shares."""
     dw, pw, params = make(c, k, stride, dw_act, pw_act)
     x = RNG.uniform(-1, 1, (n, c, h, w)).astype(np.float32)
     oh, ow = (h + 2 - 3) // stride + 1, (w + 2 - 3) // stride + 1
@@ -92,9 +97,19 @@ def check_pair(n, c, h, w, k, stride, dw_act, pw_act, res):
     nhip.timer_start("dwpw")
     fused = host(nhip.dwconv_pw_forward(dw, pw, xd, residual=rd))
     assert nhip.timer_stop()[0] == 1
+    nhip.timer_start("dwpw_lds")
+    again = host(nhip.dwconv_pw_forward(dw, pw, xd, residual=rd))
+    assert nhip.timer_stop()[0] == (1 if lds else 0)
+    np.testing.assert_array_equal(again, fused)
+    if lds:
+        env.setenv("NHIP_PW_CFG", "1,1")
     separate = host(pw.forward(dw.forward(xd), residual=rd))
+    if lds:
+        env.delenv("NHIP_PW_CFG")
     np.testing.assert_array_equal(fused, separate)
-    assert_close(fused, oracle(x, stride, dw_act, pw_act, params, r), RTOL, f"dw+pw {(n, c, h, w, k, stride)}")
+    sel = slice(None) if images is None else images
+    exp = oracle(x[sel], stride, dw_act, pw_act, params, r[sel] if res else None)
+    assert_close(fused[sel], exp, RTOL, f"dw+pw {(n, c, h, w, k, stride)}")
 
 
 CASES = [
@@ -112,9 +127,64 @@ CASES = [
 ]
 
 
+@pytest.mark.parametrize("kern", ["lds", "stream"])
 @pytest.mark.parametrize("case", CASES, ids=lambda c: "x".join(map(str, c[:5])) + f"s{c[5]}" + ("r" if c[8] else ""))
-def test_dw_pw_fused_matches_separate_and_oracle(case):
-    check_pair(*case)
+def test_dw_pw_fused_matches_separate_and_oracle(case, kern, nhip_env):
+    """Both fused kernels: the LDS-staged one (channels a multiple of 8, at
+    most 32 output channels) and the streaming 1x1 kernel's depthwise mode
+    (NHIP_DWPW_LDS=0)."""
+    n, c, h, w, k = case[:5]
+    if kern == "lds" and (c % 8 or k > 32):
+        pytest.skip("outside the LDS-staged kernel's shapes (the streaming kernel takes them)")
+    # the LDS-staged kernel is the default at stride 2 only; 2 forces it at stride 1 too
+    nhip_env.setenv("NHIP_DWPW_LDS", "0" if kern == "stream" else "2")
+    check_pair(*case, env=nhip_env, lds=kern == "lds")
+
+
+LDS_CASES = [
+    # (n, c, h, w, k, stride, dw_act, pw_act, residual): bands of 4, 2 and 1
+    # output rows, partial last bands, 16-pixel blocks across row ends
+    (1, 8, 8, 8, 1, 1, R, N0, False),
+    (3, 16, 28, 20, 17, 1, N0, S, True),
+    (2, 40, 20, 40, 32, 2, R, R, True),
+    (5, 24, 12, 16, 16, 2, R, N0, False),
+    (1, 64, 100, 4, 9, 1, R, N0, True),
+    (2, 8, 4, 200, 32, 2, N0, N0, False),
+    (4, 72, 44, 44, 30, 1, R, N0, True),
+]
+
+
+@pytest.mark.parametrize("case", LDS_CASES, ids=lambda c: "x".join(map(str, c[:5])) + f"s{c[5]}")
+def test_dw_pw_lds_shapes(case, nhip_env):
+    nhip_env.setenv("NHIP_DWPW_LDS", "2")
+    check_pair(*case, env=nhip_env, lds=True)
+
+
+MBV2_PAIRS = [
+    # MobileNetV2 at batch 32: blocks 1 (32@112 s1 -> 16), 2 (96@112 s2 ->
+    # 24), 3 (144@56 s1 -> 24 + residual), 4 (144@56 s2 -> 32)
+    (32, 32, 112, 112, 16, 1, R, N0, False),
+    (32, 96, 112, 112, 24, 2, R, N0, False),
+    (32, 144, 56, 56, 24, 1, R, N0, True),
+    (32, 144, 56, 56, 32, 2, R, N0, False),
+]
+
+
+@pytest.mark.parametrize("case", MBV2_PAIRS, ids=lambda c: f"{c[1]}at{c[2]}s{c[5]}to{c[4]}")
+def test_dw_pw_lds_mobilenetv2_batch32(case, nhip_env):
+    """The graph's fused pairs at batch 32 on the LDS-staged kernel (its
+    default at stride 2, forced at stride 1): all 32 images bit for bit
+    against the two layers, images 0 and 31 against the oracle."""
+    nhip_env.setenv("NHIP_DWPW_LDS", "2")
+    check_pair(*case, env=nhip_env, lds=True, images=[0, 31])
+
+
+def test_dw_pw_default_kernel_choice(nhip_env):
+    """Default choice: the LDS-staged kernel at stride 2, the streaming 1x1
+    kernel's depthwise mode at stride 1."""
+    nhip_env.delenv("NHIP_DWPW_LDS", raising=False)
+    for stride, lds in ((2, True), (1, False)):
+        check_pair(2, 48, 16, 16, 24, stride, R, N0, False, env=nhip_env, lds=lds)
 
 
 @pytest.mark.parametrize("stride", [1, 2])
@@ -124,6 +194,7 @@ def test_dw_pw_every_configuration(cfg, stride, nhip_env):
     C = 72: five 16-channel groups, split 2, 1, 1, 1 over four waves, the
     last group partial."""
     nhip_env.setenv("NHIP_PW_CFG", cfg)
+    nhip_env.setenv("NHIP_DWPW_LDS", "0")
     check_pair(2, 72, 12, 16, 70, stride, R, N0, True)
 
 
