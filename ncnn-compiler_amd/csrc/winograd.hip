@@ -28,6 +28,9 @@ namespace nhip {
 int launch_wino_gemm_out(const nhip_conv_plan* p, const float* V, int t_pad, const float* residual, float* out,
                          int n, int oh, int ow, float* parts, hipStream_t s);
 uint64_t wino_gemm_out_parts_bytes(const nhip_conv_plan* p, int n, int oh, int ow);
+bool wino_xt_selected(const nhip_conv_plan* p, int n, int h, int w, int oh, int ow);
+int launch_wino_gemm_xt(const nhip_conv_plan* p, const float* in, const float* residual, float* out, int n, int h,
+                        int w, int oh, int ow, hipStream_t s);
 
 // Path selection: input transform + GEMM with the output transform fused
 // (winograd_fused.hip), or the three-kernel path (M through HBM).
@@ -302,6 +305,8 @@ uint64_t conv_winograd_f32_workspace(const nhip_conv_plan* p, int n, int oh, int
   if (twin_selected(p, n, oh, ow)) return conv_igemm_f32_workspace(p->igemm_twin, n, oh, ow);
   const int th = (int)ceil_div(oh, 4), tw = (int)ceil_div(ow, 4);
   const int64_t t_pad = round_up((int64_t)n * th * tw, 128);
+  if (fused_selected(p, n, oh, ow) && wino_xt_selected(p, n, oh + 2 - p->g.pt - p->g.pb, ow + 2 - p->g.pl - p->g.pr, oh, ow))
+    return 0;  // the input transform inside the GEMM: no V
   if (fused_selected(p, n, oh, ow))  // V, then the GEMM's partial sums
     return (uint64_t)36 * t_pad * p->c_pad * sizeof(float) + wino_gemm_out_parts_bytes(p, n, oh, ow);
   const WinoGemmCfg cfg = wino_gemm_config(p->m_pad, p->c_pad, (int)t_pad);
@@ -325,6 +330,8 @@ int launch_conv_winograd_f32(const nhip_conv_plan* p, const float* in,
   if (twin_selected(p, n, oh, ow))
     return launch_conv_igemm_f32(p->igemm_twin, in, residual, out, n, h, w, oh, ow, ws, ws_bytes, s);
   const bool fused = fused_selected(p, n, oh, ow);
+  if (fused && wino_xt_selected(p, n, h, w, oh, ow))
+    return launch_wino_gemm_xt(p, in, residual, out, n, h, w, oh, ow, s);
   float* V = static_cast<float*>(ws);
   float* M = V + (int64_t)36 * ws_.c_pad * ws_.t_pad;
   {

@@ -61,7 +61,11 @@ constexpr int kLdsBytes = 2 * kPairs * kZRec * (int)sizeof(float);  // Z of both
 constexpr int kXcds = 8;            // MI355X: workgroup L runs on XCD L % 8
 
 struct FusedArgs {
-  const float* V;       // [36][c_pad/4][t_pad][4]
+  const float* V;       // [36][c_pad/4][t_pad][4] (not with XT)
+  const float* x;       // XT: the input [N][C][H][W]
+  uint32_t x_bytes;     // XT: its size (< 2^31)
+  int C, H, W, pt, pl;  // XT: input channels, extent, top / left padding
+  int xvec;             // XT: pl == 1, W % 4 == 0, 16-byte aligned input
   const float* U;       // [36][c_pad/4][m_pad][4]
   const float* bias;    // [m_pad]
   const float* residual;
@@ -87,8 +91,32 @@ __device__ __forceinline__ float activate(float v) {
 // the two 32-channel blocks of a 64-channel block (same tiles) and each
 // runs every chunk; otherwise they share one 32-channel block and take
 // alternate chunks.
-template <int ACT, bool FINAL, bool VEC, bool KS>
+// Row I of B^T (F(4x4, 3x3)) applied to six values.
+template <int I>
+__device__ __forceinline__ float bt_row(float d0, float d1, float d2, float d3, float d4, float d5) {
+  if constexpr (I == 0) return 4.f * d0 - 5.f * d2 + d4;
+  if constexpr (I == 1) return -4.f * (d1 + d2) + d3 + d4;
+  if constexpr (I == 2) return 4.f * (d1 - d2) - d3 + d4;
+  if constexpr (I == 3) return -2.f * (d1 - d3) - d2 + d4;
+  if constexpr (I == 4) return 2.f * (d1 - d3) - d2 + d4;
+  return 4.f * d1 - 5.f * d3 + d5;
+}
+
+// XT: the input transform inside the GEMM (paired channel blocks, one
+// part).  Per 8-channel chunk the workgroup's 256 (tile, channel) patches
+// are transformed by its 768 threads, thread (tile, channel, g) taking rows
+// 2g, 2g+1: first E = d B along its two patch rows (from registers loaded a
+// chunk ahead) into LDS, then, a barrier later, rows 2g, 2g+1 of V = B^T E
+// down the columns into LDS in the B-fragment layout [36][2][32][4], which
+// the twelve waves read instead of V from memory.  One barrier per chunk:
+// chunk c's MFMAs, chunk c+1's V rows and chunk c+2's E rows run between
+// two barriers (two slots each for E and V, 147 KB of LDS).
+constexpr int kXtSlot = 36 * 2 * 32 * 4;  // floats of one E or V slot
+constexpr int kXtLdsBytes = 4 * kXtSlot * (int)sizeof(float);
+
+template <int ACT, bool FINAL, bool VEC, bool KS, bool XT = false>
 __global__ __launch_bounds__(kThreads, 1) void wino_fused_kernel(FusedArgs a) {
+  static_assert(!XT || (KS && FINAL), "the in-kernel transform runs paired channel blocks in one part");
   extern __shared__ __attribute__((aligned(16))) float zs[];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -134,8 +162,9 @@ __global__ __launch_bounds__(kThreads, 1) void wino_fused_kernel(FusedArgs a) {
     const bool live = c < ce && kvalid;
     av[q] = __builtin_bit_cast(
         v4f, __builtin_amdgcn_raw_buffer_load_b128(ur, live ? uoff : kBufOOB, u_base + q * u_xi + (uint32_t)c * u_ch, 0));
-    bv[q] = __builtin_bit_cast(
-        v4f, __builtin_amdgcn_raw_buffer_load_b128(vr, live ? voff : kBufOOB, v_base + q * v_xi + (uint32_t)c * v_ch, 0));
+    if constexpr (!XT)
+      bv[q] = __builtin_bit_cast(
+          v4f, __builtin_amdgcn_raw_buffer_load_b128(vr, live ? voff : kBufOOB, v_base + q * v_xi + (uint32_t)c * v_ch, 0));
   };
   // One chunk: per point its four MFMAs (reduction index: lane half l / 32
   // supplies channel 4 (l / 32) + st at step st, for both operands), then
@@ -160,8 +189,114 @@ __global__ __launch_bounds__(kThreads, 1) void wino_fused_kernel(FusedArgs a) {
   int c = cb + (KS ? 0 : h);
 #pragma unroll
   for (int q = 0; q < 6; ++q) load(c, q);
+  if constexpr (!XT) {
 #pragma unroll
-  for (int q = 0; q < 6; ++q) __builtin_amdgcn_sched_group_barrier(0x020, 2, 0);
+    for (int q = 0; q < 6; ++q) __builtin_amdgcn_sched_group_barrier(0x020, 2, 0);
+  }
+
+  // XT: this thread's patch: tile t0 + xtl, channel 4 xchq + xcq of each
+  // chunk, patch rows 2 xg, 2 xg + 1.
+  const int xg = wave >> 2, xchq = wave & 1, xtl = ((wave >> 1) & 1) * 16 + (lane >> 2), xcq = lane & 3;
+  const int xt = t0 + xtl;
+  int xrow0 = 0, xx0 = 0;  // (image * C) * H + first patch row; first patch column
+  bool xrows_ok[2] = {false, false};
+  float dreg[2][6];
+  const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, XT ? a.x_bytes : 0u);
+  if constexpr (XT) {
+    if (xt < a.T) {
+      const int per_img = a.th * a.tw;
+      const int img = xt / per_img, rem = xt - img * per_img;
+      const int ty = rem / a.tw, tx = rem - ty * a.tw;
+      const int y = 4 * ty - a.pt + 2 * xg;
+      xrow0 = img * a.C * a.H + y;
+      xx0 = 4 * tx - a.pl;
+      xrows_ok[0] = (unsigned)y < (unsigned)a.H;
+      xrows_ok[1] = (unsigned)(y + 1) < (unsigned)a.H;
+    }
+  }
+  // the two patch rows of chunk c (zero outside the image, past C, past T)
+  auto load_d = [&](int cc, float (&dr)[2][6]) {
+    const int chn = cc * kCB + 4 * xchq + xcq;
+    const bool cok = cc < ce && chn < a.C;
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const bool yok = cok && xrows_ok[r];
+      const int rowi = xrow0 + chn * a.H + r;  // < 2^31 elements (checked on the host)
+      if (a.xvec) {
+        const uint32_t rb = (uint32_t)(rowi * a.W) * 4u;
+        dr[r][0] = buf_load_f32(xr, yok && xx0 >= 0 ? rb + (uint32_t)(xx0 * 4) : kBufOOB);
+        const int4 m = buf_load_b128(xr, yok && xx0 + 1 < a.W ? rb + (uint32_t)((xx0 + 1) * 4) : kBufOOB);
+        dr[r][1] = __builtin_bit_cast(float, m.x);
+        dr[r][2] = __builtin_bit_cast(float, m.y);
+        dr[r][3] = __builtin_bit_cast(float, m.z);
+        dr[r][4] = __builtin_bit_cast(float, m.w);
+        dr[r][5] = buf_load_f32(xr, yok && xx0 + 5 < a.W ? rb + (uint32_t)((xx0 + 5) * 4) : kBufOOB);
+      } else {
+#pragma unroll
+        for (int j = 0; j < 6; ++j) {
+          const int xx = xx0 + j;
+          dr[r][j] = buf_load_f32(
+              xr, yok && (unsigned)xx < (unsigned)a.W ? (uint32_t)(rowi * a.W + xx) * 4u : kBufOOB);
+        }
+      }
+    }
+  };
+  // E rows 2xg, 2xg+1 (E[i][q] = row i of d times column q of B) into slot eb,
+  // layout [i][q][chq][tile][cq]
+  auto e_phase = [&](float* eb, const float (&dr)[2][6]) {
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const float* d = dr[r];
+      float* e = eb + ((((2 * xg + r) * 6) * 2 + xchq) * 32 + xtl) * 4 + xcq;
+      e[0 * 256] = bt_row<0>(d[0], d[1], d[2], d[3], d[4], d[5]);
+      e[1 * 256] = bt_row<1>(d[0], d[1], d[2], d[3], d[4], d[5]);
+      e[2 * 256] = bt_row<2>(d[0], d[1], d[2], d[3], d[4], d[5]);
+      e[3 * 256] = bt_row<3>(d[0], d[1], d[2], d[3], d[4], d[5]);
+      e[4 * 256] = bt_row<4>(d[0], d[1], d[2], d[3], d[4], d[5]);
+      e[5 * 256] = bt_row<5>(d[0], d[1], d[2], d[3], d[4], d[5]);
+    }
+  };
+  // V rows p = 2G, 2G+1 (V[p][q] = row p of B^T times column q of E) from
+  // slot eb into slot vb, layout [xi][chq][tile][cq]
+  auto v_rows = [&](auto gc, const float* eb, float* vb) {
+    constexpr int G = decltype(gc)::value;
+#pragma unroll
+    for (int q = 0; q < 6; ++q) {
+      const float* e = eb + ((q * 2 + xchq) * 32 + xtl) * 4 + xcq;  // E[i][q] at + i * 6 * 256
+      const float e0 = e[0], e1 = e[1536], e2 = e[3072], e3 = e[4608], e4 = e[6144], e5 = e[7680];
+      float* v = vb + ((q * 2 + xchq) * 32 + xtl) * 4 + xcq;  // V[p][q] at + p * 6 * 256
+      v[(2 * G) * 1536] = bt_row<2 * G>(e0, e1, e2, e3, e4, e5);
+      v[(2 * G + 1) * 1536] = bt_row<2 * G + 1>(e0, e1, e2, e3, e4, e5);
+    }
+  };
+  auto v_phase = [&](const float* eb, float* vb) {
+    if (xg == 0) v_rows(std::integral_constant<int, 0>{}, eb, vb);
+    else if (xg == 1) v_rows(std::integral_constant<int, 1>{}, eb, vb);
+    else v_rows(std::integral_constant<int, 2>{}, eb, vb);
+  };
+  // XT: one chunk's MFMAs with the B fragments from V slot vb, then the
+  // next chunk's A operands
+  auto chunk_xt = [&](int cc, const float* vb) {
+    const float* vl = vb + ((6 * p * 2 + (lane >> 5)) * 32 + (lane & 31)) * 4;
+    // point q + 1's B fragment read while point q's MFMAs run
+    v4f bq = *reinterpret_cast<const v4f*>(vl);
+#pragma unroll
+    for (int q = 0; q < 6; ++q) {
+      const v4f bn = q < 5 ? *reinterpret_cast<const v4f*>(vl + (q + 1) * 256) : bq;
+#pragma unroll
+      for (int st = 0; st < 4; ++st)
+        acc[q] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[q][st], bq[st], acc[q], 0, 0, 0);
+      load(cc + 1, q);
+      bq = bn;
+    }
+    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // point 0's LDS read
+#pragma unroll
+    for (int q = 0; q < 6; ++q) {
+      if (q < 5) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // the next point's LDS read
+      __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);  // 4 MFMAs
+      __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // 1 vector-memory read
+    }
+  };
 
   // This thread's epilogue pairs (tid < 512), set up while the first
   // chunk's operands are in flight: tile t0 + tid % 32 and, per
@@ -194,10 +329,38 @@ __global__ __launch_bounds__(kThreads, 1) void wino_fused_kernel(FusedArgs a) {
     }
   }
 
-  // The first chunk is peeled, so the loop is entered with the loads in
-  // flight in the loop's own order: the compiler's wait counts at the loop
-  // head are then exact (vmcnt(10) before each point) rather than vmcnt(0).
-  if (c < ce) {
+  if constexpr (XT) {
+    float* const vs0 = zs;
+    float* const vs1 = zs + kXtSlot;
+    float* const es0 = zs + 2 * kXtSlot;
+    float* const es1 = zs + 3 * kXtSlot;
+    // Prologue: the first two chunks' rows requested together, E and V of
+    // chunk 0 and E of chunk 1 formed, chunk 2's rows on their way.
+    {
+      float d1[2][6];
+      load_d(cb, dreg);
+      load_d(cb + 1, d1);
+      e_phase(es0, dreg);
+      __syncthreads();
+      v_phase(es0, vs0);
+      e_phase(es1, d1);
+      load_d(cb + 2, dreg);
+      __syncthreads();
+    }
+    for (int cc = cb; cc < ce; ++cc) {
+      const bool odd = ((cc - cb) & 1) != 0;
+      chunk_xt(cc, odd ? vs1 : vs0);
+      if (cc + 1 < ce) v_phase(odd ? es0 : es1, odd ? vs0 : vs1);
+      if (cc + 2 < ce) {
+        e_phase(odd ? es1 : es0, dreg);
+        load_d(cc + 3, dreg);
+      }
+      __syncthreads();
+    }
+  } else if (c < ce) {
+    // The first chunk is peeled, so the loop is entered with the loads in
+    // flight in the loop's own order: the compiler's wait counts at the loop
+    // head are then exact (vmcnt(10) before each point) rather than vmcnt(0).
     chunk(c);
     for (c += kStep; c < ce; c += kStep) chunk(c);
   }
@@ -346,12 +509,19 @@ __global__ void wino_fused_reduce(ReduceArgs a) {
   }
 }
 
-template <int ACT, bool FINAL, bool VEC, bool KS>
+template <int ACT, bool FINAL, bool VEC, bool KS, bool XT = false>
 int launch_one(const FusedArgs& a, int64_t blocks, hipStream_t s) {
-  NHIP_TRY(ensure_dynamic_lds(reinterpret_cast<const void*>(&wino_fused_kernel<ACT, FINAL, VEC, KS>), kLdsBytes));
-  NHIP_LAUNCH("wino_fused", (wino_fused_kernel<ACT, FINAL, VEC, KS>), dim3((unsigned)blocks), dim3(kThreads),
-              kLdsBytes, s, a);
+  constexpr int lds = XT ? std::max(kXtLdsBytes, kLdsBytes) : kLdsBytes;
+  NHIP_TRY(ensure_dynamic_lds(reinterpret_cast<const void*>(&wino_fused_kernel<ACT, FINAL, VEC, KS, XT>), lds));
+  NHIP_LAUNCH("wino_fused", (wino_fused_kernel<ACT, FINAL, VEC, KS, XT>), dim3((unsigned)blocks), dim3(kThreads),
+              lds, s, a);
   return check_launch("wino_fused");
+}
+
+template <int ACT>
+int launch_xt(const FusedArgs& a, int64_t blocks, hipStream_t s) {
+  return a.OW % 4 == 0 ? launch_one<ACT, true, true, true, true>(a, blocks, s)
+                       : launch_one<ACT, true, false, true, true>(a, blocks, s);
 }
 
 template <int ACT, bool FINAL>
@@ -453,6 +623,14 @@ int launch_fused(const nhip_conv_plan* p, FusedArgs& a, const FusedShape& f, con
   // operand, U (the same output channels) otherwise
   a.kb_fast = a.t_pad >= p->m_pad ? 1 : 0;
   const int64_t blocks = (int64_t)f.nt * f.nk * f.splits;
+  if (a.x != nullptr) {  // XT: the input transform inside the GEMM
+    switch (p->g.act) {
+      case NHIP_ACT_NONE: return launch_xt<NHIP_ACT_NONE>(a, blocks, s);
+      case NHIP_ACT_RELU: return launch_xt<NHIP_ACT_RELU>(a, blocks, s);
+      case NHIP_ACT_SIGMOID: return launch_xt<NHIP_ACT_SIGMOID>(a, blocks, s);
+      default: return fail(NHIP_STATUS_UNSUPPORTED, "winograd GEMM: unsupported activation");
+    }
+  }
   if (f.splits == 1) {
     switch (p->g.act) {
       case NHIP_ACT_NONE: return launch_kernel<NHIP_ACT_NONE, true>(a, blocks, f.ks, s);
@@ -491,6 +669,35 @@ int launch_fused(const nhip_conv_plan* p, FusedArgs& a, const FusedShape& f, con
 }
 
 }  // namespace
+
+// The input transform inside the GEMM (XT) for launches of paired channel
+// blocks in one part (no channel split), unless NHIP_WINO_XT=0: the
+// separate transform's write and re-read of V (2.25x the input's bytes)
+// and its launch go away, for VALU work inside the GEMM.
+bool wino_xt_selected(const nhip_conv_plan* p, int n, int h, int w, int oh, int ow) {
+  if (setting_int("NHIP_WINO_XT", 1) == 0) return false;
+  if ((int64_t)n * p->g.c * h * w >= (int64_t(1) << 31) / 4) return false;  // 32-bit byte offsets into x
+  const FusedShape f = fused_shape(p, n, oh, ow);
+  return f.ks && f.splits == 1;
+}
+
+int launch_wino_gemm_xt(const nhip_conv_plan* p, const float* in, const float* residual, float* out, int n, int h,
+                        int w, int oh, int ow, hipStream_t s) {
+  const FusedShape f = fused_shape(p, n, oh, ow);
+  if (!f.ks || f.splits != 1)
+    return fail(NHIP_STATUS_CONSTRAINT_VIOLATION, "winograd GEMM (in-kernel transform): shape not supported");
+  FusedArgs a{};
+  a.x = in;
+  a.x_bytes = (uint32_t)((size_t)n * p->g.c * h * w * sizeof(float));
+  a.C = p->g.c;
+  a.H = h;
+  a.W = w;
+  a.pt = p->g.pt;
+  a.pl = p->g.pl;
+  a.xvec = p->g.pl == 1 && w % 4 == 0 && (reinterpret_cast<uintptr_t>(in) & 15) == 0;
+  a.t_pad = (int)round_up((int64_t)n * f.th * f.tw, kTB);
+  return launch_fused(p, a, f, residual, out, n, oh, ow, nullptr, s);
+}
 
 int launch_wino_gemm_out(const nhip_conv_plan* p, const float* V, int t_pad, const float* residual, float* out,
                          int n, int oh, int ow, float* parts, hipStream_t s) {

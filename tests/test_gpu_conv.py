@@ -300,6 +300,46 @@ def test_winograd_fused_random_shapes(case, mode, nhip_env):
     assert_close(got, exp, WINO_RTOL, f"winograd fused {case}")
 
 
+XT_CASES = [
+    # (n, c, h, w, k, pad): launches of paired 32-channel blocks, where the
+    # input transform runs inside the GEMM by default: rows not float4-aligned,
+    # left padding 0 and 2, channels not a multiple of 8, an odd number of
+    # 32-channel blocks (the last pair half empty), tiles not a multiple of 32
+    (32, 64, 56, 56, 64, (1, 1, 1, 1)),
+    (9, 24, 30, 22, 72, (1, 1, 1, 1)),
+    (7, 19, 26, 27, 40, (2, 0, 0, 2)),
+    (5, 40, 33, 36, 96, (0, 2, 2, 1)),
+]
+
+
+@pytest.mark.parametrize("case", XT_CASES, ids=lambda c: "x".join(map(str, c[:5])))
+def test_winograd_in_kernel_transform(case, nhip_env):
+    """The fused GEMM forming V from the input itself (no transform launch,
+    no V workspace) against the oracle, and against the separate transform
+    (NHIP_WINO_XT=0) within the Winograd budget."""
+    n, c, h, w, k, pad = case
+    nhip_env.setenv("NHIP_WINOGRAD_VARIANT", "2")
+    nhip_env.setenv("NHIP_WINO_KS", "1")
+    nhip_env.setenv("NHIP_WINO_SPLITS", "1")
+    rng = np.random.default_rng(c * 100 + k)
+    x = rng.uniform(-1, 1, (n, c, h, w)).astype(np.float32)
+    wt = workloads.he_normal(rng, (k, c, 3, 3), c * 9)
+    b = rng.normal(0, 0.05, k).astype(np.float32)
+    oh, ow = h + pad[0] + pad[1] - 2, w + pad[2] + pad[3] - 2
+    res = rng.uniform(-1, 1, (n, k, oh, ow)).astype(np.float32)
+    conv = nhip.Conv2dF32(nhip.conv_desc(c, k, pad=pad, act=nhip.ACT_RELU, algorithm=nhip.ALGO_WINOGRAD), wt, b)
+    assert conv.workspace_size(n, h, w) == 0  # no V
+    nhip.timer_start("wino_input")
+    got = host(conv.forward(dev(x), residual=dev(res)))
+    assert nhip.timer_stop()[0] == 0
+    nhip_env.setenv("NHIP_WINO_XT", "0")
+    assert conv.workspace_size(n, h, w) > 0
+    sep = host(conv.forward(dev(x), residual=dev(res)))
+    exp = oracle_conv(x, wt, b, (1, 1), (1, 1), pad, nhip.ACT_RELU, residual=res)
+    assert_close(got, exp, WINO_RTOL, f"winograd in-kernel transform {case}")
+    assert_close(got, sep, WINO_RTOL, f"winograd in-kernel transform against the transform launch {case}")
+
+
 @pytest.mark.parametrize("algo", [nhip.ALGO_IMPLICIT_GEMM, nhip.ALGO_WINOGRAD])
 def test_config1_single_conv(algo):
     x, wt, b = workloads.conv_single(seed=0)
