@@ -106,9 +106,9 @@ __device__ __forceinline__ float bt_row(float d0, float d1, float d2, float d3, 
 // part).  Per 8-channel chunk the workgroup's 256 (tile, channel) patches
 // are transformed by its 768 threads, thread (tile, channel, g) taking rows
 // 2g, 2g+1: first E = d B along its two patch rows (from registers loaded a
-// chunk ahead) into LDS, then, a barrier later, rows 2g, 2g+1 of V = B^T E
-// down the columns into LDS in the B-fragment layout [36][2][32][4], which
-// the twelve waves read instead of V from memory.  One barrier per chunk:
+// chunk ahead) into LDS, then, a barrier later, columns 2g, 2g+1 of
+// V = B^T E down the columns into LDS in the B-fragment layout
+// [36][2][32][4], which the twelve waves read instead of V from memory.  One barrier per chunk:
 // chunk c's MFMAs, chunk c+1's V rows and chunk c+2's E rows run between
 // two barriers (two slots each for E and V, 147 KB of LDS).
 constexpr int kXtSlot = 36 * 2 * 32 * 4;  // floats of one E or V slot
@@ -215,28 +215,35 @@ __global__ __launch_bounds__(kThreads, 1) void wino_fused_kernel(FusedArgs a) {
     }
   }
   // the two patch rows of chunk c (zero outside the image, past C, past T)
+  // (byte offsets of chunk 0 and per-column validity fixed per thread; the
+  // chunk moves the offset by 8 channel planes)
+  uint32_t xoff[2] = {0u, 0u};
+  if constexpr (XT) {
+#pragma unroll
+    for (int r = 0; r < 2; ++r) xoff[r] = (uint32_t)((xrow0 + (4 * xchq + xcq) * a.H + r) * a.W + xx0) * 4u;
+  }
+  const bool xl_ok = xx0 >= 0, xr_ok = xx0 + 5 < a.W, xm_ok = xx0 + 1 < a.W;
+  const uint32_t xplane8 = (uint32_t)(kCB * a.H * a.W) * 4u;
   auto load_d = [&](int cc, float (&dr)[2][6]) {
-    const int chn = cc * kCB + 4 * xchq + xcq;
-    const bool cok = cc < ce && chn < a.C;
+    const bool cok = (cc < ce) & (cc * kCB + 4 * xchq + xcq < a.C);
+    const uint32_t cofs = (uint32_t)cc * xplane8;
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
-      const bool yok = cok && xrows_ok[r];
-      const int rowi = xrow0 + chn * a.H + r;  // < 2^31 elements (checked on the host)
+      const bool yok = cok & xrows_ok[r];
+      const uint32_t o = xoff[r] + cofs;
       if (a.xvec) {
-        const uint32_t rb = (uint32_t)(rowi * a.W) * 4u;
-        dr[r][0] = buf_load_f32(xr, yok && xx0 >= 0 ? rb + (uint32_t)(xx0 * 4) : kBufOOB);
-        const int4 m = buf_load_b128(xr, yok && xx0 + 1 < a.W ? rb + (uint32_t)((xx0 + 1) * 4) : kBufOOB);
+        dr[r][0] = buf_load_f32(xr, (yok & xl_ok) ? o : kBufOOB);
+        const int4 m = buf_load_b128(xr, (yok & xm_ok) ? o + 4u : kBufOOB);
         dr[r][1] = __builtin_bit_cast(float, m.x);
         dr[r][2] = __builtin_bit_cast(float, m.y);
         dr[r][3] = __builtin_bit_cast(float, m.z);
         dr[r][4] = __builtin_bit_cast(float, m.w);
-        dr[r][5] = buf_load_f32(xr, yok && xx0 + 5 < a.W ? rb + (uint32_t)((xx0 + 5) * 4) : kBufOOB);
+        dr[r][5] = buf_load_f32(xr, (yok & xr_ok) ? o + 20u : kBufOOB);
       } else {
 #pragma unroll
         for (int j = 0; j < 6; ++j) {
-          const int xx = xx0 + j;
-          dr[r][j] = buf_load_f32(
-              xr, yok && (unsigned)xx < (unsigned)a.W ? (uint32_t)(rowi * a.W + xx) * 4u : kBufOOB);
+          const bool jok = (unsigned)(xx0 + j) < (unsigned)a.W;
+          dr[r][j] = buf_load_f32(xr, (yok & jok) ? o + (uint32_t)(4 * j) : kBufOOB);
         }
       }
     }
@@ -258,21 +265,23 @@ __global__ __launch_bounds__(kThreads, 1) void wino_fused_kernel(FusedArgs a) {
   };
   // V rows p = 2G, 2G+1 (V[p][q] = row p of B^T times column q of E) from
   // slot eb into slot vb, layout [xi][chq][tile][cq]
-  auto v_rows = [&](auto gc, const float* eb, float* vb) {
-    constexpr int G = decltype(gc)::value;
+  // V columns q = 2xg, 2xg+1 (V[p][q] = row p of B^T times column q of E)
+  // from slot eb into slot vb, layout [xi][chq][tile][cq]: twelve E values
+  // read, twelve V values written
+  auto v_phase = [&](const float* eb, float* vb) {
 #pragma unroll
-    for (int q = 0; q < 6; ++q) {
+    for (int r = 0; r < 2; ++r) {
+      const int q = 2 * xg + r;
       const float* e = eb + ((q * 2 + xchq) * 32 + xtl) * 4 + xcq;  // E[i][q] at + i * 6 * 256
       const float e0 = e[0], e1 = e[1536], e2 = e[3072], e3 = e[4608], e4 = e[6144], e5 = e[7680];
       float* v = vb + ((q * 2 + xchq) * 32 + xtl) * 4 + xcq;  // V[p][q] at + p * 6 * 256
-      v[(2 * G) * 1536] = bt_row<2 * G>(e0, e1, e2, e3, e4, e5);
-      v[(2 * G + 1) * 1536] = bt_row<2 * G + 1>(e0, e1, e2, e3, e4, e5);
+      v[0 * 1536] = bt_row<0>(e0, e1, e2, e3, e4, e5);
+      v[1 * 1536] = bt_row<1>(e0, e1, e2, e3, e4, e5);
+      v[2 * 1536] = bt_row<2>(e0, e1, e2, e3, e4, e5);
+      v[3 * 1536] = bt_row<3>(e0, e1, e2, e3, e4, e5);
+      v[4 * 1536] = bt_row<4>(e0, e1, e2, e3, e4, e5);
+      v[5 * 1536] = bt_row<5>(e0, e1, e2, e3, e4, e5);
     }
-  };
-  auto v_phase = [&](const float* eb, float* vb) {
-    if (xg == 0) v_rows(std::integral_constant<int, 0>{}, eb, vb);
-    else if (xg == 1) v_rows(std::integral_constant<int, 1>{}, eb, vb);
-    else v_rows(std::integral_constant<int, 2>{}, eb, vb);
   };
   // XT: one chunk's MFMAs with the B fragments from V slot vb, then the
   // next chunk's A operands
