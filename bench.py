@@ -702,8 +702,9 @@ def main():
         },
         "roofline": {
             "bound": "mfma",
-            "kernel": ("wino_fused (36 batched fp32 MFMA GEMMs + output transform per conv; stages "
-                       + ", ".join(f"{c}@{hw}" for c, hw in kernel_convs) + ")") if kernel == "wino_fused"
+            "kernel": ("wino_fused (36 batched fp32 MFMA GEMMs + output transform per conv, at 64@56 the input "
+                       "transform too; stages " + ", ".join(f"{c}@{hw}" for c, hw in kernel_convs) + ")")
+                      if kernel == "wino_fused"
                       else "wino_gemm (36 batched fp32 MFMA GEMMs per conv)",
             "achieved": round(achieved, 3),
             "peak": PEAK_FP32_TFLOPS,

@@ -5,10 +5,17 @@
 // (winograd.hip) in the 4-channel-group layout [36][c_pad/4][t_pad][4]; U
 // is prepacked on the host in the same layout, [36][c_pad/4][m_pad][4].
 //
-// The input transform stays a separate, HBM-bound kernel on purpose: on
+// The input transform: a separate, HBM-bound kernel, except for launches of
+// paired channel blocks (XT below), where the kernel forms V itself.  On
 // gfx950 the fp32 MFMA and fp32 VALU work of the waves on one SIMD do not
 // overlap (measured: a VALU wave beside an MFMA wave adds its whole time),
-// so transforming patches inside the GEMM costs MFMA time.
+// so transforming patches inside the GEMM costs MFMA time; with 64 output
+// channels per workgroup each patch is transformed once for 64 channels'
+// MFMAs, and the transform's VALU work (about a fifth of the MFMA time)
+// costs less than the separate kernel's write and re-read of V (2.25x the
+// input's bytes): 64@56 at batch 32, 17.6 + 30.5 us -> 40.0-40.6 us per
+// conv.  With 32 output channels per workgroup (or channel splits) the same
+// transform work meets half the MFMA work and the separate kernel wins.
 //
 // Work decomposition.  A workgroup owns a block of 32 tiles x 32 output
 // channels and runs 12 waves: wave (p, h) owns row p of the 6 x 6 transform
