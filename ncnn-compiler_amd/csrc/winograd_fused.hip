@@ -98,15 +98,19 @@ __device__ __forceinline__ float activate(float v) {
 // the two 32-channel blocks of a 64-channel block (same tiles) and each
 // runs every chunk; otherwise they share one 32-channel block and take
 // alternate chunks.
-// Row I of B^T (F(4x4, 3x3)) applied to six values.
-template <int I>
-__device__ __forceinline__ float bt_row(float d0, float d1, float d2, float d3, float d4, float d5) {
-  if constexpr (I == 0) return 4.f * d0 - 5.f * d2 + d4;
-  if constexpr (I == 1) return -4.f * (d1 + d2) + d3 + d4;
-  if constexpr (I == 2) return 4.f * (d1 - d2) - d3 + d4;
-  if constexpr (I == 3) return -2.f * (d1 - d3) - d2 + d4;
-  if constexpr (I == 4) return 2.f * (d1 - d3) - d2 + d4;
-  return 4.f * d1 - 5.f * d3 + d5;
+// B^T (F(4x4, 3x3)) applied to six values, the rows sharing their partial
+// sums (14 operations, fused multiply-adds):
+//   o0 = 4 d0 - 5 d2 + d4          o3 = (d4 - d2) - 2 (d1 - d3)
+//   o1 = (d3 + d4) - 4 (d1 + d2)   o4 = (d4 - d2) + 2 (d1 - d3)
+//   o2 = (d4 - d3) + 4 (d1 - d2)   o5 = 4 d1 - 5 d3 + d5
+__device__ __forceinline__ void bt6(float d0, float d1, float d2, float d3, float d4, float d5, float (&o)[6]) {
+  const float a = d4 - d2, b = d1 - d3;
+  o[0] = __builtin_fmaf(4.f, d0, __builtin_fmaf(-5.f, d2, d4));
+  o[1] = __builtin_fmaf(-4.f, d1 + d2, d3 + d4);
+  o[2] = __builtin_fmaf(4.f, d1 - d2, d4 - d3);
+  o[3] = __builtin_fmaf(-2.f, b, a);
+  o[4] = __builtin_fmaf(2.f, b, a);
+  o[5] = __builtin_fmaf(4.f, d1, __builtin_fmaf(-5.f, d3, d5));
 }
 
 // XT: the input transform inside the GEMM (paired channel blocks, one
@@ -121,7 +125,11 @@ __device__ __forceinline__ float bt_row(float d0, float d1, float d2, float d3, 
 constexpr int kXtSlot = 36 * 2 * 32 * 4;  // floats of one E or V slot
 constexpr int kXtLdsBytes = 4 * kXtSlot * (int)sizeof(float);
 
-template <int ACT, bool FINAL, bool VEC, bool KS, bool XT = false>
+// XV (XT only): the input rows are float4-aligned with one column of left
+// padding (a.xvec), so a patch row's centre is one 16-byte load; a template
+// argument rather than a branch, so the loop has one load sequence and the
+// compiler's wait counts stay exact.
+template <int ACT, bool FINAL, bool VEC, bool KS, bool XT = false, bool XV = false>
 __global__ __launch_bounds__(kThreads, 1) void wino_fused_kernel(FusedArgs a) {
   static_assert(!XT || (KS && FINAL), "the in-kernel transform runs paired channel blocks in one part");
   extern __shared__ __attribute__((aligned(16))) float zs[];
@@ -194,9 +202,9 @@ __global__ __launch_bounds__(kThreads, 1) void wino_fused_kernel(FusedArgs a) {
     }
   };
   int c = cb + (KS ? 0 : h);
-#pragma unroll
-  for (int q = 0; q < 6; ++q) load(c, q);
   if constexpr (!XT) {
+#pragma unroll
+    for (int q = 0; q < 6; ++q) load(c, q);
 #pragma unroll
     for (int q = 0; q < 6; ++q) __builtin_amdgcn_sched_group_barrier(0x020, 2, 0);
   }
@@ -207,7 +215,15 @@ __global__ __launch_bounds__(kThreads, 1) void wino_fused_kernel(FusedArgs a) {
   const int xt = t0 + xtl;
   int xrow0 = 0, xx0 = 0;  // (image * C) * H + first patch row; first patch column
   bool xrows_ok[2] = {false, false};
-  float dreg[2][6];
+  // a patch row's six values: column 0, columns 1..4 (one 16-byte load on
+  // the vector path, kept as a vector so that the loaded registers are used
+  // in place and no copy waits for the load), column 5
+  struct XRows {
+    float l[2];
+    v4f m[2];
+    float r[2];
+  };
+  XRows dreg;
   const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, XT ? a.x_bytes : 0u);
   if constexpr (XT) {
     if (xt < a.T) {
@@ -231,43 +247,40 @@ __global__ __launch_bounds__(kThreads, 1) void wino_fused_kernel(FusedArgs a) {
   }
   const bool xl_ok = xx0 >= 0, xr_ok = xx0 + 5 < a.W, xm_ok = xx0 + 1 < a.W;
   const uint32_t xplane8 = (uint32_t)(kCB * a.H * a.W) * 4u;
-  auto load_d = [&](int cc, float (&dr)[2][6]) {
+  auto load_d = [&](int cc, XRows& dr) {
     const bool cok = (cc < ce) & (cc * kCB + 4 * xchq + xcq < a.C);
     const uint32_t cofs = (uint32_t)cc * xplane8;
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
       const bool yok = cok & xrows_ok[r];
       const uint32_t o = xoff[r] + cofs;
-      if (a.xvec) {
-        dr[r][0] = buf_load_f32(xr, (yok & xl_ok) ? o : kBufOOB);
-        const int4 m = buf_load_b128(xr, (yok & xm_ok) ? o + 4u : kBufOOB);
-        dr[r][1] = __builtin_bit_cast(float, m.x);
-        dr[r][2] = __builtin_bit_cast(float, m.y);
-        dr[r][3] = __builtin_bit_cast(float, m.z);
-        dr[r][4] = __builtin_bit_cast(float, m.w);
-        dr[r][5] = buf_load_f32(xr, (yok & xr_ok) ? o + 20u : kBufOOB);
+      dr.l[r] = buf_load_f32(xr, (yok & xl_ok) ? o : kBufOOB);
+      if constexpr (XV) {
+        dr.m[r] = __builtin_bit_cast(
+            v4f, __builtin_amdgcn_raw_buffer_load_b128(xr, (yok & xm_ok) ? o + 4u : kBufOOB, 0, 0));
       } else {
+        v4f m;
 #pragma unroll
-        for (int j = 0; j < 6; ++j) {
-          const bool jok = (unsigned)(xx0 + j) < (unsigned)a.W;
-          dr[r][j] = buf_load_f32(xr, (yok & jok) ? o + (uint32_t)(4 * j) : kBufOOB);
+        for (int j = 0; j < 4; ++j) {
+          const bool jok = (unsigned)(xx0 + 1 + j) < (unsigned)a.W;
+          m[j] = buf_load_f32(xr, (yok & jok) ? o + (uint32_t)(4 * (j + 1)) : kBufOOB);
         }
+        dr.m[r] = m;
       }
+      dr.r[r] = buf_load_f32(xr, (yok & xr_ok) ? o + 20u : kBufOOB);
     }
   };
   // E rows 2xg, 2xg+1 (E[i][q] = row i of d times column q of B) into slot eb,
   // layout [i][q][chq][tile][cq]
-  auto e_phase = [&](float* eb, const float (&dr)[2][6]) {
+  auto e_phase = [&](float* eb, const XRows& dr) {
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
-      const float* d = dr[r];
+      const float d[6] = {dr.l[r], dr.m[r][0], dr.m[r][1], dr.m[r][2], dr.m[r][3], dr.r[r]};
       float* e = eb + ((((2 * xg + r) * 6) * 2 + xchq) * 32 + xtl) * 4 + xcq;
-      e[0 * 256] = bt_row<0>(d[0], d[1], d[2], d[3], d[4], d[5]);
-      e[1 * 256] = bt_row<1>(d[0], d[1], d[2], d[3], d[4], d[5]);
-      e[2 * 256] = bt_row<2>(d[0], d[1], d[2], d[3], d[4], d[5]);
-      e[3 * 256] = bt_row<3>(d[0], d[1], d[2], d[3], d[4], d[5]);
-      e[4 * 256] = bt_row<4>(d[0], d[1], d[2], d[3], d[4], d[5]);
-      e[5 * 256] = bt_row<5>(d[0], d[1], d[2], d[3], d[4], d[5]);
+      float o[6];
+      bt6(d[0], d[1], d[2], d[3], d[4], d[5], o);
+#pragma unroll
+      for (int q = 0; q < 6; ++q) e[q * 256] = o[q];
     }
   };
   // V rows p = 2G, 2G+1 (V[p][q] = row p of B^T times column q of E) from
@@ -282,12 +295,10 @@ __global__ __launch_bounds__(kThreads, 1) void wino_fused_kernel(FusedArgs a) {
       const float* e = eb + ((q * 2 + xchq) * 32 + xtl) * 4 + xcq;  // E[i][q] at + i * 6 * 256
       const float e0 = e[0], e1 = e[1536], e2 = e[3072], e3 = e[4608], e4 = e[6144], e5 = e[7680];
       float* v = vb + ((q * 2 + xchq) * 32 + xtl) * 4 + xcq;  // V[p][q] at + p * 6 * 256
-      v[0 * 1536] = bt_row<0>(e0, e1, e2, e3, e4, e5);
-      v[1 * 1536] = bt_row<1>(e0, e1, e2, e3, e4, e5);
-      v[2 * 1536] = bt_row<2>(e0, e1, e2, e3, e4, e5);
-      v[3 * 1536] = bt_row<3>(e0, e1, e2, e3, e4, e5);
-      v[4 * 1536] = bt_row<4>(e0, e1, e2, e3, e4, e5);
-      v[5 * 1536] = bt_row<5>(e0, e1, e2, e3, e4, e5);
+      float o[6];
+      bt6(e0, e1, e2, e3, e4, e5, o);
+#pragma unroll
+      for (int pp = 0; pp < 6; ++pp) v[pp * 1536] = o[pp];
     }
   };
   // XT: one chunk's MFMAs with the B fragments from V slot vb, then the
@@ -350,12 +361,18 @@ __global__ __launch_bounds__(kThreads, 1) void wino_fused_kernel(FusedArgs a) {
     float* const vs1 = zs + kXtSlot;
     float* const es0 = zs + 2 * kXtSlot;
     float* const es1 = zs + 3 * kXtSlot;
-    // Prologue: the first two chunks' rows requested together, E and V of
-    // chunk 0 and E of chunk 1 formed, chunk 2's rows on their way.
+    // Prologue: the first two chunks' rows requested together, then chunk
+    // 0's A operands, E and V of chunk 0 and E of chunk 1 formed, chunk 2's
+    // rows on their way: the loop is entered with chunk 0's A operands and
+    // chunk 2's rows in flight in that order, as every iteration leaves the
+    // next one, so the compiler's wait counts in the loop are exact (each
+    // MFMA waits for its own A operand only, not for the rows behind it).
     {
-      float d1[2][6];
+      XRows d1;
       load_d(cb, dreg);
       load_d(cb + 1, d1);
+#pragma unroll
+      for (int q = 0; q < 6; ++q) load(cb, q);
       e_phase(es0, dreg);
       __syncthreads();
       v_phase(es0, vs0);
@@ -367,10 +384,12 @@ __global__ __launch_bounds__(kThreads, 1) void wino_fused_kernel(FusedArgs a) {
       const bool odd = ((cc - cb) & 1) != 0;
       chunk_xt(cc, odd ? vs1 : vs0);
       if (cc + 1 < ce) v_phase(odd ? es0 : es1, odd ? vs0 : vs1);
-      if (cc + 2 < ce) {
-        e_phase(odd ? es1 : es0, dreg);
-        load_d(cc + 3, dreg);
-      }
+      if (cc + 2 < ce) e_phase(odd ? es1 : es0, dreg);
+      // unconditional (chunks past the end read nothing, out of range): every
+      // path through the loop then leaves the same loads in flight, and the
+      // compiler's wait before each point's MFMAs counts the rows behind the
+      // A operand instead of waiting for them
+      load_d(cc + 3, dreg);
       __syncthreads();
     }
   } else if (c < ce) {
@@ -525,19 +544,22 @@ __global__ void wino_fused_reduce(ReduceArgs a) {
   }
 }
 
-template <int ACT, bool FINAL, bool VEC, bool KS, bool XT = false>
+template <int ACT, bool FINAL, bool VEC, bool KS, bool XT = false, bool XV = false>
 int launch_one(const FusedArgs& a, int64_t blocks, hipStream_t s) {
   constexpr int lds = XT ? std::max(kXtLdsBytes, kLdsBytes) : kLdsBytes;
-  NHIP_TRY(ensure_dynamic_lds(reinterpret_cast<const void*>(&wino_fused_kernel<ACT, FINAL, VEC, KS, XT>), lds));
-  NHIP_LAUNCH("wino_fused", (wino_fused_kernel<ACT, FINAL, VEC, KS, XT>), dim3((unsigned)blocks), dim3(kThreads),
-              lds, s, a);
+  NHIP_TRY(ensure_dynamic_lds(reinterpret_cast<const void*>(&wino_fused_kernel<ACT, FINAL, VEC, KS, XT, XV>), lds));
+  NHIP_LAUNCH("wino_fused", (wino_fused_kernel<ACT, FINAL, VEC, KS, XT, XV>), dim3((unsigned)blocks),
+              dim3(kThreads), lds, s, a);
   return check_launch("wino_fused");
 }
 
 template <int ACT>
 int launch_xt(const FusedArgs& a, int64_t blocks, hipStream_t s) {
-  return a.OW % 4 == 0 ? launch_one<ACT, true, true, true, true>(a, blocks, s)
-                       : launch_one<ACT, true, false, true, true>(a, blocks, s);
+  if (a.xvec)
+    return a.OW % 4 == 0 ? launch_one<ACT, true, true, true, true, true>(a, blocks, s)
+                         : launch_one<ACT, true, false, true, true, true>(a, blocks, s);
+  return a.OW % 4 == 0 ? launch_one<ACT, true, true, true, true, false>(a, blocks, s)
+                       : launch_one<ACT, true, false, true, true, false>(a, blocks, s);
 }
 
 template <int ACT, bool FINAL>
