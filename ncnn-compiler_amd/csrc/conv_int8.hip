@@ -642,8 +642,14 @@ __global__ __launch_bounds__(kThreads * KP) void conv_int8_rw_kernel(Int8Args g)
       *reinterpret_cast<v4i*>(foot + (fy * g.FW + fx) * g.FS + ch * 16) = v4i{0, 0, 0, 0};
     }
     fq_store(0);
-    fq_load(1);
-    fq_store(1);
+    // the second batch only where the window has more items than the first
+    // covers (not at 128 channels x 6 rows x 28 columns: 1344 items, 1536
+    // slots); run unconditionally, its stores wait for every load in flight,
+    // the weights included, before the barrier
+    if (items > kQB * NT) {
+      fq_load(1);
+      fq_store(1);
+    }
   } else {
 #pragma unroll
     for (int q = 0; q < 8; ++q)
