@@ -340,6 +340,30 @@ def test_winograd_in_kernel_transform(case, nhip_env):
     assert_close(got, sep, WINO_RTOL, f"winograd in-kernel transform against the transform launch {case}")
 
 
+@pytest.mark.parametrize("act", [nhip.ACT_NONE, nhip.ACT_SIGMOID])
+@pytest.mark.parametrize("bias", [True, False])
+def test_winograd_in_kernel_transform_epilogues(act, bias, nhip_env):
+    """The in-kernel transform's other epilogue instances: no activation and
+    sigmoid, with and without bias, no residual; a batch whose tiles end
+    inside a 32-tile block."""
+    n, c, h, w, k = 3, 32, 20, 24, 64
+    nhip_env.setenv("NHIP_WINOGRAD_VARIANT", "2")
+    nhip_env.setenv("NHIP_WINO_KS", "1")
+    nhip_env.setenv("NHIP_WINO_SPLITS", "1")
+    rng = np.random.default_rng(7 + act)
+    x = rng.uniform(-1, 1, (n, c, h, w)).astype(np.float32)
+    wt = workloads.he_normal(rng, (k, c, 3, 3), c * 9)
+    b = rng.normal(0, 0.05, k).astype(np.float32) if bias else None
+    d = nhip.conv_desc(c, k, bias=bias, act=act, algorithm=nhip.ALGO_WINOGRAD)
+    conv = nhip.Conv2dF32(d, wt, b) if bias else nhip.Conv2dF32(d, wt)
+    assert conv.workspace_size(n, h, w) == 0  # the in-kernel transform
+    nhip.timer_start("wino_input")
+    got = host(conv.forward(dev(x)))
+    assert nhip.timer_stop()[0] == 0
+    exp = oracle_conv(x, wt, b, (1, 1), (1, 1), (1, 1, 1, 1), act)
+    assert_close(got, exp, WINO_RTOL, f"winograd in-kernel transform act {act} bias {bias}")
+
+
 @pytest.mark.parametrize("algo", [nhip.ALGO_IMPLICIT_GEMM, nhip.ALGO_WINOGRAD])
 def test_config1_single_conv(algo):
     x, wt, b = workloads.conv_single(seed=0)
