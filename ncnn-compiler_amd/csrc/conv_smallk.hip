@@ -256,12 +256,16 @@ int launch_conv_smallk(const nhip_conv_plan* p, const float* in, const float* re
   a.npix = n * oh * ow;
   a.nblk = (int)ceil_div(a.npix, 32);
   if (a.npix == 0) return ok();
-  // One wave per SIMD (grid-stride over the blocks), fewer only when there
-  // are fewer blocks: on the 224x224 stem at batch 32 (12544 blocks), 1024
-  // waves took 23.2 us, 1568 (two on half of the SIMDs) 26.0 us, 768 29.7 us;
-  // two-block-deep and three-block-deep gather rings were 1.2 and 2.3 us
-  // slower than the one-block-ahead pair of buffers kept here.
-  const int64_t waves = std::min<int64_t>(a.nblk, 4LL * cu_count());
+  // Two waves per SIMD (grid-stride over the blocks) where each still gets
+  // two blocks or more, else one; fewer only when there are fewer blocks.
+  // The 224x224 stem at batch 32 (12544 blocks) in the MobileNetV2 graph:
+  // 2048 waves 27.6-28.0 us, 1024 31.0-31.3 us, 3072 35.9-36.3 us (four or
+  // five blocks a wave); standalone, 1024 waves took 23.2 us, 1568 (two on
+  // half of the SIMDs) 26.0 us, 768 29.7 us.  Two-block-deep and
+  // three-block-deep gather rings were 1.2 and 2.3 us slower than the
+  // one-block-ahead pair of buffers kept here.
+  const int per_cu = a.nblk >= 16LL * cu_count() ? 8 : 4;
+  const int64_t waves = std::min<int64_t>(a.nblk, (int64_t)per_cu * cu_count());
   const dim3 grid((unsigned)ceil_div(waves, kThreads / 64));
   if (p->kred_pad <= 16) launch_steps<8>(a, p->g.act, grid, s);
   else launch_steps<16>(a, p->g.act, grid, s);
