@@ -112,6 +112,7 @@ __global__ __launch_bounds__(64 * WAVES) void conv_kq_kernel(KqArgs g) {
   // behind its 36-step operand set and with the index divisions ahead of the
   // first MFMA, the 1x64x56x56 layer measured 7.3-7.7 us against 6.6-6.8).
   constexpr int NE = 1024 / (64 * WAVES);
+  static_assert(NE * 64 * WAVES == 1024, "the block's 1024 entries split evenly over the threads");
   constexpr bool kEarly = TAPS == 1;
   uint32_t eoff[NE];
   float ebias[NE], eres[NE];
